@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X polynomial transcendental kernels (one GPU).
+
+Headline workload ("B1 dense SiLU, FP16"): the
+degree-3 polynomial SiLU forward on Llama-8B MLP gate activations
+[8192 tokens, 14336] drawn N(0, 2^2), resident in HBM.  One step = one pass
+of the kernel over the whole tensor.  `value` is Gelem/s over the K timed
+steps.  Alongside it the JSON line carries
+
+* `roofline`: algorithmic bytes (2 B read + 2 B written per element) per
+  launch / average kernel time (HIP events on the launch stream) against the
+  8 TB/s HBM peak, and the HBM traffic per launch measured by rocprofv3
+  counters when a committed profile holds it;
+* `cpu_baseline`: the CPU oracle (a C restatement of the same program, all
+  host threads) timed on a bounded sample of the same tensor;
+* `functions`: the per-function sweep, polynomial vs native, at an
+  L2-resident size and at 2^28 elements (HBM), plus the B3 config.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "fast-polynomial-transcendentals_amd", "python"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Gelem/s + % HBM roofline per function, poly vs native, L2 and HBM, 1 MI355X"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-sweep", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--sweep-reps", type=int, default=50)
+    return p.parse_args()
+
+
+def _capi():
+    import ctypes
+
+    import torch  # noqa: F401  (HIP runtime first)
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "fast-polynomial-transcendentals_amd", "python",
+                                   "libspline_hip.so"))
+    return lib
+
+
+def time_launches(launch, reps: int, warmup: int):
+    """Average ms per launch over `reps` launches, HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        launch()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def make_unary(lib, name, out, x):
+    import ctypes
+
+    import torch
+
+    fn = getattr(lib, name)
+    fn.restype = ctypes.c_int
+    args = (ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+            ctypes.c_int64(x.numel()))
+
+    def launch():
+        rc = fn(*args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"{name} failed with {rc}")
+
+    return launch
+
+
+def read_traffic(kernel_tag: str):
+    """HBM bytes per launch from the committed rocprofv3 counter summary."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel_tag)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(x_cpu_fp16, target_s: float = 10.0):
+    """Oracle (C restatement, OpenMP) on a bounded sample of the workload."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc  # CPU baseline leg only
+
+    sample = x_cpu_fp16.reshape(-1)[: 1 << 24].contiguous()
+    bits = sample.view(__import__("torch").int16).numpy().view(np.uint16)
+    orc.activation("swish", orc.FWD, 3, "f16", bits[:4096])  # load + warm
+    done, t0 = 0, time.perf_counter()
+    while True:
+        orc.activation("swish", orc.FWD, 3, "f16", bits)
+        done += bits.size
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    return {
+        "value": done / el / 1e9,
+        "unit": "Gelem/s",
+        "cores": orc.num_threads(),
+        "kind": "port",
+        "sample": (f"SiLU D3 FP16 oracle on the first 2^24 elements of the [8192,14336] N(0,2^2) "
+                   f"tensor, {done // bits.size} passes in {el:.1f} s"),
+    }
+
+
+def sweep(lib, reps: int):
+    import torch
+
+    out = []
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    for n_log2, regime in ((20, "l2"), (28, "hbm")):
+        n = 1 << n_log2
+        base = (torch.randn(n, generator=g) * 2.0) if n_log2 <= 20 else None
+        for dtype, sfx in ((torch.float16, ""), (torch.bfloat16, "_bf16")):
+            if base is not None:
+                x = base.to(dtype).to(dev)
+            else:
+                x = (torch.randn(n, device=dev) * 2.0).to(dtype)
+            y = torch.empty_like(x)
+            for fam, deg in (("sigmoid", 3), ("tanh", 4), ("swish", 3)):
+                row = {"function": f"{fam}_fwd", "dtype": "fp16" if not sfx else "bf16",
+                       "elements": n, "regime": regime}
+                for label, name in (("poly", f"launch_{fam}_fwd_d{deg}_kernel{sfx}"),
+                                    ("native", f"launch_{fam}_fwd_native_kernel{sfx}")):
+                    ms = time_launches(make_unary(lib, name, y, x), reps, 5)
+                    row[f"{label}_us"] = round(ms * 1e3, 3)
+                    row[f"{label}_gelem_s"] = round(n / ms / 1e6, 2)
+                    row[f"{label}_gbs"] = round(4 * n / ms / 1e6, 1)
+                row["degree"] = deg
+                row["poly_frac_hbm_peak"] = round(row["poly_gbs"] / HBM_PEAK_GBS, 4)
+                row["speedup"] = round(row["native_us"] / row["poly_us"], 3)
+                out.append(row)
+            del x, y
+            torch.cuda.empty_cache()
+    # B3 (config 0): 2^20 BF16 scores U[-16,16] seed 0 -> y, dy.
+    import ctypes
+    gs = torch.Generator().manual_seed(0)
+    s = (torch.rand(1 << 20, generator=gs) * 32 - 16).to(torch.bfloat16).to(dev)
+    y, dy = torch.empty_like(s), torch.empty_like(s)
+    fn = lib.launch_flash_sigmoid_direct_d3_d4_bf16
+    fn.restype = ctypes.c_int
+
+    def b3():
+        fn(ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(dy.data_ptr()),
+           ctypes.c_void_p(s.data_ptr()), ctypes.c_int64(s.numel()),
+           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+    ms = time_launches(b3, reps, 5)
+    out.append({"function": "b3_direct_d3_d4", "dtype": "bf16", "elements": s.numel(),
+                "regime": "l2", "poly_us": round(ms * 1e3, 3),
+                "poly_gelem_s": round(s.numel() / ms / 1e6, 2),
+                "poly_gbs": round(6 * s.numel() / ms / 1e6, 1)})
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the elementwise path needs no cross-GPU exchange; see DESIGN.md for sharding).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    lib = _capi()
+    dev = torch.device("cuda:0")
+
+    # Synthetic B1 gate activations [8192, 14336] ~ N(0, 2^2), FP16, in HBM.
+    rows, cols = 8192, 14336
+    g = torch.Generator(device="cpu").manual_seed(0)
+    x_cpu = (torch.randn(rows, cols, generator=g) * 2.0).to(torch.float16)
+    x = x_cpu.to(dev)
+    y = torch.empty_like(x)
+    n = x.numel()
+    launch = make_unary(lib, "launch_swish_fwd_d3_kernel", y, x)
+
+    for _ in range(args.warmup):
+        launch()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        launch()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    value = n / (ms_per_step * 1e-3) / 1e9
+
+    achieved_gbs = 4.0 * n / (ms_per_step * 1e-3) / 1e9
+    traffic = read_traffic("swish_fwd_d3_f16_b1")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "Gelem/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,2^2) gate activations, seed 0",
+        "config": {"workload": "B1 dense SiLU D3 forward, FP16 [8192,14336] (BASELINE config 1)",
+                   "elements": n, "kernel": "launch_swish_fwd_d3_kernel"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(x_cpu)
+    if not args.no_sweep:
+        line["functions"] = sweep(lib, args.sweep_reps)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

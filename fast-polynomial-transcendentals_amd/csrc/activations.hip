@@ -1,0 +1,56 @@
+// activations.hip -- C ABI of the unary activation programs and their
+// derivative programs (sigmoid, tanh, SiLU; FP16 and BF16; degrees 3..6,
+// native baselines and algebraic derivatives).
+#include <hip/hip_runtime.h>
+
+#include "ops.hpp"
+#include "spline_ops_hip.h"
+
+using namespace pt;
+
+#define PT_UNARY(name, PROG)                                                     \
+    extern "C" int name(void* out, const void* in, int64_t size, void* stream) { \
+        return run1<UnaryOp<PT_STRIP PROG>>(out, in, size, stream);              \
+    }
+
+#define PT_UNARY_FAMILY(fam, FAM)                                           \
+    PT_UNARY(launch_##fam##_fwd_d3_kernel, (F16Prog<FAM, kFwd, 3>))         \
+    PT_UNARY(launch_##fam##_fwd_d4_kernel, (F16Prog<FAM, kFwd, 4>))         \
+    PT_UNARY(launch_##fam##_fwd_d5_kernel, (F16Prog<FAM, kFwd, 5>))         \
+    PT_UNARY(launch_##fam##_fwd_d6_kernel, (F16Prog<FAM, kFwd, 6>))         \
+    PT_UNARY(launch_##fam##_fwd_d3_kernel_bf16, (BF16Prog<FAM, kFwd, 3>))   \
+    PT_UNARY(launch_##fam##_fwd_d4_kernel_bf16, (BF16Prog<FAM, kFwd, 4>))   \
+    PT_UNARY(launch_##fam##_fwd_d5_kernel_bf16, (BF16Prog<FAM, kFwd, 5>))   \
+    PT_UNARY(launch_##fam##_fwd_d6_kernel_bf16, (BF16Prog<FAM, kFwd, 6>))   \
+    PT_UNARY(launch_##fam##_fwd_native_kernel, (F16Native<FAM, kFwd>))      \
+    PT_UNARY(launch_##fam##_fwd_native_kernel_bf16, (BF16Native<FAM, kFwd>))
+
+PT_UNARY_FAMILY(sigmoid, kSigmoid)
+PT_UNARY_FAMILY(tanh, kTanh)
+PT_UNARY_FAMILY(swish, kSwishFam)
+
+#define PT_BINARY(name, OP)                                                                \
+    extern "C" int name(void* grad_in, const void* grad_out, const void* in, int64_t size, \
+                        void* stream) {                                                    \
+        return run2<PT_STRIP OP>(grad_in, grad_out, in, size, stream);                     \
+    }
+
+#define PT_BINARY_FAMILY(fam, FAM)                                                    \
+    PT_BINARY(launch_##fam##_bwd_d3_kernel, (F16MulOp<F16Prog<FAM, kBwd, 3>>))        \
+    PT_BINARY(launch_##fam##_bwd_d4_kernel, (F16MulOp<F16Prog<FAM, kBwd, 4>>))        \
+    PT_BINARY(launch_##fam##_bwd_d5_kernel, (F16MulOp<F16Prog<FAM, kBwd, 5>>))        \
+    PT_BINARY(launch_##fam##_bwd_d6_kernel, (F16MulOp<F16Prog<FAM, kBwd, 6>>))        \
+    PT_BINARY(launch_##fam##_bwd_d3_kernel_bf16, (BF16MulOp<BF16Prog<FAM, kBwd, 3>>)) \
+    PT_BINARY(launch_##fam##_bwd_d4_kernel_bf16, (BF16MulOp<BF16Prog<FAM, kBwd, 4>>)) \
+    PT_BINARY(launch_##fam##_bwd_d5_kernel_bf16, (BF16MulOp<BF16Prog<FAM, kBwd, 5>>)) \
+    PT_BINARY(launch_##fam##_bwd_d6_kernel_bf16, (BF16MulOp<BF16Prog<FAM, kBwd, 6>>))
+
+PT_BINARY_FAMILY(sigmoid, kSigmoid)
+PT_BINARY_FAMILY(tanh, kTanh)
+PT_BINARY_FAMILY(swish, kSwishFam)
+PT_BINARY(launch_swish_bwd_native_kernel, (F16MulOp<F16Native<kSwishFam, kBwd>>))
+PT_BINARY(launch_swish_bwd_native_kernel_bf16, (BF16MulOp<BF16Native<kSwishFam, kBwd>>))
+PT_BINARY(launch_sigmoid_bwd_alg_kernel, (F16MulOp<F16Alg<kSigmoid>>))
+PT_BINARY(launch_sigmoid_bwd_alg_kernel_bf16, (BF16MulOp<BF16Alg<kSigmoid>>))
+PT_BINARY(launch_tanh_bwd_alg_kernel, (F16MulOp<F16Alg<kTanh>>))
+PT_BINARY(launch_tanh_bwd_alg_kernel_bf16, (BF16MulOp<BF16Alg<kTanh>>))

@@ -1,0 +1,602 @@
+// spline_ops.cpp -- PyTorch-ROCm binding of the MI355X polynomial kernels.
+//
+// Mirrors the reference extension's Python surface
+// (autonumerics_zero/spline_ops/spline_ops.cpp:2212-2452): the pybind
+// functions keep their names, argument order, defaults and error messages,
+// and TORCH_LIBRARY(spline_ops) registers the same schemas with the same
+// AutogradCUDA / CUDA split (on ROCm the HIP device uses the CUDA dispatch
+// keys).  All compute goes through the C ABI of libspline_hip.so
+// (include/spline_ops_hip.h); nothing here computes on the host.
+#include <torch/extension.h>
+#include <torch/library.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <string>
+#include <vector>
+
+#include "spline_ops_hip.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// checks (spline_ops.cpp:293-323)
+// ---------------------------------------------------------------------------
+
+#define CHECK_CUDA(x) TORCH_CHECK(x.is_cuda(), #x " must be a CUDA tensor")
+#define CHECK_CONTIGUOUS(x) TORCH_CHECK(x.is_contiguous(), #x " must be contiguous")
+#define CHECK_HALF_OR_BF16(x)                                              \
+    TORCH_CHECK(x.scalar_type() == at::kHalf || x.scalar_type() == at::kBFloat16, \
+                #x " must be float16 or bfloat16")
+#define CHECK_INPUT(x) \
+    CHECK_CUDA(x);     \
+    CHECK_CONTIGUOUS(x); \
+    CHECK_HALF_OR_BF16(x)
+
+bool spline_env_flag(const char* name) {
+    const char* v = std::getenv(name);
+    if (v == nullptr || v[0] == '\0') return false;
+    for (const char* on : {"1", "true", "TRUE", "yes", "YES", "on", "ON"})
+        if (std::strcmp(v, on) == 0) return true;
+    return false;
+}
+
+void* current_stream(const at::Tensor& t) {
+    return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+// Launch-status check; with SPLINE_OPS_SYNC_DEBUG set, also synchronise the
+// stream unless it is being captured into a graph.
+void check_launch(int rc, void* stream) {
+    TORCH_CHECK(rc == 0, "spline_ops HIP launch failed: ",
+                hipGetErrorString(static_cast<hipError_t>(rc)));
+    if (spline_env_flag("SPLINE_OPS_SYNC_DEBUG")) {
+        auto s = reinterpret_cast<hipStream_t>(stream);
+        hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+        TORCH_CHECK(hipStreamIsCapturing(s, &status) == hipSuccess, "hipStreamIsCapturing failed");
+        if (status == hipStreamCaptureStatusNone) {
+            const hipError_t err = hipStreamSynchronize(s);
+            TORCH_CHECK(err == hipSuccess, "spline_ops kernel failed: ", hipGetErrorString(err));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launcher tables
+// ---------------------------------------------------------------------------
+
+using Unary = int (*)(void*, const void*, int64_t, void*);
+using Binary = int (*)(void*, const void*, const void*, int64_t, void*);
+using SwishMulBwd = int (*)(void*, void*, const void*, const void*, const void*, int64_t, void*);
+using PackedFwd = int (*)(void*, const void*, int64_t, int64_t, void*);
+using PackedBwd = int (*)(void*, const void*, const void*, int64_t, int64_t, void*);
+
+enum Fam { SIGMOID = 0, TANH = 1, SWISH = 2 };
+const char* kFamName[] = {"sigmoid", "tanh", "swish"};
+
+// [family][bf16][degree]; degree 0 = native.
+Unary kFwd[3][2][7] = {
+    {{launch_sigmoid_fwd_native_kernel, nullptr, nullptr, launch_sigmoid_fwd_d3_kernel,
+      launch_sigmoid_fwd_d4_kernel, launch_sigmoid_fwd_d5_kernel, launch_sigmoid_fwd_d6_kernel},
+     {launch_sigmoid_fwd_native_kernel_bf16, nullptr, nullptr, launch_sigmoid_fwd_d3_kernel_bf16,
+      launch_sigmoid_fwd_d4_kernel_bf16, launch_sigmoid_fwd_d5_kernel_bf16,
+      launch_sigmoid_fwd_d6_kernel_bf16}},
+    {{launch_tanh_fwd_native_kernel, nullptr, nullptr, launch_tanh_fwd_d3_kernel,
+      launch_tanh_fwd_d4_kernel, launch_tanh_fwd_d5_kernel, launch_tanh_fwd_d6_kernel},
+     {launch_tanh_fwd_native_kernel_bf16, nullptr, nullptr, launch_tanh_fwd_d3_kernel_bf16,
+      launch_tanh_fwd_d4_kernel_bf16, launch_tanh_fwd_d5_kernel_bf16,
+      launch_tanh_fwd_d6_kernel_bf16}},
+    {{launch_swish_fwd_native_kernel, nullptr, nullptr, launch_swish_fwd_d3_kernel,
+      launch_swish_fwd_d4_kernel, launch_swish_fwd_d5_kernel, launch_swish_fwd_d6_kernel},
+     {launch_swish_fwd_native_kernel_bf16, nullptr, nullptr, launch_swish_fwd_d3_kernel_bf16,
+      launch_swish_fwd_d4_kernel_bf16, launch_swish_fwd_d5_kernel_bf16,
+      launch_swish_fwd_d6_kernel_bf16}},
+};
+
+Binary kBwd[3][2][7] = {
+    {{nullptr, nullptr, nullptr, launch_sigmoid_bwd_d3_kernel, launch_sigmoid_bwd_d4_kernel,
+      launch_sigmoid_bwd_d5_kernel, launch_sigmoid_bwd_d6_kernel},
+     {nullptr, nullptr, nullptr, launch_sigmoid_bwd_d3_kernel_bf16,
+      launch_sigmoid_bwd_d4_kernel_bf16, launch_sigmoid_bwd_d5_kernel_bf16,
+      launch_sigmoid_bwd_d6_kernel_bf16}},
+    {{nullptr, nullptr, nullptr, launch_tanh_bwd_d3_kernel, launch_tanh_bwd_d4_kernel,
+      launch_tanh_bwd_d5_kernel, launch_tanh_bwd_d6_kernel},
+     {nullptr, nullptr, nullptr, launch_tanh_bwd_d3_kernel_bf16, launch_tanh_bwd_d4_kernel_bf16,
+      launch_tanh_bwd_d5_kernel_bf16, launch_tanh_bwd_d6_kernel_bf16}},
+    {{launch_swish_bwd_native_kernel, nullptr, nullptr, launch_swish_bwd_d3_kernel,
+      launch_swish_bwd_d4_kernel, launch_swish_bwd_d5_kernel, launch_swish_bwd_d6_kernel},
+     {launch_swish_bwd_native_kernel_bf16, nullptr, nullptr, launch_swish_bwd_d3_kernel_bf16,
+      launch_swish_bwd_d4_kernel_bf16, launch_swish_bwd_d5_kernel_bf16,
+      launch_swish_bwd_d6_kernel_bf16}},
+};
+
+Binary kSwishMul[2][7] = {
+    {launch_swish_mul_fwd_native_kernel, nullptr, nullptr, launch_swish_mul_fwd_d3_kernel,
+     launch_swish_mul_fwd_d4_kernel, launch_swish_mul_fwd_d5_kernel, launch_swish_mul_fwd_d6_kernel},
+    {launch_swish_mul_fwd_native_kernel_bf16, nullptr, nullptr,
+     launch_swish_mul_fwd_d3_kernel_bf16, launch_swish_mul_fwd_d4_kernel_bf16,
+     launch_swish_mul_fwd_d5_kernel_bf16, launch_swish_mul_fwd_d6_kernel_bf16},
+};
+
+SwishMulBwd kSwishMulBwd[2][7] = {
+    {launch_swish_mul_bwd_native_kernel, nullptr, nullptr, launch_swish_mul_bwd_d3_kernel,
+     launch_swish_mul_bwd_d4_kernel, launch_swish_mul_bwd_d5_kernel, launch_swish_mul_bwd_d6_kernel},
+    {launch_swish_mul_bwd_native_kernel_bf16, nullptr, nullptr,
+     launch_swish_mul_bwd_d3_kernel_bf16, launch_swish_mul_bwd_d4_kernel_bf16,
+     launch_swish_mul_bwd_d5_kernel_bf16, launch_swish_mul_bwd_d6_kernel_bf16},
+};
+
+PackedFwd kPackedFwd[2][7] = {
+    {launch_swish_mul_packed_fwd_native_kernel, nullptr, nullptr,
+     launch_swish_mul_packed_fwd_d3_kernel, launch_swish_mul_packed_fwd_d4_kernel,
+     launch_swish_mul_packed_fwd_d5_kernel, launch_swish_mul_packed_fwd_d6_kernel},
+    {launch_swish_mul_packed_fwd_native_kernel_bf16, nullptr, nullptr,
+     launch_swish_mul_packed_fwd_d3_kernel_bf16, launch_swish_mul_packed_fwd_d4_kernel_bf16,
+     launch_swish_mul_packed_fwd_d5_kernel_bf16, launch_swish_mul_packed_fwd_d6_kernel_bf16},
+};
+
+PackedBwd kPackedBwd[2][7] = {
+    {launch_swish_mul_packed_bwd_native_kernel, nullptr, nullptr,
+     launch_swish_mul_packed_bwd_d3_kernel, launch_swish_mul_packed_bwd_d4_kernel,
+     launch_swish_mul_packed_bwd_d5_kernel, launch_swish_mul_packed_bwd_d6_kernel},
+    {launch_swish_mul_packed_bwd_native_kernel_bf16, nullptr, nullptr,
+     launch_swish_mul_packed_bwd_d3_kernel_bf16, launch_swish_mul_packed_bwd_d4_kernel_bf16,
+     launch_swish_mul_packed_bwd_d5_kernel_bf16, launch_swish_mul_packed_bwd_d6_kernel_bf16},
+};
+
+// spline_ops.cpp:1179-1185
+int normalize_coeff_source_id(int64_t coeff_source_id) {
+    TORCH_CHECK(coeff_source_id == 0 || coeff_source_id == 1,
+                "coeff_source_id must be 0 (current) or 1 (sollya)");
+    return static_cast<int>(coeff_source_id);
+}
+
+// Resolution rules of resolve_*_launcher (spline_ops.cpp:1187-1502): FP16
+// accepts only the current coefficient source; degree 0 (native) exists for
+// the SiLU family only.  The Sollya BF16 coefficient set is not part of this
+// library.
+template <class T>
+T resolve(T (&table)[2][7], at::ScalarType dtype, int64_t degree, int coeff_source,
+          const char* what, bool allow_native) {
+    const bool bf = dtype == at::kBFloat16;
+    if (!bf) {
+        TORCH_CHECK(coeff_source == 0, "FP16 spline kernels only support coeff_source=current");
+    }
+    TORCH_CHECK(coeff_source == 0,
+                "coeff_source=sollya (BF16 Sollya coefficient set) is not available in the "
+                "MI355X spline_ops build");
+    const bool ok = (degree >= 3 && degree <= 6) || (degree == 0 && allow_native);
+    TORCH_CHECK(ok && table[bf][degree] != nullptr, "Unsupported ", what, " degree: ", degree);
+    return table[bf][degree];
+}
+
+at::ScalarType check_same(const at::Tensor& a, const at::Tensor& b, const char* msg_dtype,
+                          const char* msg_numel) {
+    TORCH_CHECK(a.scalar_type() == b.scalar_type(), msg_dtype);
+    TORCH_CHECK(a.numel() == b.numel(), msg_numel);
+    return a.scalar_type();
+}
+
+// ---------------------------------------------------------------------------
+// unary / binary entry points
+// ---------------------------------------------------------------------------
+
+at::Tensor run_unary(const at::Tensor& x, Unary fn) {
+    c10::OptionalDeviceGuard guard(x.device());
+    at::Tensor out = at::empty_like(x);
+    void* s = current_stream(x);
+    check_launch(fn(out.data_ptr(), x.data_ptr(), x.numel(), s), s);
+    return out;
+}
+
+at::Tensor run_binary(const at::Tensor& go, const at::Tensor& x, Binary fn) {
+    c10::OptionalDeviceGuard guard(x.device());
+    at::Tensor gi = at::empty_like(x);
+    void* s = current_stream(x);
+    check_launch(fn(gi.data_ptr(), go.data_ptr(), x.data_ptr(), x.numel(), s), s);
+    return gi;
+}
+
+at::Tensor fwd_fixed(at::Tensor x, int fam, int degree) {
+    CHECK_INPUT(x);
+    return run_unary(x, kFwd[fam][x.scalar_type() == at::kBFloat16][degree]);
+}
+
+at::Tensor bwd_fixed(at::Tensor grad_out, at::Tensor x, int fam, int degree) {
+    CHECK_INPUT(grad_out);
+    CHECK_INPUT(x);
+    check_same(grad_out, x, "grad_out and x must have the same dtype",
+               "grad_out and x must have the same number of elements");
+    return run_binary(grad_out, x, kBwd[fam][x.scalar_type() == at::kBFloat16][degree]);
+}
+
+at::Tensor fwd_variant(at::Tensor x, int64_t degree, int64_t coeff_source_id, int fam) {
+    CHECK_INPUT(x);
+    std::string what = std::string(kFamName[fam]) + " forward";
+    Unary fn = resolve(kFwd[fam], x.scalar_type(), degree,
+                       normalize_coeff_source_id(coeff_source_id), what.c_str(), fam == SWISH);
+    return run_unary(x, fn);
+}
+
+at::Tensor bwd_variant(at::Tensor grad_out, at::Tensor x, int64_t degree, int64_t coeff_source_id,
+                       int fam) {
+    CHECK_INPUT(grad_out);
+    CHECK_INPUT(x);
+    check_same(grad_out, x, "grad_out and x must have the same dtype",
+               "grad_out and x must have the same number of elements");
+    std::string what = std::string(kFamName[fam]) + " backward";
+    Binary fn = resolve(kBwd[fam], x.scalar_type(), degree,
+                        normalize_coeff_source_id(coeff_source_id), what.c_str(), fam == SWISH);
+    return run_binary(grad_out, x, fn);
+}
+
+at::Tensor bwd_alg(at::Tensor grad_out, at::Tensor y, int fam) {
+    CHECK_INPUT(grad_out);
+    CHECK_INPUT(y);
+    check_same(grad_out, y, "grad_out and y must have the same dtype",
+               "grad_out and y must have the same number of elements");
+    const bool bf = y.scalar_type() == at::kBFloat16;
+    Binary fn = fam == SIGMOID ? (bf ? launch_sigmoid_bwd_alg_kernel_bf16 : launch_sigmoid_bwd_alg_kernel)
+                               : (bf ? launch_tanh_bwd_alg_kernel_bf16 : launch_tanh_bwd_alg_kernel);
+    return run_binary(grad_out, y, fn);
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU entry points (spline_ops.cpp:1645-1828)
+// ---------------------------------------------------------------------------
+
+at::Tensor swish_mul_fwd_variant(at::Tensor gate, at::Tensor up, int64_t degree,
+                                 int64_t coeff_source_id) {
+    CHECK_INPUT(gate);
+    CHECK_INPUT(up);
+    TORCH_CHECK(gate.scalar_type() == up.scalar_type(), "gate and up must have the same dtype");
+    TORCH_CHECK(gate.numel() == up.numel(), "gate and up must have the same number of elements");
+    Binary fn = resolve(kSwishMul, gate.scalar_type(), degree,
+                        normalize_coeff_source_id(coeff_source_id), "swish_mul forward", true);
+    c10::OptionalDeviceGuard guard(gate.device());
+    at::Tensor out = at::empty_like(up);
+    void* s = current_stream(gate);
+    check_launch(fn(out.data_ptr(), gate.data_ptr(), up.data_ptr(), gate.numel(), s), s);
+    return out;
+}
+
+std::vector<at::Tensor> swish_mul_bwd_variant(at::Tensor grad_out, at::Tensor gate, at::Tensor up,
+                                              int64_t degree, int64_t coeff_source_id) {
+    CHECK_INPUT(grad_out);
+    CHECK_INPUT(gate);
+    CHECK_INPUT(up);
+    TORCH_CHECK(gate.scalar_type() == up.scalar_type(), "gate and up must have the same dtype");
+    TORCH_CHECK(grad_out.scalar_type() == gate.scalar_type(),
+                "grad_out and gate must have the same dtype");
+    TORCH_CHECK(gate.numel() == up.numel(), "gate and up must have the same number of elements");
+    TORCH_CHECK(grad_out.numel() == gate.numel(),
+                "grad_out and gate must have the same number of elements");
+    SwishMulBwd fn = resolve(kSwishMulBwd, gate.scalar_type(), degree,
+                             normalize_coeff_source_id(coeff_source_id), "swish_mul backward", true);
+    c10::OptionalDeviceGuard guard(gate.device());
+    at::Tensor grad_gate = at::empty_like(gate);
+    at::Tensor grad_up = at::empty_like(up);
+    void* s = current_stream(gate);
+    check_launch(fn(grad_gate.data_ptr(), grad_up.data_ptr(), grad_out.data_ptr(), gate.data_ptr(),
+                    up.data_ptr(), gate.numel(), s),
+                 s);
+    return {grad_gate, grad_up};
+}
+
+at::Tensor swish_mul_packed_fwd_variant(at::Tensor packed, int64_t degree,
+                                        int64_t coeff_source_id) {
+    CHECK_INPUT(packed);
+    TORCH_CHECK(packed.dim() >= 1, "packed gate/up tensor must have at least one dimension");
+    const int64_t packed_hidden_size = packed.size(-1);
+    TORCH_CHECK((packed_hidden_size % 2) == 0, "packed gate/up last dimension must be even");
+    const int64_t hidden_size = packed_hidden_size / 2;
+    TORCH_CHECK((hidden_size % 2) == 0, "packed SwiGLU hidden size must be even");
+    std::vector<int64_t> out_sizes(packed.sizes().begin(), packed.sizes().end());
+    out_sizes.back() = hidden_size;
+    c10::OptionalDeviceGuard guard(packed.device());
+    at::Tensor out = at::empty(out_sizes, packed.options());
+    if (packed.numel() == 0) return out;
+    const int64_t rows = packed.numel() / packed_hidden_size;
+    PackedFwd fn = resolve(kPackedFwd, packed.scalar_type(), degree,
+                           normalize_coeff_source_id(coeff_source_id), "swish_mul_packed forward",
+                           true);
+    void* s = current_stream(packed);
+    check_launch(fn(out.data_ptr(), packed.data_ptr(), rows, hidden_size, s), s);
+    return out;
+}
+
+at::Tensor swish_mul_packed_bwd_variant(at::Tensor grad_out, at::Tensor packed, int64_t degree,
+                                        int64_t coeff_source_id) {
+    CHECK_INPUT(grad_out);
+    CHECK_INPUT(packed);
+    TORCH_CHECK(packed.dim() >= 1, "packed gate/up tensor must have at least one dimension");
+    TORCH_CHECK(grad_out.dim() == packed.dim(), "grad_out and packed must have the same rank");
+    TORCH_CHECK(grad_out.scalar_type() == packed.scalar_type(),
+                "grad_out and packed must have the same dtype");
+    const int64_t packed_hidden_size = packed.size(-1);
+    TORCH_CHECK((packed_hidden_size % 2) == 0, "packed gate/up last dimension must be even");
+    const int64_t hidden_size = packed_hidden_size / 2;
+    TORCH_CHECK((hidden_size % 2) == 0, "packed SwiGLU hidden size must be even");
+    TORCH_CHECK(grad_out.size(-1) == hidden_size,
+                "grad_out last dimension must be half the packed last dimension");
+    for (int64_t d = 0; d + 1 < packed.dim(); ++d)
+        TORCH_CHECK(grad_out.size(d) == packed.size(d),
+                    "grad_out and packed leading dimensions must match");
+    c10::OptionalDeviceGuard guard(packed.device());
+    at::Tensor grad_packed = at::empty_like(packed);
+    if (packed.numel() == 0) return grad_packed;
+    const int64_t rows = packed.numel() / packed_hidden_size;
+    PackedBwd fn = resolve(kPackedBwd, packed.scalar_type(), degree,
+                           normalize_coeff_source_id(coeff_source_id), "swish_mul_packed backward",
+                           true);
+    void* s = current_stream(packed);
+    check_launch(fn(grad_packed.data_ptr(), grad_out.data_ptr(), packed.data_ptr(), rows,
+                    hidden_size, s),
+                 s);
+    return grad_packed;
+}
+
+// ---------------------------------------------------------------------------
+// B3 deployed direct-D3 / factored-D4 program
+// ---------------------------------------------------------------------------
+
+std::vector<at::Tensor> flash_sigmoid_direct_d3_d4(at::Tensor scores) {
+    CHECK_CUDA(scores);
+    CHECK_CONTIGUOUS(scores);
+    TORCH_CHECK(scores.scalar_type() == at::kBFloat16 || scores.scalar_type() == at::kFloat,
+                "scores must be bfloat16 or float32");
+    c10::OptionalDeviceGuard guard(scores.device());
+    auto opts = scores.options().dtype(at::kBFloat16);
+    at::Tensor y = at::empty(scores.sizes(), opts);
+    at::Tensor dy = at::empty(scores.sizes(), opts);
+    void* s = current_stream(scores);
+    const int rc = scores.scalar_type() == at::kBFloat16
+                       ? launch_flash_sigmoid_direct_d3_d4_bf16(y.data_ptr(), dy.data_ptr(),
+                                                                scores.data_ptr(), scores.numel(), s)
+                       : launch_flash_sigmoid_direct_d3_d4_f32_bf16(
+                             y.data_ptr(), dy.data_ptr(), scores.data_ptr(), scores.numel(), s);
+    check_launch(rc, s);
+    return {y, dy};
+}
+
+at::Tensor flash_sigmoid_direct_d3(at::Tensor scores) {
+    CHECK_CUDA(scores);
+    CHECK_CONTIGUOUS(scores);
+    TORCH_CHECK(scores.scalar_type() == at::kBFloat16, "scores must be bfloat16");
+    c10::OptionalDeviceGuard guard(scores.device());
+    at::Tensor y = at::empty_like(scores);
+    void* s = current_stream(scores);
+    check_launch(launch_flash_sigmoid_direct_d3_bf16(y.data_ptr(), scores.data_ptr(), scores.numel(), s),
+                 s);
+    return y;
+}
+
+// ---------------------------------------------------------------------------
+// C++ autograd functions (spline_ops.cpp:1933-2206)
+// ---------------------------------------------------------------------------
+
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+// sigmoid / tanh: D3 forward, algebraic backward from the saved output.
+template <int FAM>
+struct AlgebraicFwd : public torch::autograd::Function<AlgebraicFwd<FAM>> {
+    static at::Tensor forward(AutogradContext* ctx, at::Tensor x) {
+        CHECK_INPUT(x);
+        at::Tensor y = run_unary(x, kFwd[FAM][x.scalar_type() == at::kBFloat16][3]);
+        ctx->save_for_backward({y});
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        at::Tensor y = ctx->get_saved_variables()[0];
+        at::Tensor go = grads[0].contiguous();
+        return {bwd_alg(go, y, FAM)};
+    }
+};
+
+// SiLU: forward of `degree`, backward with the derivative program of the
+// same degree (the fixed op uses D3 forward / D4 backward, :1993-2015).
+struct SwishVariantFwd : public torch::autograd::Function<SwishVariantFwd> {
+    static at::Tensor forward(AutogradContext* ctx, at::Tensor x, int64_t fwd_degree,
+                              int64_t bwd_degree, int64_t coeff_source_id) {
+        at::Tensor out = fwd_variant(x, fwd_degree, coeff_source_id, SWISH);
+        ctx->save_for_backward({x});
+        ctx->saved_data["bwd_degree"] = bwd_degree;
+        ctx->saved_data["coeff_source_id"] = coeff_source_id;
+        return out;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        at::Tensor x = ctx->get_saved_variables()[0];
+        at::Tensor go = grads[0].contiguous();
+        at::Tensor gi = bwd_variant(go, x, ctx->saved_data["bwd_degree"].toInt(),
+                                    ctx->saved_data["coeff_source_id"].toInt(), SWISH);
+        return {gi, at::Tensor(), at::Tensor(), at::Tensor()};
+    }
+};
+
+struct SwishMulVariantFwd : public torch::autograd::Function<SwishMulVariantFwd> {
+    static at::Tensor forward(AutogradContext* ctx, at::Tensor gate, at::Tensor up, int64_t degree,
+                              int64_t coeff_source_id) {
+        at::Tensor out = swish_mul_fwd_variant(gate, up, degree, coeff_source_id);
+        ctx->save_for_backward({gate, up});
+        ctx->saved_data["degree"] = degree;
+        ctx->saved_data["coeff_source_id"] = coeff_source_id;
+        return out;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto saved = ctx->get_saved_variables();
+        at::Tensor go = grads[0].contiguous();
+        auto g = swish_mul_bwd_variant(go, saved[0], saved[1], ctx->saved_data["degree"].toInt(),
+                                       ctx->saved_data["coeff_source_id"].toInt());
+        return {g[0], g[1], at::Tensor(), at::Tensor()};
+    }
+};
+
+at::Tensor sigmoid_fwd_autograd(at::Tensor x) { return AlgebraicFwd<SIGMOID>::apply(x); }
+at::Tensor tanh_fwd_autograd(at::Tensor x) { return AlgebraicFwd<TANH>::apply(x); }
+at::Tensor swish_fwd_autograd(at::Tensor x) { return SwishVariantFwd::apply(x, 3, 4, 0); }
+at::Tensor swish_fwd_variant_autograd(at::Tensor x, int64_t degree, int64_t coeff_source_id) {
+    normalize_coeff_source_id(coeff_source_id);
+    return SwishVariantFwd::apply(x, degree, degree, coeff_source_id);
+}
+at::Tensor swish_mul_fwd_variant_autograd(at::Tensor gate, at::Tensor up, int64_t degree,
+                                          int64_t coeff_source_id) {
+    return SwishMulVariantFwd::apply(gate, up, degree, coeff_source_id);
+}
+
+// ---------------------------------------------------------------------------
+// dispatcher-facing wrappers
+// ---------------------------------------------------------------------------
+
+at::Tensor sigmoid_bwd_op(at::Tensor go, at::Tensor x) { return bwd_fixed(go, x, SIGMOID, 4); }
+at::Tensor tanh_bwd_op(at::Tensor go, at::Tensor x) { return bwd_fixed(go, x, TANH, 4); }
+at::Tensor swish_bwd_op(at::Tensor go, at::Tensor x) { return bwd_fixed(go, x, SWISH, 4); }
+at::Tensor sigmoid_bwd_alg_op(at::Tensor go, at::Tensor y) { return bwd_alg(go, y, SIGMOID); }
+at::Tensor tanh_bwd_alg_op(at::Tensor go, at::Tensor y) { return bwd_alg(go, y, TANH); }
+at::Tensor swish_fwd_variant_op(at::Tensor x, int64_t d, int64_t c) { return fwd_variant(x, d, c, SWISH); }
+at::Tensor swish_bwd_variant_op(at::Tensor go, at::Tensor x, int64_t d, int64_t c) {
+    return bwd_variant(go, x, d, c, SWISH);
+}
+
+}  // namespace
+
+// ===========================================================================
+// TORCH_LIBRARY: the reference's schemas (spline_ops.cpp:2212-2250)
+// ===========================================================================
+
+TORCH_LIBRARY(spline_ops, m) {
+    m.def("sigmoid_fwd(Tensor x) -> Tensor");
+    m.def("tanh_fwd(Tensor x) -> Tensor");
+    m.def("swish_fwd(Tensor x) -> Tensor");
+    m.def("sigmoid_bwd(Tensor grad_out, Tensor x) -> Tensor");
+    m.def("tanh_bwd(Tensor grad_out, Tensor x) -> Tensor");
+    m.def("swish_bwd(Tensor grad_out, Tensor x) -> Tensor");
+    m.def("sigmoid_bwd_alg(Tensor grad_out, Tensor y) -> Tensor");
+    m.def("tanh_bwd_alg(Tensor grad_out, Tensor y) -> Tensor");
+    m.def("swish_variant_fwd(Tensor x, int degree, int coeff_source_id) -> Tensor");
+    m.def("swish_variant_bwd(Tensor grad_out, Tensor x, int degree, int coeff_source_id) -> Tensor");
+    m.def("swish_mul_variant_fwd(Tensor gate, Tensor up, int degree, int coeff_source_id) -> Tensor");
+    m.def(
+        "swish_mul_variant_bwd(Tensor grad_out, Tensor gate, Tensor up, int degree, "
+        "int coeff_source_id) -> Tensor[]");
+    m.def("swish_mul_packed_variant_fwd(Tensor packed, int degree, int coeff_source_id) -> Tensor");
+    m.def("swish_mul_packed_native_fwd(Tensor packed, int coeff_source_id) -> Tensor");
+    m.def(
+        "swish_mul_packed_native_bwd_fwd(Tensor packed, int degree, int coeff_source_id) -> Tensor");
+    m.def(
+        "swish_mul_packed_variant_bwd(Tensor grad_out, Tensor packed, int degree, "
+        "int coeff_source_id) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(spline_ops, AutogradCUDA, m) {
+    m.impl("sigmoid_fwd", &sigmoid_fwd_autograd);
+    m.impl("tanh_fwd", &tanh_fwd_autograd);
+    m.impl("swish_fwd", &swish_fwd_autograd);
+}
+
+TORCH_LIBRARY_IMPL(spline_ops, CUDA, m) {
+    m.impl("sigmoid_bwd", &sigmoid_bwd_op);
+    m.impl("tanh_bwd", &tanh_bwd_op);
+    m.impl("swish_bwd", &swish_bwd_op);
+    m.impl("sigmoid_bwd_alg", &sigmoid_bwd_alg_op);
+    m.impl("tanh_bwd_alg", &tanh_bwd_alg_op);
+    m.impl("swish_variant_fwd", &swish_fwd_variant_op);
+    m.impl("swish_variant_bwd", &swish_bwd_variant_op);
+    m.impl("swish_mul_variant_fwd", &swish_mul_fwd_variant);
+    m.impl("swish_mul_variant_bwd", &swish_mul_bwd_variant);
+    m.impl("swish_mul_packed_variant_fwd", &swish_mul_packed_fwd_variant);
+    m.impl("swish_mul_packed_native_fwd", [](at::Tensor packed, int64_t coeff_source_id) {
+        return swish_mul_packed_fwd_variant(packed, 0, coeff_source_id);
+    });
+    m.impl("swish_mul_packed_native_bwd_fwd", &swish_mul_packed_fwd_variant);
+    m.impl("swish_mul_packed_variant_bwd", &swish_mul_packed_bwd_variant);
+}
+
+// ===========================================================================
+// pybind11 module (the reference's function names, spline_ops.cpp:2285-2452)
+// ===========================================================================
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.doc() = "MI355X (gfx950) packed polynomial transcendental kernels";
+
+#define PT_DEF_FWD(fam, FAM, deg, name) \
+    m.def(name, [](at::Tensor x) { return fwd_fixed(x, FAM, deg); }, "Polynomial " #fam " forward")
+#define PT_DEF_BWD(fam, FAM, deg, name)                                                \
+    m.def(name, [](at::Tensor go, at::Tensor x) { return bwd_fixed(go, x, FAM, deg); }, \
+          "Polynomial " #fam " backward")
+
+    PT_DEF_FWD(sigmoid, SIGMOID, 3, "sigmoid_fwd");
+    PT_DEF_FWD(sigmoid, SIGMOID, 3, "sigmoid_fwd_d3");
+    PT_DEF_FWD(sigmoid, SIGMOID, 4, "sigmoid_fwd_d4");
+    PT_DEF_FWD(sigmoid, SIGMOID, 5, "sigmoid_fwd_d5");
+    PT_DEF_FWD(sigmoid, SIGMOID, 6, "sigmoid_fwd_d6");
+    PT_DEF_BWD(sigmoid, SIGMOID, 4, "sigmoid_bwd");
+    PT_DEF_BWD(sigmoid, SIGMOID, 3, "sigmoid_bwd_d3");
+    PT_DEF_BWD(sigmoid, SIGMOID, 4, "sigmoid_bwd_d4");
+    PT_DEF_BWD(sigmoid, SIGMOID, 5, "sigmoid_bwd_d5");
+    PT_DEF_BWD(sigmoid, SIGMOID, 6, "sigmoid_bwd_d6");
+    PT_DEF_FWD(tanh, TANH, 3, "tanh_fwd");
+    PT_DEF_FWD(tanh, TANH, 3, "tanh_fwd_d3");
+    PT_DEF_FWD(tanh, TANH, 4, "tanh_fwd_d4");
+    PT_DEF_FWD(tanh, TANH, 5, "tanh_fwd_d5");
+    PT_DEF_FWD(tanh, TANH, 6, "tanh_fwd_d6");
+    PT_DEF_BWD(tanh, TANH, 4, "tanh_bwd");
+    PT_DEF_BWD(tanh, TANH, 3, "tanh_bwd_d3");
+    PT_DEF_BWD(tanh, TANH, 4, "tanh_bwd_d4");
+    PT_DEF_BWD(tanh, TANH, 5, "tanh_bwd_d5");
+    PT_DEF_BWD(tanh, TANH, 6, "tanh_bwd_d6");
+    PT_DEF_FWD(swish, SWISH, 3, "swish_fwd");
+    PT_DEF_FWD(swish, SWISH, 3, "swish_fwd_d3");
+    PT_DEF_FWD(swish, SWISH, 4, "swish_fwd_d4");
+    PT_DEF_FWD(swish, SWISH, 5, "swish_fwd_d5");
+    PT_DEF_FWD(swish, SWISH, 6, "swish_fwd_d6");
+    PT_DEF_BWD(swish, SWISH, 4, "swish_bwd");
+    PT_DEF_BWD(swish, SWISH, 3, "swish_bwd_d3");
+    PT_DEF_BWD(swish, SWISH, 4, "swish_bwd_d4");
+    PT_DEF_BWD(swish, SWISH, 5, "swish_bwd_d5");
+    PT_DEF_BWD(swish, SWISH, 6, "swish_bwd_d6");
+#undef PT_DEF_FWD
+#undef PT_DEF_BWD
+
+    m.def("sigmoid_fwd_variant",
+          [](at::Tensor x, int64_t d, int64_t c) { return fwd_variant(x, d, c, SIGMOID); },
+          "Sigmoid FWD variant by degree/source");
+    m.def("sigmoid_bwd_variant",
+          [](at::Tensor go, at::Tensor x, int64_t d, int64_t c) { return bwd_variant(go, x, d, c, SIGMOID); },
+          "Sigmoid BWD variant by degree/source");
+    m.def("tanh_fwd_variant",
+          [](at::Tensor x, int64_t d, int64_t c) { return fwd_variant(x, d, c, TANH); },
+          "Tanh FWD variant by degree/source");
+    m.def("tanh_bwd_variant",
+          [](at::Tensor go, at::Tensor x, int64_t d, int64_t c) { return bwd_variant(go, x, d, c, TANH); },
+          "Tanh BWD variant by degree/source");
+    m.def("sigmoid_bwd_alg", &sigmoid_bwd_alg_op, "Sigmoid BWD algebraic (from y)");
+    m.def("tanh_bwd_alg", &tanh_bwd_alg_op, "Tanh BWD algebraic (from y)");
+    m.def("swish_fwd_variant", &swish_fwd_variant_op, "Swish FWD variant by degree/source");
+    m.def("swish_bwd_variant", &swish_bwd_variant_op, "Swish BWD variant by degree/source");
+    m.def("swish_mul_fwd_variant", &swish_mul_fwd_variant,
+          "Swish(gate) * up FWD variant by degree/source");
+    m.def("swish_mul_bwd_variant", &swish_mul_bwd_variant,
+          "Swish(gate) * up BWD variant by degree/source");
+    m.def("swish_mul_packed_fwd_variant", &swish_mul_packed_fwd_variant,
+          "Swish(packed gate) * packed up FWD variant by degree/source");
+    m.def("swish_mul_packed_bwd_variant", &swish_mul_packed_bwd_variant,
+          "Swish(packed gate) * packed up BWD variant by degree/source");
+    m.def("swish_ag_variant", &swish_fwd_variant_autograd,
+          "Swish variant with C++ autograd by degree/source");
+    m.def("swish_mul_ag_variant", &swish_mul_fwd_variant_autograd,
+          "Swish(gate) * up variant with C++ autograd by degree/source");
+    m.def("sigmoid_ag", &sigmoid_fwd_autograd, "Sigmoid with C++ autograd");
+    m.def("tanh_ag", &tanh_fwd_autograd, "Tanh with C++ autograd");
+    m.def("swish_ag", &swish_fwd_autograd, "Swish with C++ autograd");
+
+    m.def("flash_sigmoid_direct_d3_d4_bf16", &flash_sigmoid_direct_d3_d4,
+          "B3 deployed direct-D3 probability and factored-D4 derivative (BF16 out)");
+    m.def("flash_sigmoid_direct_d3_bf16", &flash_sigmoid_direct_d3,
+          "B3 deployed direct-D3 probability (BF16)");
+}

@@ -1,0 +1,373 @@
+// programs.hpp -- the polynomial lane programs, written for CDNA4 (gfx950).
+//
+// One "pair" is a 32-bit register holding two 16-bit lanes, the unit the
+// reference's __half2 / __nv_bfloat162 programs work on.
+//
+//  * FP16 programs run natively packed: v_pk_fma_f16 / v_pk_mul_f16 /
+//    v_pk_add_f16 give the same single-rounding results as __hfma2 & co.
+//  * gfx950 has no packed BF16 arithmetic.  BF16 programs therefore run each
+//    lane in FP32 and round back to BF16 after every step with
+//    v_cvt_pk_bf16_f32 (RNE).  An FP32 FMA of BF16 operands followed by an
+//    RNE pack equals the single-rounding BF16 FMA for every input of these
+//    programs (checked exhaustively over all 65536 inputs on the CPU), so the
+//    results are bit-identical to fma.rn.bf16x2.
+//  * The clamp t = min(|x|, Lc) is an unsigned 16-bit min on the magnitude
+//    bits (v_pk_min_u16): for non-negative IEEE patterns integer order is
+//    numeric order, and NaN/Inf magnitudes select Lc, which is exactly the
+//    __hmin2 rule "a NaN operand yields the other operand".
+//
+// Coefficients: autonumerics_zero/spline_ops/spline_structs_odd.cuh (FP16) and
+// spline_structs_odd_bf16.cuh (BF16); each table row cites its struct.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pt {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// bit helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ float as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t as_u32(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+__device__ __forceinline__ uint32_t umin16x2(uint32_t a, uint32_t b) {
+    u16x2_t r = __builtin_elementwise_min(__builtin_bit_cast(u16x2_t, a),
+                                          __builtin_bit_cast(u16x2_t, b));
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// FP32 lanes of a BF16 pair.
+__device__ __forceinline__ float bf_lo(uint32_t u) { return as_f32(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return as_f32(u & 0xffff0000u); }
+
+// Round an FP32 value to BF16 (RNE) and return it as FP32: one
+// v_cvt_pk_bf16_f32 that writes bf16(x) to the high half and bf16(0) = 0 to
+// the low half.
+__device__ __forceinline__ float rbf(float x) {
+    float r;
+    asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
+// Pack two FP32 values into a BF16 pair with RNE.
+__device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
+    bf2_t r = __builtin_convertvector((f2_t){lo, hi}, bf2_t);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Two FP32 values that already hold BF16 values: take their high halves.
+__device__ __forceinline__ uint32_t pack_exact_bf(float lo, float hi) {
+    return __builtin_amdgcn_perm(as_u32(hi), as_u32(lo), 0x07060302u);
+}
+
+// ---------------------------------------------------------------------------
+// compile-time rounding of literals (__float2half2_rn / __float2bfloat162_rn
+// of a float literal: decimal -> binary32 by the compiler, then RNE)
+// ---------------------------------------------------------------------------
+
+constexpr uint16_t bf16_bits_rne(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+constexpr float bf16_value(float f) {
+    return __builtin_bit_cast(float, (uint32_t)bf16_bits_rne(f) << 16);
+}
+constexpr uint32_t bf16_pair_bits(float f) {
+    return (uint32_t)bf16_bits_rne(f) * 0x00010001u;
+}
+__host__ __device__ constexpr uint16_t f16_bits_rne(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+constexpr uint32_t f16_pair_bits(float f) { return (uint32_t)f16_bits_rne(f) * 0x00010001u; }
+
+// ---------------------------------------------------------------------------
+// program tables
+// ---------------------------------------------------------------------------
+
+enum Shape : int {
+    kHalfOdd = 0,   // 0.5 + sign(x) * t*H(t)
+    kOdd = 1,       // sign(x) * t*H(t)
+    kOddMin1 = 2,   // sign(x) * min(t*H(t), 1)
+    kSwish = 3,     // fma(|x|, t*H(t), 0.5*x)
+    kEven = 4,      // c0 + t*(c1 + t*(...))
+    kXTimes = 5,    // x * (sigmoid program `inner`)(x)
+};
+
+struct Prog {
+    int shape;
+    float lc;
+    int deg;
+    float c[7];
+    int inner;
+};
+
+enum Family : int { kSigmoid = 0, kTanh = 1, kSwishFam = 2 };
+enum Dir : int { kFwd = 0, kBwd = 1 };
+
+// [family][dir][degree-3]
+constexpr Prog kF16Progs[3][2][4] = {
+    {   // SIGMOID
+        {   // spline_structs_odd.cuh:14-127  SIGMOID_FWD_D{3..6}_ODD
+            {kHalfOdd, 6.25f, 3, {0.f, 0.2812500000f, -0.0534362793f, 0.0033779144f}, 0},
+            {kHalfOdd, 5.0f, 4, {0.f, 0.2690429688f, -0.0365905762f, -0.0029220581f, 0.0006918907f}, 0},
+            {kHalfOdd, 5.5f, 5, {0.f, 0.2607421875f, -0.0205383301f, -0.0126800537f, 0.0030593872f, -0.0001997948f}, 0},
+            {kHalfOdd, 5.5f, 6, {0.f, 0.2539062500f, -0.0053977966f, -0.0239105225f, 0.0067253113f, -0.0007462502f, 0.0000304580f}, 0},
+        },
+        {   // :339-428  SIGMOID_BWD_D{3..6}_EVEN
+            {kEven, 4.0f, 3, {0.2500000000f, -0.0423889160f, -0.0207824707f, 0.0040893555f}, 0},
+            {kEven, 5.25f, 4, {0.2500000000f, -0.0103073120f, -0.0606994629f, 0.0183105469f, -0.0015373230f}, 0},
+            {kEven, 5.5f, 5, {0.2500000000f, 0.0081405640f, -0.0934448242f, 0.0364685059f, -0.0055160522f, 0.0003011227f}, 0},
+            {kEven, 5.25f, 6, {0.2500000000f, 0.0112609863f, -0.1012573242f, 0.0428466797f, -0.0077819824f, 0.0006651878f, -0.0000216961f}, 0},
+        },
+    },
+    {   // TANH
+        {   // :133-235  TANH_FWD_D{3..6}_ODD
+            {kOdd, 3.25f, 3, {0.f, 1.1250000000f, -0.4274902344f, 0.0540466309f}, 0},
+            {kOdd, 2.75f, 4, {0.f, 1.1064453125f, -0.3747558594f, 0.0160827637f, 0.0078811646f}, 0},
+            {kOdd, 2.75f, 5, {0.f, 1.0429687500f, -0.1643066406f, -0.2028808594f, 0.0979003906f, -0.0127868652f}, 0},
+            {kOdd, 3.0f, 6, {0.f, 1.0556640625f, -0.1966552734f, -0.1898193359f, 0.1103515625f, -0.0219879150f, 0.0015487671f}, 0},
+        },
+        {   // :434-527  TANH_BWD_D{3..6}_EVEN
+            {kEven, 2.0f, 3, {1.0000000000f, -0.3391113281f, -0.3325195312f, 0.1308593750f}, 0},
+            {kEven, 2.5f, 4, {1.0000000000f, -0.0553894043f, -1.0458984375f, 0.6425781250f, -0.1112060547f}, 0},
+            {kEven, 2.75f, 5, {1.0000000000f, 0.0315551758f, -1.3740234375f, 1.0341796875f, -0.2961425781f, 0.0302276611f}, 0},
+            {kEven, 3.25f, 6, {1.0000000000f, 0.0289306641f, -1.4033203125f, 1.1250000000f, -0.3789062500f, 0.0596923828f, -0.0036144257f}, 0},
+        },
+    },
+    {   // SWISH
+        {   // :241-334  SWISH_FWD_D{3..6}_ODD (sigmoid-odd coefficients)
+            {kSwish, 6.25f, 3, {0.f, 0.2812500000f, -0.0534362793f, 0.0033779144f}, 0},
+            {kSwish, 5.0f, 4, {0.f, 0.2690429688f, -0.0365905762f, -0.0029220581f, 0.0006918907f}, 0},
+            {kSwish, 5.5f, 5, {0.f, 0.2607421875f, -0.0205383301f, -0.0126800537f, 0.0030593872f, -0.0001997948f}, 0},
+            {kSwish, 5.5f, 6, {0.f, 0.2539062500f, -0.0053977966f, -0.0239105225f, 0.0067253113f, -0.0007462502f, 0.0000304580f}, 0},
+        },
+        {   // :533-640  SWISH_BWD_D{3..6}_ODD
+            {kHalfOdd, 5.0f, 3, {0.f, 0.5703125000f, -0.1676025391f, 0.0148391724f}, 0},
+            {kHalfOdd, 5.5f, 4, {0.f, 0.5996093750f, -0.2036132812f, 0.0272979736f, -0.0012779236f}, 0},
+            {kHalfOdd, 6.25f, 5, {0.f, 0.5742187500f, -0.1582031250f, 0.0034561157f, 0.0034828186f, -0.0003206730f}, 0},
+            {kHalfOdd, 5.75f, 6, {0.f, 0.5415039062f, -0.0898437500f, -0.0439147949f, 0.0179443359f, -0.0023403168f, 0.0001055002f}, 0},
+        },
+    },
+};
+
+constexpr Prog kBF16Progs[3][2][4] = {
+    {   // SIGMOID
+        {   // spline_structs_odd_bf16.cuh:11-121  SIGMOID_FWD_D{3..6}_ODD_BF16
+            {kHalfOdd, 6.0f, 3, {0.f, 0.2810058594f, -0.0533447266f, 0.0033893585f}, 0},
+            {kHalfOdd, 5.28125f, 4, {0.f, 0.2714843750f, -0.0402832031f, -0.0014419556f, 0.0005149841f}, 0},
+            {kHalfOdd, 5.40625f, 5, {0.f, 0.2617187500f, -0.0240478516f, -0.0107421875f, 0.0026550293f, -0.0001697540f}, 0},
+            {kHalfOdd, 4.90625f, 6, {0.f, 0.2578125000f, -0.0134277344f, -0.0185546875f, 0.0051879883f, -0.0005455017f, 0.0000208616f}, 0},
+        },
+        {   // :310-403  SIGMOID_BWD_D{3..6}_EVEN_BF16
+            {kEven, 4.0f, 3, {0.2500000000f, -0.0424804688f, -0.0207519531f, 0.0040893555f}, 0},
+            {kEven, 4.75f, 4, {0.2500000000f, -0.0037994385f, -0.0698242188f, 0.0218505859f, -0.0019531250f}, 0},
+            {kEven, 4.75f, 5, {0.2500000000f, -0.0046386719f, -0.0722656250f, 0.0257568359f, -0.0034027100f, 0.0001573563f}, 0},
+            {kEven, 4.25f, 6, {0.2500000000f, 0.0117797852f, -0.1025390625f, 0.0439453125f, -0.0081787109f, 0.0007286072f, -0.0000252724f}, 0},
+        },
+    },
+    {   // TANH
+        {   // :127-241  TANH_FWD_D{3..6}_ODD_BF16 (with min(h, 1))
+            {kOddMin1, 2.75f, 3, {0.f, 1.1406250000f, -0.4472656250f, 0.0595703125f}, 0},
+            {kOddMin1, 2.75f, 4, {0.f, 1.0859375000f, -0.3222656250f, -0.0230712891f, 0.0164794922f}, 0},
+            {kOddMin1, 2.25f, 5, {0.f, 1.1171875000f, -0.4023437500f, 0.0245361328f, 0.0129394531f, -0.0018615723f}, 0},
+            {kOddMin1, 2.25f, 6, {0.f, 1.0390625000f, -0.1523437500f, -0.2412109375f, 0.1367187500f, -0.0278320312f, 0.0020446777f}, 0},
+        },
+        {   // :410-503  TANH_BWD_D{3..6}_EVEN_BF16
+            {kEven, 2.0f, 3, {1.0000000000f, -0.3398437500f, -0.3320312500f, 0.1308593750f}, 0},
+            {kEven, 2.25f, 4, {1.0000000000f, -0.0078735352f, -1.1875000000f, 0.7578125000f, -0.1396484375f}, 0},
+            {kEven, 2.25f, 5, {1.0000000000f, -0.1210937500f, -0.9257812500f, 0.6289062500f, -0.1533203125f, 0.0129394531f}, 0},
+            {kEven, 2.25f, 6, {1.0000000000f, -0.0903320312f, -1.0468750000f, 0.7773437500f, -0.2324218750f, 0.0319824219f, -0.0016632080f}, 0},
+        },
+    },
+    {   // SWISH
+        {   // :248-304  SWISH_FWD_D{3,4} fused odd form; D{5,6} = x * sigmoid D{5,6}
+            {kSwish, 6.0f, 3, {0.f, 0.2810058594f, -0.0533447266f, 0.0033893585f}, 0},
+            {kSwish, 5.28125f, 4, {0.f, 0.2714843750f, -0.0402832031f, -0.0014419556f, 0.0005149841f}, 0},
+            {kXTimes, 0.f, 5, {0.f}, 2},
+            {kXTimes, 0.f, 6, {0.f}, 3},
+        },
+        {   // :510-619  SWISH_BWD_D{3..6}_ODD_BF16
+            {kHalfOdd, 4.75f, 3, {0.f, 0.5820312500f, -0.1777343750f, 0.0164794922f}, 0},
+            {kHalfOdd, 5.25f, 4, {0.f, 0.6093750000f, -0.2128906250f, 0.0296630859f, -0.0014572144f}, 0},
+            {kHalfOdd, 4.75f, 5, {0.f, 0.5742187500f, -0.1582031250f, 0.0034484863f, 0.0034790039f, -0.0003204346f}, 0},
+            {kHalfOdd, 5.0f, 6, {0.f, 0.6015625000f, -0.2050781250f, 0.0260009766f, -0.0004787445f, -0.0001363754f, 0.0000074804f}, 0},
+        },
+    },
+};
+
+// ---------------------------------------------------------------------------
+// FP16: one packed program on a pair
+// ---------------------------------------------------------------------------
+
+template <int F, int D, int G>
+struct F16Prog {
+    static constexpr Prog P = kF16Progs[F][D][G - 3];
+
+    __device__ __forceinline__ static h2_t k(float c) {
+        return as_h2(f16_pair_bits(c));
+    }
+
+    __device__ __forceinline__ static uint32_t eval(uint32_t x) {
+        const uint32_t mag = x & 0x7fff7fffu;
+        const h2_t t = as_h2(umin16x2(mag, f16_pair_bits(P.lc)));
+        if constexpr (P.shape == kEven) {
+            h2_t r = __builtin_elementwise_fma(t, k(P.c[P.deg]), k(P.c[P.deg - 1]));
+#pragma unroll
+            for (int i = P.deg - 2; i >= 0; --i) r = __builtin_elementwise_fma(t, r, k(P.c[i]));
+            return as_u32(r);
+        } else {
+            h2_t h = __builtin_elementwise_fma(t, k(P.c[P.deg]), k(P.c[P.deg - 1]));
+#pragma unroll
+            for (int i = P.deg - 2; i >= 1; --i) h = __builtin_elementwise_fma(t, h, k(P.c[i]));
+            h = t * h;
+            if constexpr (P.shape == kHalfOdd) {
+                const h2_t hs = as_h2(as_u32(h) ^ (x & 0x80008000u));
+                return as_u32(k(0.5f) + hs);
+            } else if constexpr (P.shape == kOdd) {
+                return as_u32(h) ^ (x & 0x80008000u);
+            } else {  // kSwish
+                static_assert(P.shape == kSwish, "unsupported FP16 shape");
+                return as_u32(__builtin_elementwise_fma(as_h2(mag), h, k(0.5f) * as_h2(x)));
+            }
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// BF16: one program on a pair, lanes evaluated in FP32 with RNE after each step
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bfma(float a, float b, float c) { return rbf(__builtin_fmaf(a, b, c)); }
+
+template <int F, int D, int G>
+struct BF16Prog {
+    static constexpr Prog P = kBF16Progs[F][D][G - 3];
+
+    // Lane program on FP32 copies of the BF16 lane values.  `t` is the clamped
+    // magnitude, `x` the input, `neg` its sign bit (as 0x80000000 or 0).
+    __device__ __forceinline__ static float lane(float t, float x, uint32_t neg) {
+        constexpr float half = bf16_value(0.5f);
+        if constexpr (P.shape == kEven) {
+            float r = bfma(t, bf16_value(P.c[P.deg]), bf16_value(P.c[P.deg - 1]));
+#pragma unroll
+            for (int i = P.deg - 2; i >= 0; --i) r = bfma(t, r, bf16_value(P.c[i]));
+            return r;
+        } else {
+            float h = bfma(t, bf16_value(P.c[P.deg]), bf16_value(P.c[P.deg - 1]));
+#pragma unroll
+            for (int i = P.deg - 2; i >= 1; --i) h = bfma(t, h, bf16_value(P.c[i]));
+            h = rbf(t * h);
+            if constexpr (P.shape == kHalfOdd) {
+                return rbf(half + as_f32(as_u32(h) ^ neg));
+            } else if constexpr (P.shape == kOdd) {
+                return as_f32(as_u32(h) ^ neg);
+            } else if constexpr (P.shape == kOddMin1) {
+                // h >= 0 and finite here, so fminf is __hmin2.
+                return as_f32(as_u32(__builtin_fminf(h, 1.0f)) ^ neg);
+            } else {  // kSwish
+                static_assert(P.shape == kSwish, "unsupported BF16 shape");
+                const float ax = as_f32(as_u32(x) & 0x7fffffffu);
+                return bfma(ax, h, rbf(half * x));
+            }
+        }
+    }
+
+    // Both lanes, returned as FP32 values that hold BF16 values.
+    __device__ __forceinline__ static void eval2(uint32_t x, float& lo, float& hi) {
+        if constexpr (P.shape == kXTimes) {
+            float s_lo, s_hi;
+            BF16Prog<kSigmoid, kFwd, G>::eval2(x, s_lo, s_hi);
+            lo = rbf(bf_lo(x) * s_lo);
+            hi = rbf(bf_hi(x) * s_hi);
+        } else {
+            const uint32_t t2 = umin16x2(x & 0x7fff7fffu, bf16_pair_bits(P.lc));
+            lo = lane(bf_lo(t2), bf_lo(x), (x << 16) & 0x80000000u);
+            hi = lane(bf_hi(t2), bf_hi(x), x & 0x80000000u);
+        }
+    }
+
+    __device__ __forceinline__ static uint32_t eval(uint32_t x) {
+        float lo, hi;
+        eval2(x, lo, hi);
+        return pack_exact_bf(lo, hi);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Algebraic derivatives from cached y (SIGMOID/TANH_BWD_ALGEBRAIC{,_BF16})
+// ---------------------------------------------------------------------------
+
+template <int F>
+struct F16Alg {
+    __device__ __forceinline__ static uint32_t eval(uint32_t y) {
+        const h2_t yy = as_h2(y);
+        const h2_t one = as_h2(f16_pair_bits(1.0f));
+        if constexpr (F == kSigmoid) return as_u32(yy * (one - yy));
+        else return as_u32(one - yy * yy);
+    }
+};
+
+template <int F>
+struct BF16Alg {
+    __device__ __forceinline__ static float lane(float y) {
+        if constexpr (F == kSigmoid) return rbf(y * rbf(1.0f - y));
+        else return rbf(1.0f - rbf(y * y));
+    }
+    __device__ __forceinline__ static uint32_t eval(uint32_t y) {
+        return pack_exact_bf(lane(bf_lo(y)), lane(bf_hi(y)));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Native (hardware transcendental) baselines: FP32 math, RNE to 16 bits.
+// __expf -> v_exp_f32, __builtin_amdgcn_rcpf -> v_rcp_f32.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float nat_sigmoid(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
+template <int F, int D>
+__device__ __forceinline__ float native_lane(float x) {
+    if constexpr (F == kSigmoid) {
+        const float s = nat_sigmoid(x);
+        return D == kFwd ? s : s * (1.0f - s);
+    } else if constexpr (F == kTanh) {
+        // tanh(x) = 1 - 2 / (exp(2x) + 1)
+        const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * x) + 1.0f);
+        return D == kFwd ? th : 1.0f - th * th;
+    } else {
+        // SWISH_FWD_NATIVE / SWISH_BWD_NATIVE (spline_kernels.cu:362-381)
+        const float s = nat_sigmoid(x);
+        return D == kFwd ? x * s : s * (1.0f + x * (1.0f - s));
+    }
+}
+
+template <int F, int D>
+struct F16Native {
+    __device__ __forceinline__ static uint32_t eval(uint32_t x) {
+        const h2_t h = as_h2(x);
+        const float lo = native_lane<F, D>((float)h.x);
+        const float hi = native_lane<F, D>((float)h.y);
+        const h2_t r = {(_Float16)lo, (_Float16)hi};
+        return as_u32(r);
+    }
+};
+
+template <int F, int D>
+struct BF16Native {
+    __device__ __forceinline__ static uint32_t eval(uint32_t x) {
+        return pack_bf(native_lane<F, D>(bf_lo(x)), native_lane<F, D>(bf_hi(x)));
+    }
+};
+
+}  // namespace pt

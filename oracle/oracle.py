@@ -1,0 +1,212 @@
+"""ctypes front end of the CPU oracle (``libspline_oracle.so``).
+
+TEST INFRASTRUCTURE ONLY.  ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker or as the timed CPU baseline.  The product path never imports it.
+
+Every array argument is a NumPy array of raw 16-bit bit patterns
+(``numpy.uint16``); helpers convert to and from torch tensors by viewing the
+bits, never by value.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libspline_oracle.so")
+
+F16, BF16 = 0, 1
+SIGMOID, TANH, SWISH = 0, 1, 2
+FWD, BWD = 0, 1
+RND_SINGLE, RND_F32 = 0, 1
+
+_FAMILY = {"sigmoid": SIGMOID, "tanh": TANH, "swish": SWISH}
+_FMT = {"f16": F16, "fp16": F16, "float16": F16, "bf16": BF16, "bfloat16": BF16}
+
+_lib = None
+
+
+def build() -> str:
+    """Compile the oracle in place (gcc via the Makefile beside this file)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(l: ctypes.CDLL) -> None:
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    u8p = ctypes.POINTER(ctypes.c_uint8)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    i64 = ctypes.c_int64
+    ci = ctypes.c_int
+    l.orc_f32_to_bf16_audit.argtypes = [ctypes.c_float]
+    l.orc_f32_to_bf16_audit.restype = ctypes.c_uint16
+    l.orc_f64_to_bf16.argtypes = [ctypes.c_double]
+    l.orc_f64_to_bf16.restype = ctypes.c_uint16
+    l.orc_f64_to_f16.argtypes = [ctypes.c_double]
+    l.orc_f64_to_f16.restype = ctypes.c_uint16
+    l.orc_bf16_to_f64.argtypes = [ctypes.c_uint16]
+    l.orc_bf16_to_f64.restype = ctypes.c_double
+    l.orc_f16_to_f64.argtypes = [ctypes.c_uint16]
+    l.orc_f16_to_f64.restype = ctypes.c_double
+    l.orc_fma16.argtypes = [ci, ctypes.c_uint16, ctypes.c_uint16, ctypes.c_uint16]
+    l.orc_fma16.restype = ctypes.c_uint16
+    l.orc_bf16_fma_audit.argtypes = [ctypes.c_uint16] * 3
+    l.orc_bf16_fma_audit.restype = ctypes.c_uint16
+    l.orc_activation.argtypes = [ci, ci, ci, ci, ci, u16p, u16p, i64]
+    l.orc_activation_bwd.argtypes = [ci, ci, ci, ci, u16p, u16p, u16p, i64]
+    l.orc_activation_bwd_alg.argtypes = [ci, ci, u16p, u16p, u16p, i64]
+    l.orc_swish_mul_fwd.argtypes = [ci, ci, ci, u16p, u16p, u16p, i64]
+    l.orc_swish_mul_bwd.argtypes = [ci, ci, ci, u16p, u16p, u16p, u16p, u16p, i64]
+    l.orc_b3_direct_bf16.argtypes = [u16p, u16p, u16p, u8p, i64]
+    l.orc_b3_direct_f32.argtypes = [f32p, u16p, u16p, i64]
+    l.orc_b3_constants.argtypes = [u16p, u16p, u16p]
+    l.orc_num_threads.argtypes = []
+    for name in (
+        "orc_activation", "orc_activation_bwd", "orc_activation_bwd_alg",
+        "orc_swish_mul_fwd", "orc_swish_mul_bwd", "orc_b3_direct_bf16",
+        "orc_b3_direct_f32", "orc_b3_constants", "orc_num_threads",
+    ):
+        getattr(l, name).restype = ctypes.c_int
+
+
+def _u16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    if a.dtype != np.uint16:
+        raise TypeError(f"expected uint16 bit patterns, got {a.dtype}")
+    return a
+
+
+def _p(a: np.ndarray, ctype=ctypes.c_uint16):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise ValueError(f"oracle rejected the arguments (code {rc})")
+
+
+def fmt_id(fmt) -> int:
+    if isinstance(fmt, int):
+        return fmt
+    return _FMT[str(fmt).replace("torch.", "")]
+
+
+def family_id(family) -> int:
+    return family if isinstance(family, int) else _FAMILY[family]
+
+
+def activation(family, direction: int, degree: int, fmt, x: np.ndarray,
+               rnd: int = RND_SINGLE) -> np.ndarray:
+    x = _u16(x)
+    y = np.empty_like(x)
+    _check(lib().orc_activation(family_id(family), direction, degree, fmt_id(fmt), rnd,
+                                _p(x), _p(y), x.size))
+    return y
+
+
+def activation_bwd(family, degree: int, fmt, go: np.ndarray, x: np.ndarray,
+                   rnd: int = RND_SINGLE) -> np.ndarray:
+    go, x = _u16(go), _u16(x)
+    gi = np.empty_like(x)
+    _check(lib().orc_activation_bwd(family_id(family), degree, fmt_id(fmt), rnd,
+                                    _p(go), _p(x), _p(gi), x.size))
+    return gi
+
+
+def activation_bwd_alg(family, fmt, go: np.ndarray, y: np.ndarray) -> np.ndarray:
+    go, y = _u16(go), _u16(y)
+    gi = np.empty_like(y)
+    _check(lib().orc_activation_bwd_alg(family_id(family), fmt_id(fmt), _p(go), _p(y),
+                                        _p(gi), y.size))
+    return gi
+
+
+def swish_mul_fwd(degree: int, fmt, gate: np.ndarray, up: np.ndarray,
+                  rnd: int = RND_SINGLE) -> np.ndarray:
+    gate, up = _u16(gate), _u16(up)
+    out = np.empty_like(gate)
+    _check(lib().orc_swish_mul_fwd(degree, fmt_id(fmt), rnd, _p(gate), _p(up), _p(out),
+                                   gate.size))
+    return out
+
+
+def swish_mul_bwd(degree: int, fmt, go: np.ndarray, gate: np.ndarray, up: np.ndarray,
+                  rnd: int = RND_SINGLE):
+    go, gate, up = _u16(go), _u16(gate), _u16(up)
+    gg = np.empty_like(gate)
+    gu = np.empty_like(gate)
+    _check(lib().orc_swish_mul_bwd(degree, fmt_id(fmt), rnd, _p(go), _p(gate), _p(up),
+                                   _p(gg), _p(gu), gate.size))
+    return gg, gu
+
+
+def b3_direct_bf16(x: np.ndarray, with_row: bool = False):
+    x = _u16(x)
+    y = np.empty_like(x)
+    dy = np.empty_like(x)
+    row = np.empty(x.shape, dtype=np.uint8)
+    _check(lib().orc_b3_direct_bf16(_p(x), _p(y), _p(dy), _p(row, ctypes.c_uint8), x.size))
+    return (y, dy, row) if with_row else (y, dy)
+
+
+def b3_direct_f32(s: np.ndarray):
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    y = np.empty(s.shape, dtype=np.uint16)
+    dy = np.empty(s.shape, dtype=np.uint16)
+    _check(lib().orc_b3_direct_f32(_p(s, ctypes.c_float), _p(y), _p(dy), s.size))
+    return y, dy
+
+
+def b3_constants():
+    fwd = np.empty(8, dtype=np.uint16)
+    grad = np.empty(4, dtype=np.uint16)
+    sc = np.empty(2, dtype=np.uint16)
+    _check(lib().orc_b3_constants(_p(fwd), _p(grad), _p(sc)))
+    return fwd.reshape(2, 4), grad.reshape(2, 2), sc
+
+
+def num_threads() -> int:
+    return int(lib().orc_num_threads())
+
+
+# ---- bit-pattern helpers ---------------------------------------------------
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(v: np.ndarray) -> np.ndarray:
+    """RNE float32 -> BF16 bit patterns (NaN kept quiet)."""
+    u = np.ascontiguousarray(v, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7F800000) == 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    keep = (u >> 16).astype(np.uint16) | np.where((u & 0x7FFFFF) != 0, 0x40, 0).astype(np.uint16)
+    return np.where(nan, keep, r).astype(np.uint16)
+
+
+def f16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return np.asarray(b, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def bits_to_f32(b: np.ndarray, fmt) -> np.ndarray:
+    return f16_bits_to_f32(b) if fmt_id(fmt) == F16 else bf16_bits_to_f32(b)
+
+
+def all_bits() -> np.ndarray:
+    """Every 16-bit pattern, 0..65535."""
+    return np.arange(65536, dtype=np.uint32).astype(np.uint16)

@@ -1,0 +1,538 @@
+/*
+ * spline_oracle.c -- CPU restatement of the reference's packed 16-bit
+ * polynomial programs.  TEST INFRASTRUCTURE ONLY (see spline_oracle.h): it is
+ * the checker for the HIP kernels and the CPU baseline of bench.py, never
+ * part of the product path.
+ *
+ * Arithmetic model.  A 16-bit value is carried as a double, which holds every
+ * FP16 and BF16 value exactly.  Each packed instruction of the reference is
+ * restated as "compute exactly, round once":
+ *   - products of two 16-bit values are exact in binary64 (<= 22 bits);
+ *   - a sum is formed with TwoSum and rounded to odd at binary64, which makes
+ *     the final RNE rounding to the 16-bit format a single correct rounding
+ *     (53 >= p + 2 for p = 11 and p = 8);
+ * so hfma(a,b,c) = RNE16(a*b + c), hmul = RNE16(a*b), hadd = RNE16(a + b).
+ * This is the semantics of __hfma2/__hmul2/__hadd2 on __half2 and
+ * __nv_bfloat162 on the reference's target (fma.rn.{f16,bf16}x2).
+ *
+ * The B3 program follows scripts/audit_b3_deployed_fit.py:319-366 literally:
+ * its BF16 FMA is round_bf16(float32(a*b + c)) computed in binary64.
+ */
+#include "spline_oracle.h"
+
+#include <math.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* formats                                                                   */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    int mant;   /* explicit mantissa bits */
+    int emin;   /* exponent of the smallest normal */
+    int emax;   /* exponent of the largest finite */
+    int bias;
+} fmt_t;
+
+static const fmt_t FMT_F16 = {10, -14, 15, 15};
+static const fmt_t FMT_BF16 = {7, -126, 127, 127};
+
+static const fmt_t* fmt_of(int fmt) { return fmt == ORC_F16 ? &FMT_F16 : &FMT_BF16; }
+
+/* Round a double to the format, ties to even; returns the rounded value. */
+static double round_fmt(double v, const fmt_t* f) {
+    if (isnan(v) || isinf(v) || v == 0.0) return v;
+    double a = fabs(v);
+    int e = ilogb(a);
+    if (e < f->emin) e = f->emin;            /* subnormal quantum */
+    double q = ldexp(a, f->mant - e);        /* quantum becomes 1 */
+    double r = nearbyint(q);                 /* RNE (default mode) */
+    double res = ldexp(r, e - f->mant);
+    double maxf = ldexp(2.0 - ldexp(1.0, -f->mant), f->emax);
+    if (res > maxf) res = INFINITY;
+    return copysign(res, v);
+}
+
+/* Bit pattern of a value already representable in the format. */
+static uint16_t bits_fmt(double v, const fmt_t* f) {
+    uint16_t sign = signbit(v) ? (uint16_t)0x8000u : (uint16_t)0u;
+    uint16_t expmask = (uint16_t)(((1u << (15 - f->mant)) - 1u) << f->mant);
+    if (isnan(v)) return (uint16_t)(sign | expmask | (1u << (f->mant - 1)));
+    if (isinf(v)) return (uint16_t)(sign | expmask);
+    double a = fabs(v);
+    if (a == 0.0) return sign;
+    int e = ilogb(a);
+    if (e < f->emin) {
+        double m = ldexp(a, f->mant - f->emin);
+        return (uint16_t)(sign | (uint16_t)m);
+    }
+    double m = ldexp(a, f->mant - e) - ldexp(1.0, f->mant);
+    return (uint16_t)(sign | (uint16_t)((e + f->bias) << f->mant) | (uint16_t)m);
+}
+
+static double value_fmt(uint16_t b, const fmt_t* f) {
+    int sign = (b >> 15) & 1;
+    int e = (b >> f->mant) & ((1 << (15 - f->mant)) - 1);
+    int m = b & ((1 << f->mant) - 1);
+    double v;
+    if (e == (1 << (15 - f->mant)) - 1) {
+        v = m ? NAN : INFINITY;
+    } else if (e == 0) {
+        v = ldexp((double)m, f->emin - f->mant);
+    } else {
+        v = ldexp((double)(m + (1 << f->mant)), e - f->bias - f->mant);
+    }
+    return sign ? -v : v;
+}
+
+/* a + b rounded to odd at binary64 precision (inputs finite, sum exact-able
+ * by TwoSum). */
+static double sum_rto(double a, double b) {
+    double s = a + b;
+    if (!isfinite(s)) return s;
+    double bb = s - a;
+    double err = (a - (s - bb)) + (b - bb);
+    if (err != 0.0) {
+        uint64_t u;
+        memcpy(&u, &s, sizeof u);
+        if ((u & 1u) == 0u) s = nextafter(s, err > 0.0 ? INFINITY : -INFINITY);
+    }
+    return s;
+}
+
+/* Single-rounding operations on values of the format. */
+static double h_fma(double a, double b, double c, const fmt_t* f) {
+    double p = a * b; /* exact for 16-bit operands */
+    if (!isfinite(p) || !isfinite(c)) return round_fmt(p + c, f);
+    return round_fmt(sum_rto(p, c), f);
+}
+static double h_mul(double a, double b, const fmt_t* f) { return round_fmt(a * b, f); }
+static double h_add(double a, double b, const fmt_t* f) {
+    if (!isfinite(a) || !isfinite(b)) return round_fmt(a + b, f);
+    return round_fmt(sum_rto(a, b), f);
+}
+/* FP32-then-BF16 double rounding of a*b + c (an FP32 FMA followed by an RNE
+ * pack to BF16). */
+static double h_fma_f32(double a, double b, double c, const fmt_t* f) {
+    float r = fmaf((float)a, (float)b, (float)c);
+    return round_fmt((double)r, f);
+}
+/* __hmin2 semantics: a NaN operand yields the other operand. */
+static double h_min(double a, double b) {
+    if (isnan(a)) return b;
+    if (isnan(b)) return a;
+    return a < b ? a : b;
+}
+
+/* The constant a float literal takes after __float2half2_rn /
+ * __float2bfloat162_rn: decimal -> binary32 (by the C compiler, RNE) -> RNE. */
+static double kconst(float lit, const fmt_t* f) { return round_fmt((double)lit, f); }
+
+/* ------------------------------------------------------------------------ */
+/* public rounding primitives                                                */
+/* ------------------------------------------------------------------------ */
+
+uint16_t orc_f32_to_bf16_audit(float v) {
+    /* scripts/audit_b3_deployed_fit.py:319-326 */
+    uint32_t bits;
+    memcpy(&bits, &v, sizeof bits);
+    if ((bits & 0x7F800000u) == 0x7F800000u) {
+        /* inf/NaN pass through unrounded; as BF16 bits keep a quiet NaN. */
+        if (bits & 0x007FFFFFu) return (uint16_t)((bits >> 16) | 0x0040u);
+        return (uint16_t)(bits >> 16);
+    }
+    bits = bits + 0x7FFFu + ((bits >> 16) & 1u);
+    return (uint16_t)(bits >> 16);
+}
+uint16_t orc_f64_to_bf16(double v) { return bits_fmt(round_fmt(v, &FMT_BF16), &FMT_BF16); }
+uint16_t orc_f64_to_f16(double v) { return bits_fmt(round_fmt(v, &FMT_F16), &FMT_F16); }
+double orc_bf16_to_f64(uint16_t b) { return value_fmt(b, &FMT_BF16); }
+double orc_f16_to_f64(uint16_t b) { return value_fmt(b, &FMT_F16); }
+
+uint16_t orc_fma16(int fmt, uint16_t a, uint16_t b, uint16_t c) {
+    const fmt_t* f = fmt_of(fmt);
+    return bits_fmt(h_fma(value_fmt(a, f), value_fmt(b, f), value_fmt(c, f), f), f);
+}
+
+static double audit_round_bf16(double v) {
+    /* round_bf16(value): pack to binary32 (RNE), then the bit trick. */
+    float x = (float)v;
+    return value_fmt(orc_f32_to_bf16_audit(x), &FMT_BF16);
+}
+static double audit_bf16_fma(double a, double b, double c) {
+    /* scripts/audit_b3_deployed_fit.py:329-332: round_bf16(left*right + addend)
+     * with the expression evaluated in binary64. */
+    double p = a * b;
+    double s = p + c;
+    return audit_round_bf16(s);
+}
+uint16_t orc_bf16_fma_audit(uint16_t a, uint16_t b, uint16_t c) {
+    double r = audit_bf16_fma(value_fmt(a, &FMT_BF16), value_fmt(b, &FMT_BF16),
+                              value_fmt(c, &FMT_BF16));
+    return bits_fmt(r, &FMT_BF16);
+}
+
+/* ------------------------------------------------------------------------ */
+/* activation program tables                                                 */
+/* ------------------------------------------------------------------------ */
+
+enum {
+    SHAPE_HALF_ODD = 0,   /* 0.5 + sign(x) * t*H(t)                        */
+    SHAPE_ODD = 1,        /* sign(x) * t*H(t)                              */
+    SHAPE_ODD_MIN1 = 2,   /* sign(x) * min(t*H(t), 1)                      */
+    SHAPE_SWISH = 3,      /* fma(|x|, t*H(t), 0.5*x)                       */
+    SHAPE_EVEN = 4,       /* c0 + t*(c1 + ...)                             */
+    SHAPE_X_TIMES = 5     /* x * sigmoid-program(x)                        */
+};
+
+typedef struct {
+    int shape;
+    float lc;       /* clamp on |x| */
+    int deg;
+    float c[7];     /* c[0..deg]; c[0] unused by the odd shapes */
+    int inner;      /* SHAPE_X_TIMES: index of the sigmoid program */
+} prog_t;
+
+/* Index: [family][dir][degree-3]. */
+
+/* FP16 programs: autonumerics_zero/spline_ops/spline_structs_odd.cuh */
+static const prog_t F16_PROGS[3][2][4] = {
+    /* SIGMOID */
+    {
+        {   /* FWD, :14-127 */
+            {SHAPE_HALF_ODD, 6.25f, 3, {0.0f, 0.2812500000f, -0.0534362793f, 0.0033779144f}, -1},
+            {SHAPE_HALF_ODD, 5.0f, 4, {0.0f, 0.2690429688f, -0.0365905762f, -0.0029220581f, 0.0006918907f}, -1},
+            {SHAPE_HALF_ODD, 5.5f, 5, {0.0f, 0.2607421875f, -0.0205383301f, -0.0126800537f, 0.0030593872f, -0.0001997948f}, -1},
+            {SHAPE_HALF_ODD, 5.5f, 6, {0.0f, 0.2539062500f, -0.0053977966f, -0.0239105225f, 0.0067253113f, -0.0007462502f, 0.0000304580f}, -1},
+        },
+        {   /* BWD EVEN, :339-428 */
+            {SHAPE_EVEN, 4.0f, 3, {0.2500000000f, -0.0423889160f, -0.0207824707f, 0.0040893555f}, -1},
+            {SHAPE_EVEN, 5.25f, 4, {0.2500000000f, -0.0103073120f, -0.0606994629f, 0.0183105469f, -0.0015373230f}, -1},
+            {SHAPE_EVEN, 5.5f, 5, {0.2500000000f, 0.0081405640f, -0.0934448242f, 0.0364685059f, -0.0055160522f, 0.0003011227f}, -1},
+            {SHAPE_EVEN, 5.25f, 6, {0.2500000000f, 0.0112609863f, -0.1012573242f, 0.0428466797f, -0.0077819824f, 0.0006651878f, -0.0000216961f}, -1},
+        },
+    },
+    /* TANH */
+    {
+        {   /* FWD ODD, :133-235 */
+            {SHAPE_ODD, 3.25f, 3, {0.0f, 1.1250000000f, -0.4274902344f, 0.0540466309f}, -1},
+            {SHAPE_ODD, 2.75f, 4, {0.0f, 1.1064453125f, -0.3747558594f, 0.0160827637f, 0.0078811646f}, -1},
+            {SHAPE_ODD, 2.75f, 5, {0.0f, 1.0429687500f, -0.1643066406f, -0.2028808594f, 0.0979003906f, -0.0127868652f}, -1},
+            {SHAPE_ODD, 3.0f, 6, {0.0f, 1.0556640625f, -0.1966552734f, -0.1898193359f, 0.1103515625f, -0.0219879150f, 0.0015487671f}, -1},
+        },
+        {   /* BWD EVEN, :434-527 */
+            {SHAPE_EVEN, 2.0f, 3, {1.0000000000f, -0.3391113281f, -0.3325195312f, 0.1308593750f}, -1},
+            {SHAPE_EVEN, 2.5f, 4, {1.0000000000f, -0.0553894043f, -1.0458984375f, 0.6425781250f, -0.1112060547f}, -1},
+            {SHAPE_EVEN, 2.75f, 5, {1.0000000000f, 0.0315551758f, -1.3740234375f, 1.0341796875f, -0.2961425781f, 0.0302276611f}, -1},
+            {SHAPE_EVEN, 3.25f, 6, {1.0000000000f, 0.0289306641f, -1.4033203125f, 1.1250000000f, -0.3789062500f, 0.0596923828f, -0.0036144257f}, -1},
+        },
+    },
+    /* SWISH */
+    {
+        {   /* FWD fused, :241-334 (sigmoid-odd coefficients) */
+            {SHAPE_SWISH, 6.25f, 3, {0.0f, 0.2812500000f, -0.0534362793f, 0.0033779144f}, -1},
+            {SHAPE_SWISH, 5.0f, 4, {0.0f, 0.2690429688f, -0.0365905762f, -0.0029220581f, 0.0006918907f}, -1},
+            {SHAPE_SWISH, 5.5f, 5, {0.0f, 0.2607421875f, -0.0205383301f, -0.0126800537f, 0.0030593872f, -0.0001997948f}, -1},
+            {SHAPE_SWISH, 5.5f, 6, {0.0f, 0.2539062500f, -0.0053977966f, -0.0239105225f, 0.0067253113f, -0.0007462502f, 0.0000304580f}, -1},
+        },
+        {   /* BWD ODD, :533-640 */
+            {SHAPE_HALF_ODD, 5.0f, 3, {0.0f, 0.5703125000f, -0.1676025391f, 0.0148391724f}, -1},
+            {SHAPE_HALF_ODD, 5.5f, 4, {0.0f, 0.5996093750f, -0.2036132812f, 0.0272979736f, -0.0012779236f}, -1},
+            {SHAPE_HALF_ODD, 6.25f, 5, {0.0f, 0.5742187500f, -0.1582031250f, 0.0034561157f, 0.0034828186f, -0.0003206730f}, -1},
+            {SHAPE_HALF_ODD, 5.75f, 6, {0.0f, 0.5415039062f, -0.0898437500f, -0.0439147949f, 0.0179443359f, -0.0023403168f, 0.0001055002f}, -1},
+        },
+    },
+};
+
+/* BF16 programs: autonumerics_zero/spline_ops/spline_structs_odd_bf16.cuh */
+static const prog_t BF16_PROGS[3][2][4] = {
+    /* SIGMOID */
+    {
+        {   /* FWD ODD, :11-121 */
+            {SHAPE_HALF_ODD, 6.0f, 3, {0.0f, 0.2810058594f, -0.0533447266f, 0.0033893585f}, -1},
+            {SHAPE_HALF_ODD, 5.28125f, 4, {0.0f, 0.2714843750f, -0.0402832031f, -0.0014419556f, 0.0005149841f}, -1},
+            {SHAPE_HALF_ODD, 5.40625f, 5, {0.0f, 0.2617187500f, -0.0240478516f, -0.0107421875f, 0.0026550293f, -0.0001697540f}, -1},
+            {SHAPE_HALF_ODD, 4.90625f, 6, {0.0f, 0.2578125000f, -0.0134277344f, -0.0185546875f, 0.0051879883f, -0.0005455017f, 0.0000208616f}, -1},
+        },
+        {   /* BWD EVEN, :310-403 */
+            {SHAPE_EVEN, 4.0f, 3, {0.2500000000f, -0.0424804688f, -0.0207519531f, 0.0040893555f}, -1},
+            {SHAPE_EVEN, 4.75f, 4, {0.2500000000f, -0.0037994385f, -0.0698242188f, 0.0218505859f, -0.0019531250f}, -1},
+            {SHAPE_EVEN, 4.75f, 5, {0.2500000000f, -0.0046386719f, -0.0722656250f, 0.0257568359f, -0.0034027100f, 0.0001573563f}, -1},
+            {SHAPE_EVEN, 4.25f, 6, {0.2500000000f, 0.0117797852f, -0.1025390625f, 0.0439453125f, -0.0081787109f, 0.0007286072f, -0.0000252724f}, -1},
+        },
+    },
+    /* TANH */
+    {
+        {   /* FWD ODD with min(h, 1), :127-241 */
+            {SHAPE_ODD_MIN1, 2.75f, 3, {0.0f, 1.1406250000f, -0.4472656250f, 0.0595703125f}, -1},
+            {SHAPE_ODD_MIN1, 2.75f, 4, {0.0f, 1.0859375000f, -0.3222656250f, -0.0230712891f, 0.0164794922f}, -1},
+            {SHAPE_ODD_MIN1, 2.25f, 5, {0.0f, 1.1171875000f, -0.4023437500f, 0.0245361328f, 0.0129394531f, -0.0018615723f}, -1},
+            {SHAPE_ODD_MIN1, 2.25f, 6, {0.0f, 1.0390625000f, -0.1523437500f, -0.2412109375f, 0.1367187500f, -0.0278320312f, 0.0020446777f}, -1},
+        },
+        {   /* BWD EVEN, :410-503 */
+            {SHAPE_EVEN, 2.0f, 3, {1.0000000000f, -0.3398437500f, -0.3320312500f, 0.1308593750f}, -1},
+            {SHAPE_EVEN, 2.25f, 4, {1.0000000000f, -0.0078735352f, -1.1875000000f, 0.7578125000f, -0.1396484375f}, -1},
+            {SHAPE_EVEN, 2.25f, 5, {1.0000000000f, -0.1210937500f, -0.9257812500f, 0.6289062500f, -0.1533203125f, 0.0129394531f}, -1},
+            {SHAPE_EVEN, 2.25f, 6, {1.0000000000f, -0.0903320312f, -1.0468750000f, 0.7773437500f, -0.2324218750f, 0.0319824219f, -0.0016632080f}, -1},
+        },
+    },
+    /* SWISH */
+    {
+        {   /* FWD, :248-304: D3/D4 fused odd form, D5/D6 x * sigmoid(x) */
+            {SHAPE_SWISH, 6.0f, 3, {0.0f, 0.2810058594f, -0.0533447266f, 0.0033893585f}, -1},
+            {SHAPE_SWISH, 5.28125f, 4, {0.0f, 0.2714843750f, -0.0402832031f, -0.0014419556f, 0.0005149841f}, -1},
+            {SHAPE_X_TIMES, 0.0f, 5, {0.0f}, 2},
+            {SHAPE_X_TIMES, 0.0f, 6, {0.0f}, 3},
+        },
+        {   /* BWD ODD, :510-619 */
+            {SHAPE_HALF_ODD, 4.75f, 3, {0.0f, 0.5820312500f, -0.1777343750f, 0.0164794922f}, -1},
+            {SHAPE_HALF_ODD, 5.25f, 4, {0.0f, 0.6093750000f, -0.2128906250f, 0.0296630859f, -0.0014572144f}, -1},
+            {SHAPE_HALF_ODD, 4.75f, 5, {0.0f, 0.5742187500f, -0.1582031250f, 0.0034484863f, 0.0034790039f, -0.0003204346f}, -1},
+            {SHAPE_HALF_ODD, 5.0f, 6, {0.0f, 0.6015625000f, -0.2050781250f, 0.0260009766f, -0.0004787445f, -0.0001363754f, 0.0000074804f}, -1},
+        },
+    },
+};
+
+static const prog_t* find_prog(int family, int dir, int degree, int fmt) {
+    if (family < 0 || family > 2 || dir < 0 || dir > 1 || degree < 3 || degree > 6) return 0;
+    return fmt == ORC_F16 ? &F16_PROGS[family][dir][degree - 3]
+                          : &BF16_PROGS[family][dir][degree - 3];
+}
+
+typedef struct {
+    const fmt_t* f;
+    int rnd;
+} ctx_t;
+
+static double c_fma(const ctx_t* k, double a, double b, double c) {
+    if (k->f == &FMT_BF16 && k->rnd == ORC_RND_F32) return h_fma_f32(a, b, c, k->f);
+    return h_fma(a, b, c, k->f);
+}
+
+/* Evaluate one program on one value (the lane program of the .cuh struct). */
+static double eval_prog(const prog_t* p, double x, const ctx_t* k) {
+    const fmt_t* f = k->f;
+    if (p->shape == SHAPE_X_TIMES) {
+        /* SWISH_FWD_D{5,6}_ODD_BF16: __hmul2(val, SIGMOID_FWD_D{5,6}(val)) */
+        const prog_t* s = &BF16_PROGS[0][0][p->inner];
+        return h_mul(x, eval_prog(s, x, k), f);
+    }
+    int neg = signbit(x) != 0;
+    double ax = fabs(x);                         /* abs_bits (NaN stays NaN) */
+    double t = h_min(ax, kconst(p->lc, f));
+    if (p->shape == SHAPE_EVEN) {
+        double r = c_fma(k, t, kconst(p->c[p->deg], f), kconst(p->c[p->deg - 1], f));
+        for (int i = p->deg - 2; i >= 0; --i) r = c_fma(k, t, r, kconst(p->c[i], f));
+        return r;
+    }
+    double h = c_fma(k, t, kconst(p->c[p->deg], f), kconst(p->c[p->deg - 1], f));
+    for (int i = p->deg - 2; i >= 1; --i) h = c_fma(k, t, h, kconst(p->c[i], f));
+    h = h_mul(t, h, f);
+    switch (p->shape) {
+    case SHAPE_HALF_ODD:
+        return h_add(kconst(0.5f, f), neg ? -h : h, f);
+    case SHAPE_ODD:
+        return neg ? -h : h;
+    case SHAPE_ODD_MIN1:
+        h = h_min(h, kconst(1.0f, f));
+        return neg ? -h : h;
+    case SHAPE_SWISH:
+        return c_fma(k, ax, h, h_mul(kconst(0.5f, f), x, f));
+    default:
+        return NAN;
+    }
+}
+
+int orc_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+int orc_activation(int family, int dir, int degree, int fmt, int rnd,
+                   const uint16_t* x, uint16_t* y, int64_t n) {
+    const prog_t* p = find_prog(family, dir, degree, fmt);
+    if (!p || n < 0 || (fmt != ORC_F16 && fmt != ORC_BF16)) return -1;
+    ctx_t k = {fmt_of(fmt), rnd};
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        y[i] = bits_fmt(eval_prog(p, value_fmt(x[i], k.f), &k), k.f);
+    return 0;
+}
+
+int orc_activation_bwd(int family, int degree, int fmt, int rnd,
+                       const uint16_t* go, const uint16_t* x, uint16_t* gi,
+                       int64_t n) {
+    const prog_t* p = find_prog(family, ORC_BWD, degree, fmt);
+    if (!p || n < 0) return -1;
+    ctx_t k = {fmt_of(fmt), rnd};
+    /* binary_vec_kernel: gi = __hmul2(go, GradFunc::evaluate(x)) */
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        double d = eval_prog(p, value_fmt(x[i], k.f), &k);
+        gi[i] = bits_fmt(h_mul(value_fmt(go[i], k.f), d, k.f), k.f);
+    }
+    return 0;
+}
+
+int orc_activation_bwd_alg(int family, int fmt, const uint16_t* go,
+                           const uint16_t* y, uint16_t* gi, int64_t n) {
+    if ((family != ORC_SIGMOID && family != ORC_TANH) || n < 0) return -1;
+    const fmt_t* f = fmt_of(fmt);
+    double one = kconst(1.0f, f);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        double yy = value_fmt(y[i], f);
+        double d;
+        if (family == ORC_SIGMOID) /* SIGMOID_BWD_ALGEBRAIC: y * (1 - y) */
+            d = h_mul(yy, h_add(one, -yy, f), f);
+        else                       /* TANH_BWD_ALGEBRAIC: 1 - y*y */
+            d = h_add(one, -h_mul(yy, yy, f), f);
+        gi[i] = bits_fmt(h_mul(value_fmt(go[i], f), d, f), f);
+    }
+    return 0;
+}
+
+int orc_swish_mul_fwd(int degree, int fmt, int rnd, const uint16_t* gate,
+                      const uint16_t* up, uint16_t* out, int64_t n) {
+    const prog_t* p = find_prog(ORC_SWISH, ORC_FWD, degree, fmt);
+    if (!p || n < 0) return -1;
+    ctx_t k = {fmt_of(fmt), rnd};
+    /* swish_mul_vec_kernel: __hmul2(Func::evaluate(gate), up) */
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        double s = eval_prog(p, value_fmt(gate[i], k.f), &k);
+        out[i] = bits_fmt(h_mul(s, value_fmt(up[i], k.f), k.f), k.f);
+    }
+    return 0;
+}
+
+int orc_swish_mul_bwd(int degree, int fmt, int rnd, const uint16_t* go,
+                      const uint16_t* gate, const uint16_t* up,
+                      uint16_t* grad_gate, uint16_t* grad_up, int64_t n) {
+    const prog_t* pf = find_prog(ORC_SWISH, ORC_FWD, degree, fmt);
+    const prog_t* pb = find_prog(ORC_SWISH, ORC_BWD, degree, fmt);
+    if (!pf || !pb || n < 0) return -1;
+    ctx_t k = {fmt_of(fmt), rnd};
+    const fmt_t* f = k.f;
+    int algebraic = (fmt == ORC_BF16 && degree == 3);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        double g = value_fmt(gate[i], f);
+        double o = value_fmt(go[i], f);
+        double u = value_fmt(up[i], f);
+        double swish, deriv;
+        if (algebraic) {
+            /* spline_kernels_bf16.cu:257-265 (swish_d3_fwd_bwd_alg_bf16) */
+            double sig = eval_prog(&BF16_PROGS[0][0][0], g, &k);
+            swish = h_mul(g, sig, f);
+            deriv = c_fma(&k, swish, h_add(kconst(1.0f, f), -sig, f), sig);
+        } else {
+            swish = eval_prog(pf, g, &k);
+            deriv = eval_prog(pb, g, &k);
+        }
+        /* grad_gate = (go*up)*deriv ; grad_up = go*swish */
+        grad_gate[i] = bits_fmt(h_mul(h_mul(o, u, f), deriv, f), f);
+        grad_up[i] = bits_fmt(h_mul(o, swish, f), f);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* B3: deployed direct D3 + factored D4 (scripts/audit_b3_deployed_fit.py)   */
+/* ------------------------------------------------------------------------ */
+
+/* Manifest values as pinned by tests/test_audit_b3_deployed_fit.py:30-37 and
+ * the sequence length 4096, clamp 6, split 1.25 of the PTX listing
+ * (extras/paper/manuscript/main.tex:1046-1051). */
+static const double B3_FWD_ROWS[2][4] = {
+    {1.0, 1.0546875, 0.53515625, 0.11328125},
+    {-8.5625, 17.5, -9.0625, 2.140625},
+};
+static const double B3_GRAD_ROWS[2][2] = {
+    {1.0, -0.0087890625},
+    {1.0078125, -0.0028076171875},
+};
+static const double B3_SEQUENCE_LENGTH = 4096.0;
+static const double B3_CLAMP = 6.0;
+static const double B3_SPLIT = 1.25;
+
+/* DirectB3Spec.deployed_forward_rows / deployed_gradient_factors (:58-70). */
+static void b3_deployed(double fwd[2][4], double grad[2][2]) {
+    double scale = 1.0 / B3_SEQUENCE_LENGTH;
+    for (int r = 0; r < 2; ++r) {
+        for (int j = 0; j < 4; ++j) fwd[r][j] = audit_round_bf16(B3_FWD_ROWS[r][j] * scale);
+        for (int j = 0; j < 2; ++j) grad[r][j] = audit_round_bf16(B3_GRAD_ROWS[r][j]);
+    }
+}
+
+int orc_b3_constants(uint16_t* fwd8, uint16_t* grad4, uint16_t* split_clamp2) {
+    double fwd[2][4], grad[2][2];
+    b3_deployed(fwd, grad);
+    for (int r = 0; r < 2; ++r) {
+        for (int j = 0; j < 4; ++j) fwd8[r * 4 + j] = bits_fmt(fwd[r][j], &FMT_BF16);
+        for (int j = 0; j < 2; ++j) grad4[r * 2 + j] = bits_fmt(grad[r][j], &FMT_BF16);
+    }
+    split_clamp2[0] = bits_fmt(audit_round_bf16(B3_SPLIT), &FMT_BF16);
+    split_clamp2[1] = bits_fmt(audit_round_bf16(B3_CLAMP), &FMT_BF16);
+    return 0;
+}
+
+/* Python's built-in max(a, b) / min(a, b): the first argument is kept unless
+ * the second compares strictly greater (smaller). */
+static double py_max(double a, double b) { return b > a ? b : a; }
+static double py_min(double a, double b) { return b < a ? b : a; }
+
+/* evaluate_deployed (:341-366) on a score already rounded to BF16. */
+static void b3_eval(double input, const double fwd[2][4], const double grad[2][2],
+                    double* y, double* dy, int* row_out) {
+    double split = audit_round_bf16(B3_SPLIT);
+    double clamp = audit_round_bf16(B3_CLAMP);
+    int row = input >= split ? 1 : 0;
+    double clamped = py_min(py_max(input, -clamp), clamp);
+    const double* c = fwd[row];
+    double forward = c[3];
+    for (int j = 2; j >= 0; --j) forward = audit_bf16_fma(clamped, forward, c[j]);
+    forward = py_max(audit_round_bf16(0.0), forward);
+    double factor = audit_bf16_fma(clamped, grad[row][1], grad[row][0]);
+    double derivative = audit_round_bf16(forward * factor);
+    *y = forward;
+    *dy = derivative;
+    if (row_out) *row_out = row;
+}
+
+int orc_b3_direct_bf16(const uint16_t* x, uint16_t* y, uint16_t* dy,
+                       uint8_t* row, int64_t n) {
+    if (n < 0) return -1;
+    double fwd[2][4], grad[2][2];
+    b3_deployed(fwd, grad);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        double yy, dd;
+        int r;
+        b3_eval(value_fmt(x[i], &FMT_BF16), fwd, grad, &yy, &dd, &r);
+        y[i] = bits_fmt(yy, &FMT_BF16);
+        dy[i] = bits_fmt(dd, &FMT_BF16);
+        if (row) row[i] = (uint8_t)r;
+    }
+    return 0;
+}
+
+int orc_b3_direct_f32(const float* s, uint16_t* y, uint16_t* dy, int64_t n) {
+    if (n < 0) return -1;
+    double fwd[2][4], grad[2][2];
+    b3_deployed(fwd, grad);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        double yy, dd;
+        b3_eval(audit_round_bf16((double)s[i]), fwd, grad, &yy, &dd, 0);
+        y[i] = bits_fmt(yy, &FMT_BF16);
+        dy[i] = bits_fmt(dd, &FMT_BF16);
+    }
+    return 0;
+}

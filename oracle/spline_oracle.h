@@ -1,0 +1,83 @@
+/*
+ * spline_oracle.h -- CPU restatement of the reference's packed FP16/BF16
+ * polynomial programs.  TEST INFRASTRUCTURE ONLY: tests/, the smoke check in
+ * __graft_entry__.py and the cpu_baseline leg of bench.py may load this
+ * library, and only as the checker.  Nothing in the product path links it.
+ *
+ * All 16-bit values cross this interface as raw bit patterns (uint16_t).
+ * Every function returns 0 on success and a negative code on bad arguments.
+ */
+#ifndef SPLINE_ORACLE_H
+#define SPLINE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage formats. */
+enum { ORC_F16 = 0, ORC_BF16 = 1 };
+
+/* Activation families and directions. */
+enum { ORC_SIGMOID = 0, ORC_TANH = 1, ORC_SWISH = 2 };
+enum { ORC_FWD = 0, ORC_BWD = 1 };
+
+/* BF16 FMA semantics for the activation programs.
+ * ORC_RND_SINGLE: one rounding of the exact a*b+c (the reference's
+ *                 fma.rn.bf16x2 / __hfma2 semantics).
+ * ORC_RND_F32:    round to binary32 first, then to BF16 (what an FP32 FMA
+ *                 followed by an RNE pack computes).
+ * FP16 always uses single rounding. */
+enum { ORC_RND_SINGLE = 0, ORC_RND_F32 = 1 };
+
+/* ---- rounding primitives ---------------------------------------------- */
+uint16_t orc_f32_to_bf16_audit(float v);   /* audit round_bf16 bit trick   */
+uint16_t orc_f64_to_bf16(double v);        /* RNE                          */
+uint16_t orc_f64_to_f16(double v);         /* RNE                          */
+double orc_bf16_to_f64(uint16_t b);
+double orc_f16_to_f64(uint16_t b);
+/* Single-rounding fused multiply-add on 16-bit operands (bit patterns). */
+uint16_t orc_fma16(int fmt, uint16_t a, uint16_t b, uint16_t c);
+/* Audit emulation of one fma.rn.bf16x2 lane: round_bf16(a*b + c). */
+uint16_t orc_bf16_fma_audit(uint16_t a, uint16_t b, uint16_t c);
+
+/* ---- activation programs (spline_structs_odd*.cuh) --------------------- */
+/* y[i] = P(x[i]) for the forward program, or the derivative program for
+ * dir == ORC_BWD.  degree 3..6. */
+int orc_activation(int family, int dir, int degree, int fmt, int rnd,
+                   const uint16_t* x, uint16_t* y, int64_t n);
+/* gi = go * G(x)  (binary_vec_kernel). */
+int orc_activation_bwd(int family, int degree, int fmt, int rnd,
+                       const uint16_t* go, const uint16_t* x, uint16_t* gi,
+                       int64_t n);
+/* gi = go * alg(y): sigmoid y(1-y), tanh 1-y^2. */
+int orc_activation_bwd_alg(int family, int fmt, const uint16_t* go,
+                           const uint16_t* y, uint16_t* gi, int64_t n);
+/* out = F(gate) * up. */
+int orc_swish_mul_fwd(int degree, int fmt, int rnd, const uint16_t* gate,
+                      const uint16_t* up, uint16_t* out, int64_t n);
+/* grad_gate = (go*up)*F'(gate), grad_up = go*F(gate); BF16 degree 3 uses the
+ * algebraic derivative fma(swish, 1-sigma, sigma). */
+int orc_swish_mul_bwd(int degree, int fmt, int rnd, const uint16_t* go,
+                      const uint16_t* gate, const uint16_t* up,
+                      uint16_t* grad_gate, uint16_t* grad_up, int64_t n);
+
+/* ---- B3 deployed direct D3 / factored D4 (audit_b3_deployed_fit.py) ---- */
+/* x: BF16 scores.  y = probability, dy = derivative, both BF16.
+ * row (optional, may be NULL): selected coefficient row. */
+int orc_b3_direct_bf16(const uint16_t* x, uint16_t* y, uint16_t* dy,
+                       uint8_t* row, int64_t n);
+/* Same program on FP32 scores (rounded to BF16 first, as the audit does). */
+int orc_b3_direct_f32(const float* s, uint16_t* y, uint16_t* dy, int64_t n);
+/* Deployed constants as BF16 bit patterns: fwd[2][4] (c0..c3 after 1/4096
+ * scaling), grad[2][2] (intercept, slope), split, clamp. */
+int orc_b3_constants(uint16_t* fwd8, uint16_t* grad4, uint16_t* split_clamp2);
+
+/* Thread count used by the bulk loops (OpenMP when built with it). */
+int orc_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
