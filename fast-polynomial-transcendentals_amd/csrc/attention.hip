@@ -66,15 +66,15 @@ struct B3FwdOp {
 };
 
 // FP32 scores: 8 scores (32 B) per thread-iteration, two 16-byte loads.
-template <bool NT>
+template <bool LNT, bool SNT>
 __global__ void __launch_bounds__(kBlock)
 b3_f32_kernel(const float* __restrict__ s, uint16_t* __restrict__ y, uint16_t* __restrict__ dy,
               int64_t n, int vec_ok) {
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     const int64_t n8 = vec_ok ? (n >> 3) : 0;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n8; i += stride) {
-        const Vec4 a = ld16<NT>(s, 2 * i);
-        const Vec4 c = ld16<NT>(s, 2 * i + 1);
+        const Vec4 a = ld16<LNT>(s, 2 * i);
+        const Vec4 c = ld16<LNT>(s, 2 * i + 1);
         const uint32_t w[8] = {a.w[0], a.w[1], a.w[2], a.w[3], c.w[0], c.w[1], c.w[2], c.w[3]};
         Vec4 oy, od;
 #pragma unroll
@@ -85,8 +85,8 @@ b3_f32_kernel(const float* __restrict__ s, uint16_t* __restrict__ y, uint16_t* _
             oy.w[k] = pack_exact_bf(y0, y1);
             od.w[k] = pack_bf(d0, d1);
         }
-        st16<NT>(y, i, oy);
-        st16<NT>(dy, i, od);
+        st16<SNT>(y, i, oy);
+        st16<SNT>(dy, i, od);
     }
     for (int64_t e = (n8 << 3) + (int64_t)blockIdx.x * kBlock + threadIdx.x; e < n; e += stride) {
         float yy, dd;
@@ -117,16 +117,24 @@ extern "C" int launch_flash_sigmoid_direct_d3_d4_f32_bf16(void* y, void* dy, con
     if (bad_args(size, {y, dy, scores})) return hipErrorInvalidValue;
     if (size == 0) return hipSuccess;
     const int vec_ok = aligned16(y) && aligned16(dy) && aligned16(scores);
-    const int64_t grid = grid_for_vectors((size + 7) >> 3, 1, 8);
-    const bool nt = size * 8 >= kNonTemporalBytes;
-    if (nt)
-        hipLaunchKernelGGL((b3_f32_kernel<true>), dim3((unsigned)grid), dim3(kBlock), 0,
+    const int64_t grid = grid_one_pass(vec_ok ? (size >> 3) : size);
+    // 4 bytes read and 4 bytes written per score.
+    switch (nt_mode(4 * size, 4 * size)) {
+    case kNtBoth:
+        hipLaunchKernelGGL((b3_f32_kernel<true, true>), dim3((unsigned)grid), dim3(kBlock), 0,
                            hs(stream), (const float*)scores, (uint16_t*)y, (uint16_t*)dy, size,
                            vec_ok);
-    else
-        hipLaunchKernelGGL((b3_f32_kernel<false>), dim3((unsigned)grid), dim3(kBlock), 0,
+        break;
+    case kNtStore:
+        hipLaunchKernelGGL((b3_f32_kernel<false, true>), dim3((unsigned)grid), dim3(kBlock), 0,
                            hs(stream), (const float*)scores, (uint16_t*)y, (uint16_t*)dy, size,
                            vec_ok);
+        break;
+    default:
+        hipLaunchKernelGGL((b3_f32_kernel<false, false>), dim3((unsigned)grid), dim3(kBlock), 0,
+                           hs(stream), (const float*)scores, (uint16_t*)y, (uint16_t*)dy, size,
+                           vec_ok);
+    }
     return hipGetLastError();
 }
 

@@ -3,12 +3,13 @@
 // Layout: every tensor is a flat array of 16-bit elements.  A thread moves
 // 16-byte vectors (8 elements = 4 pairs) with global_load_dwordx4 /
 // global_store_dwordx4; a wavefront touches 1 KiB of each stream per
-// vector, fully coalesced.  Each thread keeps UNROLL vectors per stream in
-// flight before it computes, so one CU holds enough outstanding loads to
-// cover HBM latency at full occupancy.  The grid is persistent (a small
-// multiple of the CU count) and grid-strides over the vectors, so the
-// block -> address mapping is the same on every launch: a tensor that fits
-// in the aggregate L2 is re-read from the XCD that last touched it.
+// vector, fully coalesced.  The launch is one pass: one vector per thread,
+// so every wave issues its loads at once and the whole grid keeps the
+// maximum number of 16-byte requests in flight (measured on MI355X: one
+// pass at one vector per thread beats persistent grids with 2-8 vectors per
+// thread by 4-7 % at 2^28 elements).  The block -> address mapping is the
+// same on every launch, so a tensor that fits in L2 is re-read from the XCD
+// that last touched it.
 //
 // Tails: elements past the last full vector (at most 7) are processed by
 // block 0 with each element duplicated into both lanes of a pair, which is
@@ -63,68 +64,50 @@ struct Streams {
 //   __device__ static void pair(const uint32_t (&in)[NIN], uint32_t (&out)[NOUT]);
 // `pair` maps one 32-bit pair of every input stream to one pair of every
 // output stream.
-template <class Op, int UNROLL, bool NT>
+template <class Op>
+__device__ __forceinline__ void apply_vec(const Vec4 (&v)[Op::NIN], Vec4 (&o)[Op::NOUT]) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t a[Op::NIN], b[Op::NOUT];
+#pragma unroll
+        for (int k = 0; k < Op::NIN; ++k) a[k] = v[k].w[w];
+        Op::pair(a, b);
+#pragma unroll
+        for (int k = 0; k < Op::NOUT; ++k) o[k].w[w] = b[k];
+    }
+}
+
+// One 16-byte vector per stream per thread-iteration.  The launch grid
+// normally covers every vector once (one pass); the stride loop only runs
+// more than once for launches beyond the grid limit.  LNT / SNT select
+// non-temporal loads / stores.
+template <class Op, bool LNT, bool SNT>
 __global__ void __launch_bounds__(kBlock)
 pairwise_kernel(Streams<Op::NIN, Op::NOUT> s, int64_t n) {
     constexpr int NIN = Op::NIN;
     constexpr int NOUT = Op::NOUT;
     const int64_t n_vec = n >> 3;
     const int64_t stride = (int64_t)gridDim.x * kBlock;
-    int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-
-    for (; i + (UNROLL - 1) * stride < n_vec; i += UNROLL * stride) {
-        Vec4 v[UNROLL][NIN];
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n_vec; i += stride) {
+        Vec4 v[NIN], o[NOUT];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
+        for (int k = 0; k < NIN; ++k) v[k] = ld16<LNT>(s.in[k], i);
+        apply_vec<Op>(v, o);
 #pragma unroll
-            for (int k = 0; k < NIN; ++k) v[u][k] = ld16<NT>(s.in[k], i + u * stride);
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            Vec4 o[NOUT];
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                uint32_t a[NIN], b[NOUT];
-#pragma unroll
-                for (int k = 0; k < NIN; ++k) a[k] = v[u][k].w[w];
-                Op::pair(a, b);
-#pragma unroll
-                for (int k = 0; k < NOUT; ++k) o[k].w[w] = b[k];
-            }
-#pragma unroll
-            for (int k = 0; k < NOUT; ++k) st16<NT>(s.out[k], i + u * stride, o[k]);
-        }
+        for (int k = 0; k < NOUT; ++k) st16<SNT>(s.out[k], i, o[k]);
     }
-    for (; i < n_vec; i += stride) {
-        Vec4 v[NIN];
-#pragma unroll
-        for (int k = 0; k < NIN; ++k) v[k] = ld16<NT>(s.in[k], i);
-        Vec4 o[NOUT];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            uint32_t a[NIN], b[NOUT];
-#pragma unroll
-            for (int k = 0; k < NIN; ++k) a[k] = v[k].w[w];
-            Op::pair(a, b);
-#pragma unroll
-            for (int k = 0; k < NOUT; ++k) o[k].w[w] = b[k];
-        }
-#pragma unroll
-        for (int k = 0; k < NOUT; ++k) st16<NT>(s.out[k], i, o[k]);
-    }
-    if (blockIdx.x == 0) {
+    if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
         const int64_t e = (n_vec << 3) + threadIdx.x;
-        if (threadIdx.x < (n & 7)) {
-            uint32_t a[NIN], b[NOUT];
+        uint32_t a[NIN], b[NOUT];
 #pragma unroll
-            for (int k = 0; k < NIN; ++k) {
-                const uint32_t x = reinterpret_cast<const uint16_t*>(s.in[k])[e];
-                a[k] = x | (x << 16);
-            }
-            Op::pair(a, b);
-#pragma unroll
-            for (int k = 0; k < NOUT; ++k)
-                reinterpret_cast<uint16_t*>(s.out[k])[e] = (uint16_t)(b[k] & 0xffffu);
+        for (int k = 0; k < NIN; ++k) {
+            const uint32_t x = reinterpret_cast<const uint16_t*>(s.in[k])[e];
+            a[k] = x | (x << 16);
         }
+        Op::pair(a, b);
+#pragma unroll
+        for (int k = 0; k < NOUT; ++k)
+            reinterpret_cast<uint16_t*>(s.out[k])[e] = (uint16_t)(b[k] & 0xffffu);
     }
 }
 
@@ -159,16 +142,32 @@ struct DeviceShape {
 
 DeviceShape device_shape();
 
-// Streams at or above this many bytes (all inputs + outputs) bypass the
-// caches with non-temporal accesses: they cannot stay resident in the
-// 256 MiB MALL anyway.
-constexpr int64_t kNonTemporalBytes = 512ll << 20;
+// Cache policy, measured on MI355X (256 MiB MALL, 4 MiB L2 per XCD):
+//  * outputs of 64 MiB or more are stored non-temporally: they cannot stay
+//    in L2, and bypassing the MALL keeps it for the inputs (+12-15 % HBM
+//    throughput for a 1:1 read/write stream);
+//  * inputs larger than the MALL are also loaded non-temporally (+4 %);
+//    inputs that fit are loaded normally so repeated passes can hit the MALL.
+constexpr int64_t kNtStoreBytes = 64ll << 20;
+constexpr int64_t kMallBytes = 256ll << 20;
 
+enum NtMode : int { kNtNone = 0, kNtStore = 1, kNtBoth = 2 };
+
+inline int nt_mode(int64_t in_bytes, int64_t out_bytes) {
+    if (in_bytes > kMallBytes) return kNtBoth;
+    if (out_bytes >= kNtStoreBytes) return kNtStore;
+    return kNtNone;
+}
+
+// Blocks for a one-pass launch over `n_items` work items (1 per thread),
+// clamped to the grid limit (the kernels stride over any remainder).
+int64_t grid_one_pass(int64_t n_items);
+// Blocks for a persistent launch: at most `blocks_per_cu` per CU.
 int64_t grid_for_vectors(int64_t n_vec, int unroll, int blocks_per_cu);
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-template <class Op, int UNROLL = 2>
+template <class Op>
 hipError_t launch_pairwise(Streams<Op::NIN, Op::NOUT> s, int64_t n, hipStream_t stream) {
     if (n < 0) return hipErrorInvalidValue;
     if (n == 0) return hipSuccess;
@@ -176,20 +175,25 @@ hipError_t launch_pairwise(Streams<Op::NIN, Op::NOUT> s, int64_t n, hipStream_t 
     for (int k = 0; k < Op::NIN; ++k) ok = ok && aligned16(s.in[k]);
     for (int k = 0; k < Op::NOUT; ++k) ok = ok && aligned16(s.out[k]);
     if (!ok) {
-        int64_t grid = grid_for_vectors((n + 7) >> 3, 8, 8);
+        const int64_t grid = grid_one_pass(n);
         hipLaunchKernelGGL((pairwise_element_kernel<Op>), dim3((unsigned)grid), dim3(kBlock), 0,
                            stream, s, n);
         return hipGetLastError();
     }
     const int64_t n_vec = n >> 3;
-    const int64_t bytes = n * 2 * (Op::NIN + Op::NOUT);
-    const int64_t grid = grid_for_vectors(n_vec, UNROLL, 8);
-    if (bytes >= kNonTemporalBytes) {
-        hipLaunchKernelGGL((pairwise_kernel<Op, UNROLL, true>), dim3((unsigned)grid),
-                           dim3(kBlock), 0, stream, s, n);
-    } else {
-        hipLaunchKernelGGL((pairwise_kernel<Op, UNROLL, false>), dim3((unsigned)grid),
-                           dim3(kBlock), 0, stream, s, n);
+    const int64_t grid = grid_one_pass(n_vec);
+    switch (nt_mode(n * 2 * Op::NIN, n * 2 * Op::NOUT)) {
+    case kNtBoth:
+        hipLaunchKernelGGL((pairwise_kernel<Op, true, true>), dim3((unsigned)grid), dim3(kBlock),
+                           0, stream, s, n);
+        break;
+    case kNtStore:
+        hipLaunchKernelGGL((pairwise_kernel<Op, false, true>), dim3((unsigned)grid), dim3(kBlock),
+                           0, stream, s, n);
+        break;
+    default:
+        hipLaunchKernelGGL((pairwise_kernel<Op, false, false>), dim3((unsigned)grid), dim3(kBlock),
+                           0, stream, s, n);
     }
     return hipGetLastError();
 }

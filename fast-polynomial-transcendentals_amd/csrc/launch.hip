@@ -23,6 +23,13 @@ DeviceShape device_shape() {
     return DeviceShape{cus};
 }
 
+int64_t grid_one_pass(int64_t n_items) {
+    const int64_t need = (n_items + kBlock - 1) / kBlock;
+    // HSA grid sizes count work-items in 32 bits.
+    const int64_t limit = 0xffffffffll / kBlock;
+    return need < 1 ? 1 : (need > limit ? limit : need);
+}
+
 int64_t grid_for_vectors(int64_t n_vec, int unroll, int blocks_per_cu) {
     const int64_t per_block = (int64_t)kBlock * unroll;
     int64_t need = (n_vec + per_block - 1) / per_block;
@@ -35,7 +42,7 @@ int64_t grid_for_vectors(int64_t n_vec, int unroll, int blocks_per_cu) {
 
 extern "C" int spline_hip_grid_for(int64_t size, int streams, int64_t* grid_out, int* cus_out) {
     if (size < 0 || streams <= 0) return hipErrorInvalidValue;
-    if (grid_out) *grid_out = pt::grid_for_vectors(size >> 3, 2, 8);
+    if (grid_out) *grid_out = pt::grid_one_pass(size >> 3);
     if (cus_out) *cus_out = pt::device_shape().cus;
     return hipSuccess;
 }

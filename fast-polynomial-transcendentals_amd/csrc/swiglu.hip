@@ -29,7 +29,7 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
 
 // Packed forward: vector v of the output row-major [rows, H] maps to
 // gate vector r*2*hv + c and up vector r*2*hv + hv + c (hv = H/8 vectors).
-template <class Op, bool NT>
+template <class Op, bool LNT, bool SNT>
 __global__ void __launch_bounds__(kBlock)
 packed_fwd_kernel(const void* __restrict__ packed, void* __restrict__ out, uint32_t n_vec,
                   uint32_t hv, FastDiv div_hv) {
@@ -38,8 +38,8 @@ packed_fwd_kernel(const void* __restrict__ packed, void* __restrict__ out, uint3
     for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < n_vec; v += stride) {
         const uint32_t r = fast_div(v, div_hv);
         const int64_t g = (int64_t)r * hv + v;  // = r*2*hv + c
-        const Vec4 gate = ld16<NT>(packed, g);
-        const Vec4 up = ld16<NT>(packed, g + hv);
+        const Vec4 gate = ld16<LNT>(packed, g);
+        const Vec4 up = ld16<LNT>(packed, g + hv);
         Vec4 o;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -47,12 +47,12 @@ packed_fwd_kernel(const void* __restrict__ packed, void* __restrict__ out, uint3
             Op::pair(a, b);
             o.w[w] = b[0];
         }
-        st16<NT>(out, v, o);
+        st16<SNT>(out, v, o);
     }
 }
 
 // Packed backward: grad_out is [rows, H]; grad_packed mirrors packed.
-template <class Op, bool NT>
+template <class Op, bool LNT, bool SNT>
 __global__ void __launch_bounds__(kBlock)
 packed_bwd_kernel(const void* __restrict__ grad_out, const void* __restrict__ packed,
                   void* __restrict__ grad_packed, uint32_t n_vec, uint32_t hv, FastDiv div_hv) {
@@ -61,9 +61,9 @@ packed_bwd_kernel(const void* __restrict__ grad_out, const void* __restrict__ pa
     for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < n_vec; v += stride) {
         const uint32_t r = fast_div(v, div_hv);
         const int64_t g = (int64_t)r * hv + v;
-        const Vec4 go = ld16<NT>(grad_out, v);
-        const Vec4 gate = ld16<NT>(packed, g);
-        const Vec4 up = ld16<NT>(packed, g + hv);
+        const Vec4 go = ld16<LNT>(grad_out, v);
+        const Vec4 gate = ld16<LNT>(packed, g);
+        const Vec4 up = ld16<LNT>(packed, g + hv);
         Vec4 gg, gu;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -72,8 +72,8 @@ packed_bwd_kernel(const void* __restrict__ grad_out, const void* __restrict__ pa
             gg.w[w] = b[0];
             gu.w[w] = b[1];
         }
-        st16<NT>(grad_packed, g, gg);
-        st16<NT>(grad_packed, g + hv, gu);
+        st16<SNT>(grad_packed, g, gg);
+        st16<SNT>(grad_packed, g + hv, gu);
     }
 }
 
@@ -114,32 +114,33 @@ int launch_packed(void* out, const void* grad_out, const void* packed, int64_t r
     const int64_t n_vec = n / 8;
     const bool vec = (h % 8 == 0) && aligned16(out) && aligned16(packed) &&
                      (!BWD || aligned16(grad_out)) && n_vec < (int64_t(1) << 31);
-    const int streams = BWD ? 5 : 3;
     if (!vec) {
-        const int64_t grid = grid_for_vectors((n + 7) >> 3, 8, 8);
+        const int64_t grid = grid_one_pass(n);
         hipLaunchKernelGGL((packed_element_kernel<Op, BWD>), dim3((unsigned)grid), dim3(kBlock), 0,
                            hs(stream), grad_out, packed, out, rows, h);
         return hipGetLastError();
     }
     const uint32_t hv = (uint32_t)(h / 8);
     const FastDiv div = make_fastdiv(hv);
-    const int64_t grid = grid_for_vectors(n_vec, 1, 8);
-    const bool nt = n * 2 * streams >= kNonTemporalBytes;
-    if constexpr (BWD) {
-        if (nt)
-            hipLaunchKernelGGL((packed_bwd_kernel<Op, true>), dim3((unsigned)grid), dim3(kBlock), 0,
-                               hs(stream), grad_out, packed, out, (uint32_t)n_vec, hv, div);
-        else
-            hipLaunchKernelGGL((packed_bwd_kernel<Op, false>), dim3((unsigned)grid), dim3(kBlock),
-                               0, hs(stream), grad_out, packed, out, (uint32_t)n_vec, hv, div);
+    const int64_t grid = grid_one_pass(n_vec);
+    // bytes: forward reads gate+up (4n) and writes 2n; backward reads
+    // grad_out+gate+up (6n) and writes 4n.
+    const int mode = BWD ? nt_mode(6 * n, 4 * n) : nt_mode(4 * n, 2 * n);
+#define PT_PACKED_LAUNCH(LNT, SNT)                                                              \
+    if constexpr (BWD)                                                                         \
+        hipLaunchKernelGGL((packed_bwd_kernel<Op, LNT, SNT>), dim3((unsigned)grid), dim3(kBlock), \
+                           0, hs(stream), grad_out, packed, out, (uint32_t)n_vec, hv, div);     \
+    else                                                                                       \
+        hipLaunchKernelGGL((packed_fwd_kernel<Op, LNT, SNT>), dim3((unsigned)grid), dim3(kBlock), \
+                           0, hs(stream), packed, out, (uint32_t)n_vec, hv, div);
+    if (mode == kNtBoth) {
+        PT_PACKED_LAUNCH(true, true)
+    } else if (mode == kNtStore) {
+        PT_PACKED_LAUNCH(false, true)
     } else {
-        if (nt)
-            hipLaunchKernelGGL((packed_fwd_kernel<Op, true>), dim3((unsigned)grid), dim3(kBlock), 0,
-                               hs(stream), packed, out, (uint32_t)n_vec, hv, div);
-        else
-            hipLaunchKernelGGL((packed_fwd_kernel<Op, false>), dim3((unsigned)grid), dim3(kBlock),
-                               0, hs(stream), packed, out, (uint32_t)n_vec, hv, div);
+        PT_PACKED_LAUNCH(false, false)
     }
+#undef PT_PACKED_LAUNCH
     return hipGetLastError();
 }
 

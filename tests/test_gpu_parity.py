@@ -209,3 +209,21 @@ def test_zero_size_and_bad_args(capi, cuda):
     rc = capi.launch_swish_fwd_d3_kernel(ctypes.c_void_p(0), ctypes.c_void_p(0), ctypes.c_int64(-1),
                                          capi.stream())
     assert rc != 0
+
+
+@pytest.mark.parametrize("reps", [1024, 2056])
+@pytest.mark.parametrize("fmt", ["f16", "bf16"])
+def test_large_streaming_paths(capi, oracle, cuda, reps, fmt):
+    """Outputs >= 64 MiB take the non-temporal store path, inputs > 256 MiB
+    also non-temporal loads.  Tiling all 65536 patterns makes the expected
+    output the tiled oracle table (a size-independent check)."""
+    x = torch.from_numpy(oracle.all_bits().view(np.int16)).to(cuda).repeat(reps)
+    x = x.view(DTYPES[fmt])
+    want = torch.from_numpy(oracle.activation("swish", oracle.FWD, 3, fmt,
+                                              oracle.all_bits()).view(np.int16)).to(cuda)
+    y = torch.empty_like(x)
+    capi.call(_name("swish", "fwd", 3, fmt), y, x, x.numel())
+    torch.cuda.synchronize()
+    got = y.view(torch.int16).view(reps, 65536)
+    nan_ok = torch.isnan(y.view(reps, 65536).float()) & torch.isnan(want.view(DTYPES[fmt]).float())[None]
+    assert bool(((got == want[None]) | nan_ok).all())
