@@ -188,26 +188,167 @@ def sweep(lib, reps: int):
                 out.append(row)
             del x, y
         torch.cuda.empty_cache()
-    # B3: 2^20 BF16 scores U[-16,16] seed 0 -> y, dy.
-    gs = torch.Generator().manual_seed(0)
-    s = (torch.rand(1 << 20, generator=gs) * 32 - 16).to(torch.bfloat16).to(dev)
-    y, dy = torch.empty_like(s), torch.empty_like(s)
-    fn = lib.launch_flash_sigmoid_direct_d3_d4_bf16
-    fn.restype = ctypes.c_int
-
-    def b3():
-        rc = fn(ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(dy.data_ptr()),
-                ctypes.c_void_p(s.data_ptr()), ctypes.c_int64(s.numel()),
-                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-        if rc != 0:
-            raise RuntimeError(f"B3 launch failed with {rc}")
-
-    ms = time_graph(b3, reps)
-    out.append({"function": "b3_direct_d3_d4", "dtype": "bf16", "elements": s.numel(),
-                "regime": "l2", "poly_us": round(ms * 1e3, 3),
-                "poly_gelem_s": round(s.numel() / ms / 1e6, 2),
-                "poly_gbs": round(6 * s.numel() / ms / 1e6, 1)})
+    out.extend(config_rows(lib, reps))
     return out
+
+
+def _vp(t):
+    import ctypes
+
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _launcher(lib, name, *args):
+    """Launch closure for a C-ABI entry point on torch's current stream."""
+    import ctypes
+
+    import torch
+
+    fn = getattr(lib, name)
+    fn.restype = ctypes.c_int
+    conv = []
+    for a in args:
+        if isinstance(a, torch.Tensor):
+            conv.append(_vp(a))
+        elif isinstance(a, float):
+            conv.append(ctypes.c_float(a))
+        else:
+            conv.append(ctypes.c_int64(a))
+
+    def launch():
+        rc = fn(*conv, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"{name} failed with {rc}")
+
+    return launch
+
+
+def _row(function, config, dtype, elements, alg_bytes, launches, reps):
+    """Time each (label, launch) and report us, Gelem/s, GB/s, HBM fraction."""
+    row = {"function": function, "config": config, "dtype": dtype, "elements": elements,
+           "bytes_per_launch": alg_bytes}
+    for label, launch in launches:
+        ms = time_graph(launch, reps)
+        row[f"{label}_us"] = round(ms * 1e3, 3)
+        row[f"{label}_gelem_s"] = round(elements / ms / 1e6, 2)
+        row[f"{label}_gbs"] = round(alg_bytes / ms / 1e6, 1)
+    if "poly_gbs" in row:
+        row["poly_frac_hbm_peak"] = round(row["poly_gbs"] / HBM_PEAK_GBS, 4)
+    if "native_us" in row and "poly_us" in row:
+        row["speedup"] = round(row["native_us"] / row["poly_us"], 3)
+    return row
+
+
+def config_rows(lib, reps: int):
+    """The BASELINE.json configurations, polynomial vs native where a native
+    baseline exists.  Synthetic inputs follow each config's recipe."""
+    import math
+
+    import numpy as np
+    import torch
+
+    dev = torch.device("cuda:0")
+    rows = []
+    big = max(5, reps // 5)
+
+    # C0 / B3: 2^20 BF16 scores U[-16, 16], seed 0 -> y, dy.
+    g = torch.Generator().manual_seed(0)
+    s = (torch.rand(1 << 20, generator=g) * 32 - 16).to(torch.bfloat16).to(dev)
+    y, dy = torch.empty_like(s), torch.empty_like(s)
+    rows.append(_row("b3_direct_d3_d4", "C0 B3 2^20 U[-16,16]", "bf16", s.numel(), 6 * s.numel(),
+                     [("poly", _launcher(lib, "launch_flash_sigmoid_direct_d3_d4_bf16", y, dy, s,
+                                         s.numel()))], reps))
+    del s, y, dy
+
+    # C1 / B1 L2-resident variant [256, 4096] FP16 N(0, 2^2).
+    x = (torch.randn(256, 4096, generator=g) * 2).half().to(dev)
+    yy = torch.empty_like(x)
+    rows.append(_row("swish_fwd_d3", "C1 B1 L2 [256,4096]", "fp16", x.numel(), 4 * x.numel(),
+                     [("poly", _launcher(lib, "launch_swish_fwd_d3_kernel", yy, x, x.numel())),
+                      ("native", _launcher(lib, "launch_swish_fwd_native_kernel", yy, x, x.numel()))],
+                     reps))
+    del x, yy
+
+    # C3 / B2: softcap cap=30 on BF16 [4, 32, 2048, 2048], N(0, 15^2), 1 % +-200.
+    gd = torch.Generator(device=dev).manual_seed(3)
+    sc = torch.randn(4, 32, 2048, 2048, device=dev, generator=gd) * 15
+    mask = torch.rand(sc.shape, device=dev, generator=gd) < 0.01
+    sign = torch.where(torch.rand(sc.shape, device=dev, generator=gd) < 0.5, -200.0, 200.0)
+    sc = torch.where(mask, sign, sc).to(torch.bfloat16)
+    del mask, sign
+    torch.cuda.empty_cache()
+    out = torch.empty_like(sc)
+    n = sc.numel()
+    rows.append(_row("softcap_tanh_d4", "C3 B2 [4,32,2048,2048] cap=30", "bf16", n, 4 * n,
+                     [("poly", _launcher(lib, "launch_softcap_tanh_d4_bf16", out, sc, n, 30.0)),
+                      ("native", _launcher(lib, "launch_softcap_tanh_native_bf16", out, sc, n, 30.0))],
+                     big))
+    del sc, out
+    torch.cuda.empty_cache()
+
+    # C4 / B4: routed SwiGLU, 64 experts x 128 tokens (Zipf(1.1) ragged counts),
+    # hidden 2048, N(0, 1).  The activation is elementwise over [sum(counts), H].
+    p = np.arange(1, 65, dtype=np.float64) ** -1.1
+    counts = np.random.default_rng(0).multinomial(64 * 128, p / p.sum())
+    rows_total, h = int(counts.sum()), 2048
+    gate = torch.randn(rows_total, h, device=dev, generator=gd).bfloat16()
+    up = torch.randn(rows_total, h, device=dev, generator=gd).bfloat16()
+    go = torch.randn(rows_total, h, device=dev, generator=gd).bfloat16()
+    o, gg, gu = torch.empty_like(gate), torch.empty_like(gate), torch.empty_like(gate)
+    n = gate.numel()
+    cfg = f"C4 B4 experts=64 rows={rows_total} (max expert {int(counts.max())}) H=2048"
+    rows.append(_row("swish_mul_fwd_d3", cfg, "bf16", n, 6 * n,
+                     [("poly", _launcher(lib, "launch_swish_mul_fwd_d3_kernel_bf16", o, gate, up, n)),
+                      ("native", _launcher(lib, "launch_swish_mul_fwd_native_kernel_bf16", o, gate, up, n))],
+                     reps))
+    rows.append(_row("swish_mul_bwd_d3", cfg, "bf16", n, 10 * n,
+                     [("poly", _launcher(lib, "launch_swish_mul_bwd_d3_kernel_bf16", gg, gu, go, gate, up, n)),
+                      ("native", _launcher(lib, "launch_swish_mul_bwd_native_kernel_bf16", gg, gu, go, gate, up, n))],
+                     reps))
+    packed = torch.cat((gate, up), -1)
+    gp = torch.empty_like(packed)
+    rows.append(_row("swish_mul_packed_fwd_d3", cfg + " packed [rows,4096]", "bf16", n, 6 * n,
+                     [("poly", _launcher(lib, "launch_swish_mul_packed_fwd_d3_kernel_bf16", o, packed, rows_total, h)),
+                      ("native", _launcher(lib, "launch_swish_mul_packed_fwd_native_kernel_bf16", o, packed, rows_total, h))],
+                     reps))
+    rows.append(_row("swish_mul_packed_bwd_d3", cfg + " packed [rows,4096]", "bf16", n, 10 * n,
+                     [("poly", _launcher(lib, "launch_swish_mul_packed_bwd_d3_kernel_bf16", gp, go, packed, rows_total, h)),
+                      ("native", _launcher(lib, "launch_swish_mul_packed_bwd_native_kernel_bf16", gp, go, packed, rows_total, h))],
+                     reps))
+    del gate, up, go, o, gg, gu, packed, gp
+    torch.cuda.empty_cache()
+
+    # C5 / B5: exp2 on FP32 logits [4, 32, 4096, 128] N(0, 4^2) minus row max -> BF16.
+    lg = torch.randn(4, 32, 4096, 128, device=dev, generator=gd) * 4
+    lg = lg - lg.amax(-1, keepdim=True)
+    e = torch.empty(lg.shape, dtype=torch.bfloat16, device=dev)
+    n = lg.numel()
+    rows.append(_row("exp2_d2", "C5 B5 [4,32,4096,128] FP32->BF16", "f32->bf16", n, 6 * n,
+                     [("poly", _launcher(lib, "launch_exp2_d2_f32_bf16", e, lg, n)),
+                      ("poly_d3", _launcher(lib, "launch_exp2_d3_f32_bf16", e, lg, n)),
+                      ("native", _launcher(lib, "launch_exp2_native_f32_bf16", e, lg, n))],
+                     big))
+    del lg, e
+    torch.cuda.empty_cache()
+
+    # C5 / RoPE: BF16 Q, K [4, 4096, 32, 128], theta 500000, positions 0..4095.
+    b, sl, hh, d = 4, 4096, 32, 128
+    q = torch.randn(b, sl, hh, d, device=dev, generator=gd).bfloat16()
+    k = torch.randn(b, sl, hh, d, device=dev, generator=gd).bfloat16()
+    qo = torch.empty(b, hh, sl, d, dtype=torch.bfloat16, device=dev)
+    ko = torch.empty_like(qo)
+    dims = torch.arange(0, d, 2, dtype=torch.float64)
+    freq = 500000.0 ** (-dims / d)
+    inc = torch.round(freq * (2.0 ** 32) / (2 * math.pi)).to(torch.int64).to(torch.int32).to(dev)
+    fr = freq.float().to(dev)
+    n = q.numel() + k.numel()
+    rows.append(_row("rope_apply_d5_d6", "C5 RoPE Q,K [4,4096,32,128] theta=5e5", "bf16", n, 4 * n,
+                     [("poly", _launcher(lib, "launch_rope_apply_fixed_half_turn_d5_d6_bf16", qo, ko, q, k, inc, b, sl, hh, hh, d)),
+                      ("native", _launcher(lib, "launch_rope_apply_native_bf16", qo, ko, q, k, fr, b, sl, hh, hh, d))],
+                     big))
+    del q, k, qo, ko
+    torch.cuda.empty_cache()
+    return rows
 
 
 def main():

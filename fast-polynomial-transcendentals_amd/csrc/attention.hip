@@ -1,5 +1,10 @@
-// attention.hip -- score-side programs of the attention path: the deployed B3
-// sigmoid-attention program (direct D3 probability + factored D4 derivative).
+// attention.hip -- score-side programs of the attention path:
+//  * B3: the deployed sigmoid-attention program (direct D3 probability +
+//    factored D4 derivative);
+//  * B2: tanh softcap cap*tanh(s/cap) with the D4 BF16 tanh program, and its
+//    derivative from the differentiated D4 coefficients;
+//  * B5: fractional exp2 with FP32 range reduction (D2 "safe" fraction, FA4's
+//    D3 fraction, and the v_exp_f32 baseline), FP32 in, BF16 or FP32 out.
 #include <hip/hip_runtime.h>
 
 #include "ops.hpp"
@@ -96,6 +101,168 @@ b3_f32_kernel(const float* __restrict__ s, uint16_t* __restrict__ y, uint16_t* _
     }
 }
 
+// ---------------------------------------------------------------------------
+// B2: tanh softcap.  u = bf16(s * (1/cap)) (FP32 product, one RNE rounding),
+// T = TANH_FWD_D4_ODD_BF16(u) (spline_structs_odd_bf16.cuh:153-179),
+// y = bf16(T * cap).  The derivative d y / d s = T'(u) (the scale cancels,
+// extras/paper/manuscript/main.tex:443-449) evaluates the derivative of the
+// D4 odd polynomial, D(t) = c1 + 2 c2 t + 3 c3 t^2 + 4 c4 t^3 with BF16
+// coefficients k*c_k and BF16 Horner steps, at t = |u|; D = 0 once t reaches
+// 2.609375, the first BF16 magnitude at which the forward program saturates
+// at 1 (and above the 2.75 clamp).
+// ---------------------------------------------------------------------------
+
+struct SoftcapConsts {
+    using T = BF16Prog<kTanh, kFwd, 4>;
+    static constexpr float d0 = bf16_value(T::P.c[1]);
+    static constexpr float d1 = bf16_value(2.0f * bf16_value(T::P.c[2]));
+    static constexpr float d2 = bf16_value(3.0f * bf16_value(T::P.c[3]));
+    static constexpr float d3 = bf16_value(4.0f * bf16_value(T::P.c[4]));
+    static constexpr float t_sat = 2.609375f;
+};
+
+struct SoftcapFwdOp {
+    static constexpr int NIN = 1, NOUT = 1;
+    static constexpr bool kParams = true;  // prm[0] = cap, prm[1] = 1/cap (FP32)
+    __device__ __forceinline__ static void pair(const uint32_t (&a)[1], uint32_t (&b)[1],
+                                                const float (&prm)[2]) {
+        const uint32_t u = pack_bf(bf_lo(a[0]) * prm[1], bf_hi(a[0]) * prm[1]);
+        float t0, t1;
+        SoftcapConsts::T::eval2(u, t0, t1);
+        b[0] = pack_bf(t0 * prm[0], t1 * prm[0]);
+    }
+};
+
+// Native baseline: cap * tanh(s / cap) in FP32 with hardware exp/rcp,
+// tanh(u) = 1 - 2 / (exp(2u) + 1), one RNE rounding to BF16.
+struct SoftcapNativeOp {
+    static constexpr int NIN = 1, NOUT = 1;
+    static constexpr bool kParams = true;
+    __device__ __forceinline__ static void pair(const uint32_t (&a)[1], uint32_t (&b)[1],
+                                                const float (&prm)[2]) {
+        const float y0 = prm[0] * native_lane<kTanh, kFwd>(bf_lo(a[0]) * prm[1]);
+        const float y1 = prm[0] * native_lane<kTanh, kFwd>(bf_hi(a[0]) * prm[1]);
+        b[0] = pack_bf(y0, y1);
+    }
+};
+
+struct SoftcapBwdOp {
+    static constexpr int NIN = 2, NOUT = 1;  // (grad_out, scores) -> grad_scores
+    static constexpr bool kParams = true;
+    __device__ __forceinline__ static float deriv(float t) {
+        using C = SoftcapConsts;
+        float r = bfma(t, C::d3, C::d2);
+        r = bfma(t, r, C::d1);
+        r = bfma(t, r, C::d0);
+        return t < C::t_sat ? r : 0.0f;
+    }
+    __device__ __forceinline__ static void pair(const uint32_t (&a)[2], uint32_t (&b)[1],
+                                                const float (&prm)[2]) {
+        const uint32_t u = pack_bf(bf_lo(a[1]) * prm[1], bf_hi(a[1]) * prm[1]);
+        const uint32_t t2 = u & 0x7fff7fffu;  // |u|; NaN magnitudes fail t < t_sat
+        b[0] = pack_bf(bf_lo(a[0]) * deriv(bf_lo(t2)), bf_hi(a[0]) * deriv(bf_hi(t2)));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// B5: exp2 with FP32 range reduction (autonumerics_zero/cuda_benchmarks/
+// utils_exp2_cuda.cuh:13-74): x = max(x, -127); n = floor(x); f = x - n;
+// p = polynomial 2^f on [0, 1); result bits = (n << 23) + bits(p).
+// D2 "safe" fraction p = 1 + a f + (1 - a) f^2, a = 0.6602339719
+// (extras/paper/manuscript/appendix_exp2.tex:29-32; sampled-minimax fit),
+// keeps p(0) = 1 and p(1) = 2.  D3 is FA4's e2e_asm2 fraction.
+// Defined for x < 128 (softmax exponents are <= 0); -inf and NaN give +0.
+// ---------------------------------------------------------------------------
+
+enum Exp2Kind : int { kExp2D2 = 0, kExp2D3 = 1, kExp2Native = 2 };
+
+template <int KIND>
+__device__ __forceinline__ float exp2_lane(float x) {
+    if constexpr (KIND == kExp2Native) {
+        return __builtin_amdgcn_exp2f(x);
+    } else {
+        x = __builtin_fmaxf(x, -127.0f);
+        const float fl = __builtin_floorf(x);
+        const float f = x - fl;
+        float p;
+        if constexpr (KIND == kExp2D2) {
+            p = __builtin_fmaf(f, 0.33976602809999057f, 0.6602339719000094f);
+            p = __builtin_fmaf(p, f, 1.0f);
+        } else {
+            p = __builtin_fmaf(f, 0.077119089663028717041015625f, 0.227564394474029541015625f);
+            p = __builtin_fmaf(p, f, 0.695146143436431884765625f);
+            p = __builtin_fmaf(p, f, 1.0f);
+        }
+        const int n = (int)fl;  // v_cvt_i32_f32 (saturating)
+        return as_f32(((uint32_t)n << 23) + as_u32(p));
+    }
+}
+
+// FP32 -> BF16: 8 values (two 16-byte loads) per thread-iteration.
+template <int KIND, bool LNT, bool SNT>
+__global__ void __launch_bounds__(kBlock)
+exp2_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, int64_t n, int vec_ok) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    const int64_t n8 = vec_ok ? (n >> 3) : 0;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n8; i += stride) {
+        const Vec4 a = ld16<LNT>(x, 2 * i);
+        const Vec4 c = ld16<LNT>(x, 2 * i + 1);
+        const uint32_t w[8] = {a.w[0], a.w[1], a.w[2], a.w[3], c.w[0], c.w[1], c.w[2], c.w[3]};
+        Vec4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            o.w[k] = pack_bf(exp2_lane<KIND>(as_f32(w[2 * k])), exp2_lane<KIND>(as_f32(w[2 * k + 1])));
+        st16<SNT>(y, i, o);
+    }
+    for (int64_t e = (n8 << 3) + (int64_t)blockIdx.x * kBlock + threadIdx.x; e < n; e += stride) {
+        const float r = exp2_lane<KIND>(x[e]);
+        y[e] = (uint16_t)(pack_bf(r, r) & 0xffffu);
+    }
+}
+
+// FP32 -> FP32: 4 values per thread-iteration.
+template <int KIND, bool LNT, bool SNT>
+__global__ void __launch_bounds__(kBlock)
+exp2_f32_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n, int vec_ok) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    const int64_t n4 = vec_ok ? (n >> 2) : 0;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+        const Vec4 a = ld16<LNT>(x, i);
+        Vec4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o.w[k] = as_u32(exp2_lane<KIND>(as_f32(a.w[k])));
+        st16<SNT>(y, i, o);
+    }
+    for (int64_t e = (n4 << 2) + (int64_t)blockIdx.x * kBlock + threadIdx.x; e < n; e += stride)
+        y[e] = exp2_lane<KIND>(x[e]);
+}
+
+template <int KIND, bool BF_OUT>
+int launch_exp2(void* y, const void* x, int64_t n, void* stream) {
+    if (bad_args(n, {y, x})) return hipErrorInvalidValue;
+    if (n == 0) return hipSuccess;
+    const int vec_ok = aligned16(y) && aligned16(x);
+    const int per = BF_OUT ? 8 : 4;
+    const int64_t grid = grid_one_pass(vec_ok ? n / per : n);
+    const int mode = nt_mode(4 * n, (BF_OUT ? 2 : 4) * n);
+#define PT_EXP2_LAUNCH(LNT, SNT)                                                                  \
+    if constexpr (BF_OUT)                                                                         \
+        hipLaunchKernelGGL((exp2_bf16_kernel<KIND, LNT, SNT>), dim3((unsigned)grid), dim3(kBlock), \
+                           0, hs(stream), (const float*)x, (uint16_t*)y, n, vec_ok);              \
+    else                                                                                          \
+        hipLaunchKernelGGL((exp2_f32_kernel<KIND, LNT, SNT>), dim3((unsigned)grid), dim3(kBlock),  \
+                           0, hs(stream), (const float*)x, (float*)y, n, vec_ok);
+    if (mode == kNtBoth) {
+        PT_EXP2_LAUNCH(true, true)
+    } else if (mode == kNtStore) {
+        PT_EXP2_LAUNCH(false, true)
+    } else {
+        PT_EXP2_LAUNCH(false, false)
+    }
+#undef PT_EXP2_LAUNCH
+    return hipGetLastError();
+}
+
 }  // namespace pt
 
 using namespace pt;
@@ -138,3 +305,49 @@ extern "C" int launch_flash_sigmoid_direct_d3_d4_f32_bf16(void* y, void* dy, con
     return hipGetLastError();
 }
 
+
+// ---- B2 softcap ---------------------------------------------------------------
+
+extern "C" int launch_softcap_tanh_d4_bf16(void* out, const void* scores, int64_t size, float cap,
+                                           void* stream) {
+    if (bad_args(size, {out, scores}) || !(cap > 0.0f)) return hipErrorInvalidValue;
+    Streams<1, 1> s{{scores}, {out}, {cap, 1.0f / cap}};
+    return launch_pairwise<SoftcapFwdOp>(s, size, hs(stream));
+}
+
+extern "C" int launch_softcap_tanh_native_bf16(void* out, const void* scores, int64_t size,
+                                               float cap, void* stream) {
+    if (bad_args(size, {out, scores}) || !(cap > 0.0f)) return hipErrorInvalidValue;
+    Streams<1, 1> s{{scores}, {out}, {cap, 1.0f / cap}};
+    return launch_pairwise<SoftcapNativeOp>(s, size, hs(stream));
+}
+
+extern "C" int launch_softcap_tanh_d4_bwd_bf16(void* grad_scores, const void* grad_out,
+                                               const void* scores, int64_t size, float cap,
+                                               void* stream) {
+    if (bad_args(size, {grad_scores, grad_out, scores}) || !(cap > 0.0f))
+        return hipErrorInvalidValue;
+    Streams<2, 1> s{{grad_out, scores}, {grad_scores}, {cap, 1.0f / cap}};
+    return launch_pairwise<SoftcapBwdOp>(s, size, hs(stream));
+}
+
+// ---- B5 exp2 ------------------------------------------------------------------
+
+extern "C" int launch_exp2_d2_f32_bf16(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2D2, true>(y, x, size, stream);
+}
+extern "C" int launch_exp2_d3_f32_bf16(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2D3, true>(y, x, size, stream);
+}
+extern "C" int launch_exp2_native_f32_bf16(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2Native, true>(y, x, size, stream);
+}
+extern "C" int launch_exp2_d2_f32(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2D2, false>(y, x, size, stream);
+}
+extern "C" int launch_exp2_d3_f32(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2D3, false>(y, x, size, stream);
+}
+extern "C" int launch_exp2_native_f32(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2Native, false>(y, x, size, stream);
+}

@@ -377,6 +377,146 @@ at::Tensor flash_sigmoid_direct_d3(at::Tensor scores) {
 }
 
 // ---------------------------------------------------------------------------
+// B2 softcap and B5 exp2
+// ---------------------------------------------------------------------------
+
+using SoftcapLauncher = int (*)(void*, const void*, int64_t, float, void*);
+
+at::Tensor softcap_fwd(at::Tensor scores, double cap, SoftcapLauncher fn) {
+    CHECK_CUDA(scores);
+    CHECK_CONTIGUOUS(scores);
+    TORCH_CHECK(scores.scalar_type() == at::kBFloat16, "scores must be bfloat16");
+    TORCH_CHECK(cap > 0.0, "cap must be positive");
+    c10::OptionalDeviceGuard guard(scores.device());
+    at::Tensor out = at::empty_like(scores);
+    void* s = current_stream(scores);
+    check_launch(fn(out.data_ptr(), scores.data_ptr(), scores.numel(), static_cast<float>(cap), s), s);
+    return out;
+}
+
+at::Tensor softcap_tanh_fwd_bf16(at::Tensor scores, double cap) {
+    return softcap_fwd(scores, cap, launch_softcap_tanh_d4_bf16);
+}
+
+at::Tensor softcap_tanh_native_bf16(at::Tensor scores, double cap) {
+    return softcap_fwd(scores, cap, launch_softcap_tanh_native_bf16);
+}
+
+at::Tensor softcap_tanh_bwd_bf16(at::Tensor grad_out, at::Tensor scores, double cap) {
+    CHECK_CUDA(grad_out);
+    CHECK_CUDA(scores);
+    CHECK_CONTIGUOUS(grad_out);
+    CHECK_CONTIGUOUS(scores);
+    TORCH_CHECK(scores.scalar_type() == at::kBFloat16, "scores must be bfloat16");
+    TORCH_CHECK(grad_out.scalar_type() == at::kBFloat16, "grad_out must be bfloat16");
+    TORCH_CHECK(grad_out.numel() == scores.numel(),
+                "grad_out and scores must have the same number of elements");
+    TORCH_CHECK(cap > 0.0, "cap must be positive");
+    c10::OptionalDeviceGuard guard(scores.device());
+    at::Tensor g = at::empty_like(scores);
+    void* s = current_stream(scores);
+    check_launch(launch_softcap_tanh_d4_bwd_bf16(g.data_ptr(), grad_out.data_ptr(),
+                                                 scores.data_ptr(), scores.numel(),
+                                                 static_cast<float>(cap), s),
+                 s);
+    return g;
+}
+
+using Exp2Launcher = int (*)(void*, const void*, int64_t, void*);
+
+at::Tensor exp2_f32_to(at::Tensor x, Exp2Launcher fn, at::ScalarType out_type) {
+    CHECK_CUDA(x);
+    CHECK_CONTIGUOUS(x);
+    TORCH_CHECK(x.scalar_type() == at::kFloat, "x must be float32");
+    c10::OptionalDeviceGuard guard(x.device());
+    at::Tensor y = at::empty(x.sizes(), x.options().dtype(out_type));
+    void* s = current_stream(x);
+    check_launch(fn(y.data_ptr(), x.data_ptr(), x.numel(), s), s);
+    return y;
+}
+
+// ---------------------------------------------------------------------------
+// sin/cos tables and RoPE (spline_ops.cpp:326-918)
+// ---------------------------------------------------------------------------
+
+using SincosLauncher = int (*)(void*, const void*, int64_t, void*);
+
+at::Tensor sincos_table(at::Tensor angles, SincosLauncher fn, at::ScalarType out_type) {
+    CHECK_CUDA(angles);
+    CHECK_CONTIGUOUS(angles);
+    TORCH_CHECK(angles.scalar_type() == at::kFloat, "angles must be float32");
+    std::vector<int64_t> sizes = angles.sizes().vec();
+    sizes.insert(sizes.begin(), 2);
+    c10::OptionalDeviceGuard guard(angles.device());
+    at::Tensor out = at::empty(sizes, angles.options().dtype(out_type));
+    void* s = current_stream(angles);
+    check_launch(fn(out.data_ptr(), angles.data_ptr(), angles.numel(), s), s);
+    return out;
+}
+
+at::Tensor rope_sincos_fixed_half_turn_d5_d6_fp16(at::Tensor phase_increments,
+                                                  int64_t sequence_length) {
+    CHECK_CUDA(phase_increments);
+    CHECK_CONTIGUOUS(phase_increments);
+    TORCH_CHECK(phase_increments.dim() == 1, "phase_increments must be one-dimensional");
+    TORCH_CHECK(phase_increments.scalar_type() == at::kInt, "phase_increments has the wrong dtype");
+    TORCH_CHECK(sequence_length >= 0, "sequence_length must be non-negative");
+    TORCH_CHECK((phase_increments.numel() % 4) == 0,
+                "phase_increments must contain a multiple of four elements");
+    c10::OptionalDeviceGuard guard(phase_increments.device());
+    at::Tensor out = at::empty({2, sequence_length, phase_increments.numel()},
+                               phase_increments.options().dtype(at::kHalf));
+    void* s = current_stream(phase_increments);
+    check_launch(launch_rope_sincos_fixed_half_turn_d5_d6_fp16(
+                     out.data_ptr(), phase_increments.data_ptr(), sequence_length,
+                     phase_increments.numel(), s),
+                 s);
+    return out;
+}
+
+using RopeLauncher = int (*)(void*, void*, const void*, const void*, const void*, int64_t,
+                             int64_t, int64_t, int64_t, int64_t, void*);
+
+// check_rope_apply_fp16_inputs + rope_apply_parameter_fp16 (spline_ops.cpp:831-918)
+std::vector<at::Tensor> rope_apply(at::Tensor q, at::Tensor k, at::Tensor parameters,
+                                   at::ScalarType dtype, at::ScalarType parameter_type,
+                                   const char* parameter_name, RopeLauncher fn) {
+    const char* dname = dtype == at::kHalf ? "float16" : "bfloat16";
+    CHECK_CUDA(q);
+    CHECK_CUDA(k);
+    CHECK_CONTIGUOUS(q);
+    CHECK_CONTIGUOUS(k);
+    TORCH_CHECK(q.scalar_type() == dtype, "q must be ", dname);
+    TORCH_CHECK(k.scalar_type() == dtype, "k must be ", dname);
+    TORCH_CHECK(q.dim() == 4, "q must have shape [batch, sequence, heads, head_dim]");
+    TORCH_CHECK(k.dim() == 4, "k must have shape [batch, sequence, heads, head_dim]");
+    TORCH_CHECK(q.get_device() == k.get_device(), "q and k must be on the same CUDA device");
+    TORCH_CHECK(q.size(0) == k.size(0), "q and k batch sizes must match");
+    TORCH_CHECK(q.size(1) == k.size(1), "q and k sequence lengths must match");
+    TORCH_CHECK(q.size(3) == k.size(3), "q and k head dimensions must match");
+    TORCH_CHECK(q.size(2) > 0 && k.size(2) > 0, "q and k must contain at least one head");
+    TORCH_CHECK(q.size(3) > 0 && (q.size(3) % 8) == 0,
+                "head_dim must be a positive multiple of eight");
+    CHECK_CUDA(parameters);
+    CHECK_CONTIGUOUS(parameters);
+    TORCH_CHECK(parameters.dim() == 1, parameter_name, " must be one-dimensional");
+    TORCH_CHECK(parameters.scalar_type() == parameter_type, parameter_name, " has the wrong dtype");
+    TORCH_CHECK(parameters.get_device() == q.get_device(), parameter_name,
+                " must be on the same CUDA device as q and k");
+    TORCH_CHECK(parameters.numel() == q.size(3) / 2, parameter_name,
+                " must contain head_dim / 2 elements");
+    c10::OptionalDeviceGuard guard(q.device());
+    const int64_t b = q.size(0), sl = q.size(1), hq = q.size(2), hk = k.size(2), d = q.size(3);
+    at::Tensor q_out = at::empty({b, hq, sl, d}, q.options());
+    at::Tensor k_out = at::empty({b, hk, sl, d}, k.options());
+    void* s = current_stream(q);
+    check_launch(fn(q_out.data_ptr(), k_out.data_ptr(), q.data_ptr(), k.data_ptr(),
+                    parameters.data_ptr(), b, sl, hq, hk, d, s),
+                 s);
+    return {q_out, k_out};
+}
+
+// ---------------------------------------------------------------------------
 // C++ autograd functions (spline_ops.cpp:1933-2206)
 // ---------------------------------------------------------------------------
 
@@ -594,6 +734,71 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("sigmoid_ag", &sigmoid_fwd_autograd, "Sigmoid with C++ autograd");
     m.def("tanh_ag", &tanh_fwd_autograd, "Tanh with C++ autograd");
     m.def("swish_ag", &swish_fwd_autograd, "Swish with C++ autograd");
+
+    m.def("softcap_tanh_fwd_bf16", &softcap_tanh_fwd_bf16, py::arg("scores"), py::arg("cap") = 30.0,
+          "B2 tanh softcap cap*tanh(s/cap) with the D4 BF16 tanh program");
+    m.def("softcap_tanh_native_bf16", &softcap_tanh_native_bf16, py::arg("scores"),
+          py::arg("cap") = 30.0, "Native softcap baseline cap*tanh(s/cap) in FP32");
+    m.def("softcap_tanh_bwd_bf16", &softcap_tanh_bwd_bf16, py::arg("grad_out"), py::arg("scores"),
+          py::arg("cap") = 30.0, "B2 softcap gradient from the differentiated D4 program");
+    m.def("exp2_d2_f32_to_bf16", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_f32_bf16, at::kBFloat16); },
+          "B5 exp2: FP32 range reduction + D2 safe fraction, BF16 out");
+    m.def("exp2_d3_f32_to_bf16", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d3_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction + FA4 D3 fraction, BF16 out");
+    m.def("exp2_native_f32_to_bf16", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_native_f32_bf16, at::kBFloat16); },
+          "exp2 with v_exp_f32, BF16 out");
+    m.def("exp2_d2_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_f32, at::kFloat); },
+          "B5 exp2 D2 safe fraction, FP32 out");
+    m.def("exp2_d3_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d3_f32, at::kFloat); },
+          "exp2 FA4 D3 fraction, FP32 out");
+    m.def("exp2_native_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_native_f32, at::kFloat); },
+          "exp2 with v_exp_f32, FP32 out");
+
+#define PT_DEF_SINCOS(name, T, doc) \
+    m.def(#name, [](at::Tensor a) { return sincos_table(a, launch_##name, T); }, doc)
+    PT_DEF_SINCOS(sincos_native_bf16, at::kBFloat16, "Paired native sin/cos with BF16 output");
+    PT_DEF_SINCOS(sincos_d3_d4_half_turn_bf16, at::kBFloat16,
+                  "Paired half-turn polynomial sin D3/cos D4 with packed BF16 evaluation and output");
+    PT_DEF_SINCOS(sincos_d5_d6_half_turn_bf16, at::kBFloat16,
+                  "Paired half-turn polynomial sin D5/cos D6 with packed BF16 evaluation and output");
+    PT_DEF_SINCOS(sincos_d5_d4_half_turn_fp16_bf16, at::kBFloat16,
+                  "Paired half-turn polynomial sin D5/cos D4 with packed FP16 evaluation and BF16 output");
+    PT_DEF_SINCOS(sincos_native_fp16, at::kHalf, "Paired native sin/cos with FP16 output");
+    PT_DEF_SINCOS(sincos_d3_d4_half_turn_fp16, at::kHalf,
+                  "Paired half-turn polynomial sin D3/cos D4 with packed FP16 evaluation and output");
+    PT_DEF_SINCOS(sincos_d5_d4_half_turn_fp16, at::kHalf,
+                  "Paired half-turn polynomial sin D5/cos D4 with packed FP16 evaluation and output");
+    PT_DEF_SINCOS(sincos_d5_d6_half_turn_fp16, at::kHalf,
+                  "Paired half-turn polynomial sin D5/cos D6 with packed FP16 evaluation and output");
+    PT_DEF_SINCOS(sincos_d7_d6_half_turn_fp16, at::kHalf,
+                  "Paired half-turn polynomial sin D7/cos D6 with packed FP16 evaluation and output");
+#undef PT_DEF_SINCOS
+    m.def("rope_sincos_fixed_half_turn_d5_d6_fp16", &rope_sincos_fixed_half_turn_d5_d6_fp16,
+          "RoPE-specific fixed-point half-turn reduction with FP16 sin D5/cos D6");
+    m.def("rope_apply_fixed_half_turn_d5_d6_fp16",
+          [](at::Tensor q, at::Tensor k, at::Tensor inc) {
+              return rope_apply(q, k, inc, at::kHalf, at::kInt, "phase_increments",
+                                launch_rope_apply_fixed_half_turn_d5_d6_fp16);
+          },
+          "Fused polynomial FP16 Q/K rotary embedding and transpose");
+    m.def("rope_apply_native_fp16",
+          [](at::Tensor q, at::Tensor k, at::Tensor freq) {
+              return rope_apply(q, k, freq, at::kHalf, at::kFloat, "frequencies",
+                                launch_rope_apply_native_fp16);
+          },
+          "Fused native-SFU FP16 Q/K rotary embedding and transpose");
+    m.def("rope_apply_fixed_half_turn_d5_d6_bf16",
+          [](at::Tensor q, at::Tensor k, at::Tensor inc) {
+              return rope_apply(q, k, inc, at::kBFloat16, at::kInt, "phase_increments",
+                                launch_rope_apply_fixed_half_turn_d5_d6_bf16);
+          },
+          "Fused polynomial BF16 Q/K rotary embedding and transpose");
+    m.def("rope_apply_native_bf16",
+          [](at::Tensor q, at::Tensor k, at::Tensor freq) {
+              return rope_apply(q, k, freq, at::kBFloat16, at::kFloat, "frequencies",
+                                launch_rope_apply_native_bf16);
+          },
+          "Fused native BF16 Q/K rotary embedding and transpose");
 
     m.def("flash_sigmoid_direct_d3_d4_bf16", &flash_sigmoid_direct_d3_d4,
           "B3 deployed direct-D3 probability and factored-D4 derivative (BF16 out)");

@@ -57,7 +57,27 @@ template <int NIN, int NOUT>
 struct Streams {
     const void* in[NIN];
     void* out[NOUT];
+    float prm[2];  // launch-constant scalars for ops that declare kParams
 };
+
+template <class Op, class = void>
+struct UsesParams {
+    static constexpr bool value = false;
+};
+template <class Op>
+struct UsesParams<Op, decltype((void)Op::kParams)> {
+    static constexpr bool value = true;
+};
+
+template <class Op>
+__device__ __forceinline__ void call_pair(const uint32_t (&a)[Op::NIN], uint32_t (&b)[Op::NOUT],
+                                          const float (&prm)[2]) {
+    if constexpr (UsesParams<Op>::value) {
+        Op::pair(a, b, prm);
+    } else {
+        Op::pair(a, b);
+    }
+}
 
 // Op contract:
 //   static constexpr int NIN, NOUT;
@@ -65,13 +85,14 @@ struct Streams {
 // `pair` maps one 32-bit pair of every input stream to one pair of every
 // output stream.
 template <class Op>
-__device__ __forceinline__ void apply_vec(const Vec4 (&v)[Op::NIN], Vec4 (&o)[Op::NOUT]) {
+__device__ __forceinline__ void apply_vec(const Vec4 (&v)[Op::NIN], Vec4 (&o)[Op::NOUT],
+                                          const float (&prm)[2]) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         uint32_t a[Op::NIN], b[Op::NOUT];
 #pragma unroll
         for (int k = 0; k < Op::NIN; ++k) a[k] = v[k].w[w];
-        Op::pair(a, b);
+        call_pair<Op>(a, b, prm);
 #pragma unroll
         for (int k = 0; k < Op::NOUT; ++k) o[k].w[w] = b[k];
     }
@@ -92,7 +113,7 @@ pairwise_kernel(Streams<Op::NIN, Op::NOUT> s, int64_t n) {
         Vec4 v[NIN], o[NOUT];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) v[k] = ld16<LNT>(s.in[k], i);
-        apply_vec<Op>(v, o);
+        apply_vec<Op>(v, o, s.prm);
 #pragma unroll
         for (int k = 0; k < NOUT; ++k) st16<SNT>(s.out[k], i, o[k]);
     }
@@ -104,7 +125,7 @@ pairwise_kernel(Streams<Op::NIN, Op::NOUT> s, int64_t n) {
             const uint32_t x = reinterpret_cast<const uint16_t*>(s.in[k])[e];
             a[k] = x | (x << 16);
         }
-        Op::pair(a, b);
+        call_pair<Op>(a, b, s.prm);
 #pragma unroll
         for (int k = 0; k < NOUT; ++k)
             reinterpret_cast<uint16_t*>(s.out[k])[e] = (uint16_t)(b[k] & 0xffffu);
@@ -125,7 +146,7 @@ pairwise_element_kernel(Streams<Op::NIN, Op::NOUT> s, int64_t n) {
             const uint32_t x = reinterpret_cast<const uint16_t*>(s.in[k])[e];
             a[k] = x | (x << 16);
         }
-        Op::pair(a, b);
+        call_pair<Op>(a, b, s.prm);
 #pragma unroll
         for (int k = 0; k < NOUT; ++k)
             reinterpret_cast<uint16_t*>(s.out[k])[e] = (uint16_t)(b[k] & 0xffffu);

@@ -161,6 +161,74 @@ int launch_flash_sigmoid_direct_d3_d4_f32_bf16(void* y, void* dy, const void* sc
 int launch_flash_sigmoid_direct_d3_bf16(void* y, const void* scores, int64_t size,
                                         void* stream);
 
+/* ---- B2: tanh softcap cap * tanh(s / cap) on BF16 scores -----------------
+ * No C launcher exists in the reference: FA4 selects the D4 BF16 tanh
+ * program for softcap (src/sfu_repro/fa4.py:650-668) and the composition
+ * lives in the absent FA4 kernel.  Forward: u = bf16(s * (1/cap)),
+ * out = bf16(cap * TANH_FWD_D4_ODD_BF16(u)).  Backward: grad_scores =
+ * bf16(grad_out * T'(u)) with the differentiated D4 polynomial (the scale
+ * cancels, extras/paper/manuscript/main.tex:443-449, 754-758). */
+int launch_softcap_tanh_d4_bf16(void* out, const void* scores, int64_t size, float cap,
+                                void* stream);
+int launch_softcap_tanh_d4_bwd_bf16(void* grad_scores, const void* grad_out, const void* scores,
+                                    int64_t size, float cap, void* stream);
+/* Native baseline: cap * tanh(s / cap) in FP32 with v_exp_f32 / v_rcp_f32. */
+int launch_softcap_tanh_native_bf16(void* out, const void* scores, int64_t size, float cap,
+                                    void* stream);
+
+/* ---- B5: exp2 with FP32 range reduction ---------------------------------
+ * FA4's e2e_asm2 reduction (autonumerics_zero/cuda_benchmarks/
+ * utils_exp2_cuda.cuh:13-74) with the D2 "safe" fraction
+ * (extras/paper/manuscript/appendix_exp2.tex:29-32) or FA4's D3 fraction;
+ * `native` is v_exp_f32 (the reference's exp2f baseline,
+ * benchmark_exp2_pwl2.cu:101-105).  FP32 input, BF16 or FP32 output. */
+int launch_exp2_d2_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d3_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_native_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d2_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d3_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_native_f32(void* y, const void* x, int64_t size, void* stream);
+
+/* ---- paired sin/cos tables: FP32 angles [size] -> out [2, size] ----------
+ * Plane 0 holds cos, plane 1 sin.  Replaces launch_sincos_*_{bf16,fp16}
+ * (sincos_kernels.cu:2123-2978; binding spline_ops.cpp:326-560): half-turn
+ * reduction with the 1.5*2^23 shifter and a one-term FP32 pi, then the
+ * packed polynomial of each name. */
+#define SPLINE_HIP_SINCOS_LAUNCHERS(X)                                          \
+    X(launch_sincos_native_bf16) X(launch_sincos_d3_d4_half_turn_bf16)          \
+    X(launch_sincos_d5_d6_half_turn_bf16) X(launch_sincos_d5_d4_half_turn_fp16_bf16) \
+    X(launch_sincos_native_fp16) X(launch_sincos_d3_d4_half_turn_fp16)          \
+    X(launch_sincos_d5_d4_half_turn_fp16) X(launch_sincos_d5_d6_half_turn_fp16) \
+    X(launch_sincos_d7_d6_half_turn_fp16)
+#define SPLINE_HIP_DECLARE_SINCOS(name) \
+    int name(void* out, const void* angles, int64_t size, void* stream);
+SPLINE_HIP_SINCOS_LAUNCHERS(SPLINE_HIP_DECLARE_SINCOS)
+
+/* ---- RoPE ------------------------------------------------------------------
+ * Phase increments are int32 Q0.32 turns per position, round(omega_i *
+ * 2^32 / (2 pi)) (src/sfu_repro/rope/benchmark_cuda_fused_rope.py:238-241),
+ * one per frequency (head_dim / 2 of them).
+ * launch_rope_sincos_fixed_half_turn_d5_d6_fp16: table [2, S, F] FP16
+ * (replaces the launcher of sincos_kernels.cu:2871-2905).
+ * launch_rope_apply_*: Q [B, S, Hq, D], K [B, S, Hk, D] (even/odd pairs
+ * interleaved) -> rotated Q [B, Hq, S, D], K [B, Hk, S, D]; replaces
+ * launch_rope_apply_{fixed_half_turn_d5_d6,native}_fp16
+ * (sincos_kernels.cu:2769-2870); the _bf16 entry points are new (the
+ * reference's fused RoPE is FP16 only, spline_ops.cpp:838-839).  `native`
+ * takes FP32 frequencies omega_i instead of increments.  head_dim must be a
+ * multiple of 8 and every pointer 16-byte aligned. */
+int launch_rope_sincos_fixed_half_turn_d5_d6_fp16(void* out, const void* phase_increments,
+                                                  int64_t sequence_length, int64_t frequency_count,
+                                                  void* stream);
+#define SPLINE_HIP_ROPE_APPLY_LAUNCHERS(X)                                      \
+    X(launch_rope_apply_fixed_half_turn_d5_d6_fp16) X(launch_rope_apply_fixed_half_turn_d5_d6_bf16) \
+    X(launch_rope_apply_native_fp16) X(launch_rope_apply_native_bf16)
+#define SPLINE_HIP_DECLARE_ROPE_APPLY(name)                                     \
+    int name(void* q_out, void* k_out, const void* q, const void* k,            \
+             const void* angle_params, int64_t batch, int64_t sequence_length,  \
+             int64_t q_heads, int64_t k_heads, int64_t head_dim, void* stream);
+SPLINE_HIP_ROPE_APPLY_LAUNCHERS(SPLINE_HIP_DECLARE_ROPE_APPLY)
+
 /* ---- device/launch introspection --------------------------------------- */
 /* Number of compute units of the current device and the grid the
  * elementwise launchers use for `size` 16-bit elements and `streams` tensors

@@ -76,10 +76,19 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_b3_direct_f32.argtypes = [f32p, u16p, u16p, i64]
     l.orc_b3_constants.argtypes = [u16p, u16p, u16p]
     l.orc_num_threads.argtypes = []
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    l.orc_softcap_fwd_bf16.argtypes = [u16p, u16p, i64, ctypes.c_float]
+    l.orc_softcap_bwd_bf16.argtypes = [u16p, u16p, u16p, i64, ctypes.c_float]
+    l.orc_exp2.argtypes = [ci, ci, f32p, u16p, f32p, i64]
+    l.orc_sincos.argtypes = [ci, ci, ci, f32p, u16p, u16p, i64]
+    l.orc_rope_sincos_table.argtypes = [i32p, u16p, i64, i64]
+    l.orc_rope_apply.argtypes = [ci, u16p, u16p, i32p, u16p, u16p, i64, i64, i64, i64, i64]
     for name in (
         "orc_activation", "orc_activation_bwd", "orc_activation_bwd_alg",
         "orc_swish_mul_fwd", "orc_swish_mul_bwd", "orc_b3_direct_bf16",
-        "orc_b3_direct_f32", "orc_b3_constants", "orc_num_threads",
+        "orc_b3_direct_f32", "orc_b3_constants", "orc_num_threads", "orc_softcap_fwd_bf16",
+        "orc_softcap_bwd_bf16", "orc_exp2", "orc_sincos", "orc_rope_sincos_table",
+        "orc_rope_apply",
     ):
         getattr(l, name).restype = ctypes.c_int
 
@@ -178,6 +187,76 @@ def b3_constants():
     sc = np.empty(2, dtype=np.uint16)
     _check(lib().orc_b3_constants(_p(fwd), _p(grad), _p(sc)))
     return fwd.reshape(2, 4), grad.reshape(2, 2), sc
+
+
+def softcap_fwd_bf16(s: np.ndarray, cap: float) -> np.ndarray:
+    s = _u16(s)
+    y = np.empty_like(s)
+    _check(lib().orc_softcap_fwd_bf16(_p(s), _p(y), s.size, cap))
+    return y
+
+
+def softcap_bwd_bf16(go: np.ndarray, s: np.ndarray, cap: float) -> np.ndarray:
+    go, s = _u16(go), _u16(s)
+    g = np.empty_like(s)
+    _check(lib().orc_softcap_bwd_bf16(_p(go), _p(s), _p(g), s.size, cap))
+    return g
+
+
+EXP2_D2, EXP2_D3 = 0, 1
+
+
+def exp2(kind: int, x: np.ndarray, out_bf16: bool = True) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y16 = np.empty(x.shape, dtype=np.uint16)
+    y32 = np.empty(x.shape, dtype=np.float32)
+    _check(lib().orc_exp2(kind, int(out_bf16), _p(x, ctypes.c_float), _p(y16),
+                          _p(y32, ctypes.c_float), x.size))
+    return y16 if out_bf16 else y32
+
+
+# half-turn sin/cos programs (same ids as the device SinCosId enum)
+SC_BF16_D3D4, SC_BF16_D5D6, SC_F16_D3D4, SC_F16_D5D4, SC_F16_D5D6, SC_F16_D7D6 = range(6)
+
+
+def sincos(prog: int, angles: np.ndarray, out_fmt=None, rnd: int = RND_SINGLE):
+    """(cos bits, sin bits) of the half-turn program `prog`."""
+    a = np.ascontiguousarray(angles, dtype=np.float32)
+    if out_fmt is None:
+        out_fmt = BF16 if prog in (SC_BF16_D3D4, SC_BF16_D5D6) else F16
+    c = np.empty(a.shape, dtype=np.uint16)
+    s = np.empty(a.shape, dtype=np.uint16)
+    _check(lib().orc_sincos(prog, fmt_id(out_fmt), rnd, _p(a, ctypes.c_float), _p(c), _p(s),
+                            a.size))
+    return c, s
+
+
+def rope_sincos_table(inc: np.ndarray, seq: int) -> np.ndarray:
+    inc = np.ascontiguousarray(inc, dtype=np.int32)
+    out = np.empty((2, seq, inc.size), dtype=np.uint16)
+    _check(lib().orc_rope_sincos_table(_p(inc, ctypes.c_int32), _p(out), seq, inc.size))
+    return out
+
+
+def rope_apply(fmt, q: np.ndarray, k: np.ndarray, inc: np.ndarray):
+    """q [B,S,Hq,D], k [B,S,Hk,D] bit patterns -> ([B,Hq,S,D], [B,Hk,S,D])."""
+    q, k = _u16(q), _u16(k)
+    inc = np.ascontiguousarray(inc, dtype=np.int32)
+    b, s, hq, d = q.shape
+    hk = k.shape[2]
+    qo = np.empty((b, hq, s, d), dtype=np.uint16)
+    ko = np.empty((b, hk, s, d), dtype=np.uint16)
+    _check(lib().orc_rope_apply(fmt_id(fmt), _p(q), _p(k), _p(inc, ctypes.c_int32), _p(qo), _p(ko),
+                                b, s, hq, hk, d))
+    return qo, ko
+
+
+def rope_phase_increments(head_dim: int, theta: float) -> np.ndarray:
+    """round(omega_i * 2^32 / (2 pi)) as int32, omega_i = theta^(-2i/head_dim)
+    (src/sfu_repro/rope/benchmark_cuda_fused_rope.py:238-241)."""
+    dims = np.arange(0, head_dim, 2, dtype=np.float64)
+    omega = theta ** (-dims / head_dim)
+    return np.round(omega * (2.0 ** 32) / (2.0 * np.pi)).astype(np.int64).astype(np.int32)
 
 
 def num_threads() -> int:

@@ -536,3 +536,248 @@ int orc_b3_direct_f32(const float* s, uint16_t* y, uint16_t* dy, int64_t n) {
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* B2: tanh softcap (program defined for the MI355X build; the reference's   */
+/* FA4 composition is not in the repository)                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Round a binary32 value to BF16 with RNE; returns the BF16 value. */
+static double rne_bf16_f32(float v) { return round_fmt((double)v, &FMT_BF16); }
+
+static const double SOFTCAP_T_SAT = 2.609375;
+
+int orc_softcap_fwd_bf16(const uint16_t* s, uint16_t* y, int64_t n, float cap) {
+    if (n < 0 || !(cap > 0.0f)) return -1;
+    const prog_t* p = &BF16_PROGS[1][0][1]; /* TANH_FWD_D4_ODD_BF16 */
+    ctx_t k = {&FMT_BF16, ORC_RND_SINGLE};
+    float inv = 1.0f / cap;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float sf = (float)value_fmt(s[i], &FMT_BF16);
+        double u = rne_bf16_f32(sf * inv);
+        double t = eval_prog(p, u, &k);
+        y[i] = bits_fmt(rne_bf16_f32((float)t * cap), &FMT_BF16);
+    }
+    return 0;
+}
+
+int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int64_t n, float cap) {
+    if (n < 0 || !(cap > 0.0f)) return -1;
+    const prog_t* p = &BF16_PROGS[1][0][1];
+    const fmt_t* f = &FMT_BF16;
+    float inv = 1.0f / cap;
+    /* coefficients of the derivative of t*(c1 + c2 t + c3 t^2 + c4 t^3) */
+    double d[4];
+    for (int j = 0; j < 4; ++j) d[j] = round_fmt((j + 1) * kconst(p->c[j + 1], f), f);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float sf = (float)value_fmt(s[i], f);
+        double u = rne_bf16_f32(sf * inv);
+        double t = fabs(u);
+        double r = h_fma(t, d[3], d[2], f);
+        r = h_fma(t, r, d[1], f);
+        r = h_fma(t, r, d[0], f);
+        double deriv = (t < SOFTCAP_T_SAT) ? r : 0.0;
+        g[i] = bits_fmt(h_mul(value_fmt(go[i], f), deriv, f), f);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* B5: exp2 with FP32 range reduction (utils_exp2_cuda.cuh:13-74)            */
+/* ------------------------------------------------------------------------ */
+
+static int32_t sat_i32(float v) {
+    if (isnan(v)) return 0;
+    if (v >= 2147483648.0f) return INT32_MAX;
+    if (v < -2147483648.0f) return INT32_MIN;
+    return (int32_t)v;
+}
+
+static float exp2_prog(int kind, float x) {
+    x = fmaxf(x, -127.0f);
+    float fl = floorf(x);
+    float fr = x - fl;
+    float p;
+    if (kind == 0) { /* D2 safe: appendix_exp2.tex:29-32 */
+        p = fmaf(fr, 0.33976602809999057f, 0.6602339719000094f);
+        p = fmaf(p, fr, 1.0f);
+    } else {         /* FA4 D3 */
+        p = fmaf(fr, 0.077119089663028717041015625f, 0.227564394474029541015625f);
+        p = fmaf(p, fr, 0.695146143436431884765625f);
+        p = fmaf(p, fr, 1.0f);
+    }
+    uint32_t pb;
+    memcpy(&pb, &p, 4);
+    uint32_t rb = ((uint32_t)sat_i32(fl) << 23) + pb;
+    float r;
+    memcpy(&r, &rb, 4);
+    return r;
+}
+
+/* kind: 0 = D2 safe, 1 = FA4 D3.  out_bf16: BF16 bits into y16, else FP32
+ * into y32. */
+int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n) {
+    if (n < 0 || (kind != 0 && kind != 1)) return -1;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float r = exp2_prog(kind, x[i]);
+        if (out_bf16) y16[i] = bits_fmt(rne_bf16_f32(r), &FMT_BF16);
+        else y32[i] = r;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* paired sin/cos (sincos_kernels.cu)                                        */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    int fmt;
+    int ns;
+    float s[4];
+    int nc;
+    float c[4];
+} sincos_t;
+
+/* Same order as the SinCosId enum of the device code. */
+static const sincos_t SINCOS[7] = {
+    /* PolynomialD3D4HalfTurnBF16, sincos_kernels.cu:681-718 */
+    {ORC_BF16, 2, {-0.1455078125f, 0.98828125f}, 3, {0.037109375f, -0.49609375f, 1.0f}},
+    /* PolynomialD5D6HalfTurnBF16, :874-920 */
+    {ORC_BF16, 3, {0.007598876953125f, -0.166015625f, 1.0f}, 4,
+     {-0.00125885009765625f, 0.04150390625f, -0.5f, 1.0f}},
+    /* PolynomialD3D4HalfTurnFP16, :644-679 */
+    {ORC_F16, 2, {-0.14501953125f, 0.98876953125f}, 3,
+     {0.037200927734375f, -0.496337890625f, 0.99951171875f}},
+    /* evaluate_half_turn_d5_d4_fp16, :720-761 */
+    {ORC_F16, 3, {0.0074920654296875f, -0.16552734375f, 0.99951171875f}, 3,
+     {0.036773681640625f, -0.49560546875f, 0.99951171875f}},
+    /* PolynomialD5D6HalfTurnFP16, :820-860 */
+    {ORC_F16, 3, {0.0074920654296875f, -0.16552734375f, 0.99951171875f}, 4,
+     {-0.0012674331665039062f, 0.041412353515625f, -0.499755859375f, 1.0f}},
+    /* PolynomialD7D6HalfTurnFP16, :773-818 */
+    {ORC_F16, 4, {-0.00018227100372314453f, 0.00829315185546875f, -0.1666259765625f, 1.0f}, 4,
+     {-0.0012674331665039062f, 0.041412353515625f, -0.499755859375f, 1.0f}},
+    /* evaluate_half_turn_q15_d5_d6_fp16, :1289-1328 (argument in quarter turns) */
+    {ORC_F16, 3, {0.072021484375f, -0.64208984375f, 1.5703125f}, 4,
+     {-0.0190887451171875f, 0.25244140625f, -1.2333984375f, 1.0f}},
+};
+
+/* sin/cos of a reduced argument r (already a value of the format). */
+static void sincos_poly(const sincos_t* q, double r, int negate, const ctx_t* k,
+                        double* c_out, double* s_out) {
+    const fmt_t* f = k->f;
+    double sq = h_mul(r, r, f);
+    double sp = c_fma(k, kconst(q->s[0], f), sq, kconst(q->s[1], f));
+    for (int i = 2; i < q->ns; ++i) sp = c_fma(k, sp, sq, kconst(q->s[i], f));
+    double sr = h_mul(r, sp, f);
+    double cp = c_fma(k, kconst(q->c[0], f), sq, kconst(q->c[1], f));
+    for (int i = 2; i < q->nc; ++i) cp = c_fma(k, cp, sq, kconst(q->c[i], f));
+    *s_out = negate ? -sr : sr;
+    *c_out = negate ? -cp : cp;
+}
+
+/* FP32 half-turn reduction with the 1.5*2^23 shifter and FP32 pi. */
+static void reduce_half_turn(float angle, float* r, int* negate) {
+    const float inv_pi = 0.318309886183790671538f;
+    const float pi = 3.14159265358979323846f;
+    const float shifter = 12582912.0f;
+    float biased = fmaf(angle, inv_pi, shifter);
+    float kk = biased - shifter;
+    *r = fmaf(kk, -pi, angle);
+    uint32_t b;
+    memcpy(&b, &biased, 4);
+    *negate = (int)(b & 1u);
+}
+
+/* prog 0..5: half-turn programs of SINCOS[]; out_fmt: format of the output
+ * planes (a FP16 program may be written as BF16). */
+int orc_sincos(int prog, int out_fmt, int rnd, const float* angles, uint16_t* cos_out,
+               uint16_t* sin_out, int64_t n) {
+    if (prog < 0 || prog > 5 || n < 0) return -1;
+    const sincos_t* q = &SINCOS[prog];
+    ctx_t k = {fmt_of(q->fmt), rnd};
+    const fmt_t* fo = fmt_of(out_fmt);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float r32;
+        int neg;
+        reduce_half_turn(angles[i], &r32, &neg);
+        double r = round_fmt((double)r32, k.f);
+        double c, s;
+        sincos_poly(q, r, neg, &k, &c, &s);
+        cos_out[i] = bits_fmt(round_fmt(c, fo), fo);
+        sin_out[i] = bits_fmt(round_fmt(s, fo), fo);
+    }
+    return 0;
+}
+
+/* RoPE Q0.32 phase -> FP16 (cos, sin) (evaluate_rope_half_turn_q15_d5_d6_fp16,
+ * sincos_kernels.cu:1330-1348). */
+static void rope_q15(uint32_t position, uint32_t inc, double* c, double* s) {
+    uint32_t phase = position * inc;
+    int16_t q15 = (int16_t)(uint16_t)(phase >> 15);
+    double r = h_mul(round_fmt((double)q15, &FMT_F16), ldexp(1.0, -15), &FMT_F16);
+    int negate = (int)(((phase >> 31) ^ (phase >> 30)) & 1u);
+    ctx_t k = {&FMT_F16, ORC_RND_SINGLE};
+    sincos_poly(&SINCOS[6], r, negate, &k, c, s);
+}
+
+int orc_rope_sincos_table(const int32_t* inc, uint16_t* out, int64_t seq, int64_t nfreq) {
+    if (seq < 0 || nfreq < 0) return -1;
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < seq; ++p) {
+        for (int64_t f = 0; f < nfreq; ++f) {
+            double c, s;
+            rope_q15((uint32_t)p, (uint32_t)inc[f], &c, &s);
+            out[p * nfreq + f] = bits_fmt(c, &FMT_F16);
+            out[seq * nfreq + p * nfreq + f] = bits_fmt(s, &FMT_F16);
+        }
+    }
+    return 0;
+}
+
+/* Fused RoPE (sincos_kernels.cu:1504-1754): q [B,S,Hq,D], k [B,S,Hk,D] ->
+ * outputs [B,H,S,D].  fmt ORC_F16: the reference's packed-FP16 rotation;
+ * ORC_BF16: FP32 rotation of BF16 pairs with one RNE rounding per output. */
+int orc_rope_apply(int fmt, const uint16_t* q, const uint16_t* kk, const int32_t* inc,
+                   uint16_t* q_out, uint16_t* k_out, int64_t batch, int64_t seq, int64_t hq,
+                   int64_t hk, int64_t dim) {
+    if (batch < 0 || seq < 0 || hq < 0 || hk < 0 || dim <= 0 || dim % 2) return -1;
+    const fmt_t* f = fmt_of(fmt);
+    int64_t nfreq = dim / 2;
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < seq; ++p) {
+        for (int64_t i = 0; i < nfreq; ++i) {
+            double c, s;
+            rope_q15((uint32_t)p, (uint32_t)inc[i], &c, &s);
+            for (int which = 0; which < 2; ++which) {
+                const uint16_t* src = which ? kk : q;
+                uint16_t* dst = which ? k_out : q_out;
+                int64_t nh = which ? hk : hq;
+                for (int64_t b = 0; b < batch; ++b) {
+                    for (int64_t h = 0; h < nh; ++h) {
+                        int64_t in_base = ((b * seq + p) * nh + h) * dim + 2 * i;
+                        int64_t out_base = ((b * nh + h) * seq + p) * dim + 2 * i;
+                        double e = value_fmt(src[in_base], f);
+                        double o = value_fmt(src[in_base + 1], f);
+                        double ne, no;
+                        if (fmt == ORC_F16) {
+                            ne = h_fma(-s, o, h_mul(c, e, f), f);
+                            no = h_fma(s, e, h_mul(c, o, f), f);
+                        } else {
+                            float ef = (float)e, of = (float)o, cf = (float)c, sf = (float)s;
+                            ne = round_fmt((double)fmaf(ef, cf, -(of * sf)), f);
+                            no = round_fmt((double)fmaf(ef, sf, of * cf), f);
+                        }
+                        dst[out_base] = bits_fmt(ne, f);
+                        dst[out_base + 1] = bits_fmt(no, f);
+                    }
+                }
+            }
+        }
+    }
+    return 0;
+}

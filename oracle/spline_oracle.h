@@ -74,6 +74,23 @@ int orc_b3_direct_f32(const float* s, uint16_t* y, uint16_t* dy, int64_t n);
  * scaling), grad[2][2] (intercept, slope), split, clamp. */
 int orc_b3_constants(uint16_t* fwd8, uint16_t* grad4, uint16_t* split_clamp2);
 
+/* ---- B2 softcap (BF16) --------------------------------------------------- */
+int orc_softcap_fwd_bf16(const uint16_t* s, uint16_t* y, int64_t n, float cap);
+int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int64_t n, float cap);
+
+/* ---- B5 exp2: kind 0 = D2 safe, 1 = FA4 D3 -------------------------------- */
+int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n);
+
+/* ---- paired sin/cos: prog 0 BF16 D3/D4, 1 BF16 D5/D6, 2 FP16 D3/D4,
+ * 3 FP16 D5/D4, 4 FP16 D5/D6, 5 FP16 D7/D6 (half turn) ------------------- */
+int orc_sincos(int prog, int out_fmt, int rnd, const float* angles, uint16_t* cos_out,
+               uint16_t* sin_out, int64_t n);
+/* RoPE: [2, seq, nfreq] FP16 table and fused apply (fmt ORC_F16 / ORC_BF16). */
+int orc_rope_sincos_table(const int32_t* inc, uint16_t* out, int64_t seq, int64_t nfreq);
+int orc_rope_apply(int fmt, const uint16_t* q, const uint16_t* k, const int32_t* inc,
+                   uint16_t* q_out, uint16_t* k_out, int64_t batch, int64_t seq, int64_t hq,
+                   int64_t hk, int64_t dim);
+
 /* Thread count used by the bulk loops (OpenMP when built with it). */
 int orc_num_threads(void);
 

@@ -1,0 +1,43 @@
+"""Resolver errors of the sfu_repro activation layer (no GPU needed;
+src/sfu_repro/activations.py:35-45, 246-249, 307-308)."""
+
+import pytest
+
+
+def test_unknown_activation_and_sources(monkeypatch):
+    from sfu_repro import activations
+
+    with pytest.raises(ValueError, match="unknown activation 'relu'"):
+        activations.resolve_mlp_activation_impl("relu")
+    with pytest.raises(ValueError, match="unknown coeff_source"):
+        activations.resolve_mlp_activation_impl("spline_silu_compile", coeff_source="x")
+    monkeypatch.delenv("SFU_REPRO_ALLOW_SOLLYA_SWEEP", raising=False)
+    with pytest.raises(ValueError, match="Sollya coefficients are benchmark-only"):
+        activations.resolve_mlp_activation_impl("spline_silu_compile", coeff_source="sollya")
+    with pytest.raises(ValueError, match="backward_impl must be"):
+        activations.resolve_mlp_activation_packed_impl("spline_silu_compile", backward_impl="x")
+    assert activations.resolve_mlp_activation_impl("native_silu")[0] == "native_silu"
+    with pytest.raises(RuntimeError, match="GELU"):
+        activations.resolve_mlp_activation_impl("spline_gelu")
+
+
+def test_spline_compile_factories_validate_arguments():
+    import spline_compile
+
+    with pytest.raises(ValueError, match="Unknown coeff_source"):
+        spline_compile.make_spline_silu(3, "nope")
+    with pytest.raises(ValueError, match="Unknown packed SwiGLU backward_impl"):
+        spline_compile.make_spline_silu_packed(3, "current", backward_impl="bad")
+    act = spline_compile.make_spline_silu_packed(3, "current")
+    assert act.__spline_op__ == "spline_ops::swish_mul_packed_variant_fwd"
+
+
+def test_extension_rejects_host_tensors():
+    import torch
+
+    import spline_ops
+
+    with pytest.raises(RuntimeError, match="x must be a CUDA tensor"):
+        spline_ops.swish_fwd(torch.zeros(4, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="scores must be a CUDA tensor"):
+        spline_ops.flash_sigmoid_direct_d3_d4_bf16(torch.zeros(4, dtype=torch.bfloat16))

@@ -1,0 +1,100 @@
+"""GPU parity of the attention-side programs (B2 softcap, B5 exp2) against
+the CPU oracle, through the C ABI, plus error bounds of the native baselines
+against FP32 torch."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_parity import _dev, _host, assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+
+def _f32_inputs(seed, n=1 << 18):
+    rng = np.random.default_rng(seed)
+    x = np.concatenate([
+        -rng.random(n, dtype=np.float32) * 140.0,             # softmax exponents
+        np.linspace(-3.0, 1.0, 4099, dtype=np.float32),
+        np.array([0.0, -0.0, -1e-30, -1e-40, -126.5, -127.0, -127.25, -128.0,
+                  -np.inf, 0.999999, 1.5, 60.25], dtype=np.float32),
+    ])
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("cap", [30.0, 50.0])
+def test_softcap_forward_exhaustive(capi, oracle, cuda, cap):
+    s = oracle.all_bits()
+    sd = _dev(s, "bf16", cuda)
+    y = torch.empty_like(sd)
+    rc = capi.launch_softcap_tanh_d4_bf16(capi.ptr(y), capi.ptr(sd), ctypes.c_int64(s.size),
+                                          ctypes.c_float(cap), capi.stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert_bits_equal(_host(y), oracle.softcap_fwd_bf16(s, cap), "bf16", f"softcap cap={cap}")
+
+
+def test_softcap_backward(capi, oracle, cuda):
+    rng = np.random.default_rng(5)
+    s = np.tile(oracle.all_bits(), 2)
+    go = oracle.f32_to_bf16_bits(rng.standard_normal(s.size).astype(np.float32))
+    go[:65536] = 0x3F80
+    sd, god = _dev(s, "bf16", cuda), _dev(go, "bf16", cuda)
+    g = torch.empty_like(sd)
+    rc = capi.launch_softcap_tanh_d4_bwd_bf16(capi.ptr(g), capi.ptr(god), capi.ptr(sd),
+                                              ctypes.c_int64(s.size), ctypes.c_float(30.0),
+                                              capi.stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert_bits_equal(_host(g), oracle.softcap_bwd_bf16(go, s, 30.0), "bf16", "softcap bwd")
+
+
+def test_softcap_config3_distribution(spline_ops, cuda):
+    """BASELINE config 3 recipe (reduced size): N(0, 15^2) scores with 1 %
+    outliers at +-200; error against FP32 30*tanh(s/30)."""
+    g = torch.Generator().manual_seed(0)
+    s = torch.randn(1 << 20, generator=g) * 15
+    mask = torch.rand(s.shape, generator=g) < 0.01
+    sign = torch.where(torch.rand(s.shape, generator=g) < 0.5, -1.0, 1.0)
+    s = torch.where(mask, 200.0 * sign, s).to(torch.bfloat16)
+    y = spline_ops.softcap_tanh_fwd_bf16(s.to(cuda), 30.0).float().cpu()
+    ref = 30.0 * torch.tanh(s.float() / 30.0)
+    # D4 tanh error 0.0133 (x cap) plus BF16 rounding of the output
+    assert float((y - ref).abs().max()) < 0.6
+
+
+@pytest.mark.parametrize("kind,name", [(0, "d2"), (1, "d3")])
+@pytest.mark.parametrize("out_bf16", [True, False])
+def test_exp2_programs(capi, oracle, cuda, kind, name, out_bf16):
+    x = _f32_inputs(11 + kind)
+    xd = torch.from_numpy(x).to(cuda)
+    if out_bf16:
+        y = torch.empty(x.size, dtype=torch.bfloat16, device=cuda)
+        capi.call(f"launch_exp2_{name}_f32_bf16", y, xd, x.size)
+        torch.cuda.synchronize()
+        assert_bits_equal(_host(y), oracle.exp2(kind, x, True), "bf16", f"exp2 {name} bf16")
+    else:
+        y = torch.empty(x.size, dtype=torch.float32, device=cuda)
+        capi.call(f"launch_exp2_{name}_f32", y, xd, x.size)
+        torch.cuda.synchronize()
+        want = oracle.exp2(kind, x, False)
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_exp2_config5_and_native(spline_ops, cuda):
+    """BASELINE config 5 recipe (one head block): logits N(0, 4^2) minus the
+    row max; D2 relative error vs FP32 torch.exp2 and the native baseline."""
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(64, 4096, 128, generator=g) * 4
+    x = (logits - logits.amax(-1, keepdim=True)).to(cuda)
+    ref = torch.exp2(x)
+    d2 = spline_ops.exp2_d2_f32_to_bf16(x).float()
+    nat = spline_ops.exp2_native_f32_to_bf16(x).float()
+    d2_32 = spline_ops.exp2_d2_f32(x)
+    big = ref > 1e-30
+    rel = ((d2_32 - ref).abs() / ref)[big]
+    assert float(rel.max()) < 2.8e-3          # sampled-minimax D2 bound 2.679e-3
+    assert float(((d2 - ref).abs() / ref)[big].max()) < 2.8e-3 + 2 ** -8
+    assert float(((nat - ref).abs() / ref)[big].max()) < 2 ** -8 + 1e-5

@@ -1,0 +1,203 @@
+"""The drop-in Python surface on the GPU: `spline_ops` pybind functions,
+`torch.ops.spline_ops` dispatcher ops, C++ autograd, `spline_compile` under
+torch.compile and the resolver layer — restating the reference's GPU verify
+script (autonumerics_zero/spline_ops/test_spline_ops.py) as pytest."""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _eq(a, b):
+    torch.testing.assert_close(a, b, rtol=0.0, atol=0.0)
+
+
+def test_fixed_degree_functions_match_variants(spline_ops, cuda):
+    x = torch.linspace(-8, 8, 10007, device=cuda)
+    for dt in (torch.float16, torch.bfloat16):
+        xx = x.to(dt)
+        go = torch.ones_like(xx)
+        for d in (3, 4, 5, 6):
+            _eq(getattr(spline_ops, f"swish_fwd_d{d}")(xx), spline_ops.swish_fwd_variant(xx, d, 0))
+            _eq(getattr(spline_ops, f"sigmoid_fwd_d{d}")(xx), spline_ops.sigmoid_fwd_variant(xx, d, 0))
+            _eq(getattr(spline_ops, f"swish_bwd_d{d}")(go, xx), spline_ops.swish_bwd_variant(go, xx, d, 0))
+        _eq(spline_ops.swish_fwd(xx), spline_ops.swish_fwd_d3(xx))
+        _eq(spline_ops.sigmoid_bwd(go, xx), spline_ops.sigmoid_bwd_d4(go, xx))
+
+
+def test_dispatcher_ops_match_pybind(spline_ops, cuda):
+    import spline_compile  # noqa: F401  (fake / autograd registrations)
+
+    gate = torch.linspace(-12.0, 12.0, 4097, device=cuda, dtype=torch.bfloat16)
+    up = torch.linspace(-1.0, 1.0, 4097, device=cuda, dtype=torch.bfloat16)
+    go = torch.linspace(1.0, -1.0, 4097, device=cuda, dtype=torch.bfloat16)
+    ops = torch.ops.spline_ops
+    _eq(ops.swish_mul_variant_fwd(gate, up, 3, 0), spline_ops.swish_mul_fwd_variant(gate, up, 3, 0))
+    a = ops.swish_mul_variant_bwd(go, gate, up, 3, 0)
+    b = spline_ops.swish_mul_bwd_variant(go, gate, up, 3, 0)
+    _eq(a[0], b[0])
+    _eq(a[1], b[1])
+    _eq(ops.swish_variant_fwd(gate, 4, 0), spline_ops.swish_fwd_variant(gate, 4, 0))
+
+
+def test_swiglu_d3_compiled_matches_eager_and_native(cuda):
+    """test_spline_ops.py:12-50 (verify_compiled_swiglu_d3)."""
+    import spline_ops
+    from spline_compile import make_spline_silu_mul
+
+    activation = make_spline_silu_mul(3, "current")
+    gate = torch.linspace(-12.0, 12.0, 4097, device=cuda, dtype=torch.bfloat16)
+    up = torch.linspace(-1.0, 1.0, gate.numel(), device=cuda, dtype=torch.bfloat16)
+    grad_out = torch.linspace(1.0, -1.0, gate.numel(), device=cuda, dtype=torch.bfloat16)
+    expected = spline_ops.swish_mul_fwd_variant(gate, up, 3, 0)
+    eg, eu = spline_ops.swish_mul_bwd_variant(grad_out, gate, up, 3, 0)
+    compiled = torch.compile(activation, fullgraph=True)
+    cg = gate.detach().requires_grad_(True)
+    cu = up.detach().requires_grad_(True)
+    actual = compiled(cg, cu)
+    actual.backward(grad_out)
+    _eq(actual, expected)
+    _eq(cg.grad, eg)
+    _eq(cu.grad, eu)
+    ng = gate.float().requires_grad_(True)
+    nu = up.float().requires_grad_(True)
+    native = torch.nn.functional.silu(ng) * nu
+    native.backward(grad_out.float())
+    torch.testing.assert_close(actual.float(), native, rtol=0.0, atol=0.07)
+    torch.testing.assert_close(cg.grad.float(), ng.grad, rtol=0.0, atol=0.07)
+    torch.testing.assert_close(cu.grad.float(), nu.grad, rtol=0.0, atol=0.07)
+
+
+def test_packed_swiglu_compiled(cuda):
+    """test_spline_ops.py:53-81 (verify_compiled_packed_swiglu_d3)."""
+    import spline_ops
+    from spline_compile import make_spline_silu_packed
+
+    packed = (torch.linspace(-12.0, 12.0, 8192, device=cuda, dtype=torch.bfloat16)
+              .reshape(2, 4096).requires_grad_(True))
+    grad_out = torch.linspace(1.0, -1.0, 4096, device=cuda, dtype=torch.bfloat16).reshape(2, 2048)
+    gate, up = (p.contiguous() for p in packed.detach().chunk(2, dim=-1))
+    expected = spline_ops.swish_mul_fwd_variant(gate, up, 3, 0)
+    eg, eu = spline_ops.swish_mul_bwd_variant(grad_out, gate, up, 3, 0)
+    activation = torch.compile(make_spline_silu_packed(3, "current"), fullgraph=True)
+    actual = activation(packed)
+    actual.backward(grad_out)
+    _eq(actual, expected)
+    _eq(packed.grad, torch.cat((eg, eu), dim=-1))
+
+
+def test_packed_native_backward(cuda):
+    """test_spline_ops.py:84-112: D3 forward with native SiLU gradients."""
+    import spline_ops
+    from spline_compile import make_spline_silu_packed
+
+    packed = (torch.linspace(-12.0, 12.0, 8192, device=cuda, dtype=torch.bfloat16)
+              .reshape(2, 4096).requires_grad_(True))
+    grad_out = torch.linspace(1.0, -1.0, 4096, device=cuda, dtype=torch.bfloat16).reshape(2, 2048)
+    gate, up = packed.detach().float().chunk(2, dim=-1)
+    gate.requires_grad_(True)
+    up.requires_grad_(True)
+    native = torch.nn.functional.silu(gate) * up
+    native.backward(grad_out.float())
+    activation = torch.compile(make_spline_silu_packed(3, "current", backward_impl="native"),
+                               fullgraph=True)
+    actual = activation(packed)
+    actual.backward(grad_out)
+    expected = spline_ops.swish_mul_fwd_variant(gate.bfloat16(), up.bfloat16(), 3, 0)
+    _eq(actual, expected)
+    torch.testing.assert_close(packed.grad, torch.cat((gate.grad, up.grad), -1).bfloat16(),
+                               rtol=0.01, atol=0.0078125)
+
+
+def test_autograd_functions(spline_ops, cuda):
+    x = torch.linspace(-6, 6, 2049, device=cuda, dtype=torch.float16).requires_grad_(True)
+    y = spline_ops.sigmoid_ag(x)
+    y.backward(torch.ones_like(y))
+    _eq(y, spline_ops.sigmoid_fwd_d3(x.detach()))
+    _eq(x.grad, spline_ops.sigmoid_bwd_alg(torch.ones_like(y), y.detach()))
+    x.grad = None
+    y = torch.ops.spline_ops.swish_fwd(x)
+    y.backward(torch.ones_like(y))
+    _eq(x.grad, spline_ops.swish_bwd_d4(torch.ones_like(y), x.detach()))
+    x.grad = None
+    y = spline_ops.swish_ag_variant(x, 5, 0)
+    y.backward(torch.ones_like(y))
+    _eq(x.grad, spline_ops.swish_bwd_d5(torch.ones_like(y), x.detach()))
+
+
+def test_fp16_sigmoid_d3_error(spline_ops, cuda):
+    """test_spline_ops.py:249-259."""
+    x = torch.randn(1 << 24, device=cuda, dtype=torch.float16) * 3
+    y = spline_ops.sigmoid_fwd_d3(x)
+    assert float((y.float() - torch.sigmoid(x.float())).abs().max()) < 0.02
+
+
+def test_error_messages(spline_ops, cuda):
+    x = torch.zeros(8, device=cuda, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="x must be float16 or bfloat16"):
+        spline_ops.swish_fwd(x)
+    h = torch.zeros(8, device=cuda, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="coeff_source_id must be 0"):
+        spline_ops.swish_fwd_variant(h, 3, 2)
+    with pytest.raises(RuntimeError, match="FP16 spline kernels only support coeff_source=current"):
+        spline_ops.swish_fwd_variant(h, 3, 1)
+    with pytest.raises(RuntimeError, match="Unsupported swish forward degree: 7"):
+        spline_ops.swish_fwd_variant(h, 7, 0)
+    with pytest.raises(RuntimeError, match="must be contiguous"):
+        spline_ops.swish_fwd(torch.zeros(8, 2, device=cuda, dtype=torch.float16).t())
+    with pytest.raises(RuntimeError, match="packed gate/up last dimension must be even"):
+        spline_ops.swish_mul_packed_fwd_variant(torch.zeros(2, 5, device=cuda, dtype=torch.float16), 3, 0)
+
+
+def test_empty_tensors(spline_ops, cuda):
+    e = torch.empty(0, device=cuda, dtype=torch.bfloat16)
+    assert spline_ops.swish_fwd(e).numel() == 0
+    assert spline_ops.swish_mul_fwd_variant(e, e, 3, 0).numel() == 0
+    p = torch.empty(0, 8, device=cuda, dtype=torch.bfloat16)
+    assert spline_ops.swish_mul_packed_fwd_variant(p, 3, 0).shape == (0, 4)
+
+
+def test_graph_capture_replays(spline_ops, cuda):
+    """The launchers are capture-safe: every replay equals the eager result."""
+    x = torch.randn(1 << 16, device=cuda, dtype=torch.bfloat16)
+    y = torch.empty_like(x)
+    eager = spline_ops.swish_fwd_d3(x)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        y.copy_(spline_ops.swish_fwd_d3(x))
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y.copy_(spline_ops.swish_fwd_d3(x))
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _eq(y, eager)
+
+
+def test_activation_resolver_layer(cuda):
+    from sfu_repro import activations
+
+    x = torch.linspace(-6, 6, 4100, device=cuda, dtype=torch.bfloat16)
+    import spline_ops
+
+    name, act = activations.resolve_mlp_activation_impl("spline_silu_compile", degree=3,
+                                                        coeff_source="current")
+    assert name == "spline_silu_compile[d3,current]"
+    _eq(act(x), spline_ops.swish_fwd_variant(x, 3, 0))
+    name, act = activations.resolve_mlp_activation_impl("spline_silu", degree=4)
+    _eq(act(x), spline_ops.swish_fwd_variant(x, 4, 0))
+    name, mul = activations.resolve_mlp_activation_mul_impl("spline_silu_compile")
+    assert name.startswith("spline_ops::swish_mul_variant_fwd")
+    _eq(mul(x, x), spline_ops.swish_mul_fwd_variant(x, x, 3, 0))
+    packed = torch.cat((x, x)).reshape(1, -1)
+    name, pk = activations.resolve_mlp_activation_packed_impl("spline_silu_compile")
+    assert name.startswith("spline_ops::swish_mul_packed_variant_fwd")
+    _eq(pk(packed), spline_ops.swish_mul_packed_fwd_variant(packed, 3, 0))
+    _, native = activations.resolve_mlp_activation_impl("native_silu")
+    torch.testing.assert_close(native(x), torch.nn.functional.silu(x), rtol=0, atol=0)

@@ -1,0 +1,232 @@
+"""The oracle's activation, softcap, exp2, sin/cos and RoPE programs against
+the reference's known answers and against the mathematics they approximate.
+
+A dropped Horner term, a wrong sign, a swapped coefficient or a wrong clamp
+moves the maximum error far past the bounds below; the per-program bounds
+come from the `Err=` figures the reference states next to each program
+(spline_structs_odd*.cuh) and the fit tables of the paper."""
+
+import math
+
+import numpy as np
+import pytest
+
+ALL = None
+
+
+def _all(oracle):
+    return oracle.all_bits()
+
+
+def _exact(fam, direction, v):
+    s = 1.0 / (1.0 + np.exp(-v))
+    if fam == "sigmoid":
+        return s if direction == 0 else s * (1 - s)
+    if fam == "tanh":
+        return np.tanh(v) if direction == 0 else 1 - np.tanh(v) ** 2
+    return v * s if direction == 0 else s * (1 + v * (1 - s))
+
+
+# (fmt, family, direction) -> [(Li, stated Err)] for degrees 3..6, from the
+# comments of spline_structs_odd.cuh and spline_structs_odd_bf16.cuh.
+STATED = {
+    ("f16", "sigmoid", 0): [(6.5, 0.005562), (4.75, 0.004261), (6.0, 0.002594), (7.25, 0.003168)],
+    ("f16", "tanh", 0): [(3.25, 0.011089), (2.75, 0.009193), (3.0, 0.005188), (4.5, 0.006221)],
+    ("f16", "sigmoid", 1): [(4.5, 0.011002), (5.25, 0.004201), (5.75, 0.002840), (6.25, 0.002963)],
+    ("f16", "tanh", 1): [(2.25, 0.044007), (2.5, 0.019043), (3.25, 0.015758), (4.75, 0.017399)],
+    ("f16", "swish", 1): [(5.25, 0.017511), (8.0, 0.014858), (6.25, 0.010503), (7.25, 0.010162)],
+    ("bf16", "sigmoid", 0): [(6.0, 0.007420), (5.0, 0.005891), (6.25, 0.005891), (8.0, 0.008847)],
+    ("bf16", "tanh", 0): [(2.5, 0.014538), (2.5, 0.013285), (4.25, 0.016504), (4.25, 0.014477)],
+    ("bf16", "sigmoid", 1): [(4.5, 0.011549), (4.75, 0.007216), (7.5, 0.008373), (7.5, 0.009759)],
+    ("bf16", "tanh", 1): [(2.25, 0.046194), (2.25, 0.032650), (4.25, 0.038063), (5.75, 0.036270)],
+    ("bf16", "swish", 1): [(4.75, 0.021872), (7.25, 0.018683), (6.25, 0.019464), (10.0, 0.019176)],
+}
+
+
+@pytest.mark.parametrize("key", sorted(STATED))
+def test_activation_error_matches_stated_fit(oracle, key):
+    fmt, fam, direction = key
+    x = _all(oracle)
+    with np.errstate(invalid="ignore", over="ignore"):
+        v = oracle.bits_to_f32(x, fmt).astype(np.float64)
+    for degree, (li, err) in zip((3, 4, 5, 6), STATED[key]):
+        y = oracle.bits_to_f32(oracle.activation(fam, direction, degree, fmt, x), fmt)
+        m = np.isfinite(v) & (np.abs(v) <= li)
+        got = np.abs(y[m] - _exact(fam, direction, v[m])).max()
+        # The stated figure was measured on a sampled grid; the exhaustive
+        # 16-bit sweep lands within [0.5, 2.5] x of it for every program.
+        assert 0.5 * err <= got <= 2.5 * err, (key, degree, got, err)
+
+
+@pytest.mark.parametrize("degree", [3, 4, 5, 6])
+def test_bf16_swish_tails_are_exact(oracle, degree):
+    # autonumerics_zero/spline_ops/test_spline_ops.py:159-166
+    gate = oracle.f32_to_bf16_bits(np.array([-100, -20, 20, 100], dtype=np.float32))
+    up = oracle.f32_to_bf16_bits(np.ones(4, dtype=np.float32))
+    out = oracle.bf16_bits_to_f32(oracle.swish_mul_fwd(degree, "bf16", gate, up))
+    assert out.tolist() == [0.0, 0.0, 20.0, 100.0]
+
+
+def test_fp16_sigmoid_d3_error_kat(oracle):
+    # test_spline_ops.py:249-259: FP16 sigmoid D3 max error < 0.02 on randn*3
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(1 << 20) * 3).astype(np.float16)
+    y = oracle.f16_bits_to_f32(oracle.activation("sigmoid", 0, 3, "f16", x.view(np.uint16)))
+    assert np.abs(y - 1 / (1 + np.exp(-x.astype(np.float64)))).max() < 0.02
+
+
+def test_swiglu_d3_bf16_matches_native_within_reference_tolerance(oracle):
+    # test_spline_ops.py:12-50: SwiGLU D3 vs FP32 silu*up, atol 0.07
+    gate = np.linspace(-12, 12, 4097, dtype=np.float32)
+    up = np.linspace(-1, 1, 4097, dtype=np.float32)
+    go = np.linspace(1, -1, 4097, dtype=np.float32)
+    gb, ub, gob = (oracle.f32_to_bf16_bits(a) for a in (gate, up, go))
+    gq, uq = oracle.bf16_bits_to_f32(gb), oracle.bf16_bits_to_f32(ub)
+    goq = oracle.bf16_bits_to_f32(gob)
+    out = oracle.bf16_bits_to_f32(oracle.swish_mul_fwd(3, "bf16", gb, ub))
+    s = 1 / (1 + np.exp(-gq.astype(np.float64)))
+    assert np.abs(out - gq * s * uq).max() < 0.07
+    gg, gu = oracle.swish_mul_bwd(3, "bf16", gob, gb, ub)
+    assert np.abs(oracle.bf16_bits_to_f32(gg) - goq * uq * s * (1 + gq * (1 - s))).max() < 0.07
+    assert np.abs(oracle.bf16_bits_to_f32(gu) - goq * gq * s).max() < 0.07
+
+
+@pytest.mark.parametrize("fam", ["sigmoid", "tanh", "swish"])
+@pytest.mark.parametrize("direction", [0, 1])
+@pytest.mark.parametrize("degree", [3, 4, 5, 6])
+def test_bf16_fp32_fma_then_rne_equals_single_rounding(oracle, fam, direction, degree):
+    """The gfx950 BF16 path (FP32 FMA, then RNE to BF16) gives the same bits
+    as a single-rounding BF16 FMA for every input of every program."""
+    x = _all(oracle)
+    a = oracle.activation(fam, direction, degree, "bf16", x, oracle.RND_SINGLE)
+    b = oracle.activation(fam, direction, degree, "bf16", x, oracle.RND_F32)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("prog", [0, 1])
+def test_bf16_sincos_fp32_fma_then_rne_equals_single_rounding(oracle, prog):
+    # every BF16 reduced argument in [-pi/2, pi/2] (the reduction is exact there)
+    x = _all(oracle)
+    v = oracle.bf16_bits_to_f32(x)
+    with np.errstate(invalid="ignore"):
+        a = v[np.isfinite(v) & (np.abs(v) <= 1.5)]
+    c1, s1 = oracle.sincos(prog, a, rnd=oracle.RND_SINGLE)
+    c2, s2 = oracle.sincos(prog, a, rnd=oracle.RND_F32)
+    assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
+
+
+# ---- B2 softcap -------------------------------------------------------------
+
+def test_softcap_forward_error_bound(oracle):
+    x = _all(oracle)
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = oracle.bf16_bits_to_f32(x).astype(np.float64)
+    m = np.isfinite(s)
+    y = oracle.bf16_bits_to_f32(oracle.softcap_fwd_bf16(x, 30.0))[m]
+    ref = 30.0 * np.tanh(s[m] / 30.0)
+    # D4 tanh (max error 0.0133 on its fit range) scaled by cap, plus the BF16
+    # rounding of the input scale and of the output (|y| <= 30: half-ulp 0.0625)
+    assert np.abs(y - ref).max() < 30 * 0.0133 + 0.0625 + 0.2
+    assert np.all(np.abs(y) <= 30.0)
+    # odd symmetry is exact (the program restores the sign by XOR)
+    pos = x[(x < 0x7F80) & (x > 0)]
+    yp = oracle.softcap_fwd_bf16(pos, 30.0)
+    yn = oracle.softcap_fwd_bf16(pos | np.uint16(0x8000), 30.0)
+    assert np.array_equal(yn, yp ^ np.uint16(0x8000)) or np.array_equal(
+        oracle.bf16_bits_to_f32(yn), -oracle.bf16_bits_to_f32(yp))
+
+
+def test_softcap_backward_is_derivative_of_d4_program(oracle):
+    x = _all(oracle)
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = oracle.bf16_bits_to_f32(x).astype(np.float64)
+    m = np.isfinite(s)
+    ones = np.full(x.size, 0x3F80, dtype=np.uint16)
+    g = oracle.bf16_bits_to_f32(oracle.softcap_bwd_bf16(ones, x, 30.0))[m]
+    u = s[m] / 30.0
+    # derivative of the D4 odd polynomial with the BF16-rounded coefficients
+    c = [1.0859375, -0.322265625, -0.0230712891, 0.0164794922]
+    t = np.abs(u)
+    d = c[0] + 2 * c[1] * t + 3 * c[2] * t ** 2 + 4 * c[3] * t ** 3
+    d = np.where(t < 2.609375, d, 0.0)
+    assert np.abs(g - d).max() < 0.02          # BF16 Horner rounding only
+    assert np.abs(g - (1 - np.tanh(u) ** 2)).max() < 0.16  # vs the exact tanh'
+
+
+# ---- B5 exp2 ------------------------------------------------------------------
+
+def test_exp2_d2_invariants_and_fit(oracle):
+    n = np.arange(-126, 1, dtype=np.float32)
+    # p(0) = 1: integers are exact powers of two
+    assert np.array_equal(oracle.exp2(0, n, False), np.exp2(n.astype(np.float64)).astype(np.float32))
+    # p(1) = 2 continuity: just below an integer the result meets 2^x with
+    # no jump between exponent intervals
+    # (from -125 up: below -126 the reconstruction lands in FA4's exponent-0
+    # band, whose bit pattern keeps only p's mantissa)
+    below = np.nextafter(n[1:], np.float32(-np.inf)).astype(np.float32)
+    r = oracle.exp2(0, below, False) / np.exp2(below.astype(np.float64))
+    assert np.abs(r - 1).max() < 5e-7
+    x = np.linspace(-20, 0, 1_000_001, dtype=np.float32)
+    rel = np.abs(oracle.exp2(0, x, False) / np.exp2(x.astype(np.float64)) - 1)
+    assert 2.0e-3 < rel.max() < 2.8e-3        # appendix_exp2.tex: 2.679e-3
+    rel3 = np.abs(oracle.exp2(1, x, False) / np.exp2(x.astype(np.float64)) - 1)
+    assert rel3.max() < 1.0e-4                 # FA4 D3: 8.763e-5
+    # masking value and clamp
+    assert oracle.exp2(0, np.array([-np.inf, -127.0, -1000.0], dtype=np.float32), False).tolist() == [0.0, 0.0, 0.0]
+
+
+# ---- sin/cos and RoPE -------------------------------------------------------------
+
+@pytest.mark.parametrize("prog,bound", [(0, 1.3e-2), (1, 9e-3), (2, 1e-2), (3, 1.5e-3), (4, 1.2e-3), (5, 1.2e-3)])
+def test_half_turn_sincos_error(oracle, prog, bound):
+    a = np.linspace(-64.0, 64.0, 400_003, dtype=np.float32)
+    c, s = oracle.sincos(prog, a)
+    fmt = "bf16" if prog < 2 else "f16"
+    cf, sf = oracle.bits_to_f32(c, fmt), oracle.bits_to_f32(s, fmt)
+    a64 = a.astype(np.float64)
+    err = max(np.abs(cf - np.cos(a64)).max(), np.abs(sf - np.sin(a64)).max())
+    assert err < bound, err
+    # Pythagorean identity within the evaluation error
+    assert np.abs(cf.astype(np.float64) ** 2 + sf.astype(np.float64) ** 2 - 1).max() < 4 * bound
+
+
+def test_rope_phase_increments_match_reference_convention(oracle):
+    inc = oracle.rope_phase_increments(128, 500000.0)
+    assert inc.dtype == np.int32 and inc.size == 64
+    assert inc[0] == round(2 ** 32 / (2 * math.pi))
+    assert (np.diff(inc.astype(np.int64)) < 0).all()
+
+
+def test_rope_phase_table_accuracy(oracle):
+    inc = oracle.rope_phase_increments(128, 500000.0)
+    seq = 4096
+    t = oracle.rope_sincos_table(inc, seq)
+    phase = (np.arange(seq, dtype=np.uint64)[:, None] * inc.astype(np.uint64)[None]) % (1 << 32)
+    ang = phase.astype(np.float64) * (2 * math.pi / 2 ** 32)
+    err = max(np.abs(oracle.f16_bits_to_f32(t[0]) - np.cos(ang)).max(),
+              np.abs(oracle.f16_bits_to_f32(t[1]) - np.sin(ang)).max())
+    assert err < 2e-3, err
+
+
+@pytest.mark.parametrize("fmt", ["f16", "bf16"])
+def test_rope_apply_matches_float64_rotation(oracle, fmt):
+    rng = np.random.default_rng(4)
+    b, s, hq, hk, d = 1, 512, 2, 1, 64
+    q = rng.standard_normal((b, s, hq, d)).astype(np.float32)
+    k = rng.standard_normal((b, s, hk, d)).astype(np.float32)
+    if fmt == "bf16":
+        qb, kb = oracle.f32_to_bf16_bits(q), oracle.f32_to_bf16_bits(k)
+    else:
+        qb, kb = q.astype(np.float16).view(np.uint16), k.astype(np.float16).view(np.uint16)
+    inc = oracle.rope_phase_increments(d, 500000.0)
+    qo, ko = oracle.rope_apply(fmt, qb, kb, inc)
+    dims = np.arange(0, d, 2, dtype=np.float64)
+    ang = np.arange(s)[:, None] * (500000.0 ** (-dims / d))[None]
+    for src, out in ((qb, qo), (kb, ko)):
+        v = oracle.bits_to_f32(src, fmt).astype(np.float64)
+        e, o = v[..., 0::2], v[..., 1::2]
+        c, sn = np.cos(ang)[None, :, None], np.sin(ang)[None, :, None]
+        ref = np.stack((e * c - o * sn, e * sn + o * c), -1).reshape(v.shape).transpose(0, 2, 1, 3)
+        got = oracle.bits_to_f32(out, fmt)
+        ulp = 2 ** -8 if fmt == "bf16" else 2 ** -11
+        assert np.abs(got - ref).max() < np.abs(v).max() * (3e-3 + 2 * ulp)
