@@ -70,6 +70,46 @@ struct B3FwdOp {
     }
 };
 
+// ---------------------------------------------------------------------------
+// B3-D2: FlashSigmoid probability via a range-reduced degree-2 exp2
+// (model autonumerics_zero/evolution/fit_flash_sigmoid_exp2_d2.py:55-77;
+// FA4 selects it for sigmoid_degree == 2, src/sfu_repro/fa4.py:469-476).
+// t = clamp(s * log2(e), -200, 200) (FP32; beyond the clamp the result is
+// 0 or inf either way, NaN scores give 0), n = floor(t), f = t - n,
+// m = c0 + f (c1 + f c2), p = m * 2^(n - 12)  (1/4096 folded into the
+// exponent), y = bf16(p), dy = bf16(p (1 - p)) with one FMA.
+// Coefficients: the fitter's FP32 output for n = 4096 (seed 1234).
+// ---------------------------------------------------------------------------
+
+struct B3D2Consts {
+    static constexpr float c0 = 1.0018835067749023f;   // 0x3F803DB8
+    static constexpr float c1 = 0.6557925939559937f;   // 0x3F27E206
+    static constexpr float c2 = 0.33421099185943604f;  // 0x3EAB1DB4
+    static constexpr float log2e = 1.44269504088896340736f;
+};
+
+__device__ __forceinline__ void b3_d2_lane(float s, float& y, float& dy) {
+    using C = B3D2Consts;
+    const float t = __builtin_fminf(__builtin_fmaxf(s * C::log2e, -200.0f), 200.0f);
+    const float fl = __builtin_floorf(t);
+    const float f = t - fl;
+    const float m = __builtin_fmaf(__builtin_fmaf(f, C::c2, C::c1), f, C::c0);
+    const float p = __builtin_ldexpf(m, (int)fl - 12);
+    y = p;
+    dy = __builtin_fmaf(-p, p, p);
+}
+
+struct B3D2Op {
+    static constexpr int NIN = 1, NOUT = 2;
+    __device__ __forceinline__ static void pair(const uint32_t (&a)[1], uint32_t (&b)[2]) {
+        float y0, y1, d0, d1;
+        b3_d2_lane(bf_lo(a[0]), y0, d0);
+        b3_d2_lane(bf_hi(a[0]), y1, d1);
+        b[0] = pack_bf(y0, y1);
+        b[1] = pack_bf(d0, d1);
+    }
+};
+
 // FP32 scores: 8 scores (32 B) per thread-iteration, two 16-byte loads.
 template <bool LNT, bool SNT>
 __global__ void __launch_bounds__(kBlock)
@@ -350,4 +390,13 @@ extern "C" int launch_exp2_d3_f32(void* y, const void* x, int64_t size, void* st
 }
 extern "C" int launch_exp2_native_f32(void* y, const void* x, int64_t size, void* stream) {
     return launch_exp2<kExp2Native, false>(y, x, size, stream);
+}
+
+// ---- B3-D2 ----------------------------------------------------------------------
+
+extern "C" int launch_flash_sigmoid_exp2_d2_bf16(void* y, void* dy, const void* scores,
+                                                 int64_t size, void* stream) {
+    if (bad_args(size, {y, dy, scores})) return hipErrorInvalidValue;
+    Streams<1, 2> s{{scores}, {y, dy}};
+    return launch_pairwise<B3D2Op>(s, size, hs(stream));
 }

@@ -364,6 +364,20 @@ std::vector<at::Tensor> flash_sigmoid_direct_d3_d4(at::Tensor scores) {
     return {y, dy};
 }
 
+std::vector<at::Tensor> flash_sigmoid_exp2_d2(at::Tensor scores) {
+    CHECK_CUDA(scores);
+    CHECK_CONTIGUOUS(scores);
+    TORCH_CHECK(scores.scalar_type() == at::kBFloat16, "scores must be bfloat16");
+    c10::OptionalDeviceGuard guard(scores.device());
+    at::Tensor y = at::empty_like(scores);
+    at::Tensor dy = at::empty_like(scores);
+    void* s = current_stream(scores);
+    check_launch(launch_flash_sigmoid_exp2_d2_bf16(y.data_ptr(), dy.data_ptr(), scores.data_ptr(),
+                                                   scores.numel(), s),
+                 s);
+    return {y, dy};
+}
+
 at::Tensor flash_sigmoid_direct_d3(at::Tensor scores) {
     CHECK_CUDA(scores);
     CHECK_CONTIGUOUS(scores);
@@ -802,6 +816,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
 
     m.def("flash_sigmoid_direct_d3_d4_bf16", &flash_sigmoid_direct_d3_d4,
           "B3 deployed direct-D3 probability and factored-D4 derivative (BF16 out)");
+    m.def("flash_sigmoid_exp2_d2_bf16", &flash_sigmoid_exp2_d2,
+          "B3-D2 sigmoid via range-reduced degree-2 exp2 (probability, derivative), BF16");
     m.def("flash_sigmoid_direct_d3_bf16", &flash_sigmoid_direct_d3,
           "B3 deployed direct-D3 probability (BF16)");
 }

@@ -160,6 +160,14 @@ int launch_flash_sigmoid_direct_d3_d4_f32_bf16(void* y, void* dy, const void* sc
 /* Forward only (the first listing, main.tex:1041-1070). */
 int launch_flash_sigmoid_direct_d3_bf16(void* y, const void* scores, int64_t size,
                                         void* stream);
+/* B3-D2 sigmoid via a range-reduced degree-2 exp2 (FA4 sigmoid_degree == 2,
+ * src/sfu_repro/fa4.py:469-476; model and coefficients from
+ * autonumerics_zero/evolution/fit_flash_sigmoid_exp2_d2.py:55-143):
+ * y = bf16(2^(n-12) (c0 + f (c1 + f c2))) with clamp(s*log2(e), -200, 200)
+ * = n + f (NaN and -inf scores give 0),
+ * dy = bf16(y (1 - y)) from the FP32 probability. */
+int launch_flash_sigmoid_exp2_d2_bf16(void* y, void* dy, const void* scores, int64_t size,
+                                      void* stream);
 
 /* ---- B2: tanh softcap cap * tanh(s / cap) on BF16 scores -----------------
  * No C launcher exists in the reference: FA4 selects the D4 BF16 tanh

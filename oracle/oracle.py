@@ -77,6 +77,8 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_b3_constants.argtypes = [u16p, u16p, u16p]
     l.orc_num_threads.argtypes = []
     i32p = ctypes.POINTER(ctypes.c_int32)
+    l.orc_b3_exp2_d2_bf16.argtypes = [u16p, u16p, u16p, i64, f32p]
+    l.orc_b3_exp2_d2_bf16.restype = ctypes.c_int
     l.orc_softcap_fwd_bf16.argtypes = [u16p, u16p, i64, ctypes.c_float]
     l.orc_softcap_bwd_bf16.argtypes = [u16p, u16p, u16p, i64, ctypes.c_float]
     l.orc_exp2.argtypes = [ci, ci, f32p, u16p, f32p, i64]
@@ -178,6 +180,15 @@ def b3_direct_f32(s: np.ndarray):
     y = np.empty(s.shape, dtype=np.uint16)
     dy = np.empty(s.shape, dtype=np.uint16)
     _check(lib().orc_b3_direct_f32(_p(s, ctypes.c_float), _p(y), _p(dy), s.size))
+    return y, dy
+
+
+def b3_exp2_d2_bf16(x: np.ndarray, coeffs) -> tuple:
+    x = _u16(x)
+    c = np.ascontiguousarray(coeffs, dtype=np.float32)
+    y = np.empty_like(x)
+    dy = np.empty_like(x)
+    _check(lib().orc_b3_exp2_d2_bf16(_p(x), _p(y), _p(dy), x.size, _p(c, ctypes.c_float)))
     return y, dy
 
 

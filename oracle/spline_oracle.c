@@ -781,3 +781,27 @@ int orc_rope_apply(int fmt, const uint16_t* q, const uint16_t* kk, const int32_t
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* B3-D2: sigmoid via range-reduced degree-2 exp2 (program model of          */
+/* autonumerics_zero/evolution/fit_flash_sigmoid_exp2_d2.py:55-77 in FP32)    */
+/* ------------------------------------------------------------------------ */
+
+int orc_b3_exp2_d2_bf16(const uint16_t* x, uint16_t* y, uint16_t* dy, int64_t n,
+                        const float* coeffs3) {
+    if (n < 0 || !coeffs3) return -1;
+    const float c0 = coeffs3[0], c1 = coeffs3[1], c2 = coeffs3[2];
+    const float log2e = 1.44269504088896340736f;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float s = (float)value_fmt(x[i], &FMT_BF16);
+        float t = fminf(fmaxf(s * log2e, -200.0f), 200.0f);
+        float fl = floorf(t);
+        float f = t - fl;
+        float m = fmaf(fmaf(f, c2, c1), f, c0);
+        float p = ldexpf(m, (int)fl - 12);
+        y[i] = bits_fmt(rne_bf16_f32(p), &FMT_BF16);
+        dy[i] = bits_fmt(rne_bf16_f32(fmaf(-p, p, p)), &FMT_BF16);
+    }
+    return 0;
+}

@@ -74,6 +74,11 @@ int orc_b3_direct_f32(const float* s, uint16_t* y, uint16_t* dy, int64_t n);
  * scaling), grad[2][2] (intercept, slope), split, clamp. */
 int orc_b3_constants(uint16_t* fwd8, uint16_t* grad4, uint16_t* split_clamp2);
 
+/* B3-D2: sigmoid(s - ln 4096) via a range-reduced degree-2 exp2 with the
+ * given FP32 coefficients (c0, c1, c2). */
+int orc_b3_exp2_d2_bf16(const uint16_t* x, uint16_t* y, uint16_t* dy, int64_t n,
+                        const float* coeffs3);
+
 /* ---- B2 softcap (BF16) --------------------------------------------------- */
 int orc_softcap_fwd_bf16(const uint16_t* s, uint16_t* y, int64_t n, float cap);
 int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int64_t n, float cap);

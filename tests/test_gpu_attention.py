@@ -98,3 +98,19 @@ def test_exp2_config5_and_native(spline_ops, cuda):
     assert float(rel.max()) < 2.8e-3          # sampled-minimax D2 bound 2.679e-3
     assert float(((d2 - ref).abs() / ref)[big].max()) < 2.8e-3 + 2 ** -8
     assert float(((nat - ref).abs() / ref)[big].max()) < 2 ** -8 + 1e-5
+
+
+def test_b3_exp2_d2_exhaustive(capi, oracle, cuda):
+    import json
+    import os
+
+    with open(os.path.join(os.path.dirname(__file__), "golden", "b3_d2_coefficients.json")) as f:
+        coeffs = json.load(f)["coefficients_float32"]
+    s = oracle.all_bits()
+    sd = _dev(s, "bf16", cuda)
+    y, dy = torch.empty_like(sd), torch.empty_like(sd)
+    capi.call("launch_flash_sigmoid_exp2_d2_bf16", y, dy, sd, s.size)
+    torch.cuda.synchronize()
+    want_y, want_dy = oracle.b3_exp2_d2_bf16(s, coeffs)
+    assert_bits_equal(_host(y), want_y, "bf16", "B3-D2 y")
+    assert_bits_equal(_host(dy), want_dy, "bf16", "B3-D2 dy")
