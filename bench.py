@@ -258,6 +258,9 @@ def config_rows(lib, reps: int):
     rows.append(_row("b3_direct_d3_d4", "C0 B3 2^20 U[-16,16]", "bf16", s.numel(), 6 * s.numel(),
                      [("poly", _launcher(lib, "launch_flash_sigmoid_direct_d3_d4_bf16", y, dy, s,
                                          s.numel()))], reps))
+    rows.append(_row("b3_exp2_d2", "C0 B3-D2 2^20 U[-16,16]", "bf16", s.numel(), 6 * s.numel(),
+                     [("poly", _launcher(lib, "launch_flash_sigmoid_exp2_d2_bf16", y, dy, s,
+                                         s.numel()))], reps))
     del s, y, dy
 
     # C1 / B1 L2-resident variant [256, 4096] FP16 N(0, 2^2).

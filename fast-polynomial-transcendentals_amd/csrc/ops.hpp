@@ -37,8 +37,9 @@ template <class P>
 struct BF16MulOp {
     static constexpr int NIN = 2, NOUT = 1;
     __device__ __forceinline__ static void pair(const uint32_t (&a)[2], uint32_t (&b)[1]) {
-        const uint32_t d = P::eval(a[1]);
-        b[0] = pack_bf(bf_lo(a[0]) * bf_lo(d), bf_hi(a[0]) * bf_hi(d));
+        float d_lo, d_hi;
+        P::eval2(a[1], d_lo, d_hi);
+        b[0] = pack_bf(bf_lo(a[0]) * d_lo, bf_hi(a[0]) * d_hi);
     }
 };
 
@@ -56,8 +57,9 @@ template <class P>
 struct BF16SwishMulOp {
     static constexpr int NIN = 2, NOUT = 1;
     __device__ __forceinline__ static void pair(const uint32_t (&a)[2], uint32_t (&b)[1]) {
-        const uint32_t s = P::eval(a[0]);
-        b[0] = pack_bf(bf_lo(s) * bf_lo(a[1]), bf_hi(s) * bf_hi(a[1]));
+        float s_lo, s_hi;
+        P::eval2(a[0], s_lo, s_hi);
+        b[0] = pack_bf(s_lo * bf_lo(a[1]), s_hi * bf_hi(a[1]));
     }
 };
 
@@ -79,12 +81,13 @@ template <class PF, class PB>
 struct BF16SwishMulBwdOp {
     static constexpr int NIN = 3, NOUT = 2;
     __device__ __forceinline__ static void pair(const uint32_t (&a)[3], uint32_t (&b)[2]) {
-        const uint32_t s = PF::eval(a[1]);
-        const uint32_t d = PB::eval(a[1]);
+        float s_lo, s_hi, d_lo, d_hi;
+        PF::eval2(a[1], s_lo, s_hi);
+        PB::eval2(a[1], d_lo, d_hi);
         const float gu_lo = rbf(bf_lo(a[0]) * bf_lo(a[2]));
         const float gu_hi = rbf(bf_hi(a[0]) * bf_hi(a[2]));
-        b[0] = pack_bf(gu_lo * bf_lo(d), gu_hi * bf_hi(d));
-        b[1] = pack_bf(bf_lo(a[0]) * bf_lo(s), bf_hi(a[0]) * bf_hi(s));
+        b[0] = pack_bf(gu_lo * d_lo, gu_hi * d_hi);
+        b[1] = pack_bf(bf_lo(a[0]) * s_lo, bf_hi(a[0]) * s_hi);
     }
 };
 
@@ -142,8 +145,9 @@ struct PackedNativeSwishMulBwdOp {
             const float dy_lo = rbf(bf_lo(a[0]) * bf_lo(a[2]));
             const float dy_hi = rbf(bf_hi(a[0]) * bf_hi(a[2]));
             b[0] = pack_bf(gg_lane(dy_lo, bf_lo(a[1])), gg_lane(dy_hi, bf_hi(a[1])));
-            const uint32_t s = BF16Native<kSwishFam, kFwd>::eval(a[1]);
-            b[1] = pack_bf(bf_lo(a[0]) * bf_lo(s), bf_hi(a[0]) * bf_hi(s));
+            float s_lo, s_hi;
+            BF16Native<kSwishFam, kFwd>::eval2(a[1], s_lo, s_hi);
+            b[1] = pack_bf(bf_lo(a[0]) * s_lo, bf_hi(a[0]) * s_hi);
         } else {
             const h2_t dy = as_h2(a[0]) * as_h2(a[2]);
             const h2_t x = as_h2(a[1]);

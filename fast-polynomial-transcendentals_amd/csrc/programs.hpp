@@ -14,7 +14,9 @@
 //  * The clamp t = min(|x|, Lc) is an unsigned 16-bit min on the magnitude
 //    bits (v_pk_min_u16): for non-negative IEEE patterns integer order is
 //    numeric order, and NaN/Inf magnitudes select Lc, which is exactly the
-//    __hmin2 rule "a NaN operand yields the other operand".
+//    __hmin2 rule "a NaN operand yields the other operand".  The BF16 SiLU
+//    forward, whose output is NaN for a NaN input whatever the clamp gives,
+//    clamps with one FP32 minimum per lane instead.
 //
 // Coefficients: autonumerics_zero/spline_ops/spline_structs_odd.cuh (FP16) and
 // spline_structs_odd_bf16.cuh (BF16); each table row cites its struct.
@@ -248,57 +250,93 @@ struct F16Prog {
 
 __device__ __forceinline__ float bfma(float a, float b, float c) { return rbf(__builtin_fmaf(a, b, c)); }
 
+// The lane programs are written "open": they return the last step's FP32
+// result before its rounding, so a pair's two final roundings are one
+// v_cvt_pk_bf16_f32 (eval) and the callers that go on computing take rounded
+// lanes from eval2.  Rounding the open value is the program's last rounded
+// step because RNE is odd-symmetric (rbf(v ^ sign) = rbf(v) ^ sign) and
+// monotone with 1.0 representable (rbf(min(v, 1)) = min(rbf(v), 1)).
 template <int F, int D, int G>
 struct BF16Prog {
     static constexpr Prog P = kBF16Progs[F][D][G - 3];
 
-    // Lane program on FP32 copies of the BF16 lane values.  `t` is the clamped
-    // magnitude, `x` the input, `neg` its sign bit (as 0x80000000 or 0).
-    __device__ __forceinline__ static float lane(float t, float x, uint32_t neg) {
-        constexpr float half = bf16_value(0.5f);
-        if constexpr (P.shape == kEven) {
-            float r = bfma(t, bf16_value(P.c[P.deg]), bf16_value(P.c[P.deg - 1]));
+    // H(t) of the odd shapes (every step rounded); t is the clamped magnitude.
+    __device__ __forceinline__ static float odd_horner(float t) {
+        float h = bfma(t, bf16_value(P.c[P.deg]), bf16_value(P.c[P.deg - 1]));
 #pragma unroll
-            for (int i = P.deg - 2; i >= 0; --i) r = bfma(t, r, bf16_value(P.c[i]));
-            return r;
+        for (int i = P.deg - 2; i >= 1; --i) h = bfma(t, h, bf16_value(P.c[i]));
+        return h;
+    }
+
+    // Even programs, up to the final rounding; t is the clamped magnitude.
+    __device__ __forceinline__ static float even_open(float t) {
+        float r = bfma(t, bf16_value(P.c[P.deg]), bf16_value(P.c[P.deg - 1]));
+#pragma unroll
+        for (int i = P.deg - 2; i >= 1; --i) r = bfma(t, r, bf16_value(P.c[i]));
+        return __builtin_fmaf(t, r, bf16_value(P.c[0]));
+    }
+
+    // Odd programs, up to the final rounding.  `ts` is the clamped magnitude
+    // carrying the input's sign: H runs on |ts| (a free source modifier) and
+    // the last product ts*H(|ts|) is sign(x)*t*H(t) exactly, so no separate
+    // sign restore is needed.
+    __device__ __forceinline__ static float odd_signed_open(float ts) {
+        const float v = ts * odd_horner(__builtin_fabsf(ts));
+        if constexpr (P.shape == kOdd) {
+            return v;
+        } else if constexpr (P.shape == kOddMin1) {
+            // sign * min(t*H(t), 1) = clamp(v, -1, 1); v is finite.
+            return __builtin_amdgcn_fmed3f(v, -1.0f, 1.0f);
         } else {
-            float h = bfma(t, bf16_value(P.c[P.deg]), bf16_value(P.c[P.deg - 1]));
-#pragma unroll
-            for (int i = P.deg - 2; i >= 1; --i) h = bfma(t, h, bf16_value(P.c[i]));
-            h = rbf(t * h);
-            if constexpr (P.shape == kHalfOdd) {
-                return rbf(half + as_f32(as_u32(h) ^ neg));
-            } else if constexpr (P.shape == kOdd) {
-                return as_f32(as_u32(h) ^ neg);
-            } else if constexpr (P.shape == kOddMin1) {
-                // h >= 0 and finite here, so fminf is __hmin2.
-                return as_f32(as_u32(__builtin_fminf(h, 1.0f)) ^ neg);
-            } else {  // kSwish
-                static_assert(P.shape == kSwish, "unsupported BF16 shape");
-                const float ax = as_f32(as_u32(x) & 0x7fffffffu);
-                return bfma(ax, h, rbf(half * x));
+            static_assert(P.shape == kHalfOdd, "unsupported BF16 shape");
+            return bf16_value(0.5f) + rbf(v);
+        }
+    }
+
+    // Both lanes before their final rounding.
+    __device__ __forceinline__ static void open2(uint32_t x, float& lo, float& hi) {
+        if constexpr (P.shape == kXTimes) {
+            float s_lo, s_hi;
+            BF16Prog<kSigmoid, kFwd, G>::eval2(x, s_lo, s_hi);
+            lo = bf_lo(x) * s_lo;
+            hi = bf_hi(x) * s_hi;
+        } else if constexpr (P.shape == kSwish) {
+            // A NaN input gives a NaN output whatever t is (it enters through
+            // |x| and 0.5*x), so the clamp may propagate NaN: one FP32
+            // minimum per lane instead of the packed u16 minimum + unpack.
+            // bf16(0.5*x) stays rounded: for x = -2^-133 it is -0, and
+            // +0 + -0 = +0 is the reference's result, where the unrounded
+            // -2^-134 would round to -0.
+            const float xl = bf_lo(x), xh = bf_hi(x);
+            const float tl = __builtin_elementwise_minimum(__builtin_fabsf(xl), P.lc);
+            const float th = __builtin_elementwise_minimum(__builtin_fabsf(xh), P.lc);
+            lo = __builtin_fmaf(__builtin_fabsf(xl), rbf(tl * odd_horner(tl)), rbf(0.5f * xl));
+            hi = __builtin_fmaf(__builtin_fabsf(xh), rbf(th * odd_horner(th)), rbf(0.5f * xh));
+        } else {
+            const uint32_t t2 = umin16x2(x & 0x7fff7fffu, bf16_pair_bits(P.lc));
+            if constexpr (P.shape == kEven) {
+                lo = even_open(bf_lo(t2));
+                hi = even_open(bf_hi(t2));
+            } else {
+                const uint32_t ts = t2 | (x & 0x80008000u);
+                lo = odd_signed_open(bf_lo(ts));
+                hi = odd_signed_open(bf_hi(ts));
             }
         }
     }
 
-    // Both lanes, returned as FP32 values that hold BF16 values.
+    // Both lanes, rounded: FP32 values that hold BF16 values.
     __device__ __forceinline__ static void eval2(uint32_t x, float& lo, float& hi) {
-        if constexpr (P.shape == kXTimes) {
-            float s_lo, s_hi;
-            BF16Prog<kSigmoid, kFwd, G>::eval2(x, s_lo, s_hi);
-            lo = rbf(bf_lo(x) * s_lo);
-            hi = rbf(bf_hi(x) * s_hi);
-        } else {
-            const uint32_t t2 = umin16x2(x & 0x7fff7fffu, bf16_pair_bits(P.lc));
-            lo = lane(bf_lo(t2), bf_lo(x), (x << 16) & 0x80000000u);
-            hi = lane(bf_hi(t2), bf_hi(x), x & 0x80000000u);
-        }
+        float ol, oh;
+        open2(x, ol, oh);
+        lo = rbf(ol);
+        hi = rbf(oh);
     }
 
     __device__ __forceinline__ static uint32_t eval(uint32_t x) {
         float lo, hi;
-        eval2(x, lo, hi);
-        return pack_exact_bf(lo, hi);
+        open2(x, lo, hi);
+        return pack_bf(lo, hi);
     }
 };
 
@@ -318,12 +356,17 @@ struct F16Alg {
 
 template <int F>
 struct BF16Alg {
-    __device__ __forceinline__ static float lane(float y) {
-        if constexpr (F == kSigmoid) return rbf(y * rbf(1.0f - y));
-        else return rbf(1.0f - rbf(y * y));
+    // Before the final rounding.
+    __device__ __forceinline__ static float lane_open(float y) {
+        if constexpr (F == kSigmoid) return y * rbf(1.0f - y);
+        else return 1.0f - rbf(y * y);
+    }
+    __device__ __forceinline__ static void eval2(uint32_t y, float& lo, float& hi) {
+        lo = rbf(lane_open(bf_lo(y)));
+        hi = rbf(lane_open(bf_hi(y)));
     }
     __device__ __forceinline__ static uint32_t eval(uint32_t y) {
-        return pack_exact_bf(lane(bf_lo(y)), lane(bf_hi(y)));
+        return pack_bf(lane_open(bf_lo(y)), lane_open(bf_hi(y)));
     }
 };
 
@@ -365,6 +408,10 @@ struct F16Native {
 
 template <int F, int D>
 struct BF16Native {
+    __device__ __forceinline__ static void eval2(uint32_t x, float& lo, float& hi) {
+        lo = rbf(native_lane<F, D>(bf_lo(x)));
+        hi = rbf(native_lane<F, D>(bf_hi(x)));
+    }
     __device__ __forceinline__ static uint32_t eval(uint32_t x) {
         return pack_bf(native_lane<F, D>(bf_lo(x)), native_lane<F, D>(bf_hi(x)));
     }
