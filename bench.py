@@ -13,8 +13,11 @@ steps.  Alongside it the JSON line carries
   counters when a committed profile holds it;
 * `cpu_baseline`: the CPU oracle (a C restatement of the same program, all
   host threads) timed on a bounded sample of the same tensor;
-* `functions`: the per-function sweep, polynomial vs native, at an
-  L2-resident size and at 2^28 elements (HBM), plus the B3 config.
+* `copy_ceiling`: the same one-pass driver copying the same tensor, the
+  achievable ceiling of a 1-read/1-write stream of that size;
+* `functions`: the per-function sweep, polynomial vs native vs copy, over
+  2^16..2^28 elements (L2, MALL and HBM regimes; graph replay, median of 9
+  rounds, implementations interleaved), plus every BASELINE configuration.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep]
 """
@@ -76,10 +79,9 @@ def time_launches(launch, reps: int, warmup: int):
     return start.elapsed_time(stop) / reps
 
 
-def time_graph(launch, reps: int, rounds: int = 5):
-    """Average ms per launch with `reps` launches captured in one HIP graph
-    and replayed: removes the host launch cost that dominates small
-    (L2-resident) kernels.  Median over `rounds` replays."""
+def _graph(launch, reps: int):
+    """`reps` launches captured in one HIP graph (replay removes the host
+    launch cost that dominates small, L2-resident kernels)."""
     import torch
 
     launch()
@@ -90,17 +92,43 @@ def time_graph(launch, reps: int, rounds: int = 5):
             launch()
     g.replay()
     torch.cuda.synchronize()
-    times = []
-    for _ in range(rounds):
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        start.record()
-        g.replay()
-        stop.record()
-        stop.synchronize()
-        times.append(start.elapsed_time(stop) / reps)
+    return g
+
+
+def _replay_ms(g, reps: int):
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def time_graph(launch, reps: int, rounds: int = 9):
+    """Average ms per launch of a captured graph of `reps` launches; median
+    over `rounds` replays."""
+    g = _graph(launch, reps)
+    times = sorted(_replay_ms(g, reps) for _ in range(rounds))
     del g
-    return sorted(times)[len(times) // 2]
+    return times[len(times) // 2]
+
+
+def time_graphs_alternating(launches, reps: int, rounds: int = 9):
+    """Like time_graph for several launches at once, replaying them in
+    alternating order within each round (the paper's protocol: median of 9
+    rounds, implementations interleaved) so that clock or thermal drift
+    does not favour one of them."""
+    graphs = [_graph(fn, reps) for fn in launches]
+    per = [[] for _ in launches]
+    for r in range(rounds):
+        order = range(len(graphs)) if r % 2 == 0 else reversed(range(len(graphs)))
+        for i in order:
+            per[i].append(_replay_ms(graphs[i], reps))
+    del graphs
+    return [sorted(t)[len(t) // 2] for t in per]
 
 
 def make_unary(lib, name, out, x):
@@ -158,33 +186,75 @@ def cpu_baseline(x_cpu_fp16, target_s: float = 10.0):
     }
 
 
-def sweep(lib, reps: int):
-    """Per-function polynomial vs native timing: L2-resident (2^20), the
-    reference's L2 size (2^22, MALL-resident on MI355X) and HBM (2^28)."""
-    import ctypes
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
+
+def cpu_torch_native(x_cpu_fp16, target_s: float = 3.0):
+    """Informational second CPU baseline: torch's FP32 SiLU on the host's
+    threads over the same 2^24-element sample (not the program the GPU
+    runs; the oracle above is)."""
+    import torch
+
+    xs = x_cpu_fp16.reshape(-1)[: 1 << 24].float()
+    torch.nn.functional.silu(xs[:4096])
+    done, t0 = 0, time.perf_counter()
+    while True:
+        torch.nn.functional.silu(xs).half()
+        done += xs.numel()
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    return {"value": done / el / 1e9, "unit": "Gelem/s", "threads": torch.get_num_threads(),
+            "host": {"cpu_model": _cpu_model(), "nproc": os.cpu_count()},
+            "sample": "torch.nn.functional.silu FP32 -> FP16 on the same 2^24-element sample"}
+
+
+SWEEP_LOG2 = (16, 18, 20, 22, 24, 26, 28)
+
+
+def _regime(n_log2: int) -> str:
+    # aggregate L2 is 8 x 4 MB; the MALL is 256 MB
+    return "l2" if n_log2 <= 21 else ("mall" if n_log2 <= 25 else "hbm")
+
+
+def sweep(lib, reps: int):
+    """Per-function polynomial vs native timing over 2^16..2^28 elements
+    (L2-resident, MALL-resident, HBM), each size with the copy ceiling of the
+    same driver, then the BASELINE configurations."""
     import torch
 
     out = []
     dev = torch.device("cuda:0")
-    for n_log2, regime in ((20, "l2"), (22, "mall"), (28, "hbm")):
+    for n_log2 in SWEEP_LOG2:
         n = 1 << n_log2
+        r = reps if n_log2 < 26 else max(5, reps // 5)
         g = torch.Generator(device=dev).manual_seed(n_log2)
         for dtype, sfx in ((torch.float16, ""), (torch.bfloat16, "_bf16")):
             x = (torch.randn(n, device=dev, generator=g) * 2.0).to(dtype)
             y = torch.empty_like(x)
+            (copy_ms,) = time_graphs_alternating([make_unary(lib, "spline_hip_copy16", y, x)], r)
             for fam, deg in (("sigmoid", 3), ("tanh", 4), ("swish", 3)):
                 row = {"function": f"{fam}_fwd", "dtype": "fp16" if not sfx else "bf16",
-                       "degree": deg, "elements": n, "regime": regime}
-                for label, name in (("poly", f"launch_{fam}_fwd_d{deg}_kernel{sfx}"),
-                                    ("native", f"launch_{fam}_fwd_native_kernel{sfx}")):
-                    r = reps if n_log2 < 28 else max(5, reps // 5)
-                    ms = time_graph(make_unary(lib, name, y, x), r)
+                       "degree": deg, "elements": n, "regime": _regime(n_log2)}
+                poly_ms, nat_ms = time_graphs_alternating(
+                    [make_unary(lib, f"launch_{fam}_fwd_d{deg}_kernel{sfx}", y, x),
+                     make_unary(lib, f"launch_{fam}_fwd_native_kernel{sfx}", y, x)], r)
+                for label, ms in (("poly", poly_ms), ("native", nat_ms), ("copy", copy_ms)):
                     row[f"{label}_us"] = round(ms * 1e3, 3)
-                    row[f"{label}_gelem_s"] = round(n / ms / 1e6, 2)
                     row[f"{label}_gbs"] = round(4 * n / ms / 1e6, 1)
+                row["poly_gelem_s"] = round(n / poly_ms / 1e6, 2)
+                row["native_gelem_s"] = round(n / nat_ms / 1e6, 2)
                 row["poly_frac_hbm_peak"] = round(row["poly_gbs"] / HBM_PEAK_GBS, 4)
-                row["speedup"] = round(row["native_us"] / row["poly_us"], 3)
+                row["poly_frac_copy"] = round(copy_ms / poly_ms, 4)
+                row["speedup"] = round(nat_ms / poly_ms, 3)
                 out.append(row)
             del x, y
         torch.cuda.empty_cache()
@@ -227,8 +297,8 @@ def _row(function, config, dtype, elements, alg_bytes, launches, reps):
     """Time each (label, launch) and report us, Gelem/s, GB/s, HBM fraction."""
     row = {"function": function, "config": config, "dtype": dtype, "elements": elements,
            "bytes_per_launch": alg_bytes}
-    for label, launch in launches:
-        ms = time_graph(launch, reps)
+    times = time_graphs_alternating([fn for _, fn in launches], reps)
+    for (label, _), ms in zip(launches, times):
         row[f"{label}_us"] = round(ms * 1e3, 3)
         row[f"{label}_gelem_s"] = round(elements / ms / 1e6, 2)
         row[f"{label}_gbs"] = round(alg_bytes / ms / 1e6, 1)
@@ -429,8 +499,16 @@ def main():
                      "traffic": traffic},
         "wall_s_timed": round(wall, 3),
     }
+    # Achievable ceiling: the same driver copying the same tensor.
+    copy_ms = time_launches(make_unary(lib, "spline_hip_copy16", y, x), args.steps, args.warmup)
+    copy_gbs = 4.0 * n / (copy_ms * 1e-3) / 1e9
+    line["copy_ceiling"] = {"achieved": round(copy_gbs, 1), "unit": "GB/s",
+                            "frac_hbm_peak": round(copy_gbs / HBM_PEAK_GBS, 4),
+                            "kernel_frac_of_copy": round(copy_ms / ms_per_step, 4)}
+    del y
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(x_cpu)
+        line["cpu_torch_native"] = cpu_torch_native(x_cpu)
     if not args.no_sweep:
         line["functions"] = sweep(lib, args.sweep_reps)
     print(json.dumps(line), flush=True)

@@ -54,3 +54,9 @@ PT_BINARY(launch_sigmoid_bwd_alg_kernel, (F16MulOp<F16Alg<kSigmoid>>))
 PT_BINARY(launch_sigmoid_bwd_alg_kernel_bf16, (BF16MulOp<BF16Alg<kSigmoid>>))
 PT_BINARY(launch_tanh_bwd_alg_kernel, (F16MulOp<F16Alg<kTanh>>))
 PT_BINARY(launch_tanh_bwd_alg_kernel_bf16, (BF16MulOp<BF16Alg<kTanh>>))
+
+// Identity "program": the copy ceiling of the unary driver.
+struct CopyProg {
+    __device__ __forceinline__ static uint32_t eval(uint32_t x) { return x; }
+};
+PT_UNARY(spline_hip_copy16, (CopyProg))

@@ -243,6 +243,12 @@ SPLINE_HIP_ROPE_APPLY_LAUNCHERS(SPLINE_HIP_DECLARE_ROPE_APPLY)
  * (inputs + outputs).  For tests and benchmarks. */
 int spline_hip_grid_for(int64_t size, int streams, int64_t* grid_out, int* cus_out);
 
+/* Measurement helper, no counterpart in the reference: copies `size` 16-bit
+ * elements through the same one-pass driver, launch shape and cache policy
+ * as the unary launchers above.  Its time is the achievable ceiling a
+ * 1-read/1-write stream of that size reaches on this device. */
+int spline_hip_copy16(void* out, const void* in, int64_t size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -227,3 +227,18 @@ def test_large_streaming_paths(capi, oracle, cuda, reps, fmt):
     got = y.view(torch.int16).view(reps, 65536)
     nan_ok = torch.isnan(y.view(reps, 65536).float()) & torch.isnan(want.view(DTYPES[fmt]).float())[None]
     assert bool(((got == want[None]) | nan_ok).all())
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 4099, 1 << 20])
+def test_copy_helper(capi, cuda, n):
+    """spline_hip_copy16 (the bench's copy ceiling) moves every element."""
+    x = torch.arange(n, device=cuda, dtype=torch.int32).to(torch.int16)
+    y = torch.full_like(x, -1)
+    capi.call("spline_hip_copy16", y, x, n)
+    torch.cuda.synchronize()
+    assert torch.equal(x, y)
+    xu = torch.arange(n + 1, device=cuda, dtype=torch.int32).to(torch.int16)[1:]
+    yu = torch.full((n + 1,), -1, device=cuda, dtype=torch.int16)[1:]
+    capi.call("spline_hip_copy16", yu, xu, n)
+    torch.cuda.synchronize()
+    assert torch.equal(xu, yu)
