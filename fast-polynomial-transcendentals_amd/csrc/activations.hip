@@ -1,6 +1,7 @@
 // activations.hip -- C ABI of the unary activation programs and their
-// derivative programs (sigmoid, tanh, SiLU; FP16 and BF16; degrees 3..6,
-// native baselines and algebraic derivatives).
+// derivative programs (sigmoid, tanh, SiLU, GELU; FP16, BF16 and the BF16
+// Sollya coefficient set; degrees 3..6, native baselines and algebraic
+// derivatives).
 #include <hip/hip_runtime.h>
 
 #include "ops.hpp"
@@ -13,7 +14,7 @@ using namespace pt;
         return run1<UnaryOp<PT_STRIP PROG>>(out, in, size, stream);              \
     }
 
-#define PT_UNARY_FAMILY(fam, FAM)                                           \
+#define PT_UNARY_POLY(fam, FAM)                                             \
     PT_UNARY(launch_##fam##_fwd_d3_kernel, (F16Prog<FAM, kFwd, 3>))         \
     PT_UNARY(launch_##fam##_fwd_d4_kernel, (F16Prog<FAM, kFwd, 4>))         \
     PT_UNARY(launch_##fam##_fwd_d5_kernel, (F16Prog<FAM, kFwd, 5>))         \
@@ -21,13 +22,27 @@ using namespace pt;
     PT_UNARY(launch_##fam##_fwd_d3_kernel_bf16, (BF16Prog<FAM, kFwd, 3>))   \
     PT_UNARY(launch_##fam##_fwd_d4_kernel_bf16, (BF16Prog<FAM, kFwd, 4>))   \
     PT_UNARY(launch_##fam##_fwd_d5_kernel_bf16, (BF16Prog<FAM, kFwd, 5>))   \
-    PT_UNARY(launch_##fam##_fwd_d6_kernel_bf16, (BF16Prog<FAM, kFwd, 6>))   \
+    PT_UNARY(launch_##fam##_fwd_d6_kernel_bf16, (BF16Prog<FAM, kFwd, 6>))
+
+#define PT_UNARY_FAMILY(fam, FAM)                                           \
+    PT_UNARY_POLY(fam, FAM)                                                 \
     PT_UNARY(launch_##fam##_fwd_native_kernel, (F16Native<FAM, kFwd>))      \
     PT_UNARY(launch_##fam##_fwd_native_kernel_bf16, (BF16Native<FAM, kFwd>))
+
+// BF16 Sollya coefficient set (spline_kernels_bf16.cu:1146-1252)
+#define PT_UNARY_SOLLYA(fam, FAM)                                                          \
+    PT_UNARY(launch_##fam##_fwd_d3_kernel_bf16_sollya, (BF16Prog<FAM, kFwd, 3, kSollya>))  \
+    PT_UNARY(launch_##fam##_fwd_d4_kernel_bf16_sollya, (BF16Prog<FAM, kFwd, 4, kSollya>))  \
+    PT_UNARY(launch_##fam##_fwd_d5_kernel_bf16_sollya, (BF16Prog<FAM, kFwd, 5, kSollya>))  \
+    PT_UNARY(launch_##fam##_fwd_d6_kernel_bf16_sollya, (BF16Prog<FAM, kFwd, 6, kSollya>))
 
 PT_UNARY_FAMILY(sigmoid, kSigmoid)
 PT_UNARY_FAMILY(tanh, kTanh)
 PT_UNARY_FAMILY(swish, kSwishFam)
+PT_UNARY_POLY(gelu, kGelu)
+PT_UNARY_SOLLYA(sigmoid, kSigmoid)
+PT_UNARY_SOLLYA(swish, kSwishFam)
+PT_UNARY_SOLLYA(gelu, kGelu)
 
 #define PT_BINARY(name, OP)                                                                \
     extern "C" int name(void* grad_in, const void* grad_out, const void* in, int64_t size, \
@@ -45,9 +60,23 @@ PT_UNARY_FAMILY(swish, kSwishFam)
     PT_BINARY(launch_##fam##_bwd_d5_kernel_bf16, (BF16MulOp<BF16Prog<FAM, kBwd, 5>>)) \
     PT_BINARY(launch_##fam##_bwd_d6_kernel_bf16, (BF16MulOp<BF16Prog<FAM, kBwd, 6>>))
 
+#define PT_BINARY_SOLLYA(fam, FAM)                                                    \
+    PT_BINARY(launch_##fam##_bwd_d3_kernel_bf16_sollya,                               \
+              (BF16MulOp<BF16Prog<FAM, kBwd, 3, kSollya>>))                           \
+    PT_BINARY(launch_##fam##_bwd_d4_kernel_bf16_sollya,                               \
+              (BF16MulOp<BF16Prog<FAM, kBwd, 4, kSollya>>))                           \
+    PT_BINARY(launch_##fam##_bwd_d5_kernel_bf16_sollya,                               \
+              (BF16MulOp<BF16Prog<FAM, kBwd, 5, kSollya>>))                           \
+    PT_BINARY(launch_##fam##_bwd_d6_kernel_bf16_sollya,                               \
+              (BF16MulOp<BF16Prog<FAM, kBwd, 6, kSollya>>))
+
 PT_BINARY_FAMILY(sigmoid, kSigmoid)
 PT_BINARY_FAMILY(tanh, kTanh)
 PT_BINARY_FAMILY(swish, kSwishFam)
+PT_BINARY_FAMILY(gelu, kGelu)
+PT_BINARY_SOLLYA(sigmoid, kSigmoid)
+PT_BINARY_SOLLYA(swish, kSwishFam)
+PT_BINARY_SOLLYA(gelu, kGelu)
 PT_BINARY(launch_swish_bwd_native_kernel, (F16MulOp<F16Native<kSwishFam, kBwd>>))
 PT_BINARY(launch_swish_bwd_native_kernel_bf16, (BF16MulOp<BF16Native<kSwishFam, kBwd>>))
 PT_BINARY(launch_sigmoid_bwd_alg_kernel, (F16MulOp<F16Alg<kSigmoid>>))

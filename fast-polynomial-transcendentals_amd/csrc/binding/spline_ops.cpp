@@ -76,78 +76,48 @@ using SwishMulBwd = int (*)(void*, void*, const void*, const void*, const void*,
 using PackedFwd = int (*)(void*, const void*, int64_t, int64_t, void*);
 using PackedBwd = int (*)(void*, const void*, const void*, int64_t, int64_t, void*);
 
-enum Fam { SIGMOID = 0, TANH = 1, SWISH = 2 };
-const char* kFamName[] = {"sigmoid", "tanh", "swish"};
+enum Fam { SIGMOID = 0, TANH = 1, SWISH = 2, GELU = 3 };
+const char* kFamName[] = {"sigmoid", "tanh", "swish", "GeLU"};
 
-// [family][bf16][degree]; degree 0 = native.
-Unary kFwd[3][2][7] = {
-    {{launch_sigmoid_fwd_native_kernel, nullptr, nullptr, launch_sigmoid_fwd_d3_kernel,
-      launch_sigmoid_fwd_d4_kernel, launch_sigmoid_fwd_d5_kernel, launch_sigmoid_fwd_d6_kernel},
-     {launch_sigmoid_fwd_native_kernel_bf16, nullptr, nullptr, launch_sigmoid_fwd_d3_kernel_bf16,
-      launch_sigmoid_fwd_d4_kernel_bf16, launch_sigmoid_fwd_d5_kernel_bf16,
-      launch_sigmoid_fwd_d6_kernel_bf16}},
-    {{launch_tanh_fwd_native_kernel, nullptr, nullptr, launch_tanh_fwd_d3_kernel,
-      launch_tanh_fwd_d4_kernel, launch_tanh_fwd_d5_kernel, launch_tanh_fwd_d6_kernel},
-     {launch_tanh_fwd_native_kernel_bf16, nullptr, nullptr, launch_tanh_fwd_d3_kernel_bf16,
-      launch_tanh_fwd_d4_kernel_bf16, launch_tanh_fwd_d5_kernel_bf16,
-      launch_tanh_fwd_d6_kernel_bf16}},
-    {{launch_swish_fwd_native_kernel, nullptr, nullptr, launch_swish_fwd_d3_kernel,
-      launch_swish_fwd_d4_kernel, launch_swish_fwd_d5_kernel, launch_swish_fwd_d6_kernel},
-     {launch_swish_fwd_native_kernel_bf16, nullptr, nullptr, launch_swish_fwd_d3_kernel_bf16,
-      launch_swish_fwd_d4_kernel_bf16, launch_swish_fwd_d5_kernel_bf16,
-      launch_swish_fwd_d6_kernel_bf16}},
+// Columns of every table: 0 = FP16, 1 = BF16 (coeff_source current),
+// 2 = BF16 Sollya coefficient set.  Rows: degree, 0 = native.
+#define PT_POLY(n, sfx)                                                        \
+    nullptr, nullptr, launch_##n##_d3_kernel##sfx, launch_##n##_d4_kernel##sfx, \
+        launch_##n##_d5_kernel##sfx, launch_##n##_d6_kernel##sfx
+#define PT_ROW(n, sfx) {nullptr, PT_POLY(n, sfx)}
+#define PT_ROW_NATIVE(n, sfx) {launch_##n##_native_kernel##sfx, PT_POLY(n, sfx)}
+#define PT_NONE {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr}
+
+// [family][column][degree]
+Unary kFwd[4][3][7] = {
+    {PT_ROW_NATIVE(sigmoid_fwd, ), PT_ROW_NATIVE(sigmoid_fwd, _bf16), PT_ROW(sigmoid_fwd, _bf16_sollya)},
+    {PT_ROW_NATIVE(tanh_fwd, ), PT_ROW_NATIVE(tanh_fwd, _bf16), PT_NONE},
+    {PT_ROW_NATIVE(swish_fwd, ), PT_ROW_NATIVE(swish_fwd, _bf16), PT_ROW(swish_fwd, _bf16_sollya)},
+    {PT_ROW(gelu_fwd, ), PT_ROW(gelu_fwd, _bf16), PT_ROW(gelu_fwd, _bf16_sollya)},
 };
 
-Binary kBwd[3][2][7] = {
-    {{nullptr, nullptr, nullptr, launch_sigmoid_bwd_d3_kernel, launch_sigmoid_bwd_d4_kernel,
-      launch_sigmoid_bwd_d5_kernel, launch_sigmoid_bwd_d6_kernel},
-     {nullptr, nullptr, nullptr, launch_sigmoid_bwd_d3_kernel_bf16,
-      launch_sigmoid_bwd_d4_kernel_bf16, launch_sigmoid_bwd_d5_kernel_bf16,
-      launch_sigmoid_bwd_d6_kernel_bf16}},
-    {{nullptr, nullptr, nullptr, launch_tanh_bwd_d3_kernel, launch_tanh_bwd_d4_kernel,
-      launch_tanh_bwd_d5_kernel, launch_tanh_bwd_d6_kernel},
-     {nullptr, nullptr, nullptr, launch_tanh_bwd_d3_kernel_bf16, launch_tanh_bwd_d4_kernel_bf16,
-      launch_tanh_bwd_d5_kernel_bf16, launch_tanh_bwd_d6_kernel_bf16}},
-    {{launch_swish_bwd_native_kernel, nullptr, nullptr, launch_swish_bwd_d3_kernel,
-      launch_swish_bwd_d4_kernel, launch_swish_bwd_d5_kernel, launch_swish_bwd_d6_kernel},
-     {launch_swish_bwd_native_kernel_bf16, nullptr, nullptr, launch_swish_bwd_d3_kernel_bf16,
-      launch_swish_bwd_d4_kernel_bf16, launch_swish_bwd_d5_kernel_bf16,
-      launch_swish_bwd_d6_kernel_bf16}},
+Binary kBwd[4][3][7] = {
+    {PT_ROW(sigmoid_bwd, ), PT_ROW(sigmoid_bwd, _bf16), PT_ROW(sigmoid_bwd, _bf16_sollya)},
+    {PT_ROW(tanh_bwd, ), PT_ROW(tanh_bwd, _bf16), PT_NONE},
+    {PT_ROW_NATIVE(swish_bwd, ), PT_ROW_NATIVE(swish_bwd, _bf16), PT_ROW(swish_bwd, _bf16_sollya)},
+    {PT_ROW(gelu_bwd, ), PT_ROW(gelu_bwd, _bf16), PT_ROW(gelu_bwd, _bf16_sollya)},
 };
 
-Binary kSwishMul[2][7] = {
-    {launch_swish_mul_fwd_native_kernel, nullptr, nullptr, launch_swish_mul_fwd_d3_kernel,
-     launch_swish_mul_fwd_d4_kernel, launch_swish_mul_fwd_d5_kernel, launch_swish_mul_fwd_d6_kernel},
-    {launch_swish_mul_fwd_native_kernel_bf16, nullptr, nullptr,
-     launch_swish_mul_fwd_d3_kernel_bf16, launch_swish_mul_fwd_d4_kernel_bf16,
-     launch_swish_mul_fwd_d5_kernel_bf16, launch_swish_mul_fwd_d6_kernel_bf16},
-};
-
-SwishMulBwd kSwishMulBwd[2][7] = {
-    {launch_swish_mul_bwd_native_kernel, nullptr, nullptr, launch_swish_mul_bwd_d3_kernel,
-     launch_swish_mul_bwd_d4_kernel, launch_swish_mul_bwd_d5_kernel, launch_swish_mul_bwd_d6_kernel},
-    {launch_swish_mul_bwd_native_kernel_bf16, nullptr, nullptr,
-     launch_swish_mul_bwd_d3_kernel_bf16, launch_swish_mul_bwd_d4_kernel_bf16,
-     launch_swish_mul_bwd_d5_kernel_bf16, launch_swish_mul_bwd_d6_kernel_bf16},
-};
-
-PackedFwd kPackedFwd[2][7] = {
-    {launch_swish_mul_packed_fwd_native_kernel, nullptr, nullptr,
-     launch_swish_mul_packed_fwd_d3_kernel, launch_swish_mul_packed_fwd_d4_kernel,
-     launch_swish_mul_packed_fwd_d5_kernel, launch_swish_mul_packed_fwd_d6_kernel},
-    {launch_swish_mul_packed_fwd_native_kernel_bf16, nullptr, nullptr,
-     launch_swish_mul_packed_fwd_d3_kernel_bf16, launch_swish_mul_packed_fwd_d4_kernel_bf16,
-     launch_swish_mul_packed_fwd_d5_kernel_bf16, launch_swish_mul_packed_fwd_d6_kernel_bf16},
-};
-
-PackedBwd kPackedBwd[2][7] = {
-    {launch_swish_mul_packed_bwd_native_kernel, nullptr, nullptr,
-     launch_swish_mul_packed_bwd_d3_kernel, launch_swish_mul_packed_bwd_d4_kernel,
-     launch_swish_mul_packed_bwd_d5_kernel, launch_swish_mul_packed_bwd_d6_kernel},
-    {launch_swish_mul_packed_bwd_native_kernel_bf16, nullptr, nullptr,
-     launch_swish_mul_packed_bwd_d3_kernel_bf16, launch_swish_mul_packed_bwd_d4_kernel_bf16,
-     launch_swish_mul_packed_bwd_d5_kernel_bf16, launch_swish_mul_packed_bwd_d6_kernel_bf16},
-};
+Binary kSwishMul[3][7] = {PT_ROW_NATIVE(swish_mul_fwd, ), PT_ROW_NATIVE(swish_mul_fwd, _bf16),
+                          PT_ROW(swish_mul_fwd, _bf16_sollya)};
+SwishMulBwd kSwishMulBwd[3][7] = {PT_ROW_NATIVE(swish_mul_bwd, ),
+                                  PT_ROW_NATIVE(swish_mul_bwd, _bf16),
+                                  PT_ROW(swish_mul_bwd, _bf16_sollya)};
+PackedFwd kPackedFwd[3][7] = {PT_ROW_NATIVE(swish_mul_packed_fwd, ),
+                              PT_ROW_NATIVE(swish_mul_packed_fwd, _bf16),
+                              PT_ROW(swish_mul_packed_fwd, _bf16_sollya)};
+PackedBwd kPackedBwd[3][7] = {PT_ROW_NATIVE(swish_mul_packed_bwd, ),
+                              PT_ROW_NATIVE(swish_mul_packed_bwd, _bf16),
+                              PT_ROW(swish_mul_packed_bwd, _bf16_sollya)};
+#undef PT_POLY
+#undef PT_ROW
+#undef PT_ROW_NATIVE
+#undef PT_NONE
 
 // spline_ops.cpp:1179-1185
 int normalize_coeff_source_id(int64_t coeff_source_id) {
@@ -157,22 +127,22 @@ int normalize_coeff_source_id(int64_t coeff_source_id) {
 }
 
 // Resolution rules of resolve_*_launcher (spline_ops.cpp:1187-1502): FP16
-// accepts only the current coefficient source; degree 0 (native) exists for
-// the SiLU family only.  The Sollya BF16 coefficient set is not part of this
-// library.
+// accepts only the current coefficient source; BF16 takes the current or the
+// Sollya set; degree 0 (native) exists for the SiLU family's current set only.
 template <class T>
-T resolve(T (&table)[2][7], at::ScalarType dtype, int64_t degree, int coeff_source,
+T resolve(T (&table)[3][7], at::ScalarType dtype, int64_t degree, int coeff_source,
           const char* what, bool allow_native) {
     const bool bf = dtype == at::kBFloat16;
     if (!bf) {
         TORCH_CHECK(coeff_source == 0, "FP16 spline kernels only support coeff_source=current");
     }
-    TORCH_CHECK(coeff_source == 0,
-                "coeff_source=sollya (BF16 Sollya coefficient set) is not available in the "
-                "MI355X spline_ops build");
+    const int col = bf ? 1 + coeff_source : 0;
+    bool any = false;
+    for (T fn : table[col]) any = any || fn != nullptr;
+    TORCH_CHECK(any, "coeff_source=sollya has no ", what, " programs");
     const bool ok = (degree >= 3 && degree <= 6) || (degree == 0 && allow_native);
-    TORCH_CHECK(ok && table[bf][degree] != nullptr, "Unsupported ", what, " degree: ", degree);
-    return table[bf][degree];
+    TORCH_CHECK(ok && table[col][degree] != nullptr, "Unsupported ", what, " degree: ", degree);
+    return table[col][degree];
 }
 
 at::ScalarType check_same(const at::Tensor& a, const at::Tensor& b, const char* msg_dtype,
@@ -591,6 +561,30 @@ struct SwishMulVariantFwd : public torch::autograd::Function<SwishMulVariantFwd>
     }
 };
 
+// GeLU: forward and derivative programs of one degree and source
+// (SplineGeLUVariantFwd, spline_ops.cpp:2132-2180).
+struct GeluVariantFwd : public torch::autograd::Function<GeluVariantFwd> {
+    static at::Tensor forward(AutogradContext* ctx, at::Tensor x, int64_t degree,
+                              int64_t coeff_source_id) {
+        const int source = normalize_coeff_source_id(coeff_source_id);
+        at::Tensor out = fwd_variant(x, degree, source, GELU);
+        ctx->save_for_backward({x});
+        ctx->saved_data["degree"] = degree;
+        ctx->saved_data["coeff_source_id"] = static_cast<int64_t>(source);
+        return out;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        at::Tensor x = ctx->get_saved_variables()[0];
+        at::Tensor go = grads[0].contiguous();
+        at::Tensor gi = bwd_variant(go, x, ctx->saved_data["degree"].toInt(),
+                                    ctx->saved_data["coeff_source_id"].toInt(), GELU);
+        return {gi, at::Tensor(), at::Tensor()};
+    }
+};
+
+at::Tensor gelu_fwd_variant_autograd(at::Tensor x, int64_t degree, int64_t coeff_source_id) {
+    return GeluVariantFwd::apply(x, degree, coeff_source_id);
+}
 at::Tensor sigmoid_fwd_autograd(at::Tensor x) { return AlgebraicFwd<SIGMOID>::apply(x); }
 at::Tensor tanh_fwd_autograd(at::Tensor x) { return AlgebraicFwd<TANH>::apply(x); }
 at::Tensor swish_fwd_autograd(at::Tensor x) { return SwishVariantFwd::apply(x, 3, 4, 0); }
@@ -714,8 +708,26 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     PT_DEF_BWD(swish, SWISH, 4, "swish_bwd_d4");
     PT_DEF_BWD(swish, SWISH, 5, "swish_bwd_d5");
     PT_DEF_BWD(swish, SWISH, 6, "swish_bwd_d6");
+    PT_DEF_FWD(GeLU, GELU, 5, "gelu_fwd");
+    PT_DEF_FWD(GeLU, GELU, 3, "gelu_fwd_d3");
+    PT_DEF_FWD(GeLU, GELU, 4, "gelu_fwd_d4");
+    PT_DEF_FWD(GeLU, GELU, 5, "gelu_fwd_d5");
+    PT_DEF_FWD(GeLU, GELU, 6, "gelu_fwd_d6");
+    PT_DEF_BWD(GeLU, GELU, 5, "gelu_bwd");
+    PT_DEF_BWD(GeLU, GELU, 3, "gelu_bwd_d3");
+    PT_DEF_BWD(GeLU, GELU, 4, "gelu_bwd_d4");
+    PT_DEF_BWD(GeLU, GELU, 5, "gelu_bwd_d5");
+    PT_DEF_BWD(GeLU, GELU, 6, "gelu_bwd_d6");
 #undef PT_DEF_FWD
 #undef PT_DEF_BWD
+    m.def("gelu_fwd_variant",
+          [](at::Tensor x, int64_t d, int64_t c) { return fwd_variant(x, d, c, GELU); },
+          "GeLU FWD variant by degree/source");
+    m.def("gelu_bwd_variant",
+          [](at::Tensor go, at::Tensor x, int64_t d, int64_t c) { return bwd_variant(go, x, d, c, GELU); },
+          "GeLU BWD variant by degree/source");
+    m.def("gelu_ag_variant", &gelu_fwd_variant_autograd,
+          "GeLU variant with C++ autograd by degree/source");
 
     m.def("sigmoid_fwd_variant",
           [](at::Tensor x, int64_t d, int64_t c) { return fwd_variant(x, d, c, SIGMOID); },

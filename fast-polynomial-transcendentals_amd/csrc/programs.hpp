@@ -101,7 +101,8 @@ enum Shape : int {
     kOddMin1 = 2,   // sign(x) * min(t*H(t), 1)
     kSwish = 3,     // fma(|x|, t*H(t), 0.5*x)
     kEven = 4,      // c0 + t*(c1 + t*(...))
-    kXTimes = 5,    // x * (sigmoid program `inner`)(x)
+    kXTimes = 5,    // x * (sigmoid program of the same degree and source)(x)
+    kXHalfOdd = 6,  // x * (0.5 + sign(x) * t*H(t))   (GELU forward)
 };
 
 struct Prog {
@@ -112,11 +113,12 @@ struct Prog {
     int inner;
 };
 
-enum Family : int { kSigmoid = 0, kTanh = 1, kSwishFam = 2 };
+enum Family : int { kSigmoid = 0, kTanh = 1, kSwishFam = 2, kGelu = 3 };
+enum Source : int { kCurrent = 0, kSollya = 1 };  // coeff_source_id
 enum Dir : int { kFwd = 0, kBwd = 1 };
 
 // [family][dir][degree-3]
-constexpr Prog kF16Progs[3][2][4] = {
+constexpr Prog kF16Progs[4][2][4] = {
     {   // SIGMOID
         {   // spline_structs_odd.cuh:14-127  SIGMOID_FWD_D{3..6}_ODD
             {kHalfOdd, 6.25f, 3, {0.f, 0.2812500000f, -0.0534362793f, 0.0033779144f}, 0},
@@ -159,9 +161,23 @@ constexpr Prog kF16Progs[3][2][4] = {
             {kHalfOdd, 5.75f, 6, {0.f, 0.5415039062f, -0.0898437500f, -0.0439147949f, 0.0179443359f, -0.0023403168f, 0.0001055002f}, 0},
         },
     },
+    {   // GELU
+        {   // :801-920  GELU_FWD_D{3..6}_ODD: x * (0.5 + sign * t*H(t))
+            {kXHalfOdd, 3.0f, 3, {0.f, 0.4592285156f, -0.1364746094f, 0.0131378174f}, 0},
+            {kXHalfOdd, 3.0f, 4, {0.f, 0.4208984375f, -0.0592346191f, -0.0298614502f, 0.0071029663f}, 0},
+            {kXHalfOdd, 3.0f, 5, {0.f, 0.3962402344f, 0.0178222656f, -0.1052856445f, 0.0362548828f, -0.0038852692f}, 0},
+            {kXHalfOdd, 3.0f, 6, {0.f, 0.3935546875f, 0.0309448242f, -0.1257324219f, 0.0500793457f, -0.0081100464f, 0.0004782677f}, 0},
+        },
+        {   // :922-1032  GELU_BWD_D{3..6}_ODD
+            {kHalfOdd, 3.0f, 3, {0.f, 0.9707031250f, -0.4719238281f, 0.0680541992f}, 0},
+            {kHalfOdd, 3.0f, 4, {0.f, 0.9306640625f, -0.3867187500f, 0.0167694092f, 0.0092239380f}, 0},
+            {kHalfOdd, 3.0f, 5, {0.f, 0.8706054688f, -0.2055664062f, -0.1563720703f, 0.0755004883f, -0.0088424683f}, 0},
+            {kHalfOdd, 3.0f, 6, {0.f, 0.8125000000f, 0.0046691895f, -0.4064941406f, 0.2064208984f, -0.0401306152f, 0.0027942657f}, 0},
+        },
+    },
 };
 
-constexpr Prog kBF16Progs[3][2][4] = {
+constexpr Prog kBF16Progs[4][2][4] = {
     {   // SIGMOID
         {   // spline_structs_odd_bf16.cuh:11-121  SIGMOID_FWD_D{3..6}_ODD_BF16
             {kHalfOdd, 6.0f, 3, {0.f, 0.2810058594f, -0.0533447266f, 0.0033893585f}, 0},
@@ -204,6 +220,83 @@ constexpr Prog kBF16Progs[3][2][4] = {
             {kHalfOdd, 5.0f, 6, {0.f, 0.6015625000f, -0.2050781250f, 0.0260009766f, -0.0004787445f, -0.0001363754f, 0.0000074804f}, 0},
         },
     },
+    {   // GELU
+        {   // :740-858  GELU_FWD_D{3..6}_ODD_BF16
+            {kXHalfOdd, 3.0f, 3, {0.f, 0.4592285156f, -0.1364746094f, 0.0131378174f}, 0},
+            {kXHalfOdd, 3.0f, 4, {0.f, 0.4208984375f, -0.0592346191f, -0.0298614502f, 0.0071029663f}, 0},
+            {kXHalfOdd, 3.0f, 5, {0.f, 0.3962402344f, 0.0178222656f, -0.1052856445f, 0.0362548828f, -0.0038852692f}, 0},
+            {kXHalfOdd, 3.0f, 6, {0.f, 0.3935546875f, 0.0309448242f, -0.1257324219f, 0.0500793457f, -0.0081100464f, 0.0004782677f}, 0},
+        },
+        {   // :861-970  GELU_BWD_D{3..6}_ODD_BF16
+            {kHalfOdd, 3.0f, 3, {0.f, 0.9707031250f, -0.4719238281f, 0.0680541992f}, 0},
+            {kHalfOdd, 3.0f, 4, {0.f, 0.9306640625f, -0.3867187500f, 0.0167694092f, 0.0092239380f}, 0},
+            {kHalfOdd, 3.0f, 5, {0.f, 0.8706054688f, -0.2055664062f, -0.1563720703f, 0.0755004883f, -0.0088424683f}, 0},
+            {kHalfOdd, 3.0f, 6, {0.f, 0.8125000000f, 0.0046691895f, -0.4064941406f, 0.2064208984f, -0.0401306152f, 0.0027942657f}, 0},
+        },
+    },
+};
+
+// BF16 Sollya fpminimax coefficient set (coeff_source_id 1), same clamps and
+// evaluation shapes: autonumerics_zero/spline_ops/spline_structs_sollya_bf16.cuh.
+// The reference exports no launcher for the tanh rows; they are kept so the
+// table has the layout of the current set.
+constexpr Prog kBF16SollyaProgs[4][2][4] = {
+    {   // SIGMOID
+        {   // :14-131  SIGMOID_FWD_D{3..6}_ODD_SOLLYA_BF16
+            {kHalfOdd, 6.0f, 3, {0.f, 0.2812500000f, -0.0534667969f, 0.0033874512f}, 0},
+            {kHalfOdd, 5.28125f, 4, {0.f, 0.2695312500f, -0.0380859375f, -0.0020904541f, 0.0005722046f}, 0},
+            {kHalfOdd, 5.40625f, 5, {0.f, 0.2558593750f, -0.0115356445f, -0.0179443359f, 0.0042724609f, -0.0002956390f}, 0},
+            {kHalfOdd, 4.90625f, 6, {0.f, 0.2490234375f, 0.0062561035f, -0.0327148438f, 0.0095825195f, -0.0011596680f, 0.0000522137f}, 0},
+        },
+        {   // :258-360  SIGMOID_BWD_D{3..6}_EVEN_SOLLYA_BF16
+            {kEven, 4.0f, 3, {0.2558593750f, -0.0385742188f, -0.0292968750f, 0.0061035156f}, 0},
+            {kEven, 4.75f, 4, {0.2519531250f, -0.0089721680f, -0.0668945312f, 0.0213623047f, -0.0019302368f}, 0},
+            {kEven, 4.75f, 5, {0.2490234375f, 0.0139770508f, -0.1015625000f, 0.0407714844f, -0.0064697266f, 0.0003757477f}, 0},
+            {kEven, 4.25f, 6, {0.2500000000f, 0.0023956299f, -0.0742187500f, 0.0156250000f, 0.0042724609f, -0.0017700195f, 0.0001621246f}, 0},
+        },
+    },
+    {   // TANH
+        {   // :134-256  TANH_FWD_D{3..6}_ODD_SOLLYA_BF16 (with min(h, 1))
+            {kOddMin1, 2.75f, 3, {0.f, 1.1171875000f, -0.4160156250f, 0.0505371094f}, 0},
+            {kOddMin1, 2.75f, 4, {0.f, 1.0859375000f, -0.3281250000f, -0.0150146484f, 0.0140991211f}, 0},
+            {kOddMin1, 2.25f, 5, {0.f, 1.0078125000f, -0.0157470703f, -0.3964843750f, 0.1962890625f, -0.0299072266f}, 0},
+            {kOddMin1, 2.25f, 6, {0.f, 1.0000000000f, 0.0214843750f, -0.4570312500f, 0.2402343750f, -0.0444335938f, 0.0017700195f}, 0},
+        },
+        {   // :362-464  TANH_BWD_D{3..6}_EVEN_SOLLYA_BF16
+            {kEven, 2.0f, 3, {1.0234375000f, -0.3085937500f, -0.4687500000f, 0.1953125000f}, 0},
+            {kEven, 2.25f, 4, {1.0078125000f, -0.0600585938f, -1.1093750000f, 0.7187500000f, -0.1328125000f}, 0},
+            {kEven, 2.25f, 5, {0.9960937500f, 0.1005859375f, -1.5703125000f, 1.2265625000f, -0.3710937500f, 0.0400390625f}, 0},
+            {kEven, 2.25f, 6, {1.0000000000f, 0.0312500000f, -1.2578125000f, 0.6484375000f, 0.1289062500f, -0.1611328125f, 0.0303955078f}, 0},
+        },
+    },
+    {   // SWISH
+        {   // :830-852  SWISH_FWD_D{3..6}_ODD_SOLLYA_BF16 = x * Sollya sigmoid
+            {kXTimes, 0.f, 3, {0.f}, 0},
+            {kXTimes, 0.f, 4, {0.f}, 0},
+            {kXTimes, 0.f, 5, {0.f}, 0},
+            {kXTimes, 0.f, 6, {0.f}, 0},
+        },
+        {   // :466-584  SWISH_BWD_D{3..6}_ODD_SOLLYA_BF16
+            {kHalfOdd, 4.75f, 3, {0.f, 0.5781250000f, -0.1738281250f, 0.0158691406f}, 0},
+            {kHalfOdd, 5.25f, 4, {0.f, 0.5820312500f, -0.1777343750f, 0.0172119141f, -0.0001506805f}, 0},
+            {kHalfOdd, 4.75f, 5, {0.f, 0.5234375000f, -0.0537109375f, -0.0629882812f, 0.0200195312f, -0.0017318726f}, 0},
+            {kHalfOdd, 5.0f, 6, {0.f, 0.5039062500f, 0.0106201172f, -0.1289062500f, 0.0490722656f, -0.0075073242f, 0.0004253387f}, 0},
+        },
+    },
+    {   // GELU
+        {   // :586-708  GELU_FWD_D{3..6}_ODD_SOLLYA_BF16
+            {kXHalfOdd, 3.0f, 3, {0.f, 0.4726562500f, -0.1464843750f, 0.0147094727f}, 0},
+            {kXHalfOdd, 3.0f, 4, {0.f, 0.4414062500f, -0.0908203125f, -0.0148315430f, 0.0048522949f}, 0},
+            {kXHalfOdd, 3.0f, 5, {0.f, 0.4003906250f, 0.0086059570f, -0.0981445312f, 0.0339355469f, -0.0036163330f}, 0},
+            {kXHalfOdd, 3.0f, 6, {0.f, 0.3906250000f, 0.0393066406f, -0.1337890625f, 0.0534667969f, -0.0087280273f, 0.0005149841f}, 0},
+        },
+        {   // :710-828  GELU_BWD_D{3..6}_ODD_SOLLYA_BF16
+            {kHalfOdd, 3.0f, 3, {0.f, 0.9648437500f, -0.4628906250f, 0.0654296875f}, 0},
+            {kHalfOdd, 3.0f, 4, {0.f, 0.9140625000f, -0.3476562500f, -0.0084228516f, 0.0140380859f}, 0},
+            {kHalfOdd, 3.0f, 5, {0.f, 0.8046875000f, 0.0143432617f, -0.3789062500f, 0.1630859375f, -0.0206298828f}, 0},
+            {kHalfOdd, 3.0f, 6, {0.f, 0.7812500000f, 0.1166992188f, -0.5312500000f, 0.2636718750f, -0.0510253906f, 0.0034332275f}, 0},
+        },
+    },
 };
 
 // ---------------------------------------------------------------------------
@@ -234,6 +327,9 @@ struct F16Prog {
             if constexpr (P.shape == kHalfOdd) {
                 const h2_t hs = as_h2(as_u32(h) ^ (x & 0x80008000u));
                 return as_u32(k(0.5f) + hs);
+            } else if constexpr (P.shape == kXHalfOdd) {
+                const h2_t hs = as_h2(as_u32(h) ^ (x & 0x80008000u));
+                return as_u32(as_h2(x) * (k(0.5f) + hs));
             } else if constexpr (P.shape == kOdd) {
                 return as_u32(h) ^ (x & 0x80008000u);
             } else {  // kSwish
@@ -256,9 +352,10 @@ __device__ __forceinline__ float bfma(float a, float b, float c) { return rbf(__
 // lanes from eval2.  Rounding the open value is the program's last rounded
 // step because RNE is odd-symmetric (rbf(v ^ sign) = rbf(v) ^ sign) and
 // monotone with 1.0 representable (rbf(min(v, 1)) = min(rbf(v), 1)).
-template <int F, int D, int G>
+template <int F, int D, int G, int S = kCurrent>
 struct BF16Prog {
-    static constexpr Prog P = kBF16Progs[F][D][G - 3];
+    static constexpr Prog P = S == kSollya ? kBF16SollyaProgs[F][D][G - 3]
+                                           : kBF16Progs[F][D][G - 3];
 
     // H(t) of the odd shapes (every step rounded); t is the clamped magnitude.
     __device__ __forceinline__ static float odd_horner(float t) {
@@ -288,7 +385,7 @@ struct BF16Prog {
             // sign * min(t*H(t), 1) = clamp(v, -1, 1); v is finite.
             return __builtin_amdgcn_fmed3f(v, -1.0f, 1.0f);
         } else {
-            static_assert(P.shape == kHalfOdd, "unsupported BF16 shape");
+            static_assert(P.shape == kHalfOdd || P.shape == kXHalfOdd, "unsupported BF16 shape");
             return bf16_value(0.5f) + rbf(v);
         }
     }
@@ -297,7 +394,7 @@ struct BF16Prog {
     __device__ __forceinline__ static void open2(uint32_t x, float& lo, float& hi) {
         if constexpr (P.shape == kXTimes) {
             float s_lo, s_hi;
-            BF16Prog<kSigmoid, kFwd, G>::eval2(x, s_lo, s_hi);
+            BF16Prog<kSigmoid, kFwd, G, S>::eval2(x, s_lo, s_hi);
             lo = bf_lo(x) * s_lo;
             hi = bf_hi(x) * s_hi;
         } else if constexpr (P.shape == kSwish) {
@@ -321,6 +418,11 @@ struct BF16Prog {
                 const uint32_t ts = t2 | (x & 0x80008000u);
                 lo = odd_signed_open(bf_lo(ts));
                 hi = odd_signed_open(bf_hi(ts));
+                if constexpr (P.shape == kXHalfOdd) {
+                    // GELU: x * phi with phi = bf16(0.5 + sign * t*H(t))
+                    lo = bf_lo(x) * rbf(lo);
+                    hi = bf_hi(x) * rbf(hi);
+                }
             }
         }
     }

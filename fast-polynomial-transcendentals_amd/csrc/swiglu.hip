@@ -172,6 +172,13 @@ PT_SWISH_MUL(launch_swish_mul_fwd_d4_kernel_bf16, PT_BF16_SM(4))
 PT_SWISH_MUL(launch_swish_mul_fwd_d5_kernel_bf16, PT_BF16_SM(5))
 PT_SWISH_MUL(launch_swish_mul_fwd_d6_kernel_bf16, PT_BF16_SM(6))
 
+// BF16 Sollya coefficient set (spline_kernels_bf16.cu:1174-1199)
+#define PT_BF16_SM_S(G) (BF16SwishMulOp<BF16Prog<kSwishFam, kFwd, G, kSollya>>)
+PT_SWISH_MUL(launch_swish_mul_fwd_d3_kernel_bf16_sollya, PT_BF16_SM_S(3))
+PT_SWISH_MUL(launch_swish_mul_fwd_d4_kernel_bf16_sollya, PT_BF16_SM_S(4))
+PT_SWISH_MUL(launch_swish_mul_fwd_d5_kernel_bf16_sollya, PT_BF16_SM_S(5))
+PT_SWISH_MUL(launch_swish_mul_fwd_d6_kernel_bf16_sollya, PT_BF16_SM_S(6))
+
 #define PT_SWISH_MUL_BWD(name, OP)                                                          \
     extern "C" int name(void* grad_gate, void* grad_up, const void* grad_out,               \
                         const void* gate, const void* up, int64_t size, void* stream) {     \
@@ -193,6 +200,16 @@ PT_SWISH_MUL_BWD(launch_swish_mul_bwd_d4_kernel_bf16, PT_BF16_SMB(4))
 PT_SWISH_MUL_BWD(launch_swish_mul_bwd_d5_kernel_bf16, PT_BF16_SMB(5))
 PT_SWISH_MUL_BWD(launch_swish_mul_bwd_d6_kernel_bf16, PT_BF16_SMB(6))
 
+// Sollya: the generic forward/backward program pair at every degree,
+// D3 included (spline_kernels_bf16.cu:1187-1198).
+#define PT_BF16_SMB_S(G)                                            \
+    (BF16SwishMulBwdOp<BF16Prog<kSwishFam, kFwd, G, kSollya>,       \
+                       BF16Prog<kSwishFam, kBwd, G, kSollya>>)
+PT_SWISH_MUL_BWD(launch_swish_mul_bwd_d3_kernel_bf16_sollya, PT_BF16_SMB_S(3))
+PT_SWISH_MUL_BWD(launch_swish_mul_bwd_d4_kernel_bf16_sollya, PT_BF16_SMB_S(4))
+PT_SWISH_MUL_BWD(launch_swish_mul_bwd_d5_kernel_bf16_sollya, PT_BF16_SMB_S(5))
+PT_SWISH_MUL_BWD(launch_swish_mul_bwd_d6_kernel_bf16_sollya, PT_BF16_SMB_S(6))
+
 // ---- packed [rows, 2H] layout ---------------------------------------------
 
 #define PT_PACKED_FWD(name, OP)                                                            \
@@ -212,6 +229,10 @@ PT_PACKED_FWD(launch_swish_mul_packed_fwd_d3_kernel_bf16, PT_BF16_SM(3))
 PT_PACKED_FWD(launch_swish_mul_packed_fwd_d4_kernel_bf16, PT_BF16_SM(4))
 PT_PACKED_FWD(launch_swish_mul_packed_fwd_d5_kernel_bf16, PT_BF16_SM(5))
 PT_PACKED_FWD(launch_swish_mul_packed_fwd_d6_kernel_bf16, PT_BF16_SM(6))
+PT_PACKED_FWD(launch_swish_mul_packed_fwd_d3_kernel_bf16_sollya, PT_BF16_SM_S(3))
+PT_PACKED_FWD(launch_swish_mul_packed_fwd_d4_kernel_bf16_sollya, PT_BF16_SM_S(4))
+PT_PACKED_FWD(launch_swish_mul_packed_fwd_d5_kernel_bf16_sollya, PT_BF16_SM_S(5))
+PT_PACKED_FWD(launch_swish_mul_packed_fwd_d6_kernel_bf16_sollya, PT_BF16_SM_S(6))
 
 #define PT_PACKED_BWD(name, OP)                                                               \
     extern "C" int name(void* grad_packed, const void* grad_out, const void* packed,          \
@@ -230,3 +251,7 @@ PT_PACKED_BWD(launch_swish_mul_packed_bwd_d3_kernel_bf16, (BF16SwishMulBwdD3AlgO
 PT_PACKED_BWD(launch_swish_mul_packed_bwd_d4_kernel_bf16, PT_BF16_SMB(4))
 PT_PACKED_BWD(launch_swish_mul_packed_bwd_d5_kernel_bf16, PT_BF16_SMB(5))
 PT_PACKED_BWD(launch_swish_mul_packed_bwd_d6_kernel_bf16, PT_BF16_SMB(6))
+PT_PACKED_BWD(launch_swish_mul_packed_bwd_d3_kernel_bf16_sollya, PT_BF16_SMB_S(3))
+PT_PACKED_BWD(launch_swish_mul_packed_bwd_d4_kernel_bf16_sollya, PT_BF16_SMB_S(4))
+PT_PACKED_BWD(launch_swish_mul_packed_bwd_d5_kernel_bf16_sollya, PT_BF16_SMB_S(5))
+PT_PACKED_BWD(launch_swish_mul_packed_bwd_d6_kernel_bf16_sollya, PT_BF16_SMB_S(6))

@@ -5,8 +5,8 @@ Same names, return values and errors as the reference's
 ``(implementation_name, callable)``; ``native_*`` names map to PyTorch's own
 functions, ``spline_silu`` calls the pybind functions directly (with C++
 autograd when gradients are needed) and ``spline_silu_compile`` goes through
-the ``spline_compile`` dispatcher ops.  GELU programs are not part of the
-MI355X build: ``spline_gelu*`` raise ``RuntimeError``.
+the ``spline_compile`` dispatcher ops; ``spline_gelu`` /
+``spline_gelu_compile`` do the same for the GeLU programs.
 """
 
 from __future__ import annotations
@@ -118,8 +118,19 @@ def _make_direct_spline_silu_mul(degree: int, coeff_source: str):
     return activation_mul
 
 
-def _no_gelu(*_args, **_kwargs):
-    raise RuntimeError("GELU polynomial programs are not part of the MI355X spline_ops build")
+def _make_direct_spline_gelu(degree: int, coeff_source: str):
+    """src/sfu_repro/activations.py:170-181"""
+    ops = load_spline_ops()
+    cid = _coeff_source_id(coeff_source)
+
+    def activation(x: torch.Tensor) -> torch.Tensor:
+        x = _contiguous(x)
+        if torch.is_grad_enabled() and x.requires_grad:
+            return ops.gelu_ag_variant(x, degree, cid)
+        return ops.gelu_fwd_variant(x, degree, cid)
+
+    activation.__name__ = f"spline_gelu_d{degree}_{coeff_source}_direct"
+    return activation
 
 
 def resolve_mlp_activation_impl(name: str, *, degree: int | None = None,
@@ -139,9 +150,16 @@ def resolve_mlp_activation_impl(name: str, *, degree: int | None = None,
         activation = (sc.spline_silu if degree is None and coeff_source == "current"
                       else sc.make_spline_silu(degree=d, coeff_source=coeff_source))
         return f"spline_silu_compile[d{d},{coeff_source}]", activation
-    if name in ("spline_gelu", "spline_gelu_compile"):
+    if name == "spline_gelu":
+        d = 5 if degree is None else int(degree)
+        return f"spline_gelu[d{d},{coeff_source}]", _make_direct_spline_gelu(d, coeff_source)
+    if name == "spline_gelu_compile":
         _ensure_coeff_source_allowed(coeff_source)
-        _no_gelu()
+        sc = _spline_compile()
+        d = 5 if degree is None else int(degree)
+        activation = (sc.spline_gelu if degree is None and coeff_source == "current"
+                      else sc.make_spline_gelu(degree=d, coeff_source=coeff_source))
+        return f"spline_gelu_compile[d{d},{coeff_source}]", activation
     raise ValueError(f"unknown activation {name!r}; expected one of "
                      + ", ".join(PUBLIC_MLP_ACTIVATIONS))
 

@@ -7,13 +7,10 @@ Same public surface as the reference module
   extension registers in C++ (``torch.ops.spline_ops.*``, reference :34-238);
 * opaque ``torch.library.custom_op`` wrappers ``spline_compile::*`` for the
   fixed-degree activations (reference :260-540);
-* the drop-in callables ``spline_silu``, ``spline_sigmoid``, ``spline_tanh``
-  and the factories ``make_spline_silu``, ``make_spline_silu_mul``,
-  ``make_spline_silu_packed``, ``make_native_silu_packed``
-  (reference :583-720).
-
-GELU is not part of the MI355X library; ``spline_gelu`` / ``make_spline_gelu``
-raise ``NotImplementedError``.
+* the drop-in callables ``spline_silu``, ``spline_sigmoid``, ``spline_tanh``,
+  ``spline_gelu`` and the factories ``make_spline_silu``,
+  ``make_spline_silu_mul``, ``make_spline_silu_packed``,
+  ``make_native_silu_packed``, ``make_spline_gelu`` (reference :583-720).
 """
 
 from __future__ import annotations
@@ -194,10 +191,34 @@ def _swish_mul_variant_bwd(grad_out: torch.Tensor, gate: torch.Tensor, up: torch
     return grad_gate, grad_up
 
 
-for _op in (_swish_fwd, _sigmoid_fwd, _tanh_fwd):
+@torch.library.custom_op("spline_compile::gelu_fwd", mutates_args=())
+def _gelu_fwd(x: torch.Tensor) -> torch.Tensor:
+    return _spline_ops.gelu_fwd(x)
+
+
+@torch.library.custom_op("spline_compile::gelu_bwd", mutates_args=())
+def _gelu_bwd(grad_out: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    return _spline_ops.gelu_bwd(grad_out, x)
+
+
+@torch.library.custom_op("spline_compile::gelu_variant_fwd", mutates_args=())
+def _gelu_variant_fwd(x: torch.Tensor, degree: int, coeff_source_id: int) -> torch.Tensor:
+    return _spline_ops.gelu_fwd_variant(x, degree, coeff_source_id)
+
+
+@torch.library.custom_op("spline_compile::gelu_variant_bwd", mutates_args=())
+def _gelu_variant_bwd(grad_out: torch.Tensor, x: torch.Tensor, degree: int,
+                      coeff_source_id: int) -> torch.Tensor:
+    return _spline_ops.gelu_bwd_variant(grad_out, x, degree, coeff_source_id)
+
+
+for _op in (_swish_fwd, _sigmoid_fwd, _tanh_fwd, _gelu_fwd):
     _op.register_fake(lambda x: torch.empty_like(x))
-for _op in (_swish_bwd, _sigmoid_bwd_alg, _tanh_bwd_alg):
+for _op in (_swish_bwd, _sigmoid_bwd_alg, _tanh_bwd_alg, _gelu_bwd):
     _op.register_fake(lambda grad_out, x: torch.empty_like(x))
+_gelu_variant_fwd.register_fake(lambda x, degree, coeff_source_id: torch.empty_like(x))
+_gelu_variant_bwd.register_fake(
+    lambda grad_out, x, degree, coeff_source_id: torch.empty_like(x))
 _swish_variant_fwd.register_fake(lambda x, degree, coeff_source_id: torch.empty_like(x))
 _swish_variant_bwd.register_fake(
     lambda grad_out, x, degree, coeff_source_id: torch.empty_like(x))
@@ -228,6 +249,13 @@ _tanh_fwd.register_autograd(
 _swish_variant_fwd.register_autograd(
     lambda ctx, g: (_swish_variant_bwd(g.contiguous(), ctx.saved_tensors[0], ctx.degree,
                                        ctx.coeff_source_id), None, None),
+    setup_context=_save_x_and_args)
+_gelu_fwd.register_autograd(
+    lambda ctx, g: _gelu_bwd(g.contiguous(), ctx.saved_tensors[0]),
+    setup_context=_setup_save_input)
+_gelu_variant_fwd.register_autograd(
+    lambda ctx, g: (_gelu_variant_bwd(g.contiguous(), ctx.saved_tensors[0], ctx.degree,
+                                      ctx.coeff_source_id), None, None),
     setup_context=_save_x_and_args)
 
 
@@ -277,11 +305,22 @@ def spline_tanh(x):
 
 
 def spline_gelu(x):
-    raise NotImplementedError("GELU programs are not part of the MI355X spline_ops build")
+    """Polynomial GeLU (D5 forward and derivative), torch.compile-compatible."""
+    return _gelu_fwd(x)
 
 
+@lru_cache(maxsize=None)
 def make_spline_gelu(degree: int | None = None, coeff_source: str = "current"):
-    raise NotImplementedError("GELU programs are not part of the MI355X spline_ops build")
+    resolved_degree = 5 if degree is None else int(degree)
+    coeff_source_id = _coeff_source_id(coeff_source)
+    if resolved_degree == 5 and coeff_source_id == 0:
+        return spline_gelu
+
+    def activation(x):
+        return _gelu_variant_fwd(x, resolved_degree, coeff_source_id)
+
+    activation.__name__ = f"spline_gelu_d{resolved_degree}_{coeff_source}"
+    return activation
 
 
 @lru_cache(maxsize=None)

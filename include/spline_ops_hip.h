@@ -55,7 +55,26 @@ extern "C" {
     X(launch_swish_fwd_d5_kernel_bf16) X(launch_swish_fwd_d6_kernel_bf16)      \
     X(launch_swish_fwd_native_kernel) X(launch_swish_fwd_native_kernel_bf16)   \
     X(launch_sigmoid_fwd_native_kernel) X(launch_sigmoid_fwd_native_kernel_bf16) \
-    X(launch_tanh_fwd_native_kernel) X(launch_tanh_fwd_native_kernel_bf16)
+    X(launch_tanh_fwd_native_kernel) X(launch_tanh_fwd_native_kernel_bf16)    \
+    X(launch_gelu_fwd_d3_kernel) X(launch_gelu_fwd_d4_kernel)                  \
+    X(launch_gelu_fwd_d5_kernel) X(launch_gelu_fwd_d6_kernel)                  \
+    X(launch_gelu_fwd_d3_kernel_bf16) X(launch_gelu_fwd_d4_kernel_bf16)        \
+    X(launch_gelu_fwd_d5_kernel_bf16) X(launch_gelu_fwd_d6_kernel_bf16)        \
+    SPLINE_HIP_UNARY_SOLLYA_LAUNCHERS(X)
+
+/* GELU (x * Phi(x) with Phi = 0.5 + sign * t*H(t)): replaces
+ * launch_gelu_fwd_d{3..6}_kernel{,_bf16} (spline_ops.cpp:129-132,266-269;
+ * spline_kernels.cu:1338-1350, spline_kernels_bf16.cu:1119-1131).
+ * BF16 Sollya coefficient set (coeff_source_id 1): replaces
+ * launch_{sigmoid,swish,gelu}_fwd_d{3..6}_kernel_bf16_sollya
+ * (spline_ops.cpp:180-183,256-259,276-279; spline_kernels_bf16.cu:1146-1239). */
+#define SPLINE_HIP_UNARY_SOLLYA_LAUNCHERS(X)                                   \
+    X(launch_sigmoid_fwd_d3_kernel_bf16_sollya) X(launch_sigmoid_fwd_d4_kernel_bf16_sollya) \
+    X(launch_sigmoid_fwd_d5_kernel_bf16_sollya) X(launch_sigmoid_fwd_d6_kernel_bf16_sollya) \
+    X(launch_swish_fwd_d3_kernel_bf16_sollya) X(launch_swish_fwd_d4_kernel_bf16_sollya) \
+    X(launch_swish_fwd_d5_kernel_bf16_sollya) X(launch_swish_fwd_d6_kernel_bf16_sollya) \
+    X(launch_gelu_fwd_d3_kernel_bf16_sollya) X(launch_gelu_fwd_d4_kernel_bf16_sollya) \
+    X(launch_gelu_fwd_d5_kernel_bf16_sollya) X(launch_gelu_fwd_d6_kernel_bf16_sollya)
 
 /* ---- derivative programs: grad_in = grad_out * F'(in) ------------------
  * Replaces launch_{sigmoid,tanh,swish}_bwd_d{3..6}_kernel{,_bf16}
@@ -78,52 +97,84 @@ extern "C" {
     X(launch_swish_bwd_d5_kernel_bf16) X(launch_swish_bwd_d6_kernel_bf16)      \
     X(launch_swish_bwd_native_kernel) X(launch_swish_bwd_native_kernel_bf16)   \
     X(launch_sigmoid_bwd_alg_kernel) X(launch_sigmoid_bwd_alg_kernel_bf16)     \
-    X(launch_tanh_bwd_alg_kernel) X(launch_tanh_bwd_alg_kernel_bf16)
+    X(launch_tanh_bwd_alg_kernel) X(launch_tanh_bwd_alg_kernel_bf16)         \
+    X(launch_gelu_bwd_d3_kernel) X(launch_gelu_bwd_d4_kernel)                  \
+    X(launch_gelu_bwd_d5_kernel) X(launch_gelu_bwd_d6_kernel)                  \
+    X(launch_gelu_bwd_d3_kernel_bf16) X(launch_gelu_bwd_d4_kernel_bf16)        \
+    X(launch_gelu_bwd_d5_kernel_bf16) X(launch_gelu_bwd_d6_kernel_bf16)        \
+    SPLINE_HIP_BINARY_SOLLYA_LAUNCHERS(X)
+
+/* GELU derivative: replaces launch_gelu_bwd_d{3..6}_kernel{,_bf16}
+ * (spline_ops.cpp:135-138,272-275; spline_kernels.cu:1352-1364,
+ * spline_kernels_bf16.cu:1133-1145).  Sollya set: replaces
+ * launch_{sigmoid,swish,gelu}_bwd_d{3..6}_kernel_bf16_sollya
+ * (spline_ops.cpp:190-193,260-263,280-283). */
+#define SPLINE_HIP_BINARY_SOLLYA_LAUNCHERS(X)                                  \
+    X(launch_sigmoid_bwd_d3_kernel_bf16_sollya) X(launch_sigmoid_bwd_d4_kernel_bf16_sollya) \
+    X(launch_sigmoid_bwd_d5_kernel_bf16_sollya) X(launch_sigmoid_bwd_d6_kernel_bf16_sollya) \
+    X(launch_swish_bwd_d3_kernel_bf16_sollya) X(launch_swish_bwd_d4_kernel_bf16_sollya) \
+    X(launch_swish_bwd_d5_kernel_bf16_sollya) X(launch_swish_bwd_d6_kernel_bf16_sollya) \
+    X(launch_gelu_bwd_d3_kernel_bf16_sollya) X(launch_gelu_bwd_d4_kernel_bf16_sollya) \
+    X(launch_gelu_bwd_d5_kernel_bf16_sollya) X(launch_gelu_bwd_d6_kernel_bf16_sollya)
 
 /* ---- SwiGLU: out = F(gate) * up ----------------------------------------
  * Replaces launch_swish_mul_fwd_{native,d3..d6}_kernel{,_bf16}
- * (spline_kernels.cu:1255-1268, spline_kernels_bf16.cu:1030-1044). */
+ * (spline_kernels.cu:1255-1268, spline_kernels_bf16.cu:1030-1044) and the
+ * Sollya set's launch_swish_mul_fwd_d{3..6}_kernel_bf16_sollya
+ * (spline_ops.cpp:218-221; spline_kernels_bf16.cu:1174-1186). */
 #define SPLINE_HIP_SWISH_MUL_LAUNCHERS(X)                                      \
     X(launch_swish_mul_fwd_native_kernel) X(launch_swish_mul_fwd_d3_kernel)    \
     X(launch_swish_mul_fwd_d4_kernel) X(launch_swish_mul_fwd_d5_kernel)        \
     X(launch_swish_mul_fwd_d6_kernel)                                          \
     X(launch_swish_mul_fwd_native_kernel_bf16) X(launch_swish_mul_fwd_d3_kernel_bf16) \
     X(launch_swish_mul_fwd_d4_kernel_bf16) X(launch_swish_mul_fwd_d5_kernel_bf16) \
-    X(launch_swish_mul_fwd_d6_kernel_bf16)
+    X(launch_swish_mul_fwd_d6_kernel_bf16)                                     \
+    X(launch_swish_mul_fwd_d3_kernel_bf16_sollya) X(launch_swish_mul_fwd_d4_kernel_bf16_sollya) \
+    X(launch_swish_mul_fwd_d5_kernel_bf16_sollya) X(launch_swish_mul_fwd_d6_kernel_bf16_sollya)
 
 /* ---- SwiGLU backward: grad_gate = go*up*F'(gate), grad_up = go*F(gate) ---
  * Replaces launch_swish_mul_bwd_{native,d3..d6}_kernel{,_bf16}
  * (spline_kernels.cu:1270-1283, spline_kernels_bf16.cu:1047-1062; the BF16
- * degree-3 entry uses the algebraic derivative, :255-265,375-382). */
+ * degree-3 entry uses the algebraic derivative, :255-265,375-382) and
+ * launch_swish_mul_bwd_d{3..6}_kernel_bf16_sollya (spline_ops.cpp:227-230;
+ * spline_kernels_bf16.cu:1187-1198: the program pair at every degree). */
 #define SPLINE_HIP_SWISH_MUL_BWD_LAUNCHERS(X)                                  \
     X(launch_swish_mul_bwd_native_kernel) X(launch_swish_mul_bwd_d3_kernel)    \
     X(launch_swish_mul_bwd_d4_kernel) X(launch_swish_mul_bwd_d5_kernel)        \
     X(launch_swish_mul_bwd_d6_kernel)                                          \
     X(launch_swish_mul_bwd_native_kernel_bf16) X(launch_swish_mul_bwd_d3_kernel_bf16) \
     X(launch_swish_mul_bwd_d4_kernel_bf16) X(launch_swish_mul_bwd_d5_kernel_bf16) \
-    X(launch_swish_mul_bwd_d6_kernel_bf16)
+    X(launch_swish_mul_bwd_d6_kernel_bf16)                                     \
+    X(launch_swish_mul_bwd_d3_kernel_bf16_sollya) X(launch_swish_mul_bwd_d4_kernel_bf16_sollya) \
+    X(launch_swish_mul_bwd_d5_kernel_bf16_sollya) X(launch_swish_mul_bwd_d6_kernel_bf16_sollya)
 
 /* ---- packed SwiGLU on [rows, 2H] = [gate | up] -> [rows, H] -------------
  * Replaces launch_swish_mul_packed_fwd_{native,d3..d6}_kernel{,_bf16}
- * (spline_kernels.cu:1285-1302, spline_kernels_bf16.cu:1065-1083). */
+ * (spline_kernels.cu:1285-1302, spline_kernels_bf16.cu:1065-1083) and
+ * launch_swish_mul_packed_fwd_d{3..6}_kernel_bf16_sollya (spline_ops.cpp:235-238). */
 #define SPLINE_HIP_PACKED_FWD_LAUNCHERS(X)                                     \
     X(launch_swish_mul_packed_fwd_native_kernel) X(launch_swish_mul_packed_fwd_d3_kernel) \
     X(launch_swish_mul_packed_fwd_d4_kernel) X(launch_swish_mul_packed_fwd_d5_kernel) \
     X(launch_swish_mul_packed_fwd_d6_kernel)                                   \
     X(launch_swish_mul_packed_fwd_native_kernel_bf16) X(launch_swish_mul_packed_fwd_d3_kernel_bf16) \
     X(launch_swish_mul_packed_fwd_d4_kernel_bf16) X(launch_swish_mul_packed_fwd_d5_kernel_bf16) \
-    X(launch_swish_mul_packed_fwd_d6_kernel_bf16)
+    X(launch_swish_mul_packed_fwd_d6_kernel_bf16)                              \
+    X(launch_swish_mul_packed_fwd_d3_kernel_bf16_sollya) X(launch_swish_mul_packed_fwd_d4_kernel_bf16_sollya) \
+    X(launch_swish_mul_packed_fwd_d5_kernel_bf16_sollya) X(launch_swish_mul_packed_fwd_d6_kernel_bf16_sollya)
 
 /* ---- packed SwiGLU backward: grad_packed [rows, 2H] from grad_out [rows, H]
  * Replaces launch_swish_mul_packed_bwd_{native,d3..d6}_kernel{,_bf16}
- * (spline_kernels.cu:1304-1320, spline_kernels_bf16.cu:1086-1101). */
+ * (spline_kernels.cu:1304-1320, spline_kernels_bf16.cu:1086-1101) and
+ * launch_swish_mul_packed_bwd_d{3..6}_kernel_bf16_sollya (spline_ops.cpp:244-247). */
 #define SPLINE_HIP_PACKED_BWD_LAUNCHERS(X)                                     \
     X(launch_swish_mul_packed_bwd_native_kernel) X(launch_swish_mul_packed_bwd_d3_kernel) \
     X(launch_swish_mul_packed_bwd_d4_kernel) X(launch_swish_mul_packed_bwd_d5_kernel) \
     X(launch_swish_mul_packed_bwd_d6_kernel)                                   \
     X(launch_swish_mul_packed_bwd_native_kernel_bf16) X(launch_swish_mul_packed_bwd_d3_kernel_bf16) \
     X(launch_swish_mul_packed_bwd_d4_kernel_bf16) X(launch_swish_mul_packed_bwd_d5_kernel_bf16) \
-    X(launch_swish_mul_packed_bwd_d6_kernel_bf16)
+    X(launch_swish_mul_packed_bwd_d6_kernel_bf16)                              \
+    X(launch_swish_mul_packed_bwd_d3_kernel_bf16_sollya) X(launch_swish_mul_packed_bwd_d4_kernel_bf16_sollya) \
+    X(launch_swish_mul_packed_bwd_d5_kernel_bf16_sollya) X(launch_swish_mul_packed_bwd_d6_kernel_bf16_sollya)
 
 #define SPLINE_HIP_DECLARE_UNARY(name) \
     int name(void* out, const void* in, int64_t size, void* stream);

@@ -20,13 +20,16 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libspline_oracle.so")
 
-F16, BF16 = 0, 1
-SIGMOID, TANH, SWISH = 0, 1, 2
+F16, BF16, BF16_SOLLYA = 0, 1, 2
+SIGMOID, TANH, SWISH, GELU = 0, 1, 2, 3
 FWD, BWD = 0, 1
 RND_SINGLE, RND_F32 = 0, 1
 
-_FAMILY = {"sigmoid": SIGMOID, "tanh": TANH, "swish": SWISH}
-_FMT = {"f16": F16, "fp16": F16, "float16": F16, "bf16": BF16, "bfloat16": BF16}
+_FAMILY = {"sigmoid": SIGMOID, "tanh": TANH, "swish": SWISH, "gelu": GELU}
+# "bf16_sollya": BF16 storage with the Sollya coefficient set (activation
+# programs only).
+_FMT = {"f16": F16, "fp16": F16, "float16": F16, "bf16": BF16, "bfloat16": BF16,
+        "bf16_sollya": BF16_SOLLYA}
 
 _lib = None
 
@@ -69,6 +72,9 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_bf16_fma_audit.restype = ctypes.c_uint16
     l.orc_activation.argtypes = [ci, ci, ci, ci, ci, u16p, u16p, i64]
     l.orc_activation_bwd.argtypes = [ci, ci, ci, ci, u16p, u16p, u16p, i64]
+    ip = ctypes.POINTER(ctypes.c_int)
+    l.orc_program.argtypes = [ci, ci, ci, ci, ip, f32p, ip, f32p]
+    l.orc_program.restype = ctypes.c_int
     l.orc_activation_bwd_alg.argtypes = [ci, ci, u16p, u16p, u16p, i64]
     l.orc_swish_mul_fwd.argtypes = [ci, ci, ci, u16p, u16p, u16p, i64]
     l.orc_swish_mul_bwd.argtypes = [ci, ci, ci, u16p, u16p, u16p, u16p, u16p, i64]
@@ -128,6 +134,21 @@ def activation(family, direction: int, degree: int, fmt, x: np.ndarray,
     _check(lib().orc_activation(family_id(family), direction, degree, fmt_id(fmt), rnd,
                                 _p(x), _p(y), x.size))
     return y
+
+
+SHAPES = {0: "half_odd", 1: "odd", 2: "odd_min1", 3: "swish", 4: "even", 5: "x_times",
+          6: "x_half_odd"}
+
+
+def program(family, direction: int, degree: int, fmt):
+    """The oracle's table entry: (shape name, clamp, degree, coefficients
+    c[0..degree] as float32 literals)."""
+    shape, deg = ctypes.c_int(), ctypes.c_int()
+    lc = ctypes.c_float()
+    c = (ctypes.c_float * 7)()
+    _check(lib().orc_program(family_id(family), direction, degree, fmt_id(fmt),
+                             ctypes.byref(shape), ctypes.byref(lc), ctypes.byref(deg), c))
+    return SHAPES[shape.value], lc.value, deg.value, [c[i] for i in range(deg.value + 1)]
 
 
 def activation_bwd(family, degree: int, fmt, go: np.ndarray, x: np.ndarray,

@@ -41,6 +41,7 @@ static const fmt_t FMT_F16 = {10, -14, 15, 15};
 static const fmt_t FMT_BF16 = {7, -126, 127, 127};
 
 static const fmt_t* fmt_of(int fmt) { return fmt == ORC_F16 ? &FMT_F16 : &FMT_BF16; }
+static int fmt_ok(int fmt) { return fmt == ORC_F16 || fmt == ORC_BF16 || fmt == ORC_BF16_SOLLYA; }
 
 /* Round a double to the format, ties to even; returns the rounded value. */
 static double round_fmt(double v, const fmt_t* f) {
@@ -185,7 +186,8 @@ enum {
     SHAPE_ODD_MIN1 = 2,   /* sign(x) * min(t*H(t), 1)                      */
     SHAPE_SWISH = 3,      /* fma(|x|, t*H(t), 0.5*x)                       */
     SHAPE_EVEN = 4,       /* c0 + t*(c1 + ...)                             */
-    SHAPE_X_TIMES = 5     /* x * sigmoid-program(x)                        */
+    SHAPE_X_TIMES = 5,    /* x * sigmoid-program(x), same degree and table */
+    SHAPE_X_HALF_ODD = 6  /* x * (0.5 + sign(x) * t*H(t))   (GELU)         */
 };
 
 typedef struct {
@@ -193,13 +195,13 @@ typedef struct {
     float lc;       /* clamp on |x| */
     int deg;
     float c[7];     /* c[0..deg]; c[0] unused by the odd shapes */
-    int inner;      /* SHAPE_X_TIMES: index of the sigmoid program */
+    int unused;
 } prog_t;
 
 /* Index: [family][dir][degree-3]. */
 
 /* FP16 programs: autonumerics_zero/spline_ops/spline_structs_odd.cuh */
-static const prog_t F16_PROGS[3][2][4] = {
+static const prog_t F16_PROGS[4][2][4] = {
     /* SIGMOID */
     {
         {   /* FWD, :14-127 */
@@ -245,10 +247,25 @@ static const prog_t F16_PROGS[3][2][4] = {
             {SHAPE_HALF_ODD, 5.75f, 6, {0.0f, 0.5415039062f, -0.0898437500f, -0.0439147949f, 0.0179443359f, -0.0023403168f, 0.0001055002f}, -1},
         },
     },
+    /* GELU */
+    {
+        {   /* FWD, :801-920: x * (0.5 + sign * h) */
+            {SHAPE_X_HALF_ODD, 3.0f, 3, {0.0f, 0.4592285156f, -0.1364746094f, 0.0131378174f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 4, {0.0f, 0.4208984375f, -0.0592346191f, -0.0298614502f, 0.0071029663f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 5, {0.0f, 0.3962402344f, 0.0178222656f, -0.1052856445f, 0.0362548828f, -0.0038852692f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 6, {0.0f, 0.3935546875f, 0.0309448242f, -0.1257324219f, 0.0500793457f, -0.0081100464f, 0.0004782677f}, -1},
+        },
+        {   /* BWD ODD, :922-1032 */
+            {SHAPE_HALF_ODD, 3.0f, 3, {0.0f, 0.9707031250f, -0.4719238281f, 0.0680541992f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 4, {0.0f, 0.9306640625f, -0.3867187500f, 0.0167694092f, 0.0092239380f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 5, {0.0f, 0.8706054688f, -0.2055664062f, -0.1563720703f, 0.0755004883f, -0.0088424683f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 6, {0.0f, 0.8125000000f, 0.0046691895f, -0.4064941406f, 0.2064208984f, -0.0401306152f, 0.0027942657f}, -1},
+        },
+    },
 };
 
 /* BF16 programs: autonumerics_zero/spline_ops/spline_structs_odd_bf16.cuh */
-static const prog_t BF16_PROGS[3][2][4] = {
+static const prog_t BF16_PROGS[4][2][4] = {
     /* SIGMOID */
     {
         {   /* FWD ODD, :11-121 */
@@ -284,8 +301,8 @@ static const prog_t BF16_PROGS[3][2][4] = {
         {   /* FWD, :248-304: D3/D4 fused odd form, D5/D6 x * sigmoid(x) */
             {SHAPE_SWISH, 6.0f, 3, {0.0f, 0.2810058594f, -0.0533447266f, 0.0033893585f}, -1},
             {SHAPE_SWISH, 5.28125f, 4, {0.0f, 0.2714843750f, -0.0402832031f, -0.0014419556f, 0.0005149841f}, -1},
-            {SHAPE_X_TIMES, 0.0f, 5, {0.0f}, 2},
-            {SHAPE_X_TIMES, 0.0f, 6, {0.0f}, 3},
+            {SHAPE_X_TIMES, 0.0f, 5, {0.0f}, -1},
+            {SHAPE_X_TIMES, 0.0f, 6, {0.0f}, -1},
         },
         {   /* BWD ODD, :510-619 */
             {SHAPE_HALF_ODD, 4.75f, 3, {0.0f, 0.5820312500f, -0.1777343750f, 0.0164794922f}, -1},
@@ -294,17 +311,107 @@ static const prog_t BF16_PROGS[3][2][4] = {
             {SHAPE_HALF_ODD, 5.0f, 6, {0.0f, 0.6015625000f, -0.2050781250f, 0.0260009766f, -0.0004787445f, -0.0001363754f, 0.0000074804f}, -1},
         },
     },
+    /* GELU */
+    {
+        {   /* FWD, :740-858 */
+            {SHAPE_X_HALF_ODD, 3.0f, 3, {0.0f, 0.4592285156f, -0.1364746094f, 0.0131378174f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 4, {0.0f, 0.4208984375f, -0.0592346191f, -0.0298614502f, 0.0071029663f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 5, {0.0f, 0.3962402344f, 0.0178222656f, -0.1052856445f, 0.0362548828f, -0.0038852692f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 6, {0.0f, 0.3935546875f, 0.0309448242f, -0.1257324219f, 0.0500793457f, -0.0081100464f, 0.0004782677f}, -1},
+        },
+        {   /* BWD ODD, :861-970 */
+            {SHAPE_HALF_ODD, 3.0f, 3, {0.0f, 0.9707031250f, -0.4719238281f, 0.0680541992f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 4, {0.0f, 0.9306640625f, -0.3867187500f, 0.0167694092f, 0.0092239380f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 5, {0.0f, 0.8706054688f, -0.2055664062f, -0.1563720703f, 0.0755004883f, -0.0088424683f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 6, {0.0f, 0.8125000000f, 0.0046691895f, -0.4064941406f, 0.2064208984f, -0.0401306152f, 0.0027942657f}, -1},
+        },
+    },
 };
 
+/* BF16 Sollya coefficient set (coeff_source_id 1):
+ * autonumerics_zero/spline_ops/spline_structs_sollya_bf16.cuh.  Same clamps
+ * and evaluation shapes as the current set (its header says so; checked
+ * struct by struct). */
+static const prog_t BF16_SOLLYA_PROGS[4][2][4] = {
+    /* SIGMOID */
+    {
+        {   /* FWD ODD, :14-131 */
+            {SHAPE_HALF_ODD, 6.0f, 3, {0.0f, 0.2812500000f, -0.0534667969f, 0.0033874512f}, -1},
+            {SHAPE_HALF_ODD, 5.28125f, 4, {0.0f, 0.2695312500f, -0.0380859375f, -0.0020904541f, 0.0005722046f}, -1},
+            {SHAPE_HALF_ODD, 5.40625f, 5, {0.0f, 0.2558593750f, -0.0115356445f, -0.0179443359f, 0.0042724609f, -0.0002956390f}, -1},
+            {SHAPE_HALF_ODD, 4.90625f, 6, {0.0f, 0.2490234375f, 0.0062561035f, -0.0327148438f, 0.0095825195f, -0.0011596680f, 0.0000522137f}, -1},
+        },
+        {   /* BWD EVEN, :258-360 */
+            {SHAPE_EVEN, 4.0f, 3, {0.2558593750f, -0.0385742188f, -0.0292968750f, 0.0061035156f}, -1},
+            {SHAPE_EVEN, 4.75f, 4, {0.2519531250f, -0.0089721680f, -0.0668945312f, 0.0213623047f, -0.0019302368f}, -1},
+            {SHAPE_EVEN, 4.75f, 5, {0.2490234375f, 0.0139770508f, -0.1015625000f, 0.0407714844f, -0.0064697266f, 0.0003757477f}, -1},
+            {SHAPE_EVEN, 4.25f, 6, {0.2500000000f, 0.0023956299f, -0.0742187500f, 0.0156250000f, 0.0042724609f, -0.0017700195f, 0.0001621246f}, -1},
+        },
+    },
+    /* TANH */
+    {
+        {   /* FWD ODD with min(h, 1), :134-256 */
+            {SHAPE_ODD_MIN1, 2.75f, 3, {0.0f, 1.1171875000f, -0.4160156250f, 0.0505371094f}, -1},
+            {SHAPE_ODD_MIN1, 2.75f, 4, {0.0f, 1.0859375000f, -0.3281250000f, -0.0150146484f, 0.0140991211f}, -1},
+            {SHAPE_ODD_MIN1, 2.25f, 5, {0.0f, 1.0078125000f, -0.0157470703f, -0.3964843750f, 0.1962890625f, -0.0299072266f}, -1},
+            {SHAPE_ODD_MIN1, 2.25f, 6, {0.0f, 1.0000000000f, 0.0214843750f, -0.4570312500f, 0.2402343750f, -0.0444335938f, 0.0017700195f}, -1},
+        },
+        {   /* BWD EVEN, :362-464 */
+            {SHAPE_EVEN, 2.0f, 3, {1.0234375000f, -0.3085937500f, -0.4687500000f, 0.1953125000f}, -1},
+            {SHAPE_EVEN, 2.25f, 4, {1.0078125000f, -0.0600585938f, -1.1093750000f, 0.7187500000f, -0.1328125000f}, -1},
+            {SHAPE_EVEN, 2.25f, 5, {0.9960937500f, 0.1005859375f, -1.5703125000f, 1.2265625000f, -0.3710937500f, 0.0400390625f}, -1},
+            {SHAPE_EVEN, 2.25f, 6, {1.0000000000f, 0.0312500000f, -1.2578125000f, 0.6484375000f, 0.1289062500f, -0.1611328125f, 0.0303955078f}, -1},
+        },
+    },
+    /* SWISH */
+    {
+        {   /* FWD, :830-852: x * Sollya sigmoid of the same degree */
+            {SHAPE_X_TIMES, 0.0f, 3, {0.0f}, -1},
+            {SHAPE_X_TIMES, 0.0f, 4, {0.0f}, -1},
+            {SHAPE_X_TIMES, 0.0f, 5, {0.0f}, -1},
+            {SHAPE_X_TIMES, 0.0f, 6, {0.0f}, -1},
+        },
+        {   /* BWD ODD, :466-584 */
+            {SHAPE_HALF_ODD, 4.75f, 3, {0.0f, 0.5781250000f, -0.1738281250f, 0.0158691406f}, -1},
+            {SHAPE_HALF_ODD, 5.25f, 4, {0.0f, 0.5820312500f, -0.1777343750f, 0.0172119141f, -0.0001506805f}, -1},
+            {SHAPE_HALF_ODD, 4.75f, 5, {0.0f, 0.5234375000f, -0.0537109375f, -0.0629882812f, 0.0200195312f, -0.0017318726f}, -1},
+            {SHAPE_HALF_ODD, 5.0f, 6, {0.0f, 0.5039062500f, 0.0106201172f, -0.1289062500f, 0.0490722656f, -0.0075073242f, 0.0004253387f}, -1},
+        },
+    },
+    /* GELU */
+    {
+        {   /* FWD, :586-708 */
+            {SHAPE_X_HALF_ODD, 3.0f, 3, {0.0f, 0.4726562500f, -0.1464843750f, 0.0147094727f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 4, {0.0f, 0.4414062500f, -0.0908203125f, -0.0148315430f, 0.0048522949f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 5, {0.0f, 0.4003906250f, 0.0086059570f, -0.0981445312f, 0.0339355469f, -0.0036163330f}, -1},
+            {SHAPE_X_HALF_ODD, 3.0f, 6, {0.0f, 0.3906250000f, 0.0393066406f, -0.1337890625f, 0.0534667969f, -0.0087280273f, 0.0005149841f}, -1},
+        },
+        {   /* BWD ODD, :710-828 */
+            {SHAPE_HALF_ODD, 3.0f, 3, {0.0f, 0.9648437500f, -0.4628906250f, 0.0654296875f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 4, {0.0f, 0.9140625000f, -0.3476562500f, -0.0084228516f, 0.0140380859f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 5, {0.0f, 0.8046875000f, 0.0143432617f, -0.3789062500f, 0.1630859375f, -0.0206298828f}, -1},
+            {SHAPE_HALF_ODD, 3.0f, 6, {0.0f, 0.7812500000f, 0.1166992188f, -0.5312500000f, 0.2636718750f, -0.0510253906f, 0.0034332275f}, -1},
+        },
+    },
+};
+
+typedef const prog_t (*table_t)[2][4];
+
+static table_t table_of(int fmt) {
+    return fmt == ORC_F16 ? F16_PROGS : (fmt == ORC_BF16_SOLLYA ? BF16_SOLLYA_PROGS : BF16_PROGS);
+}
+
 static const prog_t* find_prog(int family, int dir, int degree, int fmt) {
-    if (family < 0 || family > 2 || dir < 0 || dir > 1 || degree < 3 || degree > 6) return 0;
-    return fmt == ORC_F16 ? &F16_PROGS[family][dir][degree - 3]
-                          : &BF16_PROGS[family][dir][degree - 3];
+    if (family < 0 || family > 3 || dir < 0 || dir > 1 || degree < 3 || degree > 6 ||
+        !fmt_ok(fmt))
+        return 0;
+    return &table_of(fmt)[family][dir][degree - 3];
 }
 
 typedef struct {
     const fmt_t* f;
     int rnd;
+    table_t tab;   /* the coefficient table the program came from */
 } ctx_t;
 
 static double c_fma(const ctx_t* k, double a, double b, double c) {
@@ -316,8 +423,9 @@ static double c_fma(const ctx_t* k, double a, double b, double c) {
 static double eval_prog(const prog_t* p, double x, const ctx_t* k) {
     const fmt_t* f = k->f;
     if (p->shape == SHAPE_X_TIMES) {
-        /* SWISH_FWD_D{5,6}_ODD_BF16: __hmul2(val, SIGMOID_FWD_D{5,6}(val)) */
-        const prog_t* s = &BF16_PROGS[0][0][p->inner];
+        /* SWISH_FWD_D{5,6}_ODD_BF16 and SWISH_FWD_D{3..6}_ODD_SOLLYA_BF16:
+         * __hmul2(val, SIGMOID_FWD_D<n>(val)) from the same coefficient set */
+        const prog_t* s = &k->tab[0][0][p->deg - 3];
         return h_mul(x, eval_prog(s, x, k), f);
     }
     int neg = signbit(x) != 0;
@@ -334,6 +442,9 @@ static double eval_prog(const prog_t* p, double x, const ctx_t* k) {
     switch (p->shape) {
     case SHAPE_HALF_ODD:
         return h_add(kconst(0.5f, f), neg ? -h : h, f);
+    case SHAPE_X_HALF_ODD:
+        /* GELU_FWD: phi = __hadd2(0.5, h_signed); __hmul2(val, phi) */
+        return h_mul(x, h_add(kconst(0.5f, f), neg ? -h : h, f), f);
     case SHAPE_ODD:
         return neg ? -h : h;
     case SHAPE_ODD_MIN1:
@@ -344,6 +455,17 @@ static double eval_prog(const prog_t* p, double x, const ctx_t* k) {
     default:
         return NAN;
     }
+}
+
+int orc_program(int family, int dir, int degree, int fmt, int* shape, float* lc,
+                int* deg, float* c7) {
+    const prog_t* p = find_prog(family, dir, degree, fmt);
+    if (!p) return -1;
+    *shape = p->shape;
+    *lc = p->lc;
+    *deg = p->deg;
+    for (int i = 0; i < 7; ++i) c7[i] = p->c[i];
+    return 0;
 }
 
 int orc_num_threads(void) {
@@ -357,8 +479,8 @@ int orc_num_threads(void) {
 int orc_activation(int family, int dir, int degree, int fmt, int rnd,
                    const uint16_t* x, uint16_t* y, int64_t n) {
     const prog_t* p = find_prog(family, dir, degree, fmt);
-    if (!p || n < 0 || (fmt != ORC_F16 && fmt != ORC_BF16)) return -1;
-    ctx_t k = {fmt_of(fmt), rnd};
+    if (!p || n < 0) return -1;
+    ctx_t k = {fmt_of(fmt), rnd, table_of(fmt)};
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i)
         y[i] = bits_fmt(eval_prog(p, value_fmt(x[i], k.f), &k), k.f);
@@ -370,7 +492,7 @@ int orc_activation_bwd(int family, int degree, int fmt, int rnd,
                        int64_t n) {
     const prog_t* p = find_prog(family, ORC_BWD, degree, fmt);
     if (!p || n < 0) return -1;
-    ctx_t k = {fmt_of(fmt), rnd};
+    ctx_t k = {fmt_of(fmt), rnd, table_of(fmt)};
     /* binary_vec_kernel: gi = __hmul2(go, GradFunc::evaluate(x)) */
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
@@ -402,7 +524,7 @@ int orc_swish_mul_fwd(int degree, int fmt, int rnd, const uint16_t* gate,
                       const uint16_t* up, uint16_t* out, int64_t n) {
     const prog_t* p = find_prog(ORC_SWISH, ORC_FWD, degree, fmt);
     if (!p || n < 0) return -1;
-    ctx_t k = {fmt_of(fmt), rnd};
+    ctx_t k = {fmt_of(fmt), rnd, table_of(fmt)};
     /* swish_mul_vec_kernel: __hmul2(Func::evaluate(gate), up) */
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
@@ -418,7 +540,7 @@ int orc_swish_mul_bwd(int degree, int fmt, int rnd, const uint16_t* go,
     const prog_t* pf = find_prog(ORC_SWISH, ORC_FWD, degree, fmt);
     const prog_t* pb = find_prog(ORC_SWISH, ORC_BWD, degree, fmt);
     if (!pf || !pb || n < 0) return -1;
-    ctx_t k = {fmt_of(fmt), rnd};
+    ctx_t k = {fmt_of(fmt), rnd, table_of(fmt)};
     const fmt_t* f = k.f;
     int algebraic = (fmt == ORC_BF16 && degree == 3);
 #pragma omp parallel for schedule(static)
@@ -550,7 +672,7 @@ static const double SOFTCAP_T_SAT = 2.609375;
 int orc_softcap_fwd_bf16(const uint16_t* s, uint16_t* y, int64_t n, float cap) {
     if (n < 0 || !(cap > 0.0f)) return -1;
     const prog_t* p = &BF16_PROGS[1][0][1]; /* TANH_FWD_D4_ODD_BF16 */
-    ctx_t k = {&FMT_BF16, ORC_RND_SINGLE};
+    ctx_t k = {&FMT_BF16, ORC_RND_SINGLE, BF16_PROGS};
     float inv = 1.0f / cap;
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
@@ -698,7 +820,7 @@ int orc_sincos(int prog, int out_fmt, int rnd, const float* angles, uint16_t* co
                uint16_t* sin_out, int64_t n) {
     if (prog < 0 || prog > 5 || n < 0) return -1;
     const sincos_t* q = &SINCOS[prog];
-    ctx_t k = {fmt_of(q->fmt), rnd};
+    ctx_t k = {fmt_of(q->fmt), rnd, 0};
     const fmt_t* fo = fmt_of(out_fmt);
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
@@ -721,7 +843,7 @@ static void rope_q15(uint32_t position, uint32_t inc, double* c, double* s) {
     int16_t q15 = (int16_t)(uint16_t)(phase >> 15);
     double r = h_mul(round_fmt((double)q15, &FMT_F16), ldexp(1.0, -15), &FMT_F16);
     int negate = (int)(((phase >> 31) ^ (phase >> 30)) & 1u);
-    ctx_t k = {&FMT_F16, ORC_RND_SINGLE};
+    ctx_t k = {&FMT_F16, ORC_RND_SINGLE, 0};
     sincos_poly(&SINCOS[6], r, negate, &k, c, s);
 }
 

@@ -16,11 +16,13 @@
 extern "C" {
 #endif
 
-/* Storage formats. */
-enum { ORC_F16 = 0, ORC_BF16 = 1 };
+/* Storage formats.  ORC_BF16_SOLLYA is BF16 storage with the Sollya
+ * coefficient set (coeff_source_id 1, spline_structs_sollya_bf16.cuh); it is
+ * accepted by the activation programs only. */
+enum { ORC_F16 = 0, ORC_BF16 = 1, ORC_BF16_SOLLYA = 2 };
 
 /* Activation families and directions. */
-enum { ORC_SIGMOID = 0, ORC_TANH = 1, ORC_SWISH = 2 };
+enum { ORC_SIGMOID = 0, ORC_TANH = 1, ORC_SWISH = 2, ORC_GELU = 3 };
 enum { ORC_FWD = 0, ORC_BWD = 1 };
 
 /* BF16 FMA semantics for the activation programs.
@@ -47,6 +49,10 @@ uint16_t orc_bf16_fma_audit(uint16_t a, uint16_t b, uint16_t c);
  * dir == ORC_BWD.  degree 3..6. */
 int orc_activation(int family, int dir, int degree, int fmt, int rnd,
                    const uint16_t* x, uint16_t* y, int64_t n);
+/* The program table entry (shape code, clamp, degree, c[0..6]) for tests
+ * that compare the oracle's tables with an independent transcription. */
+int orc_program(int family, int dir, int degree, int fmt, int* shape, float* lc,
+                int* deg, float* c7);
 /* gi = go * G(x)  (binary_vec_kernel). */
 int orc_activation_bwd(int family, int degree, int fmt, int rnd,
                        const uint16_t* go, const uint16_t* x, uint16_t* gi,

@@ -17,8 +17,15 @@ def test_unknown_activation_and_sources(monkeypatch):
     with pytest.raises(ValueError, match="backward_impl must be"):
         activations.resolve_mlp_activation_packed_impl("spline_silu_compile", backward_impl="x")
     assert activations.resolve_mlp_activation_impl("native_silu")[0] == "native_silu"
-    with pytest.raises(RuntimeError, match="GELU"):
-        activations.resolve_mlp_activation_impl("spline_gelu")
+    name, act = activations.resolve_mlp_activation_impl("spline_gelu")
+    assert name == "spline_gelu[d5,current]" and act.__name__ == "spline_gelu_d5_current_direct"
+    name, _ = activations.resolve_mlp_activation_impl("spline_gelu_compile", degree=4)
+    assert name == "spline_gelu_compile[d4,current]"
+    with pytest.raises(ValueError, match="Sollya coefficients are benchmark-only"):
+        activations.resolve_mlp_activation_impl("spline_gelu", coeff_source="sollya")
+    monkeypatch.setenv("SFU_REPRO_ALLOW_SOLLYA_SWEEP", "1")
+    assert activations.resolve_mlp_activation_impl(
+        "spline_gelu", degree=6, coeff_source="sollya")[0] == "spline_gelu[d6,sollya]"
 
 
 def test_spline_compile_factories_validate_arguments():
@@ -30,12 +37,18 @@ def test_spline_compile_factories_validate_arguments():
         spline_compile.make_spline_silu_packed(3, "current", backward_impl="bad")
     act = spline_compile.make_spline_silu_packed(3, "current")
     assert act.__spline_op__ == "spline_ops::swish_mul_packed_variant_fwd"
+    assert spline_compile.make_spline_gelu() is spline_compile.spline_gelu
+    assert spline_compile.make_spline_gelu(4, "sollya").__name__ == "spline_gelu_d4_sollya"
 
 
 def test_extension_rejects_host_tensors():
     import torch
 
     import spline_ops
+
+    for name in ("gelu_fwd", "gelu_fwd_d3", "gelu_fwd_d6", "gelu_bwd", "gelu_fwd_variant",
+                 "gelu_bwd_variant", "gelu_ag_variant"):
+        assert hasattr(spline_ops, name), name
 
     with pytest.raises(RuntimeError, match="x must be a CUDA tensor"):
         spline_ops.swish_fwd(torch.zeros(4, dtype=torch.float16))
