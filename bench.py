@@ -48,6 +48,10 @@ def parse():
     p.add_argument("--pmc-pass", action="store_true",
                    help="counter pass: 3 launches of the headline kernel and 3 plain "
                         "256 MiB copies (torch copy_) as the byte-count calibration")
+    p.add_argument("--pmc-sweep", action="store_true",
+                   help="issue-rate counter pass: 3 eager launches of each polynomial, "
+                        "native and copy kernel of the sweep at 2^20, 2^22 and 2^24 "
+                        "elements (L2- and MALL-resident sizes)")
     return p.parse_args()
 
 
@@ -262,6 +266,40 @@ def sweep(lib, reps: int):
     return out
 
 
+PMC_SWEEP_LOG2 = (20, 22, 24)
+
+
+def pmc_sweep(lib):
+    """Counter pass for the cache-resident regimes: every kernel of the sweep
+    launched 3 times, eagerly, after one warm launch of the same size (so
+    the input sits in L2 / MALL as in back-to-back timing).  Prints the
+    launch plan; rocprofv3 attributes counters by kernel name and grid
+    size."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    plan = []
+    for n_log2 in PMC_SWEEP_LOG2:
+        n = 1 << n_log2
+        g = torch.Generator(device=dev).manual_seed(n_log2)
+        for dtype, sfx in ((torch.float16, ""), (torch.bfloat16, "_bf16")):
+            x = (torch.randn(n, device=dev, generator=g) * 2.0).to(dtype)
+            y = torch.empty_like(x)
+            names = ["spline_hip_copy16"]
+            for fam, deg in (("sigmoid", 3), ("tanh", 4), ("swish", 3)):
+                names += [f"launch_{fam}_fwd_d{deg}_kernel{sfx}", f"launch_{fam}_fwd_native_kernel{sfx}"]
+            for name in names:
+                launch = make_unary(lib, name, y, x)
+                launch()
+                torch.cuda.synchronize()
+                for _ in range(3):
+                    launch()
+                torch.cuda.synchronize()
+                plan.append({"entry": name, "elements": n, "launches": 4})
+            del x, y
+    print(json.dumps({"pmc_sweep": plan}), flush=True)
+
+
 def _vp(t):
     import ctypes
 
@@ -439,6 +477,9 @@ def main():
         sys.exit(1)
     lib = _capi()
     dev = torch.device("cuda:0")
+    if args.pmc_sweep:
+        pmc_sweep(lib)
+        return
 
     # Synthetic B1 gate activations [8192, 14336] ~ N(0, 2^2), FP16, in HBM.
     rows, cols = 8192, 14336
