@@ -424,37 +424,123 @@ at::Tensor exp2_f32_to(at::Tensor x, Exp2Launcher fn, at::ScalarType out_type) {
 // ---------------------------------------------------------------------------
 
 using SincosLauncher = int (*)(void*, const void*, int64_t, void*);
+using SincosComputeLauncher = int (*)(void*, const void*, int64_t, int64_t, void*);
 
-at::Tensor sincos_table(at::Tensor angles, SincosLauncher fn, at::ScalarType out_type) {
+// sincos_f32 / sincos_bf16 / sincos_fp16 and their compute forms
+// (spline_ops.cpp:326-580, 980-1100): FP32 angles -> [2, *angles.shape].
+// The 16-bit tables need an even element count and the 16-bit probes a
+// multiple of four, as in the reference.
+at::Tensor sincos_out(const at::Tensor& angles, at::ScalarType out_type, int64_t multiple,
+                      int64_t iterations) {
     CHECK_CUDA(angles);
     CHECK_CONTIGUOUS(angles);
     TORCH_CHECK(angles.scalar_type() == at::kFloat, "angles must be float32");
+    if (multiple == 2)
+        TORCH_CHECK((angles.numel() % 2) == 0, "angles must contain an even number of elements");
+    if (multiple == 4)
+        TORCH_CHECK((angles.numel() % 4) == 0, "angles must contain a multiple of four elements");
+    if (iterations >= 0) {
+        TORCH_CHECK(iterations > 0, "iterations must be positive");
+        TORCH_CHECK(iterations <= std::numeric_limits<int>::max(),
+                    "iterations is too large for the CUDA launcher");
+    }
     std::vector<int64_t> sizes = angles.sizes().vec();
     sizes.insert(sizes.begin(), 2);
+    return at::empty(sizes, angles.options().dtype(out_type));
+}
+
+at::Tensor sincos_table(at::Tensor angles, SincosLauncher fn, at::ScalarType out_type) {
     c10::OptionalDeviceGuard guard(angles.device());
-    at::Tensor out = at::empty(sizes, angles.options().dtype(out_type));
+    at::Tensor out = sincos_out(angles, out_type, out_type == at::kFloat ? 1 : 2, -1);
     void* s = current_stream(angles);
     check_launch(fn(out.data_ptr(), angles.data_ptr(), angles.numel(), s), s);
     return out;
 }
 
-at::Tensor rope_sincos_fixed_half_turn_d5_d6_fp16(at::Tensor phase_increments,
-                                                  int64_t sequence_length) {
-    CHECK_CUDA(phase_increments);
-    CHECK_CONTIGUOUS(phase_increments);
-    TORCH_CHECK(phase_increments.dim() == 1, "phase_increments must be one-dimensional");
-    TORCH_CHECK(phase_increments.scalar_type() == at::kInt, "phase_increments has the wrong dtype");
+at::Tensor sincos_compute(at::Tensor angles, int64_t iterations, SincosComputeLauncher fn,
+                          at::ScalarType out_type) {
+    c10::OptionalDeviceGuard guard(angles.device());
+    at::Tensor out = sincos_out(angles, out_type, out_type == at::kFloat ? 1 : 4, iterations);
+    void* s = current_stream(angles);
+    check_launch(fn(out.data_ptr(), angles.data_ptr(), angles.numel(), iterations, s), s);
+    return out;
+}
+
+// allocate_rope_sincos_fp16_output + rope_sincos_fp16 / _compute
+// (spline_ops.cpp:585-760): parameters [F] (int32 increments or FP32
+// frequencies) -> [2, S, F] FP16.
+at::Tensor rope_table_out(const at::Tensor& params, int64_t sequence_length,
+                          at::ScalarType param_type, const char* param_name, int64_t multiple) {
+    CHECK_CUDA(params);
+    CHECK_CONTIGUOUS(params);
+    TORCH_CHECK(params.dim() == 1, param_name, " must be one-dimensional");
+    TORCH_CHECK(params.scalar_type() == param_type, param_name, " has the wrong dtype");
+    if (multiple == 4)
+        TORCH_CHECK((params.numel() % 4) == 0, param_name, " must contain a multiple of four elements");
+    TORCH_CHECK((params.numel() % 2) == 0, param_name, " must contain an even number of elements");
     TORCH_CHECK(sequence_length >= 0, "sequence_length must be non-negative");
-    TORCH_CHECK((phase_increments.numel() % 4) == 0,
-                "phase_increments must contain a multiple of four elements");
-    c10::OptionalDeviceGuard guard(phase_increments.device());
-    at::Tensor out = at::empty({2, sequence_length, phase_increments.numel()},
-                               phase_increments.options().dtype(at::kHalf));
-    void* s = current_stream(phase_increments);
-    check_launch(launch_rope_sincos_fixed_half_turn_d5_d6_fp16(
-                     out.data_ptr(), phase_increments.data_ptr(), sequence_length,
-                     phase_increments.numel(), s),
+    return at::empty({2, sequence_length, params.numel()}, params.options().dtype(at::kHalf));
+}
+
+using RopeTableLauncher = int (*)(void*, const void*, int64_t, int64_t, void*);
+using RopeTableComputeLauncher = int (*)(void*, const void*, int64_t, int64_t, int64_t, void*);
+
+at::Tensor rope_table(at::Tensor params, int64_t sequence_length, at::ScalarType param_type,
+                      const char* param_name, int64_t multiple, RopeTableLauncher fn) {
+    c10::OptionalDeviceGuard guard(params.device());
+    at::Tensor out = rope_table_out(params, sequence_length, param_type, param_name, multiple);
+    void* s = current_stream(params);
+    check_launch(fn(out.data_ptr(), params.data_ptr(), sequence_length, params.numel(), s), s);
+    return out;
+}
+
+at::Tensor rope_table_compute(at::Tensor params, int64_t sequence_length, int64_t iterations,
+                              at::ScalarType param_type, const char* param_name, int64_t multiple,
+                              RopeTableComputeLauncher fn) {
+    c10::OptionalDeviceGuard guard(params.device());
+    at::Tensor out = rope_table_out(params, sequence_length, param_type, param_name, multiple);
+    TORCH_CHECK(iterations > 0, "iterations must be positive");
+    TORCH_CHECK(iterations <= std::numeric_limits<int>::max(),
+                "iterations is too large for the CUDA launcher");
+    void* s = current_stream(params);
+    check_launch(fn(out.data_ptr(), params.data_ptr(), sequence_length, params.numel(), iterations,
+                    s),
                  s);
+    return out;
+}
+
+// check_rope_phase_table (spline_ops.cpp:675-691)
+void check_rope_phase_table(const at::Tensor& phase_increments, const at::Tensor& phase_table) {
+    CHECK_CUDA(phase_table);
+    CHECK_CONTIGUOUS(phase_table);
+    TORCH_CHECK(phase_table.scalar_type() == at::kHalf, "phase_table must be float16");
+    TORCH_CHECK(phase_table.dim() == 2 && phase_table.size(0) == 128 && phase_table.size(1) == 2,
+                "phase_table must have shape [128, 2]");
+    TORCH_CHECK(phase_table.get_device() == phase_increments.get_device(),
+                "phase_table and phase_increments must be on the same CUDA device");
+}
+
+at::Tensor rope_sincos_fixed_lut_fp16(at::Tensor phase_increments, at::Tensor phase_table,
+                                      int64_t sequence_length, int64_t iterations) {
+    c10::OptionalDeviceGuard guard(phase_increments.device());
+    at::Tensor out =
+        rope_table_out(phase_increments, sequence_length, at::kInt, "phase_increments", 2);
+    check_rope_phase_table(phase_increments, phase_table);
+    void* s = current_stream(phase_increments);
+    if (iterations < 0) {
+        check_launch(launch_rope_sincos_fixed_lut_fp16(out.data_ptr(), phase_increments.data_ptr(),
+                                                       phase_table.data_ptr(), sequence_length,
+                                                       phase_increments.numel(), s),
+                     s);
+    } else {
+        TORCH_CHECK(iterations > 0, "iterations must be positive");
+        TORCH_CHECK(iterations <= std::numeric_limits<int>::max(),
+                    "iterations is too large for the CUDA launcher");
+        check_launch(launch_rope_sincos_fixed_lut_fp16_compute(
+                         out.data_ptr(), phase_increments.data_ptr(), phase_table.data_ptr(),
+                         sequence_length, phase_increments.numel(), iterations, s),
+                     s);
+    }
     return out;
 }
 
@@ -481,14 +567,29 @@ std::vector<at::Tensor> rope_apply(at::Tensor q, at::Tensor k, at::Tensor parame
     TORCH_CHECK(q.size(2) > 0 && k.size(2) > 0, "q and k must contain at least one head");
     TORCH_CHECK(q.size(3) > 0 && (q.size(3) % 8) == 0,
                 "head_dim must be a positive multiple of eight");
-    CHECK_CUDA(parameters);
-    CHECK_CONTIGUOUS(parameters);
-    TORCH_CHECK(parameters.dim() == 1, parameter_name, " must be one-dimensional");
-    TORCH_CHECK(parameters.scalar_type() == parameter_type, parameter_name, " has the wrong dtype");
-    TORCH_CHECK(parameters.get_device() == q.get_device(), parameter_name,
-                " must be on the same CUDA device as q and k");
-    TORCH_CHECK(parameters.numel() == q.size(3) / 2, parameter_name,
-                " must contain head_dim / 2 elements");
+    // CHECK_CUDA / CHECK_CONTIGUOUS name the argument: `parameters` in
+    // rope_apply_parameter_fp16, `rope_table` in rope_apply_cached_fp16.
+    const bool cached = std::strcmp(parameter_name, "rope_table") == 0;
+    const char* arg = cached ? "rope_table" : "parameters";
+    TORCH_CHECK(parameters.is_cuda(), arg, " must be a CUDA tensor");
+    TORCH_CHECK(parameters.is_contiguous(), arg, " must be contiguous");
+    if (cached) {
+        // rope_apply_cached_fp16 (spline_ops.cpp:920-953)
+        TORCH_CHECK(parameters.scalar_type() == at::kHalf, "rope_table must be float16");
+        TORCH_CHECK(parameters.get_device() == q.get_device(),
+                    "rope_table must be on the same CUDA device as q and k");
+        TORCH_CHECK(parameters.dim() == 3 && parameters.size(0) == 2 &&
+                        parameters.size(1) == q.size(1) && parameters.size(2) == q.size(3) / 2,
+                    "rope_table must have shape [2, sequence_length, head_dim / 2]");
+    } else {
+        TORCH_CHECK(parameters.dim() == 1, parameter_name, " must be one-dimensional");
+        TORCH_CHECK(parameters.scalar_type() == parameter_type, parameter_name,
+                    " has the wrong dtype");
+        TORCH_CHECK(parameters.get_device() == q.get_device(), parameter_name,
+                    " must be on the same CUDA device as q and k");
+        TORCH_CHECK(parameters.numel() == q.size(3) / 2, parameter_name,
+                    " must contain head_dim / 2 elements");
+    }
     c10::OptionalDeviceGuard guard(q.device());
     const int64_t b = q.size(0), sl = q.size(1), hq = q.size(2), hk = k.size(2), d = q.size(3);
     at::Tensor q_out = at::empty({b, hq, sl, d}, q.options());
@@ -782,7 +883,52 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
 
 #define PT_DEF_SINCOS(name, T, doc) \
     m.def(#name, [](at::Tensor a) { return sincos_table(a, launch_##name, T); }, doc)
+#define PT_DEF_SINCOS_COMPUTE(name, T, doc)                                             \
+    m.def(#name, [](at::Tensor a, int64_t it) { return sincos_compute(a, it, launch_##name, T); }, \
+          doc)
+    // Paired FP32 sin/cos kernels used by the RoPE microbenchmarks.
+    PT_DEF_SINCOS(sincos_native_f32, at::kFloat, "Paired native FP32 sin/cos");
+    PT_DEF_SINCOS(sincos_d3_d4_f32, at::kFloat, "Paired polynomial FP32 sin D3/cos D4");
+    PT_DEF_SINCOS(sincos_d3_d4_cycle_f32, at::kFloat,
+                  "Paired polynomial FP32 sin D3/cos D4 with cycle-domain symmetry reduction");
+    PT_DEF_SINCOS(sincos_d3_d4_magic_bias_f32, at::kFloat,
+                  "Paired polynomial FP32 sin D3/cos D4 with conversion-free magic-bias reduction");
+    PT_DEF_SINCOS(sincos_d5_d4_half_turn_ls_f32, at::kFloat,
+                  "Paired half-turn polynomial FP32 sin D5/cos D4 with least-squares coefficients");
+    PT_DEF_SINCOS(sincos_d5_d4_half_turn_sollya_f32, at::kFloat,
+                  "Paired half-turn polynomial FP32 sin D5/cos D4 with Sollya coefficients");
+    PT_DEF_SINCOS(sincos_d5_d4_half_turn_sollya_fast_f32, at::kFloat,
+                  "Paired half-turn polynomial FP32 sin D5/cos D4 with Sollya coefficients and "
+                  "one-term pi reduction");
+    PT_DEF_SINCOS(sincos_d5_d4_f32, at::kFloat, "Paired polynomial FP32 sin D5/cos D4");
+    PT_DEF_SINCOS(sincos_d7_d6_f32, at::kFloat, "Paired polynomial FP32 sin D7/cos D6");
+    PT_DEF_SINCOS_COMPUTE(sincos_native_compute_f32, at::kFloat,
+                          "Compute-saturated paired native FP32 sin/cos");
+    PT_DEF_SINCOS_COMPUTE(sincos_d3_d4_compute_f32, at::kFloat,
+                          "Compute-saturated polynomial FP32 sin D3/cos D4");
+    PT_DEF_SINCOS_COMPUTE(sincos_d3_d4_cycle_compute_f32, at::kFloat,
+                          "Compute-saturated polynomial FP32 sin D3/cos D4 with cycle-domain "
+                          "symmetry reduction");
+    PT_DEF_SINCOS_COMPUTE(sincos_d3_d4_magic_bias_compute_f32, at::kFloat,
+                          "Compute-saturated polynomial FP32 sin D3/cos D4 with conversion-free "
+                          "magic-bias reduction");
+    PT_DEF_SINCOS_COMPUTE(sincos_d5_d4_half_turn_ls_compute_f32, at::kFloat,
+                          "Compute-saturated half-turn polynomial FP32 sin D5/cos D4 with "
+                          "least-squares coefficients");
+    PT_DEF_SINCOS_COMPUTE(sincos_d5_d4_half_turn_sollya_compute_f32, at::kFloat,
+                          "Compute-saturated half-turn polynomial FP32 sin D5/cos D4 with Sollya "
+                          "coefficients");
+    PT_DEF_SINCOS_COMPUTE(sincos_d5_d4_half_turn_sollya_fast_compute_f32, at::kFloat,
+                          "Compute-saturated half-turn polynomial FP32 sin D5/cos D4 with Sollya "
+                          "coefficients and one-term pi reduction");
+    PT_DEF_SINCOS_COMPUTE(sincos_d5_d4_compute_f32, at::kFloat,
+                          "Compute-saturated polynomial FP32 sin D5/cos D4");
+    PT_DEF_SINCOS_COMPUTE(sincos_d7_d6_compute_f32, at::kFloat,
+                          "Compute-saturated polynomial FP32 sin D7/cos D6");
     PT_DEF_SINCOS(sincos_native_bf16, at::kBFloat16, "Paired native sin/cos with BF16 output");
+    PT_DEF_SINCOS(sincos_d3_d4_bf16, at::kBFloat16, "Paired packed-BF16 polynomial sin D3/cos D4");
+    PT_DEF_SINCOS(sincos_d3_d4_quarter_turn_bf16, at::kBFloat16,
+                  "Paired quarter-turn polynomial sin D3/cos D4 with packed BF16 evaluation and output");
     PT_DEF_SINCOS(sincos_d3_d4_half_turn_bf16, at::kBFloat16,
                   "Paired half-turn polynomial sin D3/cos D4 with packed BF16 evaluation and output");
     PT_DEF_SINCOS(sincos_d5_d6_half_turn_bf16, at::kBFloat16,
@@ -790,6 +936,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     PT_DEF_SINCOS(sincos_d5_d4_half_turn_fp16_bf16, at::kBFloat16,
                   "Paired half-turn polynomial sin D5/cos D4 with packed FP16 evaluation and BF16 output");
     PT_DEF_SINCOS(sincos_native_fp16, at::kHalf, "Paired native sin/cos with FP16 output");
+    PT_DEF_SINCOS(sincos_d3_d4_quarter_turn_fp16, at::kHalf,
+                  "Paired quarter-turn polynomial sin D3/cos D4 with packed FP16 evaluation and output");
     PT_DEF_SINCOS(sincos_d3_d4_half_turn_fp16, at::kHalf,
                   "Paired half-turn polynomial sin D3/cos D4 with packed FP16 evaluation and output");
     PT_DEF_SINCOS(sincos_d5_d4_half_turn_fp16, at::kHalf,
@@ -798,9 +946,94 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                   "Paired half-turn polynomial sin D5/cos D6 with packed FP16 evaluation and output");
     PT_DEF_SINCOS(sincos_d7_d6_half_turn_fp16, at::kHalf,
                   "Paired half-turn polynomial sin D7/cos D6 with packed FP16 evaluation and output");
+    PT_DEF_SINCOS_COMPUTE(sincos_native_bf16_compute, at::kBFloat16,
+                          "Compute-saturated native sin/cos with BF16 output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d3_d4_bf16_compute, at::kBFloat16,
+                          "Compute-saturated packed-BF16 polynomial sin D3/cos D4");
+    PT_DEF_SINCOS_COMPUTE(sincos_d3_d4_quarter_turn_bf16_compute, at::kBFloat16,
+                          "Compute-saturated quarter-turn polynomial sin D3/cos D4 with packed BF16 "
+                          "evaluation and output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d3_d4_half_turn_bf16_compute, at::kBFloat16,
+                          "Compute-saturated half-turn polynomial sin D3/cos D4 with packed BF16 "
+                          "evaluation and output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d5_d6_half_turn_bf16_compute, at::kBFloat16,
+                          "Compute-saturated half-turn polynomial sin D5/cos D6 with packed BF16 "
+                          "evaluation and output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d5_d4_half_turn_fp16_bf16_compute, at::kBFloat16,
+                          "Compute-saturated half-turn polynomial sin D5/cos D4 with packed FP16 "
+                          "evaluation and BF16 output");
+    PT_DEF_SINCOS_COMPUTE(sincos_native_fp16_compute, at::kHalf,
+                          "Compute-saturated native sin/cos with FP16 output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d3_d4_quarter_turn_fp16_compute, at::kHalf,
+                          "Compute-saturated quarter-turn polynomial sin D3/cos D4 with packed FP16 "
+                          "evaluation and output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d3_d4_half_turn_fp16_compute, at::kHalf,
+                          "Compute-saturated half-turn polynomial sin D3/cos D4 with packed FP16 "
+                          "evaluation and output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d5_d4_half_turn_fp16_compute, at::kHalf,
+                          "Compute-saturated half-turn polynomial sin D5/cos D4 with packed FP16 "
+                          "evaluation and output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d5_d6_half_turn_fp16_compute, at::kHalf,
+                          "Compute-saturated half-turn polynomial sin D5/cos D6 with packed FP16 "
+                          "evaluation and output");
+    PT_DEF_SINCOS_COMPUTE(sincos_d7_d6_half_turn_fp16_compute, at::kHalf,
+                          "Compute-saturated half-turn polynomial sin D7/cos D6 with packed FP16 "
+                          "evaluation and output");
 #undef PT_DEF_SINCOS
-    m.def("rope_sincos_fixed_half_turn_d5_d6_fp16", &rope_sincos_fixed_half_turn_d5_d6_fp16,
+#undef PT_DEF_SINCOS_COMPUTE
+    m.def("rope_sincos_native_fp16",
+          [](at::Tensor f, int64_t sl) {
+              return rope_table(f, sl, at::kFloat, "frequencies", 2, launch_rope_sincos_native_fp16);
+          },
+          "RoPE-specific native sin/cos table generation with FP16 output");
+    m.def("rope_sincos_fixed_d3_d4_fp16",
+          [](at::Tensor inc, int64_t sl) {
+              return rope_table(inc, sl, at::kInt, "phase_increments", 2,
+                                launch_rope_sincos_fixed_d3_d4_fp16);
+          },
+          "RoPE-specific fixed-point phase reduction with packed FP16 sin D3/cos D4");
+    m.def("rope_sincos_fixed_half_turn_d5_d6_fp16",
+          [](at::Tensor inc, int64_t sl) {
+              return rope_table(inc, sl, at::kInt, "phase_increments", 4,
+                                launch_rope_sincos_fixed_half_turn_d5_d6_fp16);
+          },
           "RoPE-specific fixed-point half-turn reduction with FP16 sin D5/cos D6");
+    m.def("rope_sincos_fixed_lut_fp16",
+          [](at::Tensor inc, at::Tensor table, int64_t sl) {
+              return rope_sincos_fixed_lut_fp16(inc, table, sl, -1);
+          },
+          "RoPE-specific fixed-point phase lookup with packed FP16 linear correction");
+    m.def("rope_sincos_native_fp16_compute",
+          [](at::Tensor f, int64_t sl, int64_t it) {
+              return rope_table_compute(f, sl, it, at::kFloat, "frequencies", 2,
+                                        launch_rope_sincos_native_fp16_compute);
+          },
+          "Compute-saturated RoPE-specific native sin/cos with FP16 output");
+    m.def("rope_sincos_fixed_d3_d4_fp16_compute",
+          [](at::Tensor inc, int64_t sl, int64_t it) {
+              return rope_table_compute(inc, sl, it, at::kInt, "phase_increments", 2,
+                                        launch_rope_sincos_fixed_d3_d4_fp16_compute);
+          },
+          "Compute-saturated RoPE-specific fixed-point reduction with packed FP16 sin D3/cos D4");
+    m.def("rope_sincos_fixed_half_turn_d5_d6_fp16_compute",
+          [](at::Tensor inc, int64_t sl, int64_t it) {
+              return rope_table_compute(inc, sl, it, at::kInt, "phase_increments", 4,
+                                        launch_rope_sincos_fixed_half_turn_d5_d6_fp16_compute);
+          },
+          "Compute-saturated RoPE-specific fixed-point half-turn reduction with FP16 sin D5/cos D6");
+    m.def("rope_sincos_fixed_lut_fp16_compute",
+          [](at::Tensor inc, at::Tensor table, int64_t sl, int64_t it) {
+              TORCH_CHECK(it > 0, "iterations must be positive");
+              return rope_sincos_fixed_lut_fp16(inc, table, sl, it);
+          },
+          "Compute-saturated RoPE-specific fixed-point phase lookup with packed FP16 linear "
+          "correction");
+    m.def("rope_apply_cached_fp16",
+          [](at::Tensor q, at::Tensor k, at::Tensor table) {
+              return rope_apply(q, k, table, at::kHalf, at::kHalf, "rope_table",
+                                launch_rope_apply_cached_fp16);
+          },
+          "Fused cached-table FP16 Q/K rotary embedding and transpose");
     m.def("rope_apply_fixed_half_turn_d5_d6_fp16",
           [](at::Tensor q, at::Tensor k, at::Tensor inc) {
               return rope_apply(q, k, inc, at::kHalf, at::kInt, "phase_increments",

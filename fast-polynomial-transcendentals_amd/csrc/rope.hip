@@ -1,9 +1,10 @@
-// rope.hip -- paired sin/cos tables and fused rotary embedding (RoPE) for
-// gfx950, with their C ABI.
+// rope.hip -- rotary embedding (RoPE) sin/cos tables and the fused RoPE
+// apply for gfx950, with their C ABI.
 //
-// Tables: FP32 angles [n] -> [2, n] (plane 0 cos, plane 1 sin) in FP16 or
-// BF16; each thread reads 8 angles (two 16-byte loads) and writes one 16-byte
-// vector to each plane.
+// Tables: [2, S, F] FP16 (plane 0 cos, plane 1 sin) for positions 0..S-1 and
+// F frequencies; one thread per (position, frequency pair).  Fixed-point
+// programs take Q0.32 phase increments (turns per position), the native
+// baseline FP32 frequencies.
 //
 // Fused RoPE: Q [B, S, Hq, D] and K [B, S, Hk, D] (16-bit, even/odd
 // interleaved pairs) are rotated by angle position * omega_i and written
@@ -22,100 +23,46 @@
 namespace pt {
 
 // ---------------------------------------------------------------------------
-// sin/cos table evaluators: 2 angles -> (cos pair, sin pair) as 16-bit pairs
+// RoPE sin/cos tables: [2, S, F] FP16 (plane 0 cos, plane 1 sin)
+// (rope_sincos_*_fp16_kernel, sincos_kernels.cu:1387-1502, and their
+// *_compute_kernel probes, :1756-1932)
 // ---------------------------------------------------------------------------
 
-template <int P>
-struct F16HalfTurn {
-    __device__ __forceinline__ static void eval(float a0, float a1, uint32_t& c, uint32_t& s) {
-        f16_sincos<P>(a0, a1, c, s);
+// Pair sources: (position, frequency pair) -> (cos pair, sin pair).
+struct PairHalfD5D6 {  // Q0.32 phase, half-turn Q15 D5/D6
+    const uint32_t* inc;
+    __device__ __forceinline__ void eval(uint32_t pos, int64_t fp, uint32_t& c, uint32_t& s) const {
+        rope_q15_sincos(pos, inc[2 * fp], inc[2 * fp + 1], c, s);
+    }
+};
+struct PairQuarterD3D4 {  // Q0.32 phase, quarter-turn Q15 D3/D4
+    const uint32_t* inc;
+    __device__ __forceinline__ void eval(uint32_t pos, int64_t fp, uint32_t& c, uint32_t& s) const {
+        rope_q15_quarter_sincos(pos, inc[2 * fp], inc[2 * fp + 1], c, s);
+    }
+};
+struct PairLut {  // Q0.32 phase, 128-entry table + first-order correction
+    const uint32_t* inc;
+    const uint32_t* table;
+    __device__ __forceinline__ void eval(uint32_t pos, int64_t fp, uint32_t& c, uint32_t& s) const {
+        rope_lut_sincos(pos, inc[2 * fp], inc[2 * fp + 1], table, c, s);
+    }
+};
+struct PairNative {  // FP32 angle position * omega, hardware sin/cos
+    const float* freq;
+    __device__ __forceinline__ void eval(uint32_t pos, int64_t fp, uint32_t& c, uint32_t& s) const {
+        const float p = (float)pos;
+        NativeSinCos<false>::eval(p * freq[2 * fp], p * freq[2 * fp + 1], c, s);
     }
 };
 
-// FP16 evaluation, BF16 output (PolynomialD5D4HalfTurnFP16BF16, :922-940).
-template <int P>
-struct F16HalfTurnToBF16 {
-    __device__ __forceinline__ static void eval(float a0, float a1, uint32_t& c, uint32_t& s) {
-        uint32_t ch, sh;
-        f16_sincos<P>(a0, a1, ch, sh);
-        const h2_t cc = as_h2(ch), ss = as_h2(sh);
-        c = pack_bf((float)cc.x, (float)cc.y);
-        s = pack_bf((float)ss.x, (float)ss.y);
-    }
-};
-
-template <int P>
-struct BF16HalfTurn {
-    __device__ __forceinline__ static void eval(float a0, float a1, uint32_t& c, uint32_t& s) {
-        float c0, s0, c1, s1;
-        bf16_sincos_lane<P>(a0, c0, s0);
-        bf16_sincos_lane<P>(a1, c1, s1);
-        c = pack_exact_bf(c0, c1);
-        s = pack_exact_bf(s0, s1);
-    }
-};
-
-// Hardware transcendentals: __sinf/__cosf lower to v_sin_f32/v_cos_f32.
-template <bool BF>
-struct NativeSinCos {
-    __device__ __forceinline__ static void eval(float a0, float a1, uint32_t& c, uint32_t& s) {
-        const float c0 = __cosf(a0), s0 = __sinf(a0), c1 = __cosf(a1), s1 = __sinf(a1);
-        if constexpr (BF) {
-            c = pack_bf(c0, c1);
-            s = pack_bf(s0, s1);
-        } else {
-            c = as_u32((h2_t){(_Float16)c0, (_Float16)c1});
-            s = as_u32((h2_t){(_Float16)s0, (_Float16)s1});
-        }
-    }
-};
-
-template <class E>
+// iterations == 0: the table.  iterations > 0: the compute probe, whose entry
+// (pos, f) is the packed FP16 sum of the program at positions pos ..
+// pos + iterations - 1.
+template <class P>
 __global__ void __launch_bounds__(kBlock)
-sincos_table_kernel(const float* __restrict__ angles, uint16_t* __restrict__ out, int64_t n,
-                    int vec_ok) {
-    uint16_t* cos_plane = out;
-    uint16_t* sin_plane = out + n;
-    const int64_t stride = (int64_t)gridDim.x * kBlock;
-    const int64_t n8 = vec_ok ? (n >> 3) : 0;
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n8; i += stride) {
-        const Vec4 a = ld16<false>(angles, 2 * i);
-        const Vec4 b = ld16<false>(angles, 2 * i + 1);
-        const uint32_t w[8] = {a.w[0], a.w[1], a.w[2], a.w[3], b.w[0], b.w[1], b.w[2], b.w[3]};
-        Vec4 oc, os;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) E::eval(as_f32(w[2 * k]), as_f32(w[2 * k + 1]), oc.w[k], os.w[k]);
-        st16<false>(cos_plane, i, oc);
-        st16<false>(sin_plane, i, os);
-    }
-    for (int64_t e = (n8 << 3) + (int64_t)blockIdx.x * kBlock + threadIdx.x; e < n; e += stride) {
-        uint32_t c, s;
-        E::eval(angles[e], angles[e], c, s);
-        cos_plane[e] = (uint16_t)(c & 0xffffu);
-        sin_plane[e] = (uint16_t)(s & 0xffffu);
-    }
-}
-
-template <class E>
-int launch_sincos_table(void* out, const void* angles, int64_t n, void* stream) {
-    if (bad_args(n, {out, angles})) return hipErrorInvalidValue;
-    if (n == 0) return hipSuccess;
-    // Both planes are 16-byte aligned only when n is a multiple of 8.
-    const int vec_ok = aligned16(out) && aligned16(angles) && (n % 8 == 0);
-    const int64_t grid = grid_one_pass(vec_ok ? (n >> 3) : n);
-    hipLaunchKernelGGL((sincos_table_kernel<E>), dim3((unsigned)grid), dim3(kBlock), 0, hs(stream),
-                       (const float*)angles, (uint16_t*)out, n, vec_ok);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// RoPE phase table: [2, S, F] FP16 from Q0.32 phase increments
-// (rope_sincos_fixed_half_turn_d5_d6_fp16, sincos_kernels.cu:1387-1502)
-// ---------------------------------------------------------------------------
-
-__global__ void __launch_bounds__(kBlock)
-rope_sincos_table_kernel(const uint32_t* __restrict__ inc, uint16_t* __restrict__ out, int64_t seq,
-                         int64_t nfreq) {
+rope_sincos_table_kernel(P src, uint16_t* __restrict__ out, int64_t seq, int64_t nfreq,
+                         int iterations) {
     const int64_t pairs_per_row = nfreq / 2;
     const int64_t total = seq * pairs_per_row;
     const int64_t stride = (int64_t)gridDim.x * kBlock;
@@ -125,10 +72,37 @@ rope_sincos_table_kernel(const uint32_t* __restrict__ inc, uint16_t* __restrict_
         const int64_t pos = t / pairs_per_row;
         const int64_t fp = t - pos * pairs_per_row;
         uint32_t c, s;
-        rope_q15_sincos((uint32_t)pos, inc[2 * fp], inc[2 * fp + 1], c, s);
+        if (iterations == 0) {
+            src.eval((uint32_t)pos, fp, c, s);
+        } else {
+            h2_t cs = {(_Float16)0.0f, (_Float16)0.0f}, ss = cs;
+#pragma unroll 1
+            for (int it = 0; it < iterations; ++it) {
+                src.eval((uint32_t)(pos + it), fp, c, s);
+                cs = cs + as_h2(c);
+                ss = ss + as_h2(s);
+            }
+            c = as_u32(cs);
+            s = as_u32(ss);
+        }
         cos_plane[t] = c;
         sin_plane[t] = s;
     }
+}
+
+template <class P>
+int launch_rope_table(void* out, P src, const void* param, const void* extra, int64_t seq,
+                      int64_t nfreq, int64_t iterations, void* stream) {
+    if (seq < 0 || nfreq < 0 || (nfreq % 2) != 0 || iterations < 0 || iterations > 0x7fffffff)
+        return hipErrorInvalidValue;
+    if (seq == 0 || nfreq == 0) return hipSuccess;
+    if (!out || !param || !extra) return hipErrorInvalidValue;
+    if (((uintptr_t)out & 3u) != 0 || ((uintptr_t)param & 3u) != 0 || ((uintptr_t)extra & 3u) != 0)
+        return hipErrorInvalidValue;
+    const int64_t grid = grid_one_pass(seq * nfreq / 2);
+    hipLaunchKernelGGL((rope_sincos_table_kernel<P>), dim3((unsigned)grid), dim3(kBlock), 0,
+                       hs(stream), src, (uint16_t*)out, seq, nfreq, (int)iterations);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -161,6 +135,24 @@ struct RopeNativeAngle {
         const float p = (float)pos;
         NativeSinCos<false>::eval(p * f.x, p * f.y, c[0], s[0]);
         NativeSinCos<false>::eval(p * f.z, p * f.w, c[1], s[1]);
+    }
+};
+
+// Precomputed table [2, S, D/2] FP16 (rope_apply_cached_fp16_kernel,
+// sincos_kernels.cu:1614-1652): 8-byte loads of cos and sin for the four
+// frequencies of the vector.
+struct RopeCachedTable {
+    const uint16_t* table;
+    int64_t plane;  // S * D/2
+    int64_t nfreq;  // D/2
+    __device__ __forceinline__ void eval(uint32_t pos, int64_t fg, uint32_t (&c)[2], uint32_t (&s)[2]) const {
+        const int64_t off = (int64_t)pos * nfreq + 4 * fg;
+        const uint2 cv = *reinterpret_cast<const uint2*>(table + off);
+        const uint2 sv = *reinterpret_cast<const uint2*>(table + plane + off);
+        c[0] = cv.x;
+        c[1] = cv.y;
+        s[0] = sv.x;
+        s[1] = sv.y;
     }
 };
 
@@ -293,37 +285,76 @@ int launch_rope(void* q_out, void* k_out, const void* q, const void* k, Angles a
 
 using namespace pt;
 
-// ---- tables ----------------------------------------------------------------
-
-#define PT_SINCOS(name, EVAL)                                                         \
-    extern "C" int name(void* out, const void* angles, int64_t size, void* stream) {  \
-        return launch_sincos_table<PT_STRIP EVAL>(out, angles, size, stream);         \
-    }
-
-PT_SINCOS(launch_sincos_native_bf16, (NativeSinCos<true>))
-PT_SINCOS(launch_sincos_d3_d4_half_turn_bf16, (BF16HalfTurn<kBf16HalfD3D4>))
-PT_SINCOS(launch_sincos_d5_d6_half_turn_bf16, (BF16HalfTurn<kBf16HalfD5D6>))
-PT_SINCOS(launch_sincos_d5_d4_half_turn_fp16_bf16, (F16HalfTurnToBF16<kF16HalfD5D4>))
-PT_SINCOS(launch_sincos_native_fp16, (NativeSinCos<false>))
-PT_SINCOS(launch_sincos_d3_d4_half_turn_fp16, (F16HalfTurn<kF16HalfD3D4>))
-PT_SINCOS(launch_sincos_d5_d4_half_turn_fp16, (F16HalfTurn<kF16HalfD5D4>))
-PT_SINCOS(launch_sincos_d5_d6_half_turn_fp16, (F16HalfTurn<kF16HalfD5D6>))
-PT_SINCOS(launch_sincos_d7_d6_half_turn_fp16, (F16HalfTurn<kF16HalfD7D6>))
+// ---- tables and compute probes ---------------------------------------------------
 
 extern "C" int launch_rope_sincos_fixed_half_turn_d5_d6_fp16(void* out, const void* phase_increments,
                                                              int64_t sequence_length,
                                                              int64_t frequency_count, void* stream) {
-    if (sequence_length < 0 || frequency_count < 0 || (frequency_count % 2) != 0)
-        return hipErrorInvalidValue;
-    if (sequence_length == 0 || frequency_count == 0) return hipSuccess;
-    if (!out || !phase_increments) return hipErrorInvalidValue;
-    if (((uintptr_t)out & 3u) != 0 || ((uintptr_t)phase_increments & 3u) != 0)
-        return hipErrorInvalidValue;
-    const int64_t grid = grid_one_pass(sequence_length * frequency_count / 2);
-    hipLaunchKernelGGL(rope_sincos_table_kernel, dim3((unsigned)grid), dim3(kBlock), 0, hs(stream),
-                       (const uint32_t*)phase_increments, (uint16_t*)out, sequence_length,
-                       frequency_count);
-    return hipGetLastError();
+    return launch_rope_table(out, PairHalfD5D6{(const uint32_t*)phase_increments}, phase_increments,
+                             phase_increments, sequence_length, frequency_count, 0, stream);
+}
+
+extern "C" int launch_rope_sincos_fixed_d3_d4_fp16(void* out, const void* phase_increments,
+                                                   int64_t sequence_length, int64_t frequency_count,
+                                                   void* stream) {
+    return launch_rope_table(out, PairQuarterD3D4{(const uint32_t*)phase_increments},
+                             phase_increments, phase_increments, sequence_length, frequency_count,
+                             0, stream);
+}
+
+extern "C" int launch_rope_sincos_fixed_lut_fp16(void* out, const void* phase_increments,
+                                                 const void* phase_table, int64_t sequence_length,
+                                                 int64_t frequency_count, void* stream) {
+    return launch_rope_table(out,
+                             PairLut{(const uint32_t*)phase_increments, (const uint32_t*)phase_table},
+                             phase_increments, phase_table, sequence_length, frequency_count, 0,
+                             stream);
+}
+
+extern "C" int launch_rope_sincos_native_fp16(void* out, const void* frequencies,
+                                              int64_t sequence_length, int64_t frequency_count,
+                                              void* stream) {
+    return launch_rope_table(out, PairNative{(const float*)frequencies}, frequencies, frequencies,
+                             sequence_length, frequency_count, 0, stream);
+}
+
+extern "C" int launch_rope_sincos_fixed_half_turn_d5_d6_fp16_compute(
+    void* out, const void* phase_increments, int64_t sequence_length, int64_t frequency_count,
+    int64_t iterations, void* stream) {
+    if (iterations <= 0) return hipErrorInvalidValue;
+    return launch_rope_table(out, PairHalfD5D6{(const uint32_t*)phase_increments}, phase_increments,
+                             phase_increments, sequence_length, frequency_count, iterations, stream);
+}
+
+extern "C" int launch_rope_sincos_fixed_d3_d4_fp16_compute(void* out, const void* phase_increments,
+                                                           int64_t sequence_length,
+                                                           int64_t frequency_count,
+                                                           int64_t iterations, void* stream) {
+    if (iterations <= 0) return hipErrorInvalidValue;
+    return launch_rope_table(out, PairQuarterD3D4{(const uint32_t*)phase_increments},
+                             phase_increments, phase_increments, sequence_length, frequency_count,
+                             iterations, stream);
+}
+
+extern "C" int launch_rope_sincos_fixed_lut_fp16_compute(void* out, const void* phase_increments,
+                                                         const void* phase_table,
+                                                         int64_t sequence_length,
+                                                         int64_t frequency_count,
+                                                         int64_t iterations, void* stream) {
+    if (iterations <= 0) return hipErrorInvalidValue;
+    return launch_rope_table(out,
+                             PairLut{(const uint32_t*)phase_increments, (const uint32_t*)phase_table},
+                             phase_increments, phase_table, sequence_length, frequency_count,
+                             iterations, stream);
+}
+
+extern "C" int launch_rope_sincos_native_fp16_compute(void* out, const void* frequencies,
+                                                      int64_t sequence_length,
+                                                      int64_t frequency_count, int64_t iterations,
+                                                      void* stream) {
+    if (iterations <= 0) return hipErrorInvalidValue;
+    return launch_rope_table(out, PairNative{(const float*)frequencies}, frequencies, frequencies,
+                             sequence_length, frequency_count, iterations, stream);
 }
 
 // ---- fused apply -------------------------------------------------------------
@@ -366,4 +397,15 @@ extern "C" int launch_rope_apply_native_bf16(void* q_out, void* k_out, const voi
                                               RopeNativeAngle{(const float*)frequencies},
                                               frequencies, batch, sequence_length, q_heads,
                                               k_heads, head_dim, stream);
+}
+
+extern "C" int launch_rope_apply_cached_fp16(void* q_out, void* k_out, const void* q, const void* k,
+                                             const void* rope_table, int64_t batch,
+                                             int64_t sequence_length, int64_t q_heads,
+                                             int64_t k_heads, int64_t head_dim, void* stream) {
+    if (sequence_length < 0 || head_dim < 0) return hipErrorInvalidValue;
+    return launch_rope<RopeCachedTable, false>(
+        q_out, k_out, q, k,
+        RopeCachedTable{(const uint16_t*)rope_table, sequence_length * (head_dim / 2), head_dim / 2},
+        rope_table, batch, sequence_length, q_heads, k_heads, head_dim, stream);
 }

@@ -249,39 +249,111 @@ int launch_exp2_d3_f32(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_native_f32(void* y, const void* x, int64_t size, void* stream);
 
 /* ---- paired sin/cos tables: FP32 angles [size] -> out [2, size] ----------
- * Plane 0 holds cos, plane 1 sin.  Replaces launch_sincos_*_{bf16,fp16}
- * (sincos_kernels.cu:2123-2978; binding spline_ops.cpp:326-560): half-turn
- * reduction with the 1.5*2^23 shifter and a one-term FP32 pi, then the
- * packed polynomial of each name. */
+ * Plane 0 holds cos, plane 1 sin.  Replaces launch_sincos_*_{bf16,fp16,f32}
+ * (declared spline_ops.cpp:16-57, defined sincos_kernels.cu:2125-2668;
+ * binding spline_ops.cpp:326-580, 980-1100).  Programs (sincos_kernels.cu):
+ *   half_turn   1.5*2^23 shifter, one-term FP32 pi, sign = parity(k), packed
+ *               16-bit polynomial (:644-920);
+ *   quarter_turn shifter, one-term FP32 pi/2, quadrant swap + signs (:544-642);
+ *   d3_d4_bf16  Cody-Waite pi/2 with a converted quadrant, BF16 program
+ *               (:940-978);
+ *   _f32        FP32 programs (:120-406): d3_d4 / d5_d4 / d7_d6 Cody-Waite
+ *               quarter turn, d3_d4_magic_bias shifter quarter turn,
+ *               d5_d4_half_turn_{ls,sollya} two-term pi half turn,
+ *               d5_d4_half_turn_sollya_fast one-term pi, d3_d4_cycle in
+ *               turns folded to [0, 1/8];
+ *   native      v_sin_f32 / v_cos_f32 (__sinf / __cosf), rounded to the
+ *               output format (the reference calls sincosf). */
 #define SPLINE_HIP_SINCOS_LAUNCHERS(X)                                          \
-    X(launch_sincos_native_bf16) X(launch_sincos_d3_d4_half_turn_bf16)          \
+    X(launch_sincos_native_bf16) X(launch_sincos_d3_d4_bf16)                    \
+    X(launch_sincos_d3_d4_quarter_turn_bf16) X(launch_sincos_d3_d4_half_turn_bf16) \
     X(launch_sincos_d5_d6_half_turn_bf16) X(launch_sincos_d5_d4_half_turn_fp16_bf16) \
-    X(launch_sincos_native_fp16) X(launch_sincos_d3_d4_half_turn_fp16)          \
-    X(launch_sincos_d5_d4_half_turn_fp16) X(launch_sincos_d5_d6_half_turn_fp16) \
-    X(launch_sincos_d7_d6_half_turn_fp16)
+    X(launch_sincos_native_fp16) X(launch_sincos_d3_d4_quarter_turn_fp16)       \
+    X(launch_sincos_d3_d4_half_turn_fp16) X(launch_sincos_d5_d4_half_turn_fp16) \
+    X(launch_sincos_d5_d6_half_turn_fp16) X(launch_sincos_d7_d6_half_turn_fp16) \
+    X(launch_sincos_native_f32) X(launch_sincos_d3_d4_f32)                      \
+    X(launch_sincos_d3_d4_cycle_f32) X(launch_sincos_d3_d4_magic_bias_f32)      \
+    X(launch_sincos_d5_d4_half_turn_ls_f32) X(launch_sincos_d5_d4_half_turn_sollya_f32) \
+    X(launch_sincos_d5_d4_half_turn_sollya_fast_f32) X(launch_sincos_d5_d4_f32) \
+    X(launch_sincos_d7_d6_f32)
 #define SPLINE_HIP_DECLARE_SINCOS(name) \
     int name(void* out, const void* angles, int64_t size, void* stream);
 SPLINE_HIP_SINCOS_LAUNCHERS(SPLINE_HIP_DECLARE_SINCOS)
+
+/* Repeated-evaluation probes of the same programs (replace
+ * launch_sincos_*_compute*, sincos_kernels.cu:2233-2668): element i
+ * evaluates its program `iterations` (> 0) times on a probe angle that
+ * starts at angles[i] and steps p <- fma(p, 0.99999994, 2^-13), and stores
+ * the running sums of cos and sin (FP32 adds, or packed 16-bit adds for the
+ * 16-bit programs).  They time instruction issue, not memory. */
+#define SPLINE_HIP_SINCOS_COMPUTE_LAUNCHERS(X)                                  \
+    X(launch_sincos_native_bf16_compute) X(launch_sincos_d3_d4_bf16_compute)    \
+    X(launch_sincos_d3_d4_quarter_turn_bf16_compute) X(launch_sincos_d3_d4_half_turn_bf16_compute) \
+    X(launch_sincos_d5_d6_half_turn_bf16_compute) X(launch_sincos_d5_d4_half_turn_fp16_bf16_compute) \
+    X(launch_sincos_native_fp16_compute) X(launch_sincos_d3_d4_quarter_turn_fp16_compute) \
+    X(launch_sincos_d3_d4_half_turn_fp16_compute) X(launch_sincos_d5_d4_half_turn_fp16_compute) \
+    X(launch_sincos_d5_d6_half_turn_fp16_compute) X(launch_sincos_d7_d6_half_turn_fp16_compute) \
+    X(launch_sincos_native_compute_f32) X(launch_sincos_d3_d4_compute_f32)      \
+    X(launch_sincos_d3_d4_cycle_compute_f32) X(launch_sincos_d3_d4_magic_bias_compute_f32) \
+    X(launch_sincos_d5_d4_half_turn_ls_compute_f32) X(launch_sincos_d5_d4_half_turn_sollya_compute_f32) \
+    X(launch_sincos_d5_d4_half_turn_sollya_fast_compute_f32) X(launch_sincos_d5_d4_compute_f32) \
+    X(launch_sincos_d7_d6_compute_f32)
+#define SPLINE_HIP_DECLARE_SINCOS_COMPUTE(name) \
+    int name(void* out, const void* angles, int64_t size, int64_t iterations, void* stream);
+SPLINE_HIP_SINCOS_COMPUTE_LAUNCHERS(SPLINE_HIP_DECLARE_SINCOS_COMPUTE)
 
 /* ---- RoPE ------------------------------------------------------------------
  * Phase increments are int32 Q0.32 turns per position, round(omega_i *
  * 2^32 / (2 pi)) (src/sfu_repro/rope/benchmark_cuda_fused_rope.py:238-241),
  * one per frequency (head_dim / 2 of them).
- * launch_rope_sincos_fixed_half_turn_d5_d6_fp16: table [2, S, F] FP16
- * (replaces the launcher of sincos_kernels.cu:2871-2905).
+ *
+ * Tables [2, S, F] FP16 for positions 0..S-1 (F even; replace
+ * launch_rope_sincos_*_fp16, declared spline_ops.cpp:58-61, defined
+ * sincos_kernels.cu:2671-2768):
+ *   fixed_half_turn_d5_d6  Q15 half-turn residual, D5/D6 (:1289-1348);
+ *   fixed_d3_d4            Q15 quarter-turn residual + quadrant, D3/D4
+ *                          (:1242-1287);
+ *   fixed_lut              128-entry table of FP16 (sin, cos) pairs per turn
+ *                          (phase_table [128, 2], sin first) plus a
+ *                          first-order correction (:1350-1385);
+ *   native                 FP32 frequencies omega_i, angle = position *
+ *                          omega_i, v_sin_f32 / v_cos_f32.
+ * The _compute forms (replace the launchers of :2871-2978) store, for entry
+ * (pos, f), the packed FP16 sum over positions pos .. pos + iterations - 1.
+ *
  * launch_rope_apply_*: Q [B, S, Hq, D], K [B, S, Hk, D] (even/odd pairs
  * interleaved) -> rotated Q [B, Hq, S, D], K [B, Hk, S, D]; replaces
- * launch_rope_apply_{fixed_half_turn_d5_d6,native}_fp16
- * (sincos_kernels.cu:2769-2870); the _bf16 entry points are new (the
- * reference's fused RoPE is FP16 only, spline_ops.cpp:838-839).  `native`
- * takes FP32 frequencies omega_i instead of increments.  head_dim must be a
+ * launch_rope_apply_{cached,native,fixed_half_turn_d5_d6}_fp16
+ * (spline_ops.cpp:66-68; sincos_kernels.cu:2769-2870); the _bf16 entry points
+ * are new (the reference's fused RoPE is FP16 only, spline_ops.cpp:838-839).
+ * `angle_params` is the increments (fixed), the FP32 frequencies omega_i
+ * (native) or a [2, S, D/2] FP16 cos/sin table (cached).  head_dim must be a
  * multiple of 8 and every pointer 16-byte aligned. */
-int launch_rope_sincos_fixed_half_turn_d5_d6_fp16(void* out, const void* phase_increments,
-                                                  int64_t sequence_length, int64_t frequency_count,
-                                                  void* stream);
+#define SPLINE_HIP_ROPE_TABLE_LAUNCHERS(X)                                      \
+    X(launch_rope_sincos_fixed_half_turn_d5_d6_fp16) X(launch_rope_sincos_fixed_d3_d4_fp16) \
+    X(launch_rope_sincos_native_fp16)
+#define SPLINE_HIP_DECLARE_ROPE_TABLE(name)                                     \
+    int name(void* out, const void* params, int64_t sequence_length,            \
+             int64_t frequency_count, void* stream);
+SPLINE_HIP_ROPE_TABLE_LAUNCHERS(SPLINE_HIP_DECLARE_ROPE_TABLE)
+#define SPLINE_HIP_ROPE_TABLE_COMPUTE_LAUNCHERS(X)                              \
+    X(launch_rope_sincos_fixed_half_turn_d5_d6_fp16_compute)                    \
+    X(launch_rope_sincos_fixed_d3_d4_fp16_compute) X(launch_rope_sincos_native_fp16_compute)
+#define SPLINE_HIP_DECLARE_ROPE_TABLE_COMPUTE(name)                             \
+    int name(void* out, const void* params, int64_t sequence_length,            \
+             int64_t frequency_count, int64_t iterations, void* stream);
+SPLINE_HIP_ROPE_TABLE_COMPUTE_LAUNCHERS(SPLINE_HIP_DECLARE_ROPE_TABLE_COMPUTE)
+int launch_rope_sincos_fixed_lut_fp16(void* out, const void* phase_increments,
+                                      const void* phase_table, int64_t sequence_length,
+                                      int64_t frequency_count, void* stream);
+int launch_rope_sincos_fixed_lut_fp16_compute(void* out, const void* phase_increments,
+                                              const void* phase_table, int64_t sequence_length,
+                                              int64_t frequency_count, int64_t iterations,
+                                              void* stream);
 #define SPLINE_HIP_ROPE_APPLY_LAUNCHERS(X)                                      \
     X(launch_rope_apply_fixed_half_turn_d5_d6_fp16) X(launch_rope_apply_fixed_half_turn_d5_d6_bf16) \
-    X(launch_rope_apply_native_fp16) X(launch_rope_apply_native_bf16)
+    X(launch_rope_apply_native_fp16) X(launch_rope_apply_native_bf16)          \
+    X(launch_rope_apply_cached_fp16)
 #define SPLINE_HIP_DECLARE_ROPE_APPLY(name)                                     \
     int name(void* q_out, void* k_out, const void* q, const void* k,            \
              const void* angle_params, int64_t batch, int64_t sequence_length,  \

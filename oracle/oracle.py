@@ -91,12 +91,17 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_sincos.argtypes = [ci, ci, ci, f32p, u16p, u16p, i64]
     l.orc_rope_sincos_table.argtypes = [i32p, u16p, i64, i64]
     l.orc_rope_apply.argtypes = [ci, u16p, u16p, i32p, u16p, u16p, i64, i64, i64, i64, i64]
+    l.orc_sincos_f32.argtypes = [ci, f32p, f32p, f32p, i64, ci]
+    l.orc_sincos16.argtypes = [ci, ci, ci, f32p, u16p, u16p, i64, ci]
+    l.orc_rope_table.argtypes = [ci, i32p, u16p, u16p, i64, i64, ci]
+    l.orc_rope_apply_cached.argtypes = [u16p, u16p, u16p, u16p, u16p, i64, i64, i64, i64, i64]
     for name in (
         "orc_activation", "orc_activation_bwd", "orc_activation_bwd_alg",
         "orc_swish_mul_fwd", "orc_swish_mul_bwd", "orc_b3_direct_bf16",
         "orc_b3_direct_f32", "orc_b3_constants", "orc_num_threads", "orc_softcap_fwd_bf16",
         "orc_softcap_bwd_bf16", "orc_exp2", "orc_sincos", "orc_rope_sincos_table",
-        "orc_rope_apply",
+        "orc_rope_apply", "orc_sincos_f32", "orc_sincos16", "orc_rope_table",
+        "orc_rope_apply_cached",
     ):
         getattr(l, name).restype = ctypes.c_int
 
@@ -261,6 +266,66 @@ def sincos(prog: int, angles: np.ndarray, out_fmt=None, rnd: int = RND_SINGLE):
     _check(lib().orc_sincos(prog, fmt_id(out_fmt), rnd, _p(a, ctypes.c_float), _p(c), _p(s),
                             a.size))
     return c, s
+
+
+# every 16-bit program (orc_sincos16): the half-turn ids above plus
+SC_F16_QUARTER_D3D4, SC_BF16_QUARTER_D3D4, SC_BF16_CW_D3D4 = 6, 7, 8
+# FP32 programs (orc_sincos_f32)
+SC32_D3D4, SC32_D3D4_SHIFT, SC32_D5D4, SC32_D7D6 = 0, 1, 2, 3
+SC32_HALF_D5D4_LS, SC32_HALF_D5D4_SOLLYA, SC32_HALF_D5D4_SOLLYA_FAST, SC32_CYCLE = 4, 5, 6, 7
+
+
+def sincos16(prog: int, angles: np.ndarray, out_fmt=None, iterations: int = 0,
+             rnd: int = RND_SINGLE):
+    """(cos bits, sin bits) of any 16-bit program; iterations > 0 gives the
+    compute probe's sums."""
+    a = np.ascontiguousarray(angles, dtype=np.float32)
+    if out_fmt is None:
+        out_fmt = BF16 if prog in (SC_BF16_D3D4, SC_BF16_D5D6, SC_BF16_QUARTER_D3D4,
+                                   SC_BF16_CW_D3D4) else F16
+    c = np.empty(a.shape, dtype=np.uint16)
+    s = np.empty(a.shape, dtype=np.uint16)
+    _check(lib().orc_sincos16(prog, fmt_id(out_fmt), rnd, _p(a, ctypes.c_float), _p(c), _p(s),
+                              a.size, iterations))
+    return c, s
+
+
+def sincos_f32(prog: int, angles: np.ndarray, iterations: int = 0):
+    """(cos, sin) float32 of an FP32 program; iterations > 0: probe sums."""
+    a = np.ascontiguousarray(angles, dtype=np.float32)
+    c = np.empty(a.shape, dtype=np.float32)
+    s = np.empty(a.shape, dtype=np.float32)
+    _check(lib().orc_sincos_f32(prog, _p(a, ctypes.c_float), _p(c, ctypes.c_float),
+                                _p(s, ctypes.c_float), a.size, iterations))
+    return c, s
+
+
+ROPE_HALF_D5D6, ROPE_QUARTER_D3D4, ROPE_LUT = 0, 1, 2
+
+
+def rope_table(kind: int, inc: np.ndarray, seq: int, lut: np.ndarray = None,
+               iterations: int = 0) -> np.ndarray:
+    """[2, seq, F] FP16 bits of a RoPE table program (or its probe sums)."""
+    inc = np.ascontiguousarray(inc, dtype=np.int32)
+    out = np.empty((2, seq, inc.size), dtype=np.uint16)
+    lp = None
+    if lut is not None:
+        lut = _u16(lut)
+        lp = _p(lut)
+    _check(lib().orc_rope_table(kind, _p(inc, ctypes.c_int32), lp, _p(out), seq, inc.size,
+                                iterations))
+    return out
+
+
+def rope_apply_cached(q: np.ndarray, k: np.ndarray, table: np.ndarray):
+    """FP16 q [B,S,Hq,D], k [B,S,Hk,D] rotated by a [2,S,D/2] FP16 table."""
+    q, k, table = _u16(q), _u16(k), _u16(table)
+    b, s, hq, d = q.shape
+    hk = k.shape[2]
+    qo = np.empty((b, hq, s, d), dtype=np.uint16)
+    ko = np.empty((b, hk, s, d), dtype=np.uint16)
+    _check(lib().orc_rope_apply_cached(_p(q), _p(k), _p(table), _p(qo), _p(ko), b, s, hq, hk, d))
+    return qo, ko
 
 
 def rope_sincos_table(inc: np.ndarray, seq: int) -> np.ndarray:

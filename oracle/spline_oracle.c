@@ -905,6 +905,357 @@ int orc_rope_apply(int fmt, const uint16_t* q, const uint16_t* kk, const int32_t
 }
 
 /* ------------------------------------------------------------------------ */
+/* quarter-turn and FP32 sin/cos programs, compute probes, RoPE variants     */
+/* (sincos_kernels.cu:24-406, 544-642, 940-978, 1014-1240, 1242-1934)        */
+/* ------------------------------------------------------------------------ */
+
+/* cvt.rni.s32.f32: round to nearest even, saturate, NaN -> 0. */
+static int32_t cvt_rni(float v) {
+    if (isnan(v)) return 0;
+    float r = rintf(v);
+    if (r >= 2147483648.0f) return INT32_MAX;
+    if (r < -2147483648.0f) return INT32_MIN;
+    return (int32_t)r;
+}
+
+static uint32_t f32_bits(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    return u;
+}
+
+static float xor_sign32(float v, uint32_t sign) {
+    uint32_t u = f32_bits(v) ^ sign;
+    memcpy(&v, &u, 4);
+    return v;
+}
+
+/* reduce_to_quarter_turn (:24-37): Cody-Waite pi/2, converted quadrant. */
+static void reduce_quarter_cw(float angle, float* r, uint32_t* quadrant) {
+    const float inv_half_pi = 0.63661977236758134308f;
+    const float hi = 1.57079625129699707031f, lo = 7.54978941586159635335e-08f;
+    int32_t q = cvt_rni(angle * inv_half_pi);
+    float qf = (float)q;
+    float red = fmaf(qf, -hi, angle);
+    *r = fmaf(qf, -lo, red);
+    *quadrant = (uint32_t)q;
+}
+
+/* reduce_to_quarter_turn_magic_bias{,_fast} (:39-70): shifter rounding,
+ * quadrant from the low bits of the biased sum. */
+static void reduce_quarter_shift(float angle, int two_term, float* r, uint32_t* quadrant) {
+    const float inv_half_pi = 0.63661977236758134308f;
+    const float shifter = 12582912.0f;
+    float biased = fmaf(angle, inv_half_pi, shifter);
+    float kk = biased - shifter;
+    if (two_term) {
+        float red = fmaf(kk, -1.57079625129699707031f, angle);
+        *r = fmaf(kk, -7.54978941586159635335e-08f, red);
+    } else {
+        *r = fmaf(kk, -1.57079637050628662109375f, angle);
+    }
+    *quadrant = f32_bits(biased);
+}
+
+/* reduce_to_half_turn_magic_bias (:72-86): two-term pi. */
+static void reduce_half_turn_two_term(float angle, float* r, uint32_t* sign) {
+    const float inv_pi = 0.31830988618379067154f;
+    const float shifter = 12582912.0f;
+    float biased = fmaf(angle, inv_pi, shifter);
+    float kk = biased - shifter;
+    float red = fmaf(kk, -3.141592502593994140625f, angle);
+    *r = fmaf(kk, -1.50995788317231927067e-07f, red);
+    *sign = (f32_bits(biased) & 1u) << 31;
+}
+
+/* restore_quadrant (:104-118) on values of any format (sign flips are exact). */
+static void restore_quadrant_d(double sr, double cr, uint32_t q, double* s, double* c) {
+    int swap = (q & 1u) != 0;
+    double sm = swap ? cr : sr, cm = swap ? sr : cr;
+    *s = (q & 2u) ? -sm : sm;
+    *c = ((q + 1u) & 2u) ? -cm : cm;
+}
+
+typedef struct {
+    int red;    /* 0 Cody-Waite quarter, 1 two-term shifter quarter,
+                   2 two-term half, 3 one-term half */
+    int ns;
+    float s[4];
+    int nc;
+    float c[4];
+} sincos32_t;
+
+/* Same order as F32SinCosId of the device code. */
+static const sincos32_t SINCOS32[7] = {
+    /* PolynomialD3D4, :129-160 */
+    {0, 2, {-0.16034401953220367431640625f, 0.99903142452239990234375f}, 3,
+     {0.0403986163437366485595703125f, -0.4997082054615020751953125f, 0.999990046024322509765625f}},
+    /* PolynomialD3D4MagicBias, :207-237 */
+    {1, 2, {-0.16034401953220367431640625f, 0.99903142452239990234375f}, 3,
+     {0.0403986163437366485595703125f, -0.4997082054615020751953125f, 0.999990046024322509765625f}},
+    /* PolynomialD5D4, :331-365 */
+    {0, 3, {0.008137642405927181f, -0.16661198437213898f, 0.9999962449073792f}, 3,
+     {0.04051213711500168f, -0.499763548374176f, 0.999993085861206f}},
+    /* PolynomialD7D6, :367-406 */
+    {0, 4, {-0.00019484198128338903f, 0.00833179522305727f, -0.1666664183139801f, 1.0f}, 4,
+     {-0.0013605882413685322f, 0.041656624525785446f, -0.49999886751174927f, 1.0f}},
+    /* PolynomialD5D4HalfTurnLS, :263-279 */
+    {2, 3, {0.00757423602044582366943359375f, -0.16582702100276947021484375f,
+            0.999771416187286376953125f}, 3,
+     {0.0372092612087726593017578125f, -0.4963922202587127685546875f, 0.999579489231109619140625f}},
+    /* PolynomialD5D4HalfTurnSollya, :281-297 */
+    {2, 3, {0.0075143859721720218658447265625f, -0.1656731069087982177734375f,
+            0.999696791172027587890625f}, 3,
+     {0.03679168224334716796875f, -0.495580852031707763671875f, 0.9994032382965087890625f}},
+    /* PolynomialD5D4HalfTurnSollyaFast, :299-329 */
+    {3, 3, {0.0075143859721720218658447265625f, -0.1656731069087982177734375f,
+            0.999696791172027587890625f}, 3,
+     {0.03679168224334716796875f, -0.495580852031707763671875f, 0.9994032382965087890625f}},
+};
+
+/* prog 0..6: SINCOS32[]; prog 7: PolynomialD3D4Cycle (:162-205). */
+static void sincos32_eval(int prog, float angle, float* c_out, float* s_out) {
+    if (prog == 7) {
+        const float inv_two_pi = 0.15915494309189533577f;
+        float cycles = angle * inv_two_pi;
+        float wrapped = cycles - rintf(cycles);
+        uint32_t sin_sign = f32_bits(wrapped) & 0x80000000u;
+        float r = fabsf(wrapped);
+        int outer = r > 0.25f;
+        if (outer) r = 0.5f - r;
+        int swap = r > 0.125f;
+        if (swap) r = 0.25f - r;
+        float sq = r * r;
+        float sr = r * fmaf(-39.77336883544921875f, sq, 6.277099609375f);
+        float cr = fmaf(62.96308135986328125f, sq, -19.7276897430419921875f);
+        cr = fmaf(cr, sq, 0.999990046024322509765625f);
+        float sm = swap ? cr : sr, cm = swap ? sr : cr;
+        *s_out = xor_sign32(sm, sin_sign);
+        *c_out = xor_sign32(cm, (uint32_t)outer << 31);
+        return;
+    }
+    const sincos32_t* q = &SINCOS32[prog];
+    float r;
+    uint32_t qd;
+    switch (q->red) {
+    case 0: reduce_quarter_cw(angle, &r, &qd); break;
+    case 1: reduce_quarter_shift(angle, 1, &r, &qd); break;
+    case 2: reduce_half_turn_two_term(angle, &r, &qd); break;
+    default: {
+        int neg;
+        reduce_half_turn(angle, &r, &neg);
+        qd = (uint32_t)neg << 31;
+    }
+    }
+    float sq = r * r;
+    float sp = fmaf(q->s[0], sq, q->s[1]);
+    for (int i = 2; i < q->ns; ++i) sp = fmaf(sp, sq, q->s[i]);
+    float sr = r * sp;
+    float cp = fmaf(q->c[0], sq, q->c[1]);
+    for (int i = 2; i < q->nc; ++i) cp = fmaf(cp, sq, q->c[i]);
+    if (q->red <= 1) {
+        int swap = (qd & 1u) != 0;
+        float sm = swap ? cp : sr, cm = swap ? sr : cp;
+        *s_out = xor_sign32(sm, (qd & 2u) << 30);
+        *c_out = xor_sign32(cm, ((qd + 1u) & 2u) << 30);
+    } else {
+        *s_out = xor_sign32(sr, qd);
+        *c_out = xor_sign32(cp, qd);
+    }
+}
+
+static float probe_step(float p) { return fmaf(p, 0.999999940395355224609375f, 0.0001220703125f); }
+
+int orc_sincos_f32(int prog, const float* angles, float* cos_out, float* sin_out, int64_t n,
+                   int iterations) {
+    if (prog < 0 || prog > 7 || n < 0 || iterations < 0) return -1;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float c, s;
+        if (iterations == 0) {
+            sincos32_eval(prog, angles[i], &c, &s);
+        } else {
+            float p = angles[i];
+            c = 0.0f;
+            s = 0.0f;
+            for (int it = 0; it < iterations; ++it) {
+                float ci, si;
+                sincos32_eval(prog, p, &ci, &si);
+                c += ci;
+                s += si;
+                p = probe_step(p);
+            }
+        }
+        cos_out[i] = c;
+        sin_out[i] = s;
+    }
+    return 0;
+}
+
+/* 16-bit quarter-turn programs, highest power of sq first. */
+static const sincos_t SINCOS_QUARTER[3] = {
+    /* evaluate_quarter_turn_d3_d4_fp16, :544-571 (shifter, one-term pi/2) */
+    {ORC_F16, 2, {-0.1602783203125f, 0.9990234375f}, 3, {0.040435791015625f, -0.499755859375f, 1.0f}},
+    /* PolynomialD3D4QuarterTurnBF16, :597-642 (shifter, one-term pi/2) */
+    {ORC_BF16, 2, {-0.162109375f, 1.0f}, 3, {0.041015625f, -0.5f, 1.0f}},
+    /* PolynomialD3D4BF16, :940-978 (Cody-Waite, FP32 Sollya coefficients) */
+    {ORC_BF16, 2, {-0.16034401953220367431640625f, 0.99903142452239990234375f}, 3,
+     {0.0403986163437366485595703125f, -0.4997082054615020751953125f, 0.999990046024322509765625f}},
+};
+
+/* Every 16-bit program on one angle: prog 0..5 half turn (SINCOS[]),
+ * 6..8 quarter turn (SINCOS_QUARTER[]).  Results are values of the
+ * program's format. */
+static void sincos16_eval(int prog, int rnd, float angle, double* c, double* s) {
+    if (prog < 6) {
+        const sincos_t* q = &SINCOS[prog];
+        ctx_t k = {fmt_of(q->fmt), rnd, 0};
+        float r32;
+        int neg;
+        reduce_half_turn(angle, &r32, &neg);
+        sincos_poly(q, round_fmt((double)r32, k.f), neg, &k, c, s);
+        return;
+    }
+    const sincos_t* q = &SINCOS_QUARTER[prog - 6];
+    ctx_t k = {fmt_of(q->fmt), rnd, 0};
+    float r32;
+    uint32_t qd;
+    if (prog == 8) reduce_quarter_cw(angle, &r32, &qd);
+    else reduce_quarter_shift(angle, 0, &r32, &qd);
+    double cr, sr;
+    sincos_poly(q, round_fmt((double)r32, k.f), 0, &k, &cr, &sr);
+    restore_quadrant_d(sr, cr, qd, s, c);
+}
+
+/* Tables (iterations == 0) or compute probes (iterations > 0, sums with
+ * single-rounding adds in the output format) of the 16-bit programs. */
+int orc_sincos16(int prog, int out_fmt, int rnd, const float* angles, uint16_t* cos_out,
+                 uint16_t* sin_out, int64_t n, int iterations) {
+    if (prog < 0 || prog > 8 || n < 0 || iterations < 0 || !fmt_ok(out_fmt)) return -1;
+    const fmt_t* fo = fmt_of(out_fmt);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        double c, s;
+        if (iterations == 0) {
+            sincos16_eval(prog, rnd, angles[i], &c, &s);
+            c = round_fmt(c, fo);
+            s = round_fmt(s, fo);
+        } else {
+            float p = angles[i];
+            c = 0.0;
+            s = 0.0;
+            for (int it = 0; it < iterations; ++it) {
+                double ci, si;
+                sincos16_eval(prog, rnd, p, &ci, &si);
+                c = h_add(c, round_fmt(ci, fo), fo);
+                s = h_add(s, round_fmt(si, fo), fo);
+                p = probe_step(p);
+            }
+        }
+        cos_out[i] = bits_fmt(c, fo);
+        sin_out[i] = bits_fmt(s, fo);
+    }
+    return 0;
+}
+
+/* RoPE Q0.32 phase, quarter turn (reduce_rope_phase_to_quarter_turn_q15 and
+ * evaluate_quarter_turn_q15_d3_d4_fp16, :1242-1287). */
+static void rope_q15_quarter(uint32_t position, uint32_t inc, double* c, double* s) {
+    static const sincos_t Q = {ORC_F16, 2, {-0.07763671875f, 0.78466796875f}, 3,
+                               {0.01538848876953125f, -0.308349609375f, 1.0f}};
+    uint32_t phase = position * inc;
+    uint32_t quadrant = (phase + 0x20000000u) >> 30;
+    int32_t residual = (int32_t)(phase - (quadrant << 30));
+    int16_t q15 = (int16_t)(residual >> 14);
+    double r = h_mul(round_fmt((double)q15, &FMT_F16), ldexp(1.0, -15), &FMT_F16);
+    ctx_t k = {&FMT_F16, ORC_RND_SINGLE, 0};
+    double cr, sr;
+    sincos_poly(&Q, r, 0, &k, &cr, &sr);
+    restore_quadrant_d(sr, cr, quadrant, s, c);
+}
+
+/* RoPE phase through a 128-entry FP16 (sin, cos) table and a first-order
+ * correction (evaluate_rope_phase_lut_fp16, :1350-1385). */
+static void rope_lut(uint32_t position, uint32_t inc, const uint16_t* table, double* c,
+                     double* s) {
+    uint32_t phase = position * inc;
+    uint32_t idx = ((phase + (1u << 24)) >> 25) & 127u;
+    int32_t residual = (int32_t)(phase - (idx << 25));
+    float d32 = (float)residual * 0x1.921fb6p-30f;
+    double d = round_fmt((double)d32, &FMT_F16);
+    double sb = value_fmt(table[2 * idx], &FMT_F16);
+    double cb = value_fmt(table[2 * idx + 1], &FMT_F16);
+    *s = h_fma(d, cb, sb, &FMT_F16);
+    *c = h_fma(-d, sb, cb, &FMT_F16);
+}
+
+/* kind 0: half-turn Q15 D5/D6, 1: quarter-turn Q15 D3/D4, 2: LUT (table
+ * [128, 2] FP16 bits, sin first).  iterations > 0: packed-FP16 sums over
+ * positions p .. p + iterations - 1. */
+int orc_rope_table(int kind, const int32_t* inc, const uint16_t* lut, uint16_t* out, int64_t seq,
+                   int64_t nfreq, int iterations) {
+    if (kind < 0 || kind > 2 || seq < 0 || nfreq < 0 || iterations < 0) return -1;
+    if (kind == 2 && !lut) return -1;
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < seq; ++p) {
+        for (int64_t f = 0; f < nfreq; ++f) {
+            int its = iterations == 0 ? 1 : iterations;
+            double c = 0.0, s = 0.0;
+            for (int it = 0; it < its; ++it) {
+                uint32_t pos = (uint32_t)(p + it);
+                double ci, si;
+                if (kind == 0) rope_q15(pos, (uint32_t)inc[f], &ci, &si);
+                else if (kind == 1) rope_q15_quarter(pos, (uint32_t)inc[f], &ci, &si);
+                else rope_lut(pos, (uint32_t)inc[f], lut, &ci, &si);
+                if (iterations == 0) {
+                    c = ci;
+                    s = si;
+                } else {
+                    c = h_add(c, ci, &FMT_F16);
+                    s = h_add(s, si, &FMT_F16);
+                }
+            }
+            out[p * nfreq + f] = bits_fmt(c, &FMT_F16);
+            out[seq * nfreq + p * nfreq + f] = bits_fmt(s, &FMT_F16);
+        }
+    }
+    return 0;
+}
+
+/* Fused RoPE with a precomputed [2, S, D/2] FP16 table
+ * (rope_apply_cached_fp16_kernel, :1614-1652), packed-FP16 rotation. */
+int orc_rope_apply_cached(const uint16_t* q, const uint16_t* kk, const uint16_t* table,
+                          uint16_t* q_out, uint16_t* k_out, int64_t batch, int64_t seq, int64_t hq,
+                          int64_t hk, int64_t dim) {
+    if (batch < 0 || seq < 0 || hq < 0 || hk < 0 || dim <= 0 || dim % 2) return -1;
+    const fmt_t* f = &FMT_F16;
+    int64_t nfreq = dim / 2;
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < seq; ++p) {
+        for (int64_t i = 0; i < nfreq; ++i) {
+            double c = value_fmt(table[p * nfreq + i], f);
+            double s = value_fmt(table[seq * nfreq + p * nfreq + i], f);
+            for (int which = 0; which < 2; ++which) {
+                const uint16_t* src = which ? kk : q;
+                uint16_t* dst = which ? k_out : q_out;
+                int64_t nh = which ? hk : hq;
+                for (int64_t b = 0; b < batch; ++b) {
+                    for (int64_t h = 0; h < nh; ++h) {
+                        int64_t in_base = ((b * seq + p) * nh + h) * dim + 2 * i;
+                        int64_t out_base = ((b * nh + h) * seq + p) * dim + 2 * i;
+                        double e = value_fmt(src[in_base], f);
+                        double o = value_fmt(src[in_base + 1], f);
+                        dst[out_base] = bits_fmt(h_fma(-s, o, h_mul(c, e, f), f), f);
+                        dst[out_base + 1] = bits_fmt(h_fma(s, e, h_mul(c, o, f), f), f);
+                    }
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* B3-D2: sigmoid via range-reduced degree-2 exp2 (program model of          */
 /* autonumerics_zero/evolution/fit_flash_sigmoid_exp2_d2.py:55-77 in FP32)    */
 /* ------------------------------------------------------------------------ */

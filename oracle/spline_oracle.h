@@ -102,6 +102,27 @@ int orc_rope_apply(int fmt, const uint16_t* q, const uint16_t* k, const int32_t*
                    uint16_t* q_out, uint16_t* k_out, int64_t batch, int64_t seq, int64_t hq,
                    int64_t hk, int64_t dim);
 
+/* ---- FP32 sin/cos programs: prog 0 D3/D4, 1 D3/D4 magic bias, 2 D5/D4,
+ * 3 D7/D6 (Cody-Waite quarter turn), 4 half-turn D5/D4 LS, 5 half-turn
+ * D5/D4 Sollya, 6 its one-term-pi fast form, 7 D3/D4 cycle.  iterations 0:
+ * table; > 0: compute probe sums (FP32 adds). */
+int orc_sincos_f32(int prog, const float* angles, float* cos_out, float* sin_out, int64_t n,
+                   int iterations);
+/* ---- every 16-bit sin/cos program: prog 0..5 as orc_sincos, 6 FP16 quarter
+ * turn D3/D4, 7 BF16 quarter turn D3/D4, 8 BF16 Cody-Waite D3/D4; outputs in
+ * out_fmt; iterations > 0: compute probe sums in out_fmt. */
+int orc_sincos16(int prog, int out_fmt, int rnd, const float* angles, uint16_t* cos_out,
+                 uint16_t* sin_out, int64_t n, int iterations);
+/* RoPE tables [2, seq, nfreq] FP16: kind 0 half-turn D5/D6, 1 quarter-turn
+ * D3/D4, 2 LUT (lut = [128, 2] FP16 bits, sin first); iterations > 0: sums
+ * over positions p .. p + iterations - 1. */
+int orc_rope_table(int kind, const int32_t* inc, const uint16_t* lut, uint16_t* out, int64_t seq,
+                   int64_t nfreq, int iterations);
+/* Fused FP16 RoPE with a [2, seq, dim/2] FP16 cos/sin table. */
+int orc_rope_apply_cached(const uint16_t* q, const uint16_t* k, const uint16_t* table,
+                          uint16_t* q_out, uint16_t* k_out, int64_t batch, int64_t seq, int64_t hq,
+                          int64_t hk, int64_t dim);
+
 /* Thread count used by the bulk loops (OpenMP when built with it). */
 int orc_num_threads(void);
 
