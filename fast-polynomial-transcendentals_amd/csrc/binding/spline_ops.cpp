@@ -602,6 +602,83 @@ std::vector<at::Tensor> rope_apply(at::Tensor q, at::Tensor k, at::Tensor parame
 }
 
 // ---------------------------------------------------------------------------
+// FP16 experiments: hybrid, fused, forward-with-derivative, multiply
+// (spline_ops.cpp:1548-1926)
+// ---------------------------------------------------------------------------
+
+#define CHECK_HALF(x) \
+    TORCH_CHECK(x.scalar_type() == at::kHalf, #x " must be float16 (no BF16 support for this op)")
+#define CHECK_INPUT_FP16(x) \
+    CHECK_CUDA(x);          \
+    CHECK_CONTIGUOUS(x);    \
+    CHECK_HALF(x)
+
+using UnaryLauncher = int (*)(void*, const void*, int64_t, void*);
+using BinaryLauncher = int (*)(void*, const void*, const void*, int64_t, void*);
+using PairLauncher = int (*)(void*, void*, const void*, int64_t, void*);
+using FusedLauncher = int (*)(void*, void*, const void*, const void*, int64_t, void*);
+
+// Shapes must agree: the kernels read both inputs over x.numel() elements.
+void check_same_numel(const at::Tensor& a, const at::Tensor& b, const char* an, const char* bn) {
+    TORCH_CHECK(a.numel() == b.numel(), an, " and ", bn, " must have the same number of elements");
+}
+
+at::Tensor fp16_fwd(at::Tensor x, UnaryLauncher fn) {
+    CHECK_INPUT_FP16(x);
+    c10::OptionalDeviceGuard guard(x.device());
+    at::Tensor out = at::empty_like(x);
+    void* s = current_stream(x);
+    check_launch(fn(out.data_ptr(), x.data_ptr(), x.numel(), s), s);
+    return out;
+}
+
+at::Tensor fp16_bwd(at::Tensor grad_out, at::Tensor x, BinaryLauncher fn) {
+    CHECK_INPUT_FP16(grad_out);
+    CHECK_INPUT_FP16(x);
+    check_same_numel(grad_out, x, "grad_out", "x");
+    c10::OptionalDeviceGuard guard(x.device());
+    at::Tensor grad_in = at::empty_like(x);
+    void* s = current_stream(x);
+    check_launch(fn(grad_in.data_ptr(), grad_out.data_ptr(), x.data_ptr(), x.numel(), s), s);
+    return grad_in;
+}
+
+std::vector<at::Tensor> fp16_fused(at::Tensor x, at::Tensor grad_out, FusedLauncher fn) {
+    CHECK_INPUT_FP16(x);
+    CHECK_INPUT_FP16(grad_out);
+    check_same_numel(x, grad_out, "x", "grad_out");
+    c10::OptionalDeviceGuard guard(x.device());
+    at::Tensor y = at::empty_like(x);
+    at::Tensor gi = at::empty_like(x);
+    void* s = current_stream(x);
+    check_launch(fn(y.data_ptr(), gi.data_ptr(), x.data_ptr(), grad_out.data_ptr(), x.numel(), s), s);
+    return {y, gi};
+}
+
+std::vector<at::Tensor> fp16_fwd_deriv(at::Tensor x, PairLauncher fn) {
+    CHECK_INPUT_FP16(x);
+    c10::OptionalDeviceGuard guard(x.device());
+    at::Tensor y = at::empty_like(x);
+    at::Tensor dy = at::empty_like(x);
+    void* s = current_stream(x);
+    check_launch(fn(y.data_ptr(), dy.data_ptr(), x.data_ptr(), x.numel(), s), s);
+    return {y, dy};
+}
+
+at::Tensor multiply(at::Tensor a, at::Tensor b) {
+    CHECK_INPUT(a);
+    CHECK_INPUT(b);
+    TORCH_CHECK(a.scalar_type() == b.scalar_type(), "a and b must have the same dtype");
+    check_same_numel(a, b, "a", "b");
+    c10::OptionalDeviceGuard guard(a.device());
+    at::Tensor out = at::empty_like(a);
+    void* s = current_stream(a);
+    auto fn = a.scalar_type() == at::kHalf ? launch_multiply_kernel : launch_multiply_kernel_bf16;
+    check_launch(fn(out.data_ptr(), a.data_ptr(), b.data_ptr(), a.numel(), s), s);
+    return out;
+}
+
+// ---------------------------------------------------------------------------
 // C++ autograd functions (spline_ops.cpp:1933-2206)
 // ---------------------------------------------------------------------------
 
@@ -1058,6 +1135,38 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                                 launch_rope_apply_native_bf16);
           },
           "Fused native BF16 Q/K rotary embedding and transpose");
+
+    // FP16 experiments
+#define PT_DEF_FP16_FWD(name, doc) \
+    m.def(#name, [](at::Tensor x) { return fp16_fwd(x, launch_##name##_kernel); }, doc)
+#define PT_DEF_FP16_BWD(name, doc)                                                       \
+    m.def(#name, [](at::Tensor go, at::Tensor x) { return fp16_bwd(go, x, launch_##name##_kernel); }, \
+          doc)
+#define PT_DEF_FUSED(name, doc)                                                          \
+    m.def(#name, [](at::Tensor x, at::Tensor go) { return fp16_fused(x, go, launch_##name##_kernel); }, \
+          doc)
+#define PT_DEF_FWD_DERIV(name, doc) \
+    m.def(#name, [](at::Tensor x) { return fp16_fwd_deriv(x, launch_##name##_kernel); }, doc)
+    PT_DEF_FP16_FWD(sigmoid_fwd_hybrid, "Sigmoid FWD hybrid 1SFU+3Poly");
+    PT_DEF_FP16_FWD(tanh_fwd_hybrid, "Tanh FWD hybrid 1SFU+3Poly");
+    PT_DEF_FP16_FWD(swish_fwd_hybrid, "Swish FWD hybrid 1SFU+3Poly");
+    PT_DEF_FP16_BWD(sigmoid_bwd_hybrid, "Sigmoid BWD hybrid 1SFU+3Poly");
+    PT_DEF_FP16_BWD(tanh_bwd_hybrid, "Tanh BWD hybrid 1SFU+3Poly");
+    PT_DEF_FP16_BWD(swish_bwd_hybrid, "Swish BWD hybrid 1SFU+3Poly");
+    PT_DEF_FUSED(sigmoid_fused, "Sigmoid fused FWD+BWD");
+    PT_DEF_FUSED(tanh_fused, "Tanh fused FWD+BWD");
+    PT_DEF_FUSED(swish_fused, "Swish fused FWD+BWD");
+    PT_DEF_FWD_DERIV(sigmoid_fwd_deriv_alg, "Sigmoid FWD+deriv (poly+algebraic)");
+    PT_DEF_FWD_DERIV(sigmoid_fwd_deriv_poly, "Sigmoid FWD+deriv (poly+poly)");
+    PT_DEF_FWD_DERIV(tanh_fwd_deriv_alg, "Tanh FWD+deriv (poly+algebraic)");
+    PT_DEF_FWD_DERIV(tanh_fwd_deriv_poly, "Tanh FWD+deriv (poly+poly)");
+    PT_DEF_FWD_DERIV(swish_fwd_deriv, "Swish FWD+deriv (shared sigmoid)");
+    PT_DEF_FWD_DERIV(swish_fwd_deriv_poly, "Swish FWD+deriv (poly+poly)");
+#undef PT_DEF_FP16_FWD
+#undef PT_DEF_FP16_BWD
+#undef PT_DEF_FUSED
+#undef PT_DEF_FWD_DERIV
+    m.def("multiply", &multiply, "Element-wise multiply (for backward)");
 
     m.def("flash_sigmoid_direct_d3_d4_bf16", &flash_sigmoid_direct_d3_d4,
           "B3 deployed direct-D3 probability and factored-D4 derivative (BF16 out)");

@@ -79,6 +79,18 @@ __device__ __forceinline__ void call_pair(const uint32_t (&a)[Op::NIN], uint32_t
     }
 }
 
+// Ops that treat the pairs of a 16-byte vector differently declare
+// kPositional and `pair_at<W>(in, out)` (W = pair index 0..3 within the
+// vector); their `pair` is what element and tail paths use.
+template <class Op, class = void>
+struct IsPositional {
+    static constexpr bool value = false;
+};
+template <class Op>
+struct IsPositional<Op, decltype((void)Op::kPositional)> {
+    static constexpr bool value = true;
+};
+
 // Op contract:
 //   static constexpr int NIN, NOUT;
 //   __device__ static void pair(const uint32_t (&in)[NIN], uint32_t (&out)[NOUT]);
@@ -92,7 +104,16 @@ __device__ __forceinline__ void apply_vec(const Vec4 (&v)[Op::NIN], Vec4 (&o)[Op
         uint32_t a[Op::NIN], b[Op::NOUT];
 #pragma unroll
         for (int k = 0; k < Op::NIN; ++k) a[k] = v[k].w[w];
-        call_pair<Op>(a, b, prm);
+        if constexpr (IsPositional<Op>::value) {
+            switch (w) {  // w is a constant after unrolling
+            case 0: Op::template pair_at<0>(a, b); break;
+            case 1: Op::template pair_at<1>(a, b); break;
+            case 2: Op::template pair_at<2>(a, b); break;
+            default: Op::template pair_at<3>(a, b);
+            }
+        } else {
+            call_pair<Op>(a, b, prm);
+        }
 #pragma unroll
         for (int k = 0; k < Op::NOUT; ++k) o[k].w[w] = b[k];
     }

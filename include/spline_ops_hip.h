@@ -198,6 +198,50 @@ SPLINE_HIP_SWISH_MUL_BWD_LAUNCHERS(SPLINE_HIP_DECLARE_SWISH_MUL_BWD)
 SPLINE_HIP_PACKED_FWD_LAUNCHERS(SPLINE_HIP_DECLARE_PACKED_FWD)
 SPLINE_HIP_PACKED_BWD_LAUNCHERS(SPLINE_HIP_DECLARE_PACKED_BWD)
 
+/* ---- FP16 experiment kernels (spline_ops.cpp:1573-1926 binding;
+ * spline_kernels.cu:776-1168, 1394-1480) --------------------------------------
+ * Hybrid (replace launch_{sigmoid,tanh,swish}_{fwd,bwd}_hybrid_kernel,
+ * :1394-1414): in tensors of at least 8192 elements, a multiple of 8, the
+ * first pair of every 8 elements goes through the hardware transcendental
+ * program (v_exp_f32 / v_rcp_f32, rounded to FP16) and the other three
+ * pairs through the polynomial (forward: sigmoid/tanh/SiLU D3; backward:
+ * grad_out * sigmoid/tanh D4 even or SiLU D4 odd); smaller or ragged tensors
+ * are all polynomial, as in the reference. */
+#define SPLINE_HIP_HYBRID_FWD_LAUNCHERS(X)                                      \
+    X(launch_sigmoid_fwd_hybrid_kernel) X(launch_tanh_fwd_hybrid_kernel)        \
+    X(launch_swish_fwd_hybrid_kernel)
+#define SPLINE_HIP_HYBRID_BWD_LAUNCHERS(X)                                      \
+    X(launch_sigmoid_bwd_hybrid_kernel) X(launch_tanh_bwd_hybrid_kernel)        \
+    X(launch_swish_bwd_hybrid_kernel)
+SPLINE_HIP_HYBRID_FWD_LAUNCHERS(SPLINE_HIP_DECLARE_UNARY)
+SPLINE_HIP_HYBRID_BWD_LAUNCHERS(SPLINE_HIP_DECLARE_BINARY)
+/* Fused forward + backward (replace launch_{sigmoid,tanh,swish}_fused_kernel,
+ * :1416-1443): y = D3(x) and grad_in = grad_out * alg(y) (sigmoid y(1-y),
+ * tanh 1-y^2); SiLU: y = SILU_D3(x), grad_in = grad_out * SILU'_D4(x). */
+#define SPLINE_HIP_FUSED_LAUNCHERS(X)                                           \
+    X(launch_sigmoid_fused_kernel) X(launch_tanh_fused_kernel) X(launch_swish_fused_kernel)
+#define SPLINE_HIP_DECLARE_FUSED(name)                                          \
+    int name(void* y, void* grad_in, const void* x, const void* grad_out, int64_t size, void* stream);
+SPLINE_HIP_FUSED_LAUNCHERS(SPLINE_HIP_DECLARE_FUSED)
+/* Forward with derivative, (y, f'(x)) (replace launch_*_fwd_deriv*_kernel,
+ * :1448-1474): _alg derives from y; _poly evaluates the D4 derivative
+ * program of x; swish_fwd_deriv shares one sigmoid D3: y = x*s,
+ * dy = s * fma(x, 1 - s, 1).  Every size gets the vector-path result (the
+ * reference's small-size fallback of _alg returns y * alg(y) and that of
+ * swish_fwd_deriv switches to the SiLU D3/D4 programs). */
+#define SPLINE_HIP_FWD_DERIV_LAUNCHERS(X)                                       \
+    X(launch_sigmoid_fwd_deriv_alg_kernel) X(launch_sigmoid_fwd_deriv_poly_kernel) \
+    X(launch_tanh_fwd_deriv_alg_kernel) X(launch_tanh_fwd_deriv_poly_kernel)    \
+    X(launch_swish_fwd_deriv_kernel) X(launch_swish_fwd_deriv_poly_kernel)
+#define SPLINE_HIP_DECLARE_FWD_DERIV(name) \
+    int name(void* y, void* dy, const void* x, int64_t size, void* stream);
+SPLINE_HIP_FWD_DERIV_LAUNCHERS(SPLINE_HIP_DECLARE_FWD_DERIV)
+/* out = a * b (replaces launch_multiply_kernel, :1477-1480, whose scalar
+ * fallback drops the tail); the _bf16 form is new (the reference binding
+ * accepts BF16 but multiplies it as FP16). */
+int launch_multiply_kernel(void* out, const void* a, const void* b, int64_t size, void* stream);
+int launch_multiply_kernel_bf16(void* out, const void* a, const void* b, int64_t size, void* stream);
+
 /* ---- B3: deployed direct-D3 sigmoid with factored-D4 derivative ---------
  * No C launcher exists in the reference: the program is FA4 inline PTX
  * (extras/paper/manuscript/main.tex:1041-1117), emulated on the CPU by

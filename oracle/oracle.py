@@ -95,13 +95,15 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_sincos16.argtypes = [ci, ci, ci, f32p, u16p, u16p, i64, ci]
     l.orc_rope_table.argtypes = [ci, i32p, u16p, u16p, i64, i64, ci]
     l.orc_rope_apply_cached.argtypes = [u16p, u16p, u16p, u16p, u16p, i64, i64, i64, i64, i64]
+    l.orc_swish_fwd_deriv_shared.argtypes = [u16p, u16p, u16p, i64]
+    l.orc_multiply.argtypes = [ci, u16p, u16p, u16p, i64]
     for name in (
         "orc_activation", "orc_activation_bwd", "orc_activation_bwd_alg",
         "orc_swish_mul_fwd", "orc_swish_mul_bwd", "orc_b3_direct_bf16",
         "orc_b3_direct_f32", "orc_b3_constants", "orc_num_threads", "orc_softcap_fwd_bf16",
         "orc_softcap_bwd_bf16", "orc_exp2", "orc_sincos", "orc_rope_sincos_table",
         "orc_rope_apply", "orc_sincos_f32", "orc_sincos16", "orc_rope_table",
-        "orc_rope_apply_cached",
+        "orc_rope_apply_cached", "orc_swish_fwd_deriv_shared", "orc_multiply",
     ):
         getattr(l, name).restype = ctypes.c_int
 
@@ -346,6 +348,22 @@ def rope_apply(fmt, q: np.ndarray, k: np.ndarray, inc: np.ndarray):
     _check(lib().orc_rope_apply(fmt_id(fmt), _p(q), _p(k), _p(inc, ctypes.c_int32), _p(qo), _p(ko),
                                 b, s, hq, hk, d))
     return qo, ko
+
+
+def swish_fwd_deriv_shared(x: np.ndarray):
+    """FP16 (y, dy) of the shared-sigmoid SiLU forward-with-derivative."""
+    x = _u16(x)
+    y = np.empty_like(x)
+    dy = np.empty_like(x)
+    _check(lib().orc_swish_fwd_deriv_shared(_p(x), _p(y), _p(dy), x.size))
+    return y, dy
+
+
+def multiply(fmt, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a, b = _u16(a), _u16(b)
+    out = np.empty_like(a)
+    _check(lib().orc_multiply(fmt_id(fmt), _p(a), _p(b), _p(out), a.size))
+    return out
 
 
 def rope_phase_increments(head_dim: int, theta: float) -> np.ndarray:

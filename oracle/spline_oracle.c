@@ -905,6 +905,38 @@ int orc_rope_apply(int fmt, const uint16_t* q, const uint16_t* kk, const int32_t
 }
 
 /* ------------------------------------------------------------------------ */
+/* FP16 experiments (spline_kernels.cu:976-1030)                             */
+/* ------------------------------------------------------------------------ */
+
+/* fwd_deriv_swish_kernel (:976-1010): s = SIGMOID_FWD_D3_ODD(x),
+ * y = __hmul2(x, s), dy = __hmul2(s, __hfma2(x, __hsub2(1, s), 1)). */
+int orc_swish_fwd_deriv_shared(const uint16_t* x, uint16_t* y, uint16_t* dy, int64_t n) {
+    if (n < 0) return -1;
+    const fmt_t* f = &FMT_F16;
+    const prog_t* sp = find_prog(ORC_SIGMOID, ORC_FWD, 3, ORC_F16);
+    ctx_t k = {f, ORC_RND_SINGLE, F16_PROGS};
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        double xv = value_fmt(x[i], f);
+        double s = eval_prog(sp, xv, &k);
+        y[i] = bits_fmt(h_mul(xv, s, f), f);
+        double one = kconst(1.0f, f);
+        dy[i] = bits_fmt(h_mul(s, h_fma(xv, h_add(one, -s, f), one, f), f), f);
+    }
+    return 0;
+}
+
+/* out = a * b with one rounding (multiply_vec_kernel, :1012-1030). */
+int orc_multiply(int fmt, const uint16_t* a, const uint16_t* b, uint16_t* out, int64_t n) {
+    if (n < 0 || (fmt != ORC_F16 && fmt != ORC_BF16)) return -1;
+    const fmt_t* f = fmt_of(fmt);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = bits_fmt(h_mul(value_fmt(a[i], f), value_fmt(b[i], f), f), f);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* quarter-turn and FP32 sin/cos programs, compute probes, RoPE variants     */
 /* (sincos_kernels.cu:24-406, 544-642, 940-978, 1014-1240, 1242-1934)        */
 /* ------------------------------------------------------------------------ */

@@ -123,6 +123,11 @@ int orc_rope_apply_cached(const uint16_t* q, const uint16_t* k, const uint16_t* 
                           uint16_t* q_out, uint16_t* k_out, int64_t batch, int64_t seq, int64_t hq,
                           int64_t hk, int64_t dim);
 
+/* ---- FP16 experiments: SiLU value and derivative from one shared sigmoid
+ * D3 (y = x*s, dy = s*fma(x, 1-s, 1)); elementwise product (FP16 / BF16). */
+int orc_swish_fwd_deriv_shared(const uint16_t* x, uint16_t* y, uint16_t* dy, int64_t n);
+int orc_multiply(int fmt, const uint16_t* a, const uint16_t* b, uint16_t* out, int64_t n);
+
 /* Thread count used by the bulk loops (OpenMP when built with it). */
 int orc_num_threads(void);
 

@@ -230,3 +230,47 @@ def test_rope_apply_matches_float64_rotation(oracle, fmt):
         got = oracle.bits_to_f32(out, fmt)
         ulp = 2 ** -8 if fmt == "bf16" else 2 ** -11
         assert np.abs(got - ref).max() < np.abs(v).max() * (3e-3 + 2 * ulp)
+
+
+# ---- FP16 experiments: shared-sigmoid SiLU derivative, multiply ------------------
+
+def test_swish_fwd_deriv_shared_matches_half_precision_arithmetic(oracle):
+    """y = x*s, dy = s*fma(x, 1-s, 1) with s = sigmoid D3 (fwd_deriv_swish_kernel,
+    spline_kernels.cu:976-1010), restated with numpy float16 (each op correctly
+    rounded; the FMA computed exactly in float64, then rounded once)."""
+    x = _all(oracle)
+    xf = oracle.f16_bits_to_f32(x).astype(np.float16)
+    s = oracle.f16_bits_to_f32(oracle.activation("sigmoid", oracle.FWD, 3, "f16", x)).astype(np.float16)
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = xf * s
+        one_minus = np.float16(1.0) - s
+        fma = (xf.astype(np.float64) * one_minus.astype(np.float64) + 1.0).astype(np.float16)
+        dy = s * fma
+    gy, gdy = oracle.swish_fwd_deriv_shared(x)
+    fin = np.isfinite(xf)
+    assert np.array_equal(gy[fin], y.view(np.uint16)[fin])
+    assert np.array_equal(gdy[fin], dy.view(np.uint16)[fin])
+    # and it is the SiLU derivative within the sigmoid D3 error (0.02 in s,
+    # amplified by |1 + x(1 - s)| <= 1.3 on the fit range)
+    xm = xf.astype(np.float64)[fin & (np.abs(xf) < 8)]
+    sg = 1 / (1 + np.exp(-xm))
+    ref = sg * (1 + xm * (1 - sg))
+    got = oracle.f16_bits_to_f32(gdy[fin & (np.abs(xf) < 8)])
+    assert np.abs(got - ref).max() < 0.05
+
+
+@pytest.mark.parametrize("fmt", ["f16", "bf16"])
+def test_multiply_is_one_rounding_of_the_product(oracle, fmt):
+    rng = np.random.default_rng(11)
+    a = rng.integers(0, 65536, 200_000, dtype=np.uint32).astype(np.uint16)
+    b = rng.integers(0, 65536, 200_000, dtype=np.uint32).astype(np.uint16)
+    got = oracle.multiply(fmt, a, b)
+    with np.errstate(over="ignore", invalid="ignore"):
+        if fmt == "f16":
+            want = (a.view(np.float16) * b.view(np.float16)).view(np.uint16)
+        else:
+            want = oracle.f32_to_bf16_bits(oracle.bf16_bits_to_f32(a) * oracle.bf16_bits_to_f32(b))
+    gv = oracle.bits_to_f32(got, fmt)
+    wv = oracle.bits_to_f32(want, fmt)
+    both_nan = np.isnan(gv) & np.isnan(wv)
+    assert np.array_equal(got[~both_nan], want[~both_nan])
