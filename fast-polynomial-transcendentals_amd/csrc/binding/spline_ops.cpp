@@ -602,6 +602,74 @@ std::vector<at::Tensor> rope_apply(at::Tensor q, at::Tensor k, at::Tensor parame
 }
 
 // ---------------------------------------------------------------------------
+// RoPE reference evaluator (src/sfu_repro/rope/polynomial_sincos.py:85-165)
+// ---------------------------------------------------------------------------
+
+// FP32 or FP64 storage the kernel reads directly; 16-bit angles are widened
+// exactly to FP32 first.
+at::Tensor ref_angles(const at::Tensor& angles, const char* name) {
+    TORCH_CHECK(at::isFloatingType(angles.scalar_type()), name, " must be a floating-point tensor");
+    CHECK_CUDA(angles);
+    at::Tensor a = angles.contiguous();
+    if (a.scalar_type() != at::kFloat && a.scalar_type() != at::kDouble) a = a.to(at::kFloat);
+    return a;
+}
+
+void check_coeffs(const std::vector<double>& c, const char* name) {
+    TORCH_CHECK(!c.empty() && c.size() <= 8, name, " must hold 1 to 8 coefficients");
+}
+
+std::vector<float> to_f32(const std::vector<double>& c) {
+    return std::vector<float>(c.begin(), c.end());  // each rounded to FP32 (RNE)
+}
+
+std::vector<at::Tensor> polynomial_sincos_f32(at::Tensor angles, std::vector<double> sin_coeffs,
+                                              std::vector<double> cos_coeffs, bool accurate) {
+    at::Tensor a = ref_angles(angles, "angles");
+    check_coeffs(sin_coeffs, "sin_coefficients");
+    check_coeffs(cos_coeffs, "cos_coefficients");
+    const std::vector<float> sc = to_f32(sin_coeffs), cc = to_f32(cos_coeffs);
+    c10::OptionalDeviceGuard guard(a.device());
+    at::Tensor c = at::empty(a.sizes(), a.options().dtype(at::kFloat));
+    at::Tensor sn = at::empty_like(c);
+    void* s = current_stream(a);
+    check_launch(launch_polynomial_sincos_f32(c.data_ptr(), sn.data_ptr(), a.data_ptr(),
+                                              a.scalar_type() == at::kDouble, a.numel(), accurate,
+                                              sc.data(), (int)sc.size(), cc.data(), (int)cc.size(), s),
+                 s);
+    return {c, sn};
+}
+
+std::vector<at::Tensor> reduce_to_quarter_turn_f32(at::Tensor angles, bool accurate) {
+    at::Tensor a = ref_angles(angles, "angles");
+    c10::OptionalDeviceGuard guard(a.device());
+    at::Tensor r = at::empty(a.sizes(), a.options().dtype(at::kFloat));
+    at::Tensor q = at::empty(a.sizes(), a.options().dtype(at::kLong));
+    void* s = current_stream(a);
+    check_launch(launch_reduce_to_quarter_turn(r.data_ptr(), q.data_ptr(), a.data_ptr(),
+                                               a.scalar_type() == at::kDouble, a.numel(), accurate, s),
+                 s);
+    return {r, q};
+}
+
+std::vector<at::Tensor> evaluate_reduced_sincos_f32(at::Tensor reduced, std::vector<double> sin_coeffs,
+                                                    std::vector<double> cos_coeffs) {
+    at::Tensor r = ref_angles(reduced, "reduced");
+    check_coeffs(sin_coeffs, "sin_coefficients");
+    check_coeffs(cos_coeffs, "cos_coefficients");
+    const std::vector<float> sc = to_f32(sin_coeffs), cc = to_f32(cos_coeffs);
+    c10::OptionalDeviceGuard guard(r.device());
+    at::Tensor sn = at::empty(r.sizes(), r.options().dtype(at::kFloat));
+    at::Tensor c = at::empty_like(sn);
+    void* s = current_stream(r);
+    check_launch(launch_evaluate_reduced_sincos(sn.data_ptr(), c.data_ptr(), r.data_ptr(),
+                                                r.scalar_type() == at::kDouble, r.numel(), sc.data(),
+                                                (int)sc.size(), cc.data(), (int)cc.size(), s),
+                 s);
+    return {sn, c};
+}
+
+// ---------------------------------------------------------------------------
 // FP16 experiments: hybrid, fused, forward-with-derivative, multiply
 // (spline_ops.cpp:1548-1926)
 // ---------------------------------------------------------------------------
@@ -1135,6 +1203,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                                 launch_rope_apply_native_bf16);
           },
           "Fused native BF16 Q/K rotary embedding and transpose");
+
+    // RoPE reference evaluator (sfu_repro.rope.polynomial_sincos on the device)
+    m.def("polynomial_sincos_f32", &polynomial_sincos_f32, py::arg("angles"),
+          py::arg("sin_coefficients"), py::arg("cos_coefficients"), py::arg("accurate") = true,
+          "Quarter-turn reduction (FP64 or FP32 Cody-Waite) and paired parity polynomials "
+          "in FP32; returns [cos, sin]");
+    m.def("reduce_to_quarter_turn_f32", &reduce_to_quarter_turn_f32, py::arg("angles"),
+          py::arg("accurate") = true, "Quarter-turn reduction; returns [reduced (FP32), quadrant (int64)]");
+    m.def("evaluate_reduced_sincos_f32", &evaluate_reduced_sincos_f32, py::arg("reduced"),
+          py::arg("sin_coefficients"), py::arg("cos_coefficients"),
+          "Paired parity polynomials on reduced FP32 arguments; returns [sin, cos]");
 
     // FP16 experiments
 #define PT_DEF_FP16_FWD(name, doc) \

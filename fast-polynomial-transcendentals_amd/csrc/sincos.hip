@@ -284,3 +284,132 @@ PT_SINCOS_F32(d5_d4_half_turn_sollya, (F32Prog<kF32HalfD5D4Sollya>))
 PT_SINCOS_F32(d5_d4_half_turn_sollya_fast, (F32Prog<kF32HalfD5D4SollyaFast>))
 PT_SINCOS_F32(d5_d4, (F32Prog<kF32D5D4>))
 PT_SINCOS_F32(d7_d6, (F32Prog<kF32D7D6>))
+
+// ---------------------------------------------------------------------------
+// RoPE reference evaluator (src/sfu_repro/rope/polynomial_sincos.py:85-165):
+// quarter-turn reduction in FP64 ("accurate", for cached tables) or FP32
+// Cody-Waite ("fast"), then sin = r * S(r^2), cos = C(r^2) with Horner steps
+// that round the product and the sum separately (value * x + c, as the
+// reference's tensor arithmetic does), then the quadrant swap and signs.
+// Coefficients arrive by value, lowest power first.
+// ---------------------------------------------------------------------------
+
+namespace pt {
+
+constexpr int kMaxRefCoeffs = 8;
+
+struct RefPoly {
+    int ns, nc;
+    float s[kMaxRefCoeffs], c[kMaxRefCoeffs];
+};
+
+__device__ __forceinline__ float ref_horner(float x, const float* c, int n) {
+    float v = c[n - 1];
+    for (int i = n - 2; i >= 0; --i) v = v * x + c[i];  // two roundings per step
+    return v;
+}
+
+// float -> int64 conversion with the host's conventions for NaN and
+// out-of-range values (INT64_MIN), so quadrant = q & 3 is defined for all.
+template <class T>
+__device__ __forceinline__ int64_t ref_to_i64(T q) {
+    const T lim = (T)9223372036854775808.0;
+    return (q < lim && q > -lim) ? (int64_t)q : INT64_MIN;
+}
+
+__device__ __forceinline__ void ref_reduce(const void* angles, int f64, int64_t i, int accurate,
+                                           float& r, int64_t& quadrant) {
+    if (accurate) {
+        const double w = f64 ? ((const double*)angles)[i] : (double)((const float*)angles)[i];
+        const double q = __builtin_rint(w * 0.6366197723675814);
+        r = (float)(w - q * 1.5707963267948966);
+        quadrant = ref_to_i64(q) & 3;
+    } else {
+        const float w = f64 ? (float)((const double*)angles)[i] : ((const float*)angles)[i];
+        const float q = __builtin_rintf(w * 0.63661977236758134f);
+        r = (w - q * 1.570796251296997f) - q * 7.549789415861596e-08f;
+        quadrant = ref_to_i64(q) & 3;
+    }
+}
+
+// mode 0: (cos, sin) of angles; 1: (reduced, quadrant); 2: (sin, cos) of
+// reduced arguments (evaluate_reduced_sincos).
+__global__ void __launch_bounds__(kBlock)
+ref_sincos_kernel(const void* __restrict__ in, int in_f64, void* __restrict__ out0,
+                  void* __restrict__ out1, int64_t n, int mode, int accurate, RefPoly p) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float r;
+        int64_t q = 0;
+        if (mode == 2) {
+            r = in_f64 ? (float)((const double*)in)[i] : ((const float*)in)[i];
+        } else {
+            ref_reduce(in, in_f64, i, accurate, r, q);
+            if (mode == 1) {
+                ((float*)out0)[i] = r;
+                ((int64_t*)out1)[i] = q;
+                continue;
+            }
+        }
+        const float sq = r * r;
+        const float sr = r * ref_horner(sq, p.s, p.ns);
+        const float cr = ref_horner(sq, p.c, p.nc);
+        if (mode == 2) {
+            ((float*)out0)[i] = sr;
+            ((float*)out1)[i] = cr;
+            continue;
+        }
+        const bool swap = (q & 1) != 0;
+        const float sm = swap ? cr : sr;
+        const float cm = swap ? sr : cr;
+        ((float*)out0)[i] = ((q + 1) & 2) ? -cm : cm;  // cos < 0 in quadrants 1, 2
+        ((float*)out1)[i] = (q & 2) ? -sm : sm;         // sin < 0 in quadrants 2, 3
+    }
+}
+
+}  // namespace pt
+
+// Returns hipErrorInvalidValue for more than 8 coefficients per polynomial or
+// none at all.
+static int launch_ref_sincos(const void* in, int in_f64, void* out0, void* out1, int64_t n, int mode,
+                             int accurate, const float* s, int ns, const float* c, int nc,
+                             void* stream) {
+    if (bad_args(n, {in, out0, out1})) return hipErrorInvalidValue;
+    RefPoly p{};
+    if (mode != 1) {
+        if (!s || !c || ns < 1 || nc < 1 || ns > kMaxRefCoeffs || nc > kMaxRefCoeffs)
+            return hipErrorInvalidValue;
+        p.ns = ns;
+        p.nc = nc;
+        for (int k = 0; k < ns; ++k) p.s[k] = s[k];
+        for (int k = 0; k < nc; ++k) p.c[k] = c[k];
+    }
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(ref_sincos_kernel, dim3((unsigned)grid_one_pass(n)), dim3(kBlock), 0,
+                       hs(stream), in, in_f64, out0, out1, n, mode, accurate, p);
+    return hipGetLastError();
+}
+
+extern "C" int launch_polynomial_sincos_f32(void* cos_out, void* sin_out, const void* angles,
+                                            int angles_f64, int64_t size, int accurate,
+                                            const float* sin_coeffs, int n_sin,
+                                            const float* cos_coeffs, int n_cos, void* stream) {
+    // mode 0 writes cos then sin (the kernel's out0 is the cosine)
+    return launch_ref_sincos(angles, angles_f64, cos_out, sin_out, size, 0, accurate, sin_coeffs,
+                             n_sin, cos_coeffs, n_cos, stream);
+}
+
+extern "C" int launch_reduce_to_quarter_turn(void* reduced_out, void* quadrant_out,
+                                             const void* angles, int angles_f64, int64_t size,
+                                             int accurate, void* stream) {
+    return launch_ref_sincos(angles, angles_f64, reduced_out, quadrant_out, size, 1, accurate,
+                             nullptr, 0, nullptr, 0, stream);
+}
+
+extern "C" int launch_evaluate_reduced_sincos(void* sin_out, void* cos_out, const void* reduced,
+                                              int reduced_f64, int64_t size,
+                                              const float* sin_coeffs, int n_sin,
+                                              const float* cos_coeffs, int n_cos, void* stream) {
+    return launch_ref_sincos(reduced, reduced_f64, sin_out, cos_out, size, 2, 1, sin_coeffs, n_sin,
+                             cos_coeffs, n_cos, stream);
+}

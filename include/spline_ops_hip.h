@@ -404,6 +404,25 @@ int launch_rope_sincos_fixed_lut_fp16_compute(void* out, const void* phase_incre
              int64_t q_heads, int64_t k_heads, int64_t head_dim, void* stream);
 SPLINE_HIP_ROPE_APPLY_LAUNCHERS(SPLINE_HIP_DECLARE_ROPE_APPLY)
 
+/* ---- RoPE reference evaluator (src/sfu_repro/rope/polynomial_sincos.py:85-165)
+ * FP32 or FP64 angles (angles_f64 = 1) -> FP32 cos and sin planes.  accurate = 1
+ * reduces to a quarter turn in FP64 (q = rint(a * 2/pi), r = a - q * pi/2), 0 in
+ * FP32 with the two-term Cody-Waite pi/2; then sin = r * S(r^2), cos = C(r^2),
+ * each Horner step `v * x + c` rounded after the product and after the sum,
+ * then the quadrant swap and signs.  Coefficients are host arrays, lowest power
+ * first, 1..8 of each.  No counterpart launcher exists in the reference (its
+ * evaluator is tensor arithmetic); these replace that arithmetic on the device. */
+int launch_polynomial_sincos_f32(void* cos_out, void* sin_out, const void* angles, int angles_f64,
+                                 int64_t size, int accurate, const float* sin_coeffs, int n_sin,
+                                 const float* cos_coeffs, int n_cos, void* stream);
+/* reduced (FP32) and quadrant (int64, 0..3) of the same reduction. */
+int launch_reduce_to_quarter_turn(void* reduced_out, void* quadrant_out, const void* angles,
+                                  int angles_f64, int64_t size, int accurate, void* stream);
+/* (sin, cos) of reduced FP32 (or FP64, rounded to FP32 first) arguments. */
+int launch_evaluate_reduced_sincos(void* sin_out, void* cos_out, const void* reduced,
+                                   int reduced_f64, int64_t size, const float* sin_coeffs,
+                                   int n_sin, const float* cos_coeffs, int n_cos, void* stream);
+
 /* ---- device/launch introspection --------------------------------------- */
 /* Number of compute units of the current device and the grid the
  * elementwise launchers use for `size` 16-bit elements and `streams` tensors

@@ -366,6 +366,55 @@ def multiply(fmt, a: np.ndarray, b: np.ndarray) -> np.ndarray:
     return out
 
 
+# ---- RoPE reference evaluator (src/sfu_repro/rope/polynomial_sincos.py:85-165)
+# A numpy restatement with the same operation sequence: every numpy float32 /
+# float64 operation is one IEEE round-to-nearest-even step, as the
+# reference's tensor arithmetic is.
+
+def ref_reduce_to_quarter_turn(angles: np.ndarray, accurate: bool = True):
+    """(float32 residual, int64 quadrant 0..3)  (polynomial_sincos.py:85-122)."""
+    with np.errstate(invalid="ignore", over="ignore"):
+        if accurate:
+            work = np.asarray(angles).astype(np.float64)
+            q = np.rint(work * (2.0 / np.pi))
+            reduced = work - q * (np.pi / 2.0)
+        else:
+            work = np.asarray(angles).astype(np.float32)
+            q = np.rint(work * np.float32(2.0 / np.pi))
+            reduced = (work - q * np.float32(1.570796251296997)) - q * np.float32(7.549789415861596e-08)
+        qi = np.where(np.abs(q) < 2.0 ** 63, q, 0).astype(np.int64)
+        qi = np.where(np.abs(q) < 2.0 ** 63, qi, np.iinfo(np.int64).min)
+    return reduced.astype(np.float32), qi & 3
+
+
+def _ref_horner(x: np.ndarray, coefficients) -> np.ndarray:
+    value = np.full_like(x, np.float32(coefficients[-1]))
+    for c in reversed(coefficients[:-1]):
+        value = value * x + np.float32(c)
+    return value
+
+
+def ref_evaluate_reduced_sincos(reduced: np.ndarray, sin_coefficients, cos_coefficients):
+    """(sin, cos) float32 of reduced arguments (polynomial_sincos.py:125-135)."""
+    r = np.asarray(reduced).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        sq = r * r
+        return r * _ref_horner(sq, sin_coefficients), _ref_horner(sq, cos_coefficients)
+
+
+def ref_polynomial_sincos(angles: np.ndarray, sin_coefficients, cos_coefficients,
+                          accurate: bool = True):
+    """(cos, sin) float32 (polynomial_sincos.py:138-165)."""
+    reduced, q = ref_reduce_to_quarter_turn(angles, accurate)
+    s, c = ref_evaluate_reduced_sincos(reduced, sin_coefficients, cos_coefficients)
+    swap = (q & 1).astype(bool)
+    sm = np.where(swap, c, s)
+    cm = np.where(swap, s, c)
+    sin = np.where((q & 2).astype(bool), -sm, sm)
+    cos = np.where(((q + 1) & 2).astype(bool), -cm, cm)
+    return cos.astype(np.float32), sin.astype(np.float32)
+
+
 def rope_phase_increments(head_dim: int, theta: float) -> np.ndarray:
     """round(omega_i * 2^32 / (2 pi)) as int32, omega_i = theta^(-2i/head_dim)
     (src/sfu_repro/rope/benchmark_cuda_fused_rope.py:238-241)."""
