@@ -17,7 +17,9 @@ steps.  Alongside it the JSON line carries
   achievable ceiling of a 1-read/1-write stream of that size;
 * `functions`: the per-function sweep, polynomial vs native vs copy, over
   2^16..2^28 elements (L2, MALL and HBM regimes; graph replay, median of 9
-  rounds, implementations interleaved), plus every BASELINE configuration.
+  rounds, implementations interleaved), every BASELINE configuration, and
+  the sin/cos repeated-evaluation probes (the compute-bound regime, where
+  Gevals/s is the issue rate of each program).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep]
 """
@@ -48,6 +50,9 @@ def parse():
     p.add_argument("--pmc-pass", action="store_true",
                    help="counter pass: 3 launches of the headline kernel and 3 plain "
                         "256 MiB copies (torch copy_) as the byte-count calibration")
+    p.add_argument("--pmc-probes", action="store_true",
+                   help="counter pass over the sin/cos repeated-evaluation probes: each "
+                        "polynomial and native probe of the bench launched 4 times")
     p.add_argument("--pmc-sweep", action="store_true",
                    help="issue-rate counter pass: 3 eager launches of each polynomial, "
                         "native and copy kernel of the sweep at 2^20, 2^22 and 2^24 "
@@ -263,7 +268,91 @@ def sweep(lib, reps: int):
             del x, y
         torch.cuda.empty_cache()
     out.extend(config_rows(lib, reps))
+    out.extend(probe_rows(lib, reps))
     return out
+
+
+PROBE_ITERS = 32
+
+
+def probe_rows(lib, reps: int, eager_launches: int = 0):
+    """Issue-rate comparison in the compute-bound regime: the reference's
+    repeated-evaluation sin/cos probes (sincos_compute_*, rope_*_compute),
+    polynomial vs hardware v_sin/v_cos, on 2^22 RoPE-sized angles (enough
+    threads for every SIMD to hold 8 waves) with 32 evaluations each.  The
+    loads and stores are negligible, so Gevals/s is the instruction issue
+    rate of each program.  With eager_launches > 0 each probe is only
+    launched that many times (a counter pass) and nothing is timed."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    n = 1 << 22
+    g = torch.Generator(device=dev).manual_seed(20)
+    a = torch.rand(n, device=dev, generator=g) * 200 - 100
+    rows = []
+    groups = [
+        ("sincos_compute_f32", torch.float32,
+         [("poly_d3_d4", "launch_sincos_d3_d4_compute_f32"), ("poly_d7_d6", "launch_sincos_d7_d6_compute_f32"),
+          ("native", "launch_sincos_native_compute_f32")]),
+        ("sincos_compute_fp16", torch.float16,
+         [("poly_d3_d4", "launch_sincos_d3_d4_half_turn_fp16_compute"),
+          ("poly_d5_d6", "launch_sincos_d5_d6_half_turn_fp16_compute"),
+          ("native", "launch_sincos_native_fp16_compute")]),
+        ("sincos_compute_bf16", torch.bfloat16,
+         [("poly_d3_d4", "launch_sincos_d3_d4_half_turn_bf16_compute"),
+          ("poly_d5_d6", "launch_sincos_d5_d6_half_turn_bf16_compute"),
+          ("native", "launch_sincos_native_bf16_compute")]),
+    ]
+    for function, dt, impls in groups:
+        out = torch.empty(2, n, dtype=dt, device=dev)
+        launches = [(label, _launcher(lib, name, out, a, n, PROBE_ITERS)) for label, name in impls]
+        if eager_launches:
+            for _, fn in launches:
+                for _ in range(eager_launches):
+                    fn()
+            torch.cuda.synchronize()
+            continue
+        times = time_graphs_alternating([fn for _, fn in launches], max(5, reps // 10))
+        row = {"function": function, "config": f"2^22 angles U[-100,100], {PROBE_ITERS} evaluations each",
+               "evaluations": n * PROBE_ITERS}
+        for (label, _), ms in zip(launches, times):
+            row[f"{label}_us"] = round(ms * 1e3, 2)
+            row[f"{label}_gevals_s"] = round(n * PROBE_ITERS / ms / 1e6, 1)
+        for label, _ in launches[:-1]:
+            row[f"{label}_speedup"] = round(row["native_us"] / row[f"{label}_us"], 3)
+        rows.append(row)
+        del out
+    # RoPE tables: positions 0..4095 x 64 frequencies, 16 positions summed per entry
+    import math
+
+    seq, d, it = 4096, 128, 16
+    dims = torch.arange(0, d, 2, dtype=torch.float64)
+    freq = 500000.0 ** (-dims / d)
+    inc = torch.round(freq * (2.0 ** 32) / (2 * math.pi)).to(torch.int64).to(torch.int32).to(dev)
+    fr = freq.float().to(dev)
+    out = torch.empty(2, seq, d // 2, dtype=torch.float16, device=dev)
+    launches = [("poly_half_d5_d6", _launcher(lib, "launch_rope_sincos_fixed_half_turn_d5_d6_fp16_compute",
+                                              out, inc, seq, d // 2, it)),
+                ("poly_quarter_d3_d4", _launcher(lib, "launch_rope_sincos_fixed_d3_d4_fp16_compute",
+                                                 out, inc, seq, d // 2, it)),
+                ("native", _launcher(lib, "launch_rope_sincos_native_fp16_compute", out, fr, seq, d // 2, it))]
+    if eager_launches:
+        for _, fn in launches:
+            for _ in range(eager_launches):
+                fn()
+        torch.cuda.synchronize()
+        return rows
+    times = time_graphs_alternating([fn for _, fn in launches], max(5, reps // 10))
+    ev = seq * (d // 2) * it
+    row = {"function": "rope_sincos_compute_fp16", "config": f"S={seq}, F={d // 2}, theta=5e5, {it} positions each",
+           "evaluations": ev}
+    for (label, _), ms in zip(launches, times):
+        row[f"{label}_us"] = round(ms * 1e3, 2)
+        row[f"{label}_gevals_s"] = round(ev / ms / 1e6, 1)
+    for label, _ in launches[:-1]:
+        row[f"{label}_speedup"] = round(row["native_us"] / row[f"{label}_us"], 3)
+    rows.append(row)
+    return rows
 
 
 PMC_SWEEP_LOG2 = (20, 22, 24)
@@ -479,6 +568,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.pmc_sweep:
         pmc_sweep(lib)
+        return
+    if args.pmc_probes:
+        probe_rows(lib, 40, eager_launches=4)
         return
 
     # Synthetic B1 gate activations [8192, 14336] ~ N(0, 2^2), FP16, in HBM.
