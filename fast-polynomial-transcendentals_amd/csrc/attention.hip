@@ -8,46 +8,10 @@
 #include <hip/hip_runtime.h>
 
 #include "ops.hpp"
+#include "score_programs.hpp"
 #include "spline_ops_hip.h"
 
 namespace pt {
-
-// ---------------------------------------------------------------------------
-// B3: deployed direct-D3 probability and factored-D4 derivative
-// (scripts/audit_b3_deployed_fit.py:341-366; PTX main.tex:1072-1117).
-// ---------------------------------------------------------------------------
-
-struct B3Consts {
-    // Manifest rows (tests/test_audit_b3_deployed_fit.py:30-37) scaled by
-    // 1/4096 and rounded to BF16 (DirectB3Spec.deployed_forward_rows).
-    static constexpr float r0[4] = {bf16_value(1.0f / 4096), bf16_value(1.0546875f / 4096),
-                                    bf16_value(0.53515625f / 4096), bf16_value(0.11328125f / 4096)};
-    static constexpr float r1[4] = {bf16_value(-8.5625f / 4096), bf16_value(17.5f / 4096),
-                                    bf16_value(-9.0625f / 4096), bf16_value(2.140625f / 4096)};
-    // (intercept, slope) of the factored derivative.
-    static constexpr float g0[2] = {bf16_value(1.0f), bf16_value(-0.0087890625f)};
-    static constexpr float g1[2] = {bf16_value(1.0078125f), bf16_value(-0.0028076171875f)};
-    static constexpr float split = bf16_value(1.25f);
-    static constexpr float clamp = bf16_value(6.0f);
-};
-
-// One lane on a BF16 value held in FP32.  NaN follows the audit's Python
-// semantics: the clamp keeps NaN, max(0, NaN) gives 0, the derivative is NaN.
-template <bool WITH_GRAD>
-__device__ __forceinline__ void b3_lane(float x, float& y, float& dy) {
-    using C = B3Consts;
-    const bool row = x >= C::split;
-    const float xc = __builtin_elementwise_minimum(
-        __builtin_elementwise_maximum(x, -C::clamp), C::clamp);
-    float f = bfma(xc, row ? C::r1[3] : C::r0[3], row ? C::r1[2] : C::r0[2]);
-    f = bfma(xc, f, row ? C::r1[1] : C::r0[1]);
-    f = bfma(xc, f, row ? C::r1[0] : C::r0[0]);
-    y = f > 0.0f ? f : 0.0f;
-    if constexpr (WITH_GRAD) {
-        const float fac = bfma(xc, row ? C::g1[1] : C::g0[1], row ? C::g1[0] : C::g0[0]);
-        dy = y * fac;  // rounded once by the final pack
-    }
-}
 
 struct B3Op {
     static constexpr int NIN = 1, NOUT = 2;
@@ -69,35 +33,6 @@ struct B3FwdOp {
         b[0] = pack_exact_bf(y0, y1);
     }
 };
-
-// ---------------------------------------------------------------------------
-// B3-D2: FlashSigmoid probability via a range-reduced degree-2 exp2
-// (model autonumerics_zero/evolution/fit_flash_sigmoid_exp2_d2.py:55-77;
-// FA4 selects it for sigmoid_degree == 2, src/sfu_repro/fa4.py:469-476).
-// t = clamp(s * log2(e), -200, 200) (FP32; beyond the clamp the result is
-// 0 or inf either way, NaN scores give 0), n = floor(t), f = t - n,
-// m = c0 + f (c1 + f c2), p = m * 2^(n - 12)  (1/4096 folded into the
-// exponent), y = bf16(p), dy = bf16(p (1 - p)) with one FMA.
-// Coefficients: the fitter's FP32 output for n = 4096 (seed 1234).
-// ---------------------------------------------------------------------------
-
-struct B3D2Consts {
-    static constexpr float c0 = 1.0018835067749023f;   // 0x3F803DB8
-    static constexpr float c1 = 0.6557925939559937f;   // 0x3F27E206
-    static constexpr float c2 = 0.33421099185943604f;  // 0x3EAB1DB4
-    static constexpr float log2e = 1.44269504088896340736f;
-};
-
-__device__ __forceinline__ void b3_d2_lane(float s, float& y, float& dy) {
-    using C = B3D2Consts;
-    const float t = __builtin_fminf(__builtin_fmaxf(s * C::log2e, -200.0f), 200.0f);
-    const float fl = __builtin_floorf(t);
-    const float f = t - fl;
-    const float m = __builtin_fmaf(__builtin_fmaf(f, C::c2, C::c1), f, C::c0);
-    const float p = __builtin_ldexpf(m, (int)fl - 12);
-    y = p;
-    dy = __builtin_fmaf(-p, p, p);
-}
 
 struct B3D2Op {
     static constexpr int NIN = 1, NOUT = 2;
@@ -141,26 +76,6 @@ b3_f32_kernel(const float* __restrict__ s, uint16_t* __restrict__ y, uint16_t* _
     }
 }
 
-// ---------------------------------------------------------------------------
-// B2: tanh softcap.  u = bf16(s * (1/cap)) (FP32 product, one RNE rounding),
-// T = TANH_FWD_D4_ODD_BF16(u) (spline_structs_odd_bf16.cuh:153-179),
-// y = bf16(T * cap).  The derivative d y / d s = T'(u) (the scale cancels,
-// extras/paper/manuscript/main.tex:443-449) evaluates the derivative of the
-// D4 odd polynomial, D(t) = c1 + 2 c2 t + 3 c3 t^2 + 4 c4 t^3 with BF16
-// coefficients k*c_k and BF16 Horner steps, at t = |u|; D = 0 once t reaches
-// 2.609375, the first BF16 magnitude at which the forward program saturates
-// at 1 (and above the 2.75 clamp).
-// ---------------------------------------------------------------------------
-
-struct SoftcapConsts {
-    using T = BF16Prog<kTanh, kFwd, 4>;
-    static constexpr float d0 = bf16_value(T::P.c[1]);
-    static constexpr float d1 = bf16_value(2.0f * bf16_value(T::P.c[2]));
-    static constexpr float d2 = bf16_value(3.0f * bf16_value(T::P.c[3]));
-    static constexpr float d3 = bf16_value(4.0f * bf16_value(T::P.c[4]));
-    static constexpr float t_sat = 2.609375f;
-};
-
 struct SoftcapFwdOp {
     static constexpr int NIN = 1, NOUT = 1;
     static constexpr bool kParams = true;  // prm[0] = cap, prm[1] = 1/cap (FP32)
@@ -203,40 +118,6 @@ struct SoftcapBwdOp {
         b[0] = pack_bf(bf_lo(a[0]) * deriv(bf_lo(t2)), bf_hi(a[0]) * deriv(bf_hi(t2)));
     }
 };
-
-// ---------------------------------------------------------------------------
-// B5: exp2 with FP32 range reduction (autonumerics_zero/cuda_benchmarks/
-// utils_exp2_cuda.cuh:13-74): x = max(x, -127); n = floor(x); f = x - n;
-// p = polynomial 2^f on [0, 1); result bits = (n << 23) + bits(p).
-// D2 "safe" fraction p = 1 + a f + (1 - a) f^2, a = 0.6602339719
-// (extras/paper/manuscript/appendix_exp2.tex:29-32; sampled-minimax fit),
-// keeps p(0) = 1 and p(1) = 2.  D3 is FA4's e2e_asm2 fraction.
-// Defined for x < 128 (softmax exponents are <= 0); -inf and NaN give +0.
-// ---------------------------------------------------------------------------
-
-enum Exp2Kind : int { kExp2D2 = 0, kExp2D3 = 1, kExp2Native = 2 };
-
-template <int KIND>
-__device__ __forceinline__ float exp2_lane(float x) {
-    if constexpr (KIND == kExp2Native) {
-        return __builtin_amdgcn_exp2f(x);
-    } else {
-        x = __builtin_fmaxf(x, -127.0f);
-        const float fl = __builtin_floorf(x);
-        const float f = x - fl;
-        float p;
-        if constexpr (KIND == kExp2D2) {
-            p = __builtin_fmaf(f, 0.33976602809999057f, 0.6602339719000094f);
-            p = __builtin_fmaf(p, f, 1.0f);
-        } else {
-            p = __builtin_fmaf(f, 0.077119089663028717041015625f, 0.227564394474029541015625f);
-            p = __builtin_fmaf(p, f, 0.695146143436431884765625f);
-            p = __builtin_fmaf(p, f, 1.0f);
-        }
-        const int n = (int)fl;  // v_cvt_i32_f32 (saturating)
-        return as_f32(((uint32_t)n << 23) + as_u32(p));
-    }
-}
 
 // FP32 -> BF16: 8 values (two 16-byte loads) per thread-iteration.
 template <int KIND, bool LNT, bool SNT>

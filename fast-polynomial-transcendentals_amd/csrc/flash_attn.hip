@@ -1,0 +1,314 @@
+// flash_attn.hip -- fused attention forward for gfx950 with the paper's
+// score programs inside the tile loop: the attention-side integration site
+// the reference reaches through its FA4 fork (src/sfu_repro/fa4.py:454-752,
+// extras/paper/manuscript/main.tex:483-509), whose kernel is not part of the
+// reference tree.
+//
+// Modes (AttnMode): softmax with hardware exp2 (v_exp_f32), the B5 D2 "safe"
+// or FA4 D3 exp2 polynomial; tanh softcap (B2) cap*tanh(s/cap) with FP32
+// hardware tanh or the D4 BF16 program, followed by the hardware softmax;
+// sigmoid attention p = sigmoid(s - ln n) with hardware exp/rcp or the B3
+// direct D3 program (fitted for n = 4096), unnormalised O = P V.
+//
+// Layout: Q [B, Hq, S, 128], K and V [B, Hkv, S, 128], O [B, Hq, S, 128],
+// BF16, grouped-query heads (Hq a multiple of Hkv), S a multiple of 128,
+// optional causal mask.  s = q.k * scale.
+//
+// Design (all-transposed MFMA formulation, v_mfma_f32_32x32x16_bf16):
+//  * a block of 4 waves owns 128 queries; each wave owns 32 queries, held
+//    as the B operand Q^T (8 fragments of 8 BF16 per lane, loaded once);
+//  * the block stages 64-key tiles of K (row-major, 16-byte padded rows) and
+//    V^T (transposed while staging) in LDS;
+//  * S^T = K Q^T: lane (h, c) of a wave accumulates 16 keys x query c for
+//    each 32-key tile, so every per-query reduction is lane-local plus one
+//    exchange with lane c + 32;
+//  * O^T = V^T P^T: the S^T accumulator registers become the P^T fragments
+//    with no data movement by numbering the MFMA k index in the order the
+//    accumulator holds the keys; the V^T fragments are read from LDS in the
+//    same order (two 8-byte reads per fragment), and O^T keeps each lane on
+//    its own query, so the online-softmax rescale is lane-local too;
+//  * causal blocks run from the heaviest query block down.
+#include <hip/hip_runtime.h>
+
+#include "ops.hpp"
+#include "score_programs.hpp"
+#include "spline_ops_hip.h"
+
+namespace pt {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+enum AttnMode : int {
+    kAttnSoftmaxNative = 0,
+    kAttnSoftmaxExp2D2 = 1,
+    kAttnSoftmaxExp2D3 = 2,
+    kAttnSoftcapNative = 3,
+    kAttnSoftcapD4 = 4,
+    kAttnSigmoidNative = 5,
+    kAttnSigmoidB3 = 6,
+    kAttnModes = 7,
+};
+
+constexpr int kHeadDim = 128;
+constexpr int kAttnBlockQ = 128;  // 4 waves x 32 queries
+constexpr int kAttnBlockK = 64;   // keys per staged tile
+constexpr int kKStride = kHeadDim + 8;    // BF16 elements per LDS K row
+constexpr int kVStride = kAttnBlockK + 8;  // BF16 elements per LDS V^T row
+constexpr float kLog2e = 1.44269504088896340736f;
+
+struct AttnParams {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    uint16_t* o;
+    int64_t hq, hkv, seq;
+    float scale;       // s = q.k * scale
+    float cap;         // softcap
+    float sig_bias;    // sigmoid attention (hardware): p = sigmoid(s + sig_bias)
+    int causal;
+};
+
+__device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Softmax exponents x = s * log2(e) of 16 accumulator registers (one
+// 32-key tile), with the softcap transform where the mode has one.  The D4
+// program runs on BF16 pairs: u = bf16(bf16(s) * (1/cap)),
+// y = bf16(cap * TANH_D4_BF16(u)), the B2 program on the BF16 score.
+template <int MODE>
+__device__ __forceinline__ void softmax_exponents(const f32x16_t& acc, float scale, float cap,
+                                                  float inv_cap, float (&x)[16]) {
+    if constexpr (MODE == kAttnSoftcapD4) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            const uint32_t u = pack_bf(rbf(acc[r] * scale) * inv_cap, rbf(acc[r + 1] * scale) * inv_cap);
+            float t0, t1;
+            SoftcapConsts::T::eval2(u, t0, t1);
+            x[r] = rbf(t0 * cap) * kLog2e;
+            x[r + 1] = rbf(t1 * cap) * kLog2e;
+        }
+    } else if constexpr (MODE == kAttnSoftcapNative) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            x[r] = cap * native_lane<kTanh, kFwd>(acc[r] * scale * inv_cap) * kLog2e;
+    } else {
+        const float sl = scale * kLog2e;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = acc[r] * sl;
+    }
+}
+
+// exp2 of a softmax exponent x <= 0.
+template <int MODE>
+__device__ __forceinline__ float softmax_exp2(float x) {
+    if constexpr (MODE == kAttnSoftmaxExp2D2) return exp2_lane<kExp2D2>(x);
+    else if constexpr (MODE == kAttnSoftmaxExp2D3) return exp2_lane<kExp2D3>(x);
+    else return __builtin_amdgcn_exp2f(x);
+}
+
+template <int MODE>
+__device__ __forceinline__ float sigmoid_prob(float s, float bias) {
+    if constexpr (MODE == kAttnSigmoidB3) {
+        float y, dy;
+        b3_lane<false>(rbf(s), y, dy);
+        return y;
+    } else {
+        return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(s + bias) * kLog2e));
+    }
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
+    constexpr bool kSigmoid = MODE == kAttnSigmoidNative || MODE == kAttnSigmoidB3;
+    __shared__ __align__(16) uint16_t ks[kAttnBlockK * kKStride];
+    __shared__ __align__(16) uint16_t vt[kHeadDim * kVStride];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, c32 = lane & 31;
+    const int64_t nqb = p.seq / kAttnBlockQ;
+    const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x;
+    const int64_t head = blockIdx.y, b = blockIdx.z;
+    const int64_t kvh = head / (p.hq / p.hkv);
+    const uint16_t* qp = p.q + (b * p.hq + head) * p.seq * kHeadDim;
+    const uint16_t* kp = p.k + (b * p.hkv + kvh) * p.seq * kHeadDim;
+    const uint16_t* vp = p.v + (b * p.hkv + kvh) * p.seq * kHeadDim;
+    const int64_t q0 = qb * kAttnBlockQ + wave * 32;  // first query of this wave
+    const int64_t qrow = q0 + c32;                     // this lane's query
+
+    bf16x8_t qf[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        qf[c] = *reinterpret_cast<const bf16x8_t*>(qp + qrow * kHeadDim + c * 16 + h * 8);
+
+    f32x16_t oacc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) oacc[dt] = (f32x16_t){};
+    float m = -__builtin_inff(), l = 0.0f;
+    const float inv_cap = 1.0f / p.cap;
+
+    const int64_t nkb = p.causal ? (qb + 1) * (kAttnBlockQ / kAttnBlockK) : p.seq / kAttnBlockK;
+    for (int64_t kb = 0; kb < nkb; ++kb) {
+        const int64_t k0 = kb * kAttnBlockK;
+        // ---- stage K (row-major) and V^T ----
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = j * 16 + (tid >> 4), col = (tid & 15) * 8;
+            const u32x4_t val = *reinterpret_cast<const u32x4_t*>(kp + (k0 + row) * kHeadDim + col);
+            *reinterpret_cast<u32x4_t*>(ks + row * kKStride + col) = val;
+        }
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int key = 2 * (tid & 31), d0 = ((tid >> 5) + 8 * r) * 8;
+            const u32x4_t a = *reinterpret_cast<const u32x4_t*>(vp + (k0 + key) * kHeadDim + d0);
+            const u32x4_t c = *reinterpret_cast<const u32x4_t*>(vp + (k0 + key + 1) * kHeadDim + d0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                // (V[key][d], V[key+1][d]) for d = d0 + 2j and d0 + 2j + 1
+                *reinterpret_cast<uint32_t*>(vt + (d0 + 2 * j) * kVStride + key) =
+                    __builtin_amdgcn_perm(c[j], a[j], 0x05040100u);
+                *reinterpret_cast<uint32_t*>(vt + (d0 + 2 * j + 1) * kVStride + key) =
+                    __builtin_amdgcn_perm(c[j], a[j], 0x07060302u);
+            }
+        }
+        __syncthreads();
+
+        if (k0 <= q0 + 31 || !p.causal) {  // wave-uniform: some key of the tile is visible
+            // ---- S^T = K Q^T for two 32-key tiles ----
+            f32x16_t sacc[2];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                sacc[kt] = (f32x16_t){};
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const bf16x8_t a =
+                        *reinterpret_cast<const bf16x8_t*>(ks + (kt * 32 + c32) * kKStride + c * 16 + h * 8);
+                    sacc[kt] = mfma32(a, qf[c], sacc[kt]);
+                }
+            }
+            // key of accumulator register r in tile kt: k0 + kt*32 + 8*(r/4) + 4h + r%4
+            const bool need_mask = p.causal && (k0 + kAttnBlockK - 1 > q0);
+            float prob[2][16];
+            if constexpr (kSigmoid) {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t key = k0 + kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                        const float pr = sigmoid_prob<MODE>(sacc[kt][r] * p.scale, p.sig_bias);
+                        prob[kt][r] = (need_mask && key > qrow) ? 0.0f : pr;
+                    }
+            } else {
+                float x[2][16];
+                float mt = -__builtin_inff();
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt) {
+                    softmax_exponents<MODE>(sacc[kt], p.scale, p.cap, inv_cap, x[kt]);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t key = k0 + kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                        if (need_mask && key > qrow) x[kt][r] = -__builtin_inff();
+                        mt = __builtin_fmaxf(mt, x[kt][r]);
+                    }
+                }
+                mt = __builtin_fmaxf(mt, __shfl_xor(mt, 32));
+                const float m_new = __builtin_fmaxf(m, mt);
+                const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+                m = m_new;
+                float ls = 0.0f;
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float e = x[kt][r] == -__builtin_inff() ? 0.0f : softmax_exp2<MODE>(x[kt][r] - m_new);
+                        prob[kt][r] = e;
+                        ls += e;
+                    }
+                l = l * alpha + ls;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+            }
+            // ---- O^T += V^T P^T ----
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc) {
+                    bf16x8_t pf;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) pf[e] = (__bf16)prob[kt][8 * cc + e];
+                    const int kbase = kt * 32 + cc * 16 + 4 * h;
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt) {
+                        const uint16_t* row = vt + (dt * 32 + c32) * kVStride + kbase;
+                        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
+                        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 8);
+                        const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
+                        oacc[dt] = mfma32(__builtin_bit_cast(bf16x8_t, w), pf, oacc[dt]);
+                    }
+                }
+        }
+        __syncthreads();
+    }
+
+    // ---- normalise and store: oacc[dt][r] = O^T[dt*32 + 8*(r/4) + 4h + r%4][qrow] ----
+    float inv = 1.0f;
+    if constexpr (!kSigmoid) {
+        l += __shfl_xor(l, 32);
+        inv = 1.0f / l;
+    }
+    uint16_t* orow = p.o + ((b * p.hq + head) * p.seq + qrow) * kHeadDim;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = dt * 32 + 8 * g + 4 * h;
+            const u32x2_t w = {pack_bf(oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv),
+                               pack_bf(oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv)};
+            *reinterpret_cast<u32x2_t*>(orow + d) = w;
+        }
+}
+
+}  // namespace pt
+
+using namespace pt;
+
+extern "C" int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k,
+                                               const void* v, int64_t batch, int64_t q_heads,
+                                               int64_t kv_heads, int64_t seq, int64_t head_dim,
+                                               int mode, int causal, float scale, float cap,
+                                               void* stream) {
+    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || head_dim != kHeadDim)
+        return hipErrorInvalidValue;
+    if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
+        return hipErrorInvalidValue;
+    if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f))
+        return hipErrorInvalidValue;
+    // the direct B3 program is fitted for n = 4096 (src/sfu_repro/fa4.py:404-413)
+    if (mode == kAttnSigmoidB3 && seq != 4096) return hipErrorInvalidValue;
+    if (batch == 0 || seq == 0) return hipSuccess;
+    if (!out || !q || !k || !v || !aligned16(out) || !aligned16(q) || !aligned16(k) || !aligned16(v))
+        return hipErrorInvalidValue;
+    if (batch > 65535 || q_heads > 65535) return hipErrorInvalidValue;
+    AttnParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out,
+                   q_heads, kv_heads, seq, scale, cap > 0.0f ? cap : 1.0f,
+                   -__builtin_logf((float)seq), causal != 0};
+    const dim3 grid((unsigned)(seq / kAttnBlockQ), (unsigned)q_heads, (unsigned)batch);
+#define PT_ATTN(M)                                                                            \
+    case M:                                                                                   \
+        hipLaunchKernelGGL((flash_fwd_kernel<M>), grid, dim3(256), 0, hs(stream), prm); \
+        break;
+    switch (mode) {
+        PT_ATTN(kAttnSoftmaxNative)
+        PT_ATTN(kAttnSoftmaxExp2D2)
+        PT_ATTN(kAttnSoftmaxExp2D3)
+        PT_ATTN(kAttnSoftcapNative)
+        PT_ATTN(kAttnSoftcapD4)
+        PT_ATTN(kAttnSigmoidNative)
+        PT_ATTN(kAttnSigmoidB3)
+    }
+#undef PT_ATTN
+    return hipGetLastError();
+}

@@ -423,6 +423,27 @@ int launch_evaluate_reduced_sincos(void* sin_out, void* cos_out, const void* red
                                    int reduced_f64, int64_t size, const float* sin_coeffs,
                                    int n_sin, const float* cos_coeffs, int n_cos, void* stream);
 
+/* ---- fused attention forward with the score programs in the tile loop -----
+ * No counterpart launcher exists in the reference: its attention programs (B2
+ * softcap, B3 sigmoid attention, B5 exp2) run inside a FlashAttention-4 fork
+ * that is not part of the reference tree (src/sfu_repro/fa4.py:454-752 selects
+ * them; extras/paper/manuscript/main.tex:483-509 describes the fusion).
+ * q [B, Hq, S, 128], k and v [B, Hkv, S, 128] -> out [B, Hq, S, 128], BF16;
+ * Hq a multiple of Hkv (grouped-query), S a multiple of 128, head_dim 128,
+ * every pointer 16-byte aligned; s = q.k * scale.  mode:
+ *   0 softmax, hardware exp2 (v_exp_f32)      1 softmax, B5 D2 "safe" exp2
+ *   2 softmax, FA4 D3 exp2                     3 softcap cap*tanh(s/cap), FP32
+ *     hardware tanh, then softmax              4 softcap with the D4 BF16
+ *     program on bf16(s) (B2), then softmax    5 sigmoid attention,
+ *     p = sigmoid(s - ln S) (hardware exp/rcp), O = P V unnormalised
+ *   6 sigmoid attention with the B3 direct D3 program on bf16(s)
+ *     (fitted for S = 4096; other lengths are rejected).
+ * causal != 0 masks keys after the query. */
+int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k, const void* v,
+                                    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
+                                    int64_t head_dim, int mode, int causal, float scale, float cap,
+                                    void* stream);
+
 /* ---- device/launch introspection --------------------------------------- */
 /* Number of compute units of the current device and the grid the
  * elementwise launchers use for `size` 16-bit elements and `streams` tensors

@@ -1,0 +1,137 @@
+"""GPU parity of the fused attention forward (every score mode, causal and
+not, grouped-query heads) against a float32 CPU reference that applies the
+same score programs through the oracle: exp2 D2/D3 (B5), the D4 softcap
+(B2) and the B3 direct program, with hardware-mode references in float64
+math.  Tolerances cover the kernel's BF16 rounding of P before the P V
+product and of the output."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+MODES = {"softmax_native": 0, "softmax_exp2_d2": 1, "softmax_exp2_d3": 2, "softcap_native": 3,
+         "softcap_d4": 4, "sigmoid_native": 5, "sigmoid_b3": 6}
+
+
+def _inputs(b, hq, hkv, s, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, hq, s, 128, generator=g).bfloat16()
+    k = torch.randn(b, hkv, s, 128, generator=g).bfloat16()
+    v = torch.randn(b, hkv, s, 128, generator=g).bfloat16()
+    return q, k, v
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def reference(oracle, q, k, v, mode, causal, scale, cap):
+    """float32 CPU reference; the polynomial modes evaluate the same score
+    program through the oracle."""
+    hq, hkv = q.shape[1], k.shape[1]
+    qf = q.float()
+    kf = k.float().repeat_interleave(hq // hkv, dim=1)
+    vf = v.float().repeat_interleave(hq // hkv, dim=1)
+    s = (qf @ kf.transpose(-1, -2)) * scale
+    n = s.shape[-1]
+    mask = torch.ones(n, n, dtype=torch.bool).triu(1) if causal else torch.zeros(n, n, dtype=torch.bool)
+    if mode.startswith("sigmoid"):
+        if mode == "sigmoid_b3":
+            y, _ = oracle.b3_direct_f32(s.numpy().reshape(-1))
+            p = torch.from_numpy(oracle.bf16_bits_to_f32(y).reshape(s.shape))
+        else:
+            p = torch.sigmoid(s.double() - math.log(n)).float()
+        p = p.masked_fill(mask, 0.0)
+        return p @ vf
+    if mode == "softcap_native":
+        s = (cap * torch.tanh(s.double() / cap)).float()
+    elif mode == "softcap_d4":
+        sb = oracle.f32_to_bf16_bits(s.numpy().reshape(-1))
+        s = torch.from_numpy(oracle.bf16_bits_to_f32(oracle.softcap_fwd_bf16(sb, cap)).reshape(s.shape))
+    x = s * math.log2(math.e)
+    x = x.masked_fill(mask, -math.inf)
+    m = x.amax(-1, keepdim=True)
+    if mode in ("softmax_exp2_d2", "softmax_exp2_d3"):
+        kind = oracle.EXP2_D2 if mode == "softmax_exp2_d2" else oracle.EXP2_D3
+        p = torch.from_numpy(oracle.exp2(kind, (x - m).numpy().reshape(-1), out_bf16=False)).reshape(x.shape)
+        p = p.masked_fill(mask, 0.0)
+    else:
+        p = torch.exp2((x - m).double()).float()
+    return (p @ vf) / p.sum(-1, keepdim=True)
+
+
+def _run(capi, cuda, q, k, v, mode, causal, scale, cap):
+    b, hq, s, d = q.shape
+    out = torch.empty(b, hq, s, d, dtype=torch.bfloat16, device=cuda)
+    qd, kd, vd = q.to(cuda), k.to(cuda), v.to(cuda)
+    import ctypes
+    capi.call("launch_flash_attention_fwd_bf16", out, qd, kd, vd, b, hq, k.shape[1], s, d,
+              ctypes.c_int(MODES[mode]), ctypes.c_int(int(causal)), ctypes.c_float(scale),
+              ctypes.c_float(cap))
+    torch.cuda.synchronize()
+    return out.cpu().float()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("mode", [m for m in MODES if m != "sigmoid_b3"])
+def test_attention_modes_match_reference(capi, oracle, cuda, mode, causal):
+    q, k, v = _inputs(1, 4, 2, 384, seed=MODES[mode] + 10 * causal)
+    scale = 1 / math.sqrt(128)
+    # softcap 30 on scaled scores: raise the score spread so the cap bites
+    if mode.startswith("softcap"):
+        q = (q.float() * 6).bfloat16()
+    got = _run(capi, cuda, q, k, v, mode, causal, scale, 30.0)
+    ref = reference(oracle, q, k, v, mode, causal, scale, 30.0)
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs().max().item()
+    tol = 1.5e-2 * ref.abs().max().item() + 2e-3
+    assert err <= tol, (mode, causal, err, tol)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_sigmoid_b3_at_its_fitted_length(capi, oracle, cuda, causal):
+    q, k, v = _inputs(1, 2, 1, 4096, seed=77 + causal)
+    scale = 1 / math.sqrt(128)
+    got = _run(capi, cuda, q, k, v, "sigmoid_b3", causal, scale, 30.0)
+    ref = reference(oracle, q, k, v, "sigmoid_b3", causal, scale, 30.0)
+    err = (got - ref).abs().max().item()
+    assert err <= 1.5e-2 * ref.abs().max().item() + 2e-3, err
+    # and it tracks hardware sigmoid attention: the program's fit error is a
+    # few percent per probability (clamped at |s| = 6), so the unnormalised
+    # sums agree in direction rather than element by element
+    nat = _run(capi, cuda, q, k, v, "sigmoid_native", causal, scale, 30.0)
+    cos = torch.nn.functional.cosine_similarity(got.reshape(-1), nat.reshape(-1), dim=0).item()
+    assert cos > 0.95, cos
+
+
+def test_polynomial_softmax_is_close_to_hardware(capi, cuda):
+    q, k, v = _inputs(1, 2, 2, 256, seed=5)
+    scale = 1 / math.sqrt(128)
+    nat = _run(capi, cuda, q, k, v, "softmax_native", True, scale, 30.0)
+    for mode, bound in (("softmax_exp2_d2", 2e-2), ("softmax_exp2_d3", 4e-3)):
+        got = _run(capi, cuda, q, k, v, mode, True, scale, 30.0)
+        assert (got - nat).abs().max().item() <= bound * nat.abs().max().item() + 2e-3
+
+
+def test_rejected_arguments(capi, cuda):
+    import ctypes
+    q = torch.zeros(1, 2, 128, 128, dtype=torch.bfloat16, device=cuda)
+    out = torch.empty_like(q)
+    fn = capi.launch_flash_attention_fwd_bf16
+    def call(seq, d, mode, hq=2, hkv=1, cap=30.0):
+        return fn(capi.ptr(out), capi.ptr(q), capi.ptr(q), capi.ptr(q), ctypes.c_int64(1),
+                  ctypes.c_int64(hq), ctypes.c_int64(hkv), ctypes.c_int64(seq), ctypes.c_int64(d),
+                  ctypes.c_int(mode), ctypes.c_int(1), ctypes.c_float(0.1), ctypes.c_float(cap),
+                  capi.stream())
+    assert call(100, 128, 0) != 0        # S not a multiple of 128
+    assert call(128, 64, 0) != 0         # head_dim 64
+    assert call(128, 128, 6) != 0        # B3 program outside its fitted length
+    assert call(128, 128, 9) != 0        # unknown mode
+    assert call(128, 128, 0, hq=3, hkv=2) != 0
+    assert call(128, 128, 4, cap=0.0) != 0
+    assert call(128, 128, 0) == 0
+    torch.cuda.synchronize()
