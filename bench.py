@@ -19,7 +19,9 @@ steps.  Alongside it the JSON line carries
   2^16..2^28 elements (L2, MALL and HBM regimes; graph replay, median of 9
   rounds, implementations interleaved), every BASELINE configuration, and
   the sin/cos repeated-evaluation probes (the compute-bound regime, where
-  Gevals/s is the issue rate of each program).
+  Gevals/s is the issue rate of each program), and the fused attention
+  forward at the reference's B2/B3/B5 component shape, polynomial score
+  programs against hardware transcendentals (TFLOP/s vs the BF16 MFMA peak).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep]
 """
@@ -53,6 +55,11 @@ def parse():
     p.add_argument("--pmc-probes", action="store_true",
                    help="counter pass over the sin/cos repeated-evaluation probes: each "
                         "polynomial and native probe of the bench launched 4 times")
+    p.add_argument("--pmc-attention", action="store_true",
+                   help="counter pass over the attention forward: each score mode at the "
+                        "component shape launched 3 times")
+    p.add_argument("--attention-only", action="store_true",
+                   help="time only the attention forward rows")
     p.add_argument("--pmc-sweep", action="store_true",
                    help="issue-rate counter pass: 3 eager launches of each polynomial, "
                         "native and copy kernel of the sweep at 2^20, 2^22 and 2^24 "
@@ -269,7 +276,66 @@ def sweep(lib, reps: int):
         torch.cuda.empty_cache()
     out.extend(config_rows(lib, reps))
     out.extend(probe_rows(lib, reps))
+    out.extend(attention_rows(lib, reps))
     return out
+
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+ATTN_SHAPE = (1, 32, 8, 4096, 128)  # B, Hq, Hkv, S, D
+
+
+def attention_rows(lib, reps: int, eager_launches: int = 0):
+    """The attention programs inside the fused forward at the reference's
+    component shape (causal GQA, B=1, S=4096, Hq=32, Hkv=8, D=128): B5
+    softmax with the D2 / D3 exp2 against hardware exp2, B2 softcap 30
+    with the D4 tanh against hardware tanh, B3 sigmoid attention with the
+    direct D3 program against hardware exp/rcp.  Causal FLOPs are
+    4 B Hq S^2 D / 2 (the two products over the lower triangle); the bound
+    is the dense BF16 MFMA peak.  With eager_launches > 0 each mode is only
+    launched that many times (a counter pass) and nothing is timed."""
+    import ctypes
+    import math
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    b, hq, hkv, s, d = ATTN_SHAPE
+    g = torch.Generator(device=dev).manual_seed(30)
+    q = torch.randn(b, hq, s, d, device=dev, generator=g).bfloat16()
+    k = torch.randn(b, hkv, s, d, device=dev, generator=g).bfloat16()
+    v = torch.randn(b, hkv, s, d, device=dev, generator=g).bfloat16()
+    # scores spread as after QK-norm with a learnt scale: s = q.k / sqrt(d) * 4
+    qs = (q.float() * 4).bfloat16()
+    o = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(d)
+    flops = 4 * b * hq * s * s * d / 2
+
+    def fa(mode, qq):
+        return _launcher(lib, "launch_flash_attention_fwd_bf16", o, qq, k, v, b, hq, hkv, s, d,
+                         ctypes.c_int(mode), ctypes.c_int(1), ctypes.c_float(scale), ctypes.c_float(30.0))
+
+    groups = [("B5 softmax exp2", [("poly_d2", fa(1, q)), ("poly_d3", fa(2, q)), ("native", fa(0, q))]),
+              ("B2 softcap 30", [("poly_d4", fa(4, qs)), ("native", fa(3, qs))]),
+              ("B3 sigmoid attention", [("poly_b3", fa(6, q)), ("native", fa(5, q))])]
+    rows = []
+    for function, launches in groups:
+        if eager_launches:
+            for _, fn in launches:
+                for _ in range(eager_launches):
+                    fn()
+            torch.cuda.synchronize()
+            continue
+        times = time_graphs_alternating([fn for _, fn in launches], max(5, reps // 10))
+        row = {"function": f"attention_fwd {function}", "dtype": "bf16",
+               "config": f"causal GQA B={b} S={s} Hq={hq} Hkv={hkv} D={d}", "flops": flops}
+        for (label, _), ms in zip(launches, times):
+            row[f"{label}_us"] = round(ms * 1e3, 2)
+            row[f"{label}_tflops"] = round(flops / ms / 1e9, 1)
+            row[f"{label}_frac_mfma_peak"] = round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)
+        for label, _ in launches[:-1]:
+            row[f"{label}_speedup"] = round(row["native_us"] / row[f"{label}_us"], 3)
+        rows.append(row)
+    return rows
 
 
 PROBE_ITERS = 32
@@ -405,7 +471,9 @@ def _launcher(lib, name, *args):
     fn.restype = ctypes.c_int
     conv = []
     for a in args:
-        if isinstance(a, torch.Tensor):
+        if isinstance(a, ctypes._SimpleCData):
+            conv.append(a)
+        elif isinstance(a, torch.Tensor):
             conv.append(_vp(a))
         elif isinstance(a, float):
             conv.append(ctypes.c_float(a))
@@ -571,6 +639,12 @@ def main():
         return
     if args.pmc_probes:
         probe_rows(lib, 40, eager_launches=4)
+        return
+    if args.pmc_attention:
+        attention_rows(lib, 40, eager_launches=3)
+        return
+    if args.attention_only:
+        print(json.dumps({"functions": attention_rows(lib, args.sweep_reps)}), flush=True)
         return
 
     # Synthetic B1 gate activations [8192, 14336] ~ N(0, 2^2), FP16, in HBM.

@@ -27,6 +27,9 @@
 //    accumulator holds the keys; the V^T fragments are read from LDS in the
 //    same order (two 8-byte reads per fragment), and O^T keeps each lane on
 //    its own query, so the online-softmax rescale is lane-local too;
+//  * the next K / V tile is loaded into registers while the current one is
+//    used and written to the second LDS buffer afterwards (one barrier per
+//    tile);
 //  * causal blocks run from the heaviest query block down.
 #include <hip/hip_runtime.h>
 
@@ -120,18 +123,129 @@ __device__ __forceinline__ float sigmoid_prob(float s, float bias) {
     }
 }
 
+// Rescale threshold of the online softmax (log2 units): the running maximum
+// m is only moved when a tile raises it by more than this, so exponents stay
+// <= 8 and P <= 256; O and l carry the same stale m, so the final O / l is
+// unchanged.  Most tiles skip the 64-register rescale of O.
+constexpr float kRescaleThreshold = 8.0f;
+
+// One 64-key tile for one wave: S^T = K Q^T, the score program, the online
+// softmax (or sigmoid) and O^T += V^T P^T.  MASKED: the tile crosses the
+// causal diagonal of this wave's 32 queries.
+template <int MODE, bool MASKED>
+__device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t* __restrict__ ks,
+                                            const uint16_t* __restrict__ vt, const bf16x8_t (&qf)[8],
+                                            f32x16_t (&oacc)[4], float& m, float& l, int diag,
+                                            int h, int c32, float inv_cap) {
+    constexpr bool kSigmoid = MODE == kAttnSigmoidNative || MODE == kAttnSigmoidB3;
+    constexpr bool kPlain = MODE <= kAttnSoftmaxExp2D3;
+    // ---- S^T = K Q^T for two 32-key tiles ----
+    f32x16_t sacc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+        sacc[kt] = (f32x16_t){};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const bf16x8_t a =
+                *reinterpret_cast<const bf16x8_t*>(ks + (kt * 32 + c32) * kKStride + c * 16 + h * 8);
+            sacc[kt] = mfma32(a, qf[c], sacc[kt]);
+        }
+    }
+    // accumulator register r of tile kt holds key k0 + kt*32 + 8*(r/4) + 4h + r%4;
+    // diag = k0 + 4h - query, so the key is masked when diag + offset > 0
+    auto masked = [&](int kt, int r) {
+        return MASKED && diag + kt * 32 + 8 * (r >> 2) + (r & 3) > 0;
+    };
+    float prob[2][16];
+    if constexpr (kSigmoid) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pr = sigmoid_prob<MODE>(sacc[kt][r] * p.scale, p.sig_bias);
+                prob[kt][r] = masked(kt, r) ? 0.0f : pr;
+            }
+    } else {
+        // exponents: plain softmax keeps the raw dot products and folds the
+        // scale into the exp2 argument; softcap modes transform first
+        float x[2][16];
+        const float sl = kPlain ? p.scale * kLog2e : 1.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            if constexpr (kPlain) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) x[kt][r] = sacc[kt][r];
+            } else {
+                softmax_exponents<MODE>(sacc[kt], p.scale, p.cap, inv_cap, x[kt]);
+            }
+        }
+        float mt = -__builtin_inff();
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if (masked(kt, r)) x[kt][r] = -__builtin_inff();
+                mt = __builtin_fmaxf(mt, x[kt][r]);
+            }
+        mt = __builtin_fmaxf(mt, __shfl_xor(mt, 32)) * sl;
+        // lanes c and c + 32 hold the same query and take the same decision
+        const bool move = mt > m + kRescaleThreshold;
+        if (__any(move)) {
+            const float m_use = move ? mt : m;
+            const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+            m = m_use;
+            l *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+        }
+        float ls = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = softmax_exp2<MODE>(__builtin_fmaf(x[kt][r], sl, -m));
+                prob[kt][r] = (MODE != kAttnSoftmaxNative && MODE != kAttnSoftcapNative && masked(kt, r))
+                                  ? 0.0f : e;
+                ls += prob[kt][r];
+            }
+        l += ls;
+    }
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            bf16x8_t pf;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pf[e] = (__bf16)prob[kt][8 * cc + e];
+            const int kbase = kt * 32 + cc * 16 + 4 * h;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const uint16_t* row = vt + (dt * 32 + c32) * kVStride + kbase;
+                const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
+                const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 8);
+                const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
+                oacc[dt] = mfma32(__builtin_bit_cast(bf16x8_t, w), pf, oacc[dt]);
+            }
+        }
+}
+
+// Grid (q_heads, S / 128, batch): blockIdx.y runs over query blocks, heaviest
+// first under the causal mask, and the head index varies fastest, so the
+// first wave of resident blocks takes the longest query blocks of every head.
 template <int MODE>
 __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     constexpr bool kSigmoid = MODE == kAttnSigmoidNative || MODE == kAttnSigmoidB3;
-    __shared__ __align__(16) uint16_t ks[kAttnBlockK * kKStride];
-    __shared__ __align__(16) uint16_t vt[kHeadDim * kVStride];
+    // two buffers: the next tile is written while the current one is read
+    __shared__ __align__(16) uint16_t ks[2][kAttnBlockK * kKStride];
+    __shared__ __align__(16) uint16_t vt[2][kHeadDim * kVStride];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, c32 = lane & 31;
     const int64_t nqb = p.seq / kAttnBlockQ;
-    const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x;
-    const int64_t head = blockIdx.y, b = blockIdx.z;
+    const int64_t head = blockIdx.x, b = blockIdx.z;
+    const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
     const int64_t kvh = head / (p.hq / p.hkv);
     const uint16_t* qp = p.q + (b * p.hq + head) * p.seq * kHeadDim;
     const uint16_t* kp = p.k + (b * p.hkv + kvh) * p.seq * kHeadDim;
@@ -150,106 +264,56 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     float m = -__builtin_inff(), l = 0.0f;
     const float inv_cap = 1.0f / p.cap;
 
-    const int64_t nkb = p.causal ? (qb + 1) * (kAttnBlockQ / kAttnBlockK) : p.seq / kAttnBlockK;
-    for (int64_t kb = 0; kb < nkb; ++kb) {
-        const int64_t k0 = kb * kAttnBlockK;
-        // ---- stage K (row-major) and V^T ----
+    // staging: K rows krow + 16 j (16 bytes at kcol); V rows vkey, vkey + 1
+    // (16 bytes at vd + 64 r), transposed into V^T while written to LDS
+    const int krow = tid >> 4, kcol = (tid & 15) * 8;
+    const int vkey = 2 * (tid & 31), vd = (tid >> 5) * 8;
+    u32x4_t kr[4], va[2], vc[2];
+    auto load = [&](int64_t k0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = j * 16 + (tid >> 4), col = (tid & 15) * 8;
-            const u32x4_t val = *reinterpret_cast<const u32x4_t*>(kp + (k0 + row) * kHeadDim + col);
-            *reinterpret_cast<u32x4_t*>(ks + row * kKStride + col) = val;
-        }
+        for (int j = 0; j < 4; ++j)
+            kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (k0 + krow + 16 * j) * kHeadDim + kcol);
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const int key = 2 * (tid & 31), d0 = ((tid >> 5) + 8 * r) * 8;
-            const u32x4_t a = *reinterpret_cast<const u32x4_t*>(vp + (k0 + key) * kHeadDim + d0);
-            const u32x4_t c = *reinterpret_cast<const u32x4_t*>(vp + (k0 + key + 1) * kHeadDim + d0);
+            va[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey) * kHeadDim + vd + 64 * r);
+            vc[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey + 1) * kHeadDim + vd + 64 * r);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<u32x4_t*>(&ks[buf][(krow + 16 * j) * kKStride + kcol]) = kr[j];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int d0 = vd + 64 * r;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 // (V[key][d], V[key+1][d]) for d = d0 + 2j and d0 + 2j + 1
-                *reinterpret_cast<uint32_t*>(vt + (d0 + 2 * j) * kVStride + key) =
-                    __builtin_amdgcn_perm(c[j], a[j], 0x05040100u);
-                *reinterpret_cast<uint32_t*>(vt + (d0 + 2 * j + 1) * kVStride + key) =
-                    __builtin_amdgcn_perm(c[j], a[j], 0x07060302u);
+                *reinterpret_cast<uint32_t*>(&vt[buf][(d0 + 2 * j) * kVStride + vkey]) =
+                    __builtin_amdgcn_perm(vc[r][j], va[r][j], 0x05040100u);
+                *reinterpret_cast<uint32_t*>(&vt[buf][(d0 + 2 * j + 1) * kVStride + vkey]) =
+                    __builtin_amdgcn_perm(vc[r][j], va[r][j], 0x07060302u);
             }
         }
-        __syncthreads();
+    };
 
-        if (k0 <= q0 + 31 || !p.causal) {  // wave-uniform: some key of the tile is visible
-            // ---- S^T = K Q^T for two 32-key tiles ----
-            f32x16_t sacc[2];
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                sacc[kt] = (f32x16_t){};
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const bf16x8_t a =
-                        *reinterpret_cast<const bf16x8_t*>(ks + (kt * 32 + c32) * kKStride + c * 16 + h * 8);
-                    sacc[kt] = mfma32(a, qf[c], sacc[kt]);
-                }
-            }
-            // key of accumulator register r in tile kt: k0 + kt*32 + 8*(r/4) + 4h + r%4
-            const bool need_mask = p.causal && (k0 + kAttnBlockK - 1 > q0);
-            float prob[2][16];
-            if constexpr (kSigmoid) {
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int64_t key = k0 + kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                        const float pr = sigmoid_prob<MODE>(sacc[kt][r] * p.scale, p.sig_bias);
-                        prob[kt][r] = (need_mask && key > qrow) ? 0.0f : pr;
-                    }
-            } else {
-                float x[2][16];
-                float mt = -__builtin_inff();
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt) {
-                    softmax_exponents<MODE>(sacc[kt], p.scale, p.cap, inv_cap, x[kt]);
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int64_t key = k0 + kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                        if (need_mask && key > qrow) x[kt][r] = -__builtin_inff();
-                        mt = __builtin_fmaxf(mt, x[kt][r]);
-                    }
-                }
-                mt = __builtin_fmaxf(mt, __shfl_xor(mt, 32));
-                const float m_new = __builtin_fmaxf(m, mt);
-                const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-                m = m_new;
-                float ls = 0.0f;
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float e = x[kt][r] == -__builtin_inff() ? 0.0f : softmax_exp2<MODE>(x[kt][r] - m_new);
-                        prob[kt][r] = e;
-                        ls += e;
-                    }
-                l = l * alpha + ls;
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
-            }
-            // ---- O^T += V^T P^T ----
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int cc = 0; cc < 2; ++cc) {
-                    bf16x8_t pf;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) pf[e] = (__bf16)prob[kt][8 * cc + e];
-                    const int kbase = kt * 32 + cc * 16 + 4 * h;
-#pragma unroll
-                    for (int dt = 0; dt < 4; ++dt) {
-                        const uint16_t* row = vt + (dt * 32 + c32) * kVStride + kbase;
-                        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
-                        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 8);
-                        const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
-                        oacc[dt] = mfma32(__builtin_bit_cast(bf16x8_t, w), pf, oacc[dt]);
-                    }
-                }
+    const int64_t nkb = p.causal ? (qb + 1) * (kAttnBlockQ / kAttnBlockK) : p.seq / kAttnBlockK;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int64_t kb = 0; kb < nkb; ++kb) {
+        const int buf = (int)(kb & 1);
+        const int64_t k0 = kb * kAttnBlockK;
+        const bool more = kb + 1 < nkb;
+        if (more) load(k0 + kAttnBlockK);  // in flight during this tile's math
+        if (!p.causal || k0 <= q0 + 31) {  // wave-uniform: some key of the tile is visible
+            const int diag = (int)(k0 - qrow) + 4 * h;
+            if (p.causal && k0 + kAttnBlockK - 1 > q0)
+                attend_tile<MODE, true>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
+            else
+                attend_tile<MODE, false>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
         }
+        if (more) store(buf ^ 1);
         __syncthreads();
     }
 
@@ -291,11 +355,11 @@ extern "C" int launch_flash_attention_fwd_bf16(void* out, const void* q, const v
     if (batch == 0 || seq == 0) return hipSuccess;
     if (!out || !q || !k || !v || !aligned16(out) || !aligned16(q) || !aligned16(k) || !aligned16(v))
         return hipErrorInvalidValue;
-    if (batch > 65535 || q_heads > 65535) return hipErrorInvalidValue;
+    if (batch > 65535 || seq / kAttnBlockQ > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
     AttnParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out,
                    q_heads, kv_heads, seq, scale, cap > 0.0f ? cap : 1.0f,
                    -__builtin_logf((float)seq), causal != 0};
-    const dim3 grid((unsigned)(seq / kAttnBlockQ), (unsigned)q_heads, (unsigned)batch);
+    const dim3 grid((unsigned)q_heads, (unsigned)(seq / kAttnBlockQ), (unsigned)batch);
 #define PT_ATTN(M)                                                                            \
     case M:                                                                                   \
         hipLaunchKernelGGL((flash_fwd_kernel<M>), grid, dim3(256), 0, hs(stream), prm); \
