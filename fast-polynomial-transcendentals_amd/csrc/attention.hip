@@ -104,13 +104,7 @@ struct SoftcapNativeOp {
 struct SoftcapBwdOp {
     static constexpr int NIN = 2, NOUT = 1;  // (grad_out, scores) -> grad_scores
     static constexpr bool kParams = true;
-    __device__ __forceinline__ static float deriv(float t) {
-        using C = SoftcapConsts;
-        float r = bfma(t, C::d3, C::d2);
-        r = bfma(t, r, C::d1);
-        r = bfma(t, r, C::d0);
-        return t < C::t_sat ? r : 0.0f;
-    }
+    __device__ __forceinline__ static float deriv(float t) { return SoftcapConsts::deriv(t); }
     __device__ __forceinline__ static void pair(const uint32_t (&a)[2], uint32_t (&b)[1],
                                                 const float (&prm)[2]) {
         const uint32_t u = pack_bf(bf_lo(a[1]) * prm[1], bf_hi(a[1]) * prm[1]);

@@ -640,6 +640,90 @@ std::vector<at::Tensor> polynomial_sincos_f32(at::Tensor angles, std::vector<dou
     return {c, sn};
 }
 
+// ---------------------------------------------------------------------------
+// fused attention (the runtime behind sfu_repro.fa4; FA4's flash_attn_fwd,
+// src/sfu_repro/fa4.py:356-428): q [B, S, Hq, 128], k and v [B, S, Hkv, 128]
+// BF16 with a contiguous head dimension -> out [B, S, Hq, 128], lse [B, Hq, S]
+// ---------------------------------------------------------------------------
+
+void check_attn_operand(const at::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+    TORCH_CHECK(t.scalar_type() == at::kBFloat16, name, " must be bfloat16");
+    TORCH_CHECK(t.dim() == 4, name, " must have shape [batch, seqlen, heads, head_dim]");
+    TORCH_CHECK(t.stride(3) == 1, name, " must be contiguous in head_dim");
+}
+
+std::vector<at::Tensor> flash_attn_fwd_bf16(at::Tensor q, at::Tensor k, at::Tensor v, int64_t mode,
+                                            int64_t exp2_route, bool causal, double softmax_scale,
+                                            double softcap, double sigmoid_bias) {
+    check_attn_operand(q, "q");
+    check_attn_operand(k, "k");
+    check_attn_operand(v, "v");
+    TORCH_CHECK(k.sizes() == v.sizes(), "k and v must have the same shape");
+    TORCH_CHECK(q.size(0) == k.size(0) && q.size(1) == k.size(1) && q.size(3) == k.size(3),
+                "q, k and v must agree in batch, seqlen and head_dim");
+    TORCH_CHECK(q.size(3) == 128, "head_dim must be 128, got ", q.size(3));
+    TORCH_CHECK(q.size(2) % k.size(2) == 0, "q heads (", q.size(2),
+                ") must be a multiple of kv heads (", k.size(2), ")");
+    TORCH_CHECK(q.size(1) % 128 == 0, "seqlen must be a multiple of 128, got ", q.size(1));
+    c10::OptionalDeviceGuard guard(q.device());
+    const int64_t b = q.size(0), sq = q.size(1), hq = q.size(2), hkv = k.size(2);
+    at::Tensor out = at::empty({b, sq, hq, 128}, q.options());
+    at::Tensor lse = at::zeros({b, hq, sq}, q.options().dtype(at::kFloat));
+    const int64_t strides[12] = {q.stride(0), q.stride(2), q.stride(1), k.stride(0), k.stride(2),
+                                 k.stride(1), v.stride(0), v.stride(2), v.stride(1), out.stride(0),
+                                 out.stride(2), out.stride(1)};
+    void* s = current_stream(q);
+    check_launch(launch_flash_attention_fwd_strided_bf16(
+                     out.data_ptr(), lse.data_ptr<float>(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                     b, hq, hkv, sq, 128, strides, (int)mode, (int)exp2_route, causal ? 1 : 0,
+                     (float)softmax_scale, (float)softcap, (float)sigmoid_bias, s),
+                 s);
+    return {out, lse};
+}
+
+std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor out,
+                                            at::Tensor dout, at::Tensor lse, int64_t mode, int64_t grad,
+                                            int64_t exp2_route, bool causal, double softmax_scale,
+                                            double softcap, double sigmoid_bias) {
+    check_attn_operand(q, "q");
+    check_attn_operand(k, "k");
+    check_attn_operand(v, "v");
+    check_attn_operand(out, "out");
+    check_attn_operand(dout, "dout");
+    TORCH_CHECK(k.sizes() == v.sizes(), "k and v must have the same shape");
+    TORCH_CHECK(out.sizes() == q.sizes() && dout.sizes() == q.sizes(), "out and dout must have q's shape");
+    TORCH_CHECK(q.size(0) == k.size(0) && q.size(1) == k.size(1) && q.size(3) == k.size(3),
+                "q, k and v must agree in batch, seqlen and head_dim");
+    TORCH_CHECK(q.size(3) == 128, "head_dim must be 128, got ", q.size(3));
+    TORCH_CHECK(q.size(2) % k.size(2) == 0, "q heads must be a multiple of kv heads");
+    TORCH_CHECK(q.size(1) % 128 == 0, "seqlen must be a multiple of 128, got ", q.size(1));
+    const int64_t b = q.size(0), sq = q.size(1), hq = q.size(2), hkv = k.size(2);
+    TORCH_CHECK(lse.is_cuda() && lse.scalar_type() == at::kFloat && lse.is_contiguous() &&
+                    lse.dim() == 3 && lse.size(0) == b && lse.size(1) == hq && lse.size(2) == sq,
+                "lse must be a contiguous float32 CUDA tensor [batch, heads, seqlen]");
+    c10::OptionalDeviceGuard guard(q.device());
+    at::Tensor dq = at::empty({b, sq, hq, 128}, q.options());
+    at::Tensor dk = at::empty({b, sq, hkv, 128}, q.options());
+    at::Tensor dv = at::empty({b, sq, hkv, 128}, q.options());
+    at::Tensor delta = at::empty({b, hq, sq}, q.options().dtype(at::kFloat));
+    const int64_t strides[24] = {q.stride(0),    q.stride(2),    q.stride(1),    k.stride(0),
+                                 k.stride(2),    k.stride(1),    v.stride(0),    v.stride(2),
+                                 v.stride(1),    out.stride(0),  out.stride(2),  out.stride(1),
+                                 dout.stride(0), dout.stride(2), dout.stride(1), dq.stride(0),
+                                 dq.stride(2),   dq.stride(1),   dk.stride(0),   dk.stride(2),
+                                 dk.stride(1),   dv.stride(0),   dv.stride(2),   dv.stride(1)};
+    void* s = current_stream(q);
+    check_launch(launch_flash_attention_bwd_strided_bf16(
+                     dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr<float>(),
+                     q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
+                     lse.data_ptr<float>(), b, hq, hkv, sq, 128, strides, (int)mode, (int)grad,
+                     (int)exp2_route, causal ? 1 : 0, (float)softmax_scale, (float)softcap,
+                     (float)sigmoid_bias, s),
+                 s);
+    return {dq, dk, dv};
+}
+
 std::vector<at::Tensor> reduce_to_quarter_turn_f32(at::Tensor angles, bool accurate) {
     at::Tensor a = ref_angles(angles, "angles");
     c10::OptionalDeviceGuard guard(a.device());
@@ -1205,6 +1289,16 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Fused native BF16 Q/K rotary embedding and transpose");
 
     // RoPE reference evaluator (sfu_repro.rope.polynomial_sincos on the device)
+    m.def("flash_attn_fwd_bf16", &flash_attn_fwd_bf16, py::arg("q"), py::arg("k"), py::arg("v"),
+          py::arg("mode"), py::arg("exp2_route") = 4, py::arg("causal") = true,
+          py::arg("softmax_scale"), py::arg("softcap") = 0.0, py::arg("sigmoid_bias") = 0.0,
+          "Fused attention forward with the score programs in the tile loop; "
+          "q [B,S,Hq,128], k/v [B,S,Hkv,128] BF16 -> [out [B,S,Hq,128], lse [B,Hq,S] FP32]");
+    m.def("flash_attn_bwd_bf16", &flash_attn_bwd_bf16, py::arg("q"), py::arg("k"), py::arg("v"),
+          py::arg("out"), py::arg("dout"), py::arg("lse"), py::arg("mode"), py::arg("grad") = 0,
+          py::arg("exp2_route") = 0, py::arg("causal") = true, py::arg("softmax_scale"),
+          py::arg("softcap") = 0.0, py::arg("sigmoid_bias") = 0.0,
+          "Fused attention backward -> [dq [B,S,Hq,128], dk, dv [B,S,Hkv,128]] BF16");
     m.def("polynomial_sincos_f32", &polynomial_sincos_f32, py::arg("angles"),
           py::arg("sin_coefficients"), py::arg("cos_coefficients"), py::arg("accurate") = true,
           "Quarter-turn reduction (FP64 or FP32 Cody-Waite) and paired parity polynomials "

@@ -33,49 +33,24 @@
 //  * causal blocks run from the heaviest query block down.
 #include <hip/hip_runtime.h>
 
-#include "ops.hpp"
-#include "score_programs.hpp"
+#include "flash_attn.hpp"
 #include "spline_ops_hip.h"
 
 namespace pt {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-
-enum AttnMode : int {
-    kAttnSoftmaxNative = 0,
-    kAttnSoftmaxExp2D2 = 1,
-    kAttnSoftmaxExp2D3 = 2,
-    kAttnSoftcapNative = 3,
-    kAttnSoftcapD4 = 4,
-    kAttnSigmoidNative = 5,
-    kAttnSigmoidB3 = 6,
-    kAttnModes = 7,
-};
-
-constexpr int kHeadDim = 128;
-constexpr int kAttnBlockQ = 128;  // 4 waves x 32 queries
-constexpr int kAttnBlockK = 64;   // keys per staged tile
-constexpr int kKStride = kHeadDim + 8;    // BF16 elements per LDS K row
-constexpr int kVStride = kAttnBlockK + 8;  // BF16 elements per LDS V^T row
-constexpr float kLog2e = 1.44269504088896340736f;
 
 struct AttnParams {
     const uint16_t* q;
     const uint16_t* k;
     const uint16_t* v;
     uint16_t* o;
+    float* lse;  // [B, Hq, S] natural-log partition function, or null
+    AttnStrides qs, ks, vs, os;
     int64_t hq, hkv, seq;
-    float scale;       // s = q.k * scale
-    float cap;         // softcap
-    float sig_bias;    // sigmoid attention (hardware): p = sigmoid(s + sig_bias)
+    float scale;     // s = q.k * scale
+    float cap;       // softcap
+    float sig_bias;  // sigmoid attention: p = sigmoid(s + sig_bias)
     int causal;
 };
-
-__device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
 
 // Softmax exponents x = s * log2(e) of 16 accumulator registers (one
 // 32-key tile), with the softcap transform where the mode has one.  The D4
@@ -104,22 +79,36 @@ __device__ __forceinline__ void softmax_exponents(const f32x16_t& acc, float sca
     }
 }
 
-// exp2 of a softmax exponent x <= 0.
-template <int MODE>
-__device__ __forceinline__ float softmax_exp2(float x) {
-    if constexpr (MODE == kAttnSoftmaxExp2D2) return exp2_lane<kExp2D2>(x);
-    else if constexpr (MODE == kAttnSoftmaxExp2D3) return exp2_lane<kExp2D3>(x);
-    else return __builtin_amdgcn_exp2f(x);
+// exp2 of a softmax exponent (x <= 8 under the lazy rescale).  Of every
+// ROUTE consecutive exponents of a lane, the first four take the mode's
+// polynomial and the rest v_exp_f32 (FA4's routed exp2, four lanes per group
+// of exp2_emu_freq, src/sfu_repro/fa4.py:313-353); ROUTE 4 routes all.
+template <int MODE, int ROUTE>
+__device__ __forceinline__ float softmax_exp2(float x, int i) {
+    if (ROUTE >= 4 && i % ROUTE < 4) {
+        if constexpr (MODE == kAttnSoftmaxExp2D2) return exp2_lane<kExp2D2>(x);
+        else if constexpr (MODE == kAttnSoftmaxExp2D3) return exp2_lane<kExp2D3>(x);
+        else if constexpr (MODE == kAttnSoftmaxExp2Pwl2) return exp2_lane<kExp2Pwl2>(x);
+    }
+    return __builtin_amdgcn_exp2f(x);
 }
 
+// Sigmoid-attention probabilities of two scores.
 template <int MODE>
-__device__ __forceinline__ float sigmoid_prob(float s, float bias) {
+__device__ __forceinline__ void sigmoid_prob2(float s0, float s1, float bias, float& p0, float& p1) {
     if constexpr (MODE == kAttnSigmoidB3) {
-        float y, dy;
-        b3_lane<false>(rbf(s), y, dy);
-        return y;
+        float dy;
+        b3_lane<false>(rbf(s0), p0, dy);
+        b3_lane<false>(rbf(s1), p1, dy);
+    } else if constexpr (MODE == kAttnSigmoidB3D2) {
+        float dy;
+        b3_d2_lane(rbf(s0), p0, dy);
+        b3_d2_lane(rbf(s1), p1, dy);
+    } else if constexpr (MODE >= kAttnSigmoidD3 && MODE <= kAttnSigmoidD6) {
+        BF16Prog<kSigmoid, kFwd, MODE - kAttnSigmoidD3 + 3>::eval2(pack_bf(s0 + bias, s1 + bias), p0, p1);
     } else {
-        return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(s + bias) * kLog2e));
+        p0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(s0 + bias) * kLog2e));
+        p1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(s1 + bias) * kLog2e));
     }
 }
 
@@ -132,13 +121,13 @@ constexpr float kRescaleThreshold = 8.0f;
 // One 64-key tile for one wave: S^T = K Q^T, the score program, the online
 // softmax (or sigmoid) and O^T += V^T P^T.  MASKED: the tile crosses the
 // causal diagonal of this wave's 32 queries.
-template <int MODE, bool MASKED>
+template <int MODE, int ROUTE, bool MASKED>
 __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t* __restrict__ ks,
                                             const uint16_t* __restrict__ vt, const bf16x8_t (&qf)[8],
                                             f32x16_t (&oacc)[4], float& m, float& l, int diag,
                                             int h, int c32, float inv_cap) {
-    constexpr bool kSigmoid = MODE == kAttnSigmoidNative || MODE == kAttnSigmoidB3;
-    constexpr bool kPlain = MODE <= kAttnSoftmaxExp2D3;
+    constexpr bool kSigmoid = attn_is_sigmoid(MODE);
+    constexpr bool kPlain = attn_is_plain_softmax(MODE);
     // ---- S^T = K Q^T for two 32-key tiles ----
     f32x16_t sacc[2];
 #pragma unroll
@@ -161,9 +150,11 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float pr = sigmoid_prob<MODE>(sacc[kt][r] * p.scale, p.sig_bias);
-                prob[kt][r] = masked(kt, r) ? 0.0f : pr;
+            for (int r = 0; r < 16; r += 2) {
+                float p0, p1;
+                sigmoid_prob2<MODE>(sacc[kt][r] * p.scale, sacc[kt][r + 1] * p.scale, p.sig_bias, p0, p1);
+                prob[kt][r] = masked(kt, r) ? 0.0f : p0;
+                prob[kt][r + 1] = masked(kt, r + 1) ? 0.0f : p1;
             }
     } else {
         // exponents: plain softmax keeps the raw dot products and folds the
@@ -203,9 +194,9 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float e = softmax_exp2<MODE>(__builtin_fmaf(x[kt][r], sl, -m));
-                prob[kt][r] = (MODE != kAttnSoftmaxNative && MODE != kAttnSoftcapNative && masked(kt, r))
-                                  ? 0.0f : e;
+                const float e = softmax_exp2<MODE, ROUTE>(__builtin_fmaf(x[kt][r], sl, -m), kt * 16 + r);
+                // v_exp_f32(-inf) is 0; the polynomial programs clamp at -127
+                prob[kt][r] = (attn_has_exp2_program(MODE) && masked(kt, r)) ? 0.0f : e;
                 ls += prob[kt][r];
             }
         l += ls;
@@ -233,9 +224,9 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
 // Grid (q_heads, S / 128, batch): blockIdx.y runs over query blocks, heaviest
 // first under the causal mask, and the head index varies fastest, so the
 // first wave of resident blocks takes the longest query blocks of every head.
-template <int MODE>
+template <int MODE, int ROUTE>
 __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
-    constexpr bool kSigmoid = MODE == kAttnSigmoidNative || MODE == kAttnSigmoidB3;
+    constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     // two buffers: the next tile is written while the current one is read
     __shared__ __align__(16) uint16_t ks[2][kAttnBlockK * kKStride];
     __shared__ __align__(16) uint16_t vt[2][kHeadDim * kVStride];
@@ -247,16 +238,17 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     const int64_t head = blockIdx.x, b = blockIdx.z;
     const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
     const int64_t kvh = head / (p.hq / p.hkv);
-    const uint16_t* qp = p.q + (b * p.hq + head) * p.seq * kHeadDim;
-    const uint16_t* kp = p.k + (b * p.hkv + kvh) * p.seq * kHeadDim;
-    const uint16_t* vp = p.v + (b * p.hkv + kvh) * p.seq * kHeadDim;
+    const uint16_t* qp = p.q + b * p.qs.b + head * p.qs.h;
+    const uint16_t* kp = p.k + b * p.ks.b + kvh * p.ks.h;
+    const uint16_t* vp = p.v + b * p.vs.b + kvh * p.vs.h;
+    const int64_t kss = p.ks.s, vss = p.vs.s;
     const int64_t q0 = qb * kAttnBlockQ + wave * 32;  // first query of this wave
     const int64_t qrow = q0 + c32;                     // this lane's query
 
     bf16x8_t qf[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c)
-        qf[c] = *reinterpret_cast<const bf16x8_t*>(qp + qrow * kHeadDim + c * 16 + h * 8);
+        qf[c] = *reinterpret_cast<const bf16x8_t*>(qp + qrow * p.qs.s + c * 16 + h * 8);
 
     f32x16_t oacc[4];
 #pragma unroll
@@ -272,11 +264,11 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     auto load = [&](int64_t k0) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (k0 + krow + 16 * j) * kHeadDim + kcol);
+            kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (k0 + krow + 16 * j) * kss + kcol);
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            va[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey) * kHeadDim + vd + 64 * r);
-            vc[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey + 1) * kHeadDim + vd + 64 * r);
+            va[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey) * vss + vd + 64 * r);
+            vc[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey + 1) * vss + vd + 64 * r);
         }
     };
     auto store = [&](int buf) {
@@ -309,9 +301,9 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
         if (!p.causal || k0 <= q0 + 31) {  // wave-uniform: some key of the tile is visible
             const int diag = (int)(k0 - qrow) + 4 * h;
             if (p.causal && k0 + kAttnBlockK - 1 > q0)
-                attend_tile<MODE, true>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
+                attend_tile<MODE, ROUTE, true>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
             else
-                attend_tile<MODE, false>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
+                attend_tile<MODE, ROUTE, false>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
         }
         if (more) store(buf ^ 1);
         __syncthreads();
@@ -322,8 +314,12 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     if constexpr (!kSigmoid) {
         l += __shfl_xor(l, 32);
         inv = 1.0f / l;
+        // log sum exp(s') with s' the (capped) scaled score: m and log2(l) are
+        // in log2 units
+        if (p.lse != nullptr && h == 0)
+            p.lse[(b * p.hq + head) * p.seq + qrow] = (m + __builtin_log2f(l)) * kLn2;
     }
-    uint16_t* orow = p.o + ((b * p.hq + head) * p.seq + qrow) * kHeadDim;
+    uint16_t* orow = p.o + b * p.os.b + head * p.os.h + qrow * p.os.s;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -339,40 +335,100 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
 
 using namespace pt;
 
-extern "C" int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k,
-                                               const void* v, int64_t batch, int64_t q_heads,
-                                               int64_t kv_heads, int64_t seq, int64_t head_dim,
-                                               int mode, int causal, float scale, float cap,
-                                               void* stream) {
-    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || head_dim != kHeadDim)
+namespace {
+
+constexpr int kRoutes[] = {4, 6, 8, 10, 12, 16, 20, 24, 32};
+
+bool route_supported(int route) {
+    for (int r : kRoutes)
+        if (r == route) return true;
+    return false;
+}
+
+template <int MODE, int ROUTE>
+void launch_fwd(const AttnParams& prm, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE>), grid, dim3(256), 0, st, prm);
+}
+
+template <int MODE>
+void launch_routed(const AttnParams& prm, dim3 grid, hipStream_t st, int route) {
+    switch (route) {
+        case 6: launch_fwd<MODE, 6>(prm, grid, st); break;
+        case 8: launch_fwd<MODE, 8>(prm, grid, st); break;
+        case 10: launch_fwd<MODE, 10>(prm, grid, st); break;
+        case 12: launch_fwd<MODE, 12>(prm, grid, st); break;
+        case 16: launch_fwd<MODE, 16>(prm, grid, st); break;
+        case 20: launch_fwd<MODE, 20>(prm, grid, st); break;
+        case 24: launch_fwd<MODE, 24>(prm, grid, st); break;
+        case 32: launch_fwd<MODE, 32>(prm, grid, st); break;
+        default: launch_fwd<MODE, 4>(prm, grid, st); break;
+    }
+}
+
+bool stride_ok(const AttnStrides& t) { return t.b >= 0 && t.h >= 0 && t.s >= 0 && t.s % 8 == 0 && t.h % 8 == 0 && t.b % 8 == 0; }
+
+}  // namespace
+
+extern "C" int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q,
+                                                       const void* k, const void* v, int64_t batch,
+                                                       int64_t q_heads, int64_t kv_heads, int64_t seq,
+                                                       int64_t head_dim, const int64_t* strides,
+                                                       int mode, int exp2_route, int causal,
+                                                       float scale, float cap, float sigmoid_bias,
+                                                       void* stream) {
+    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || head_dim != kHeadDim || !strides)
         return hipErrorInvalidValue;
     if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
         return hipErrorInvalidValue;
     if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f))
         return hipErrorInvalidValue;
-    // the direct B3 program is fitted for n = 4096 (src/sfu_repro/fa4.py:404-413)
-    if (mode == kAttnSigmoidB3 && seq != 4096) return hipErrorInvalidValue;
+    if (attn_has_exp2_program(mode) && !route_supported(exp2_route)) return hipErrorInvalidValue;
+    // the B3 programs are fitted for n = 4096 (src/sfu_repro/fa4.py:404-413;
+    // autonumerics_zero/evolution/fit_flash_sigmoid_exp2_d2.py)
+    if ((mode == kAttnSigmoidB3 || mode == kAttnSigmoidB3D2) && seq != 4096) return hipErrorInvalidValue;
+    const AttnStrides st[4] = {{strides[0], strides[1], strides[2]}, {strides[3], strides[4], strides[5]},
+                               {strides[6], strides[7], strides[8]}, {strides[9], strides[10], strides[11]}};
+    for (const AttnStrides& t : st)
+        if (!stride_ok(t)) return hipErrorInvalidValue;
     if (batch == 0 || seq == 0) return hipSuccess;
     if (!out || !q || !k || !v || !aligned16(out) || !aligned16(q) || !aligned16(k) || !aligned16(v))
         return hipErrorInvalidValue;
+    if (lse && (reinterpret_cast<uintptr_t>(lse) & 3)) return hipErrorInvalidValue;
+    if (attn_is_sigmoid(mode)) lse = nullptr;  // sigmoid attention has no partition function
     if (batch > 65535 || seq / kAttnBlockQ > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
-    AttnParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out,
-                   q_heads, kv_heads, seq, scale, cap > 0.0f ? cap : 1.0f,
-                   -__builtin_logf((float)seq), causal != 0};
+    AttnParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out, lse,
+                   st[0], st[1], st[2], st[3], q_heads, kv_heads, seq, scale,
+                   cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0};
     const dim3 grid((unsigned)q_heads, (unsigned)(seq / kAttnBlockQ), (unsigned)batch);
-#define PT_ATTN(M)                                                                            \
-    case M:                                                                                   \
-        hipLaunchKernelGGL((flash_fwd_kernel<M>), grid, dim3(256), 0, hs(stream), prm); \
-        break;
+    hipStream_t hst = hs(stream);
     switch (mode) {
-        PT_ATTN(kAttnSoftmaxNative)
-        PT_ATTN(kAttnSoftmaxExp2D2)
-        PT_ATTN(kAttnSoftmaxExp2D3)
-        PT_ATTN(kAttnSoftcapNative)
-        PT_ATTN(kAttnSoftcapD4)
-        PT_ATTN(kAttnSigmoidNative)
-        PT_ATTN(kAttnSigmoidB3)
+        case kAttnSoftmaxNative: launch_fwd<kAttnSoftmaxNative, 0>(prm, grid, hst); break;
+        case kAttnSoftmaxExp2D2: launch_routed<kAttnSoftmaxExp2D2>(prm, grid, hst, exp2_route); break;
+        case kAttnSoftmaxExp2D3: launch_routed<kAttnSoftmaxExp2D3>(prm, grid, hst, exp2_route); break;
+        case kAttnSoftmaxExp2Pwl2: launch_routed<kAttnSoftmaxExp2Pwl2>(prm, grid, hst, exp2_route); break;
+        case kAttnSoftcapNative: launch_fwd<kAttnSoftcapNative, 0>(prm, grid, hst); break;
+        case kAttnSoftcapD4: launch_fwd<kAttnSoftcapD4, 0>(prm, grid, hst); break;
+        case kAttnSigmoidNative: launch_fwd<kAttnSigmoidNative, 0>(prm, grid, hst); break;
+        case kAttnSigmoidB3: launch_fwd<kAttnSigmoidB3, 0>(prm, grid, hst); break;
+        case kAttnSigmoidB3D2: launch_fwd<kAttnSigmoidB3D2, 0>(prm, grid, hst); break;
+        case kAttnSigmoidD3: launch_fwd<kAttnSigmoidD3, 0>(prm, grid, hst); break;
+        case kAttnSigmoidD3 + 1: launch_fwd<kAttnSigmoidD3 + 1, 0>(prm, grid, hst); break;
+        case kAttnSigmoidD3 + 2: launch_fwd<kAttnSigmoidD3 + 2, 0>(prm, grid, hst); break;
+        case kAttnSigmoidD6: launch_fwd<kAttnSigmoidD6, 0>(prm, grid, hst); break;
     }
-#undef PT_ATTN
     return hipGetLastError();
+}
+
+extern "C" int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k,
+                                               const void* v, int64_t batch, int64_t q_heads,
+                                               int64_t kv_heads, int64_t seq, int64_t head_dim,
+                                               int mode, int causal, float scale, float cap,
+                                               void* stream) {
+    if (mode < 0 || mode > kAttnSigmoidB3) return hipErrorInvalidValue;
+    const int64_t qh = seq * kHeadDim, kh = seq * kHeadDim;
+    const int64_t strides[12] = {q_heads * qh, qh, kHeadDim, kv_heads * kh, kh, kHeadDim,
+                                 kv_heads * kh, kh, kHeadDim, q_heads * qh, qh, kHeadDim};
+    return launch_flash_attention_fwd_strided_bf16(out, nullptr, q, k, v, batch, q_heads, kv_heads,
+                                                   seq, head_dim, strides, mode, 4, causal, scale,
+                                                   cap, -__builtin_logf((float)seq), stream);
 }

@@ -1,0 +1,59 @@
+// flash_attn.hpp -- definitions shared by the fused attention forward
+// (flash_attn.hip) and backward (flash_attn_bwd.hip): score modes, tile
+// constants, operand strides and the MFMA wrapper.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "ops.hpp"
+#include "score_programs.hpp"
+
+namespace pt {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+enum AttnMode : int {
+    kAttnSoftmaxNative = 0,
+    kAttnSoftmaxExp2D2 = 1,
+    kAttnSoftmaxExp2D3 = 2,
+    kAttnSoftcapNative = 3,
+    kAttnSoftcapD4 = 4,
+    kAttnSigmoidNative = 5,
+    kAttnSigmoidB3 = 6,
+    kAttnSigmoidB3D2 = 7,
+    kAttnSigmoidD3 = 8,  // 8..11: BF16 sigmoid D3..D6 on bf16(s + bias)
+    kAttnSigmoidD6 = 11,
+    kAttnSoftmaxExp2Pwl2 = 12,
+    kAttnModes = 13,
+};
+
+constexpr bool attn_is_sigmoid(int mode) { return mode >= kAttnSigmoidNative && mode <= kAttnSigmoidD6; }
+constexpr bool attn_is_plain_softmax(int mode) {
+    return mode <= kAttnSoftmaxExp2D3 || mode == kAttnSoftmaxExp2Pwl2;
+}
+constexpr bool attn_has_exp2_program(int mode) {
+    return mode == kAttnSoftmaxExp2D2 || mode == kAttnSoftmaxExp2D3 || mode == kAttnSoftmaxExp2Pwl2;
+}
+
+constexpr int kHeadDim = 128;
+constexpr int kAttnBlockQ = 128;  // 4 waves x 32 queries
+constexpr int kAttnBlockK = 64;   // keys per staged tile
+constexpr int kKStride = kHeadDim + 8;    // BF16 elements per LDS K row
+constexpr int kVStride = kAttnBlockK + 8;  // BF16 elements per LDS V^T row
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kLn2 = 0.69314718055994530942f;
+
+// Element strides (batch, head, sequence) of one [*, *, *, 128] operand; the
+// head dimension is contiguous.
+struct AttnStrides {
+    int64_t b, h, s;
+};
+
+__device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace pt

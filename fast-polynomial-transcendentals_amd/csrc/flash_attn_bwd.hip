@@ -1,0 +1,606 @@
+// flash_attn_bwd.hip -- fused attention backward for gfx950 with the same
+// score programs as the forward (flash_attn.hip): the gradient side of the
+// FA4 integration site (src/sfu_repro/fa4.py:430-461 calls flash_attn_bwd;
+// the FA4 kernel itself is not part of the reference tree).
+//
+// Three kernels, no atomics:
+//  * delta: D[q] = sum_d dO[q][d] O[q][d] (FP32), for the softmax modes;
+//  * dK/dV: a block owns 128 keys (32 per wave, K and V held in registers)
+//    and streams 32-query tiles of Q, Q^T, dO, dO^T (+ lse, D) through LDS;
+//    S = Q K^T and dP = dO V^T come out with one key per lane, so P and dS
+//    are ready-made B fragments of dV^T += dO^T P and dK^T += Q^T dS (the
+//    k index numbered in accumulator order, as in the forward);
+//  * dQ: a block owns 128 queries (32 per wave, Q and dO in registers) and
+//    streams 32-key tiles of K, K^T and V: S^T = K Q^T and dP^T = V dO^T have
+//    one query per lane, dQ^T += K^T dS^T.
+// P is recomputed from the saved log-sum-exp (softmax) or directly (sigmoid
+// attention); the score program's derivative enters dS:
+//   softmax        dS = P (dP - D)
+//   softcap        dS = P (dP - D) g(u),  g = 1 - tanh^2 (hardware), the D4
+//                  derivative polynomial, 1 - T(u)^2, or 1 (straight-through)
+//   sigmoid        dS = dP g,  g = p (1 - p), or the B3 factored D4 derivative
+// and dq.k = dS * scale.
+#include <hip/hip_runtime.h>
+
+#include "flash_attn.hpp"
+#include "spline_ops_hip.h"
+
+namespace pt {
+
+// Derivative program of the backward (AttnBwdGrad in the C ABI).
+enum AttnGrad : int {
+    kGradNatural = 0,     // the mode's own derivative
+    kGradAnalytical = 1,  // softcap D4: derivative polynomial T'(u)
+    kGradSte = 2,         // softcap D4: straight-through, g = 1
+    kGradExact1mt2 = 3,   // softcap D4: g = 1 - T(u)^2
+    kGradAlgebraic = 4,   // sigmoid B3: g = y (1 - y)
+    kGradDirect = 5,      // sigmoid B3: the factored D4 derivative
+};
+
+constexpr int kBwdTile = 32;              // queries (dK/dV) or keys (dQ) per staged tile
+constexpr int kRowStride = kHeadDim + 8;  // row-major tile rows in LDS (BF16 elements)
+constexpr int kTStride = kBwdTile + 4;    // transposed tile rows [128][36]
+constexpr int kRouteRuntime = -1;
+
+struct AttnBwdParams {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const uint16_t* dout;
+    const float* lse;    // [B, Hq, S] natural log (softmax modes)
+    const float* delta;  // [B, Hq, S] rowsum(dO * O) (softmax modes)
+    uint16_t* dq;
+    uint16_t* dk;
+    uint16_t* dv;
+    AttnStrides qs, ks, vs, dos, dqs, dks, dvs;
+    int64_t hq, hkv, seq;
+    float scale, cap, sig_bias;
+    int route;  // routed exp2: a key takes the polynomial when key % route < 4
+    int causal;
+};
+
+template <int MODE>
+constexpr int exp2_kind() {
+    return MODE == kAttnSoftmaxExp2D2 ? kExp2D2 : MODE == kAttnSoftmaxExp2D3 ? kExp2D3 : kExp2Pwl2;
+}
+
+// Probability and gradient w.r.t. the raw dot product (q.k) of two scores.
+// a: raw dot products; dp: dO.v; lse2: log-sum-exp in log2 units; dl: D;
+// poly: the key takes the exp2 polynomial (routed modes).
+template <int MODE, int GRAD, int ROUTE>
+__device__ __forceinline__ void score_grad2(const AttnBwdParams& p, float inv_cap, float a0, float a1,
+                                            float dp0, float dp1, float lse0, float lse1, float dl0,
+                                            float dl1, bool poly0, bool poly1, float& p0, float& p1,
+                                            float& ds0, float& ds1) {
+    auto ex2 = [&](float x, bool poly) {
+        if constexpr (attn_has_exp2_program(MODE) && ROUTE == 4) {
+            return exp2_lane<exp2_kind<MODE>()>(x);
+        } else if constexpr (attn_has_exp2_program(MODE) && ROUTE == kRouteRuntime) {
+            return poly ? exp2_lane<exp2_kind<MODE>()>(x) : __builtin_amdgcn_exp2f(x);
+        } else {
+            return __builtin_amdgcn_exp2f(x);
+        }
+    };
+    if constexpr (attn_is_plain_softmax(MODE)) {
+        const float sl = p.scale * kLog2e;
+        p0 = ex2(__builtin_fmaf(a0, sl, -lse0), poly0);
+        p1 = ex2(__builtin_fmaf(a1, sl, -lse1), poly1);
+        ds0 = p0 * (dp0 - dl0) * p.scale;
+        ds1 = p1 * (dp1 - dl1) * p.scale;
+    } else if constexpr (MODE == kAttnSoftcapNative) {
+        const float t0 = native_lane<kTanh, kFwd>(a0 * p.scale * inv_cap);
+        const float t1 = native_lane<kTanh, kFwd>(a1 * p.scale * inv_cap);
+        p0 = __builtin_amdgcn_exp2f(p.cap * t0 * kLog2e - lse0);
+        p1 = __builtin_amdgcn_exp2f(p.cap * t1 * kLog2e - lse1);
+        ds0 = p0 * (dp0 - dl0) * (1.0f - t0 * t0) * p.scale;
+        ds1 = p1 * (dp1 - dl1) * (1.0f - t1 * t1) * p.scale;
+    } else if constexpr (MODE == kAttnSoftcapD4) {
+        const uint32_t u = pack_bf(rbf(a0 * p.scale) * inv_cap, rbf(a1 * p.scale) * inv_cap);
+        float t0, t1;
+        SoftcapConsts::T::eval2(u, t0, t1);
+        p0 = __builtin_amdgcn_exp2f(rbf(t0 * p.cap) * kLog2e - lse0);
+        p1 = __builtin_amdgcn_exp2f(rbf(t1 * p.cap) * kLog2e - lse1);
+        float g0 = 1.0f, g1 = 1.0f;
+        if constexpr (GRAD == kGradAnalytical) {
+            const uint32_t t2 = u & 0x7fff7fffu;
+            g0 = SoftcapConsts::deriv(bf_lo(t2));
+            g1 = SoftcapConsts::deriv(bf_hi(t2));
+        } else if constexpr (GRAD == kGradExact1mt2) {
+            g0 = 1.0f - t0 * t0;
+            g1 = 1.0f - t1 * t1;
+        }
+        ds0 = p0 * (dp0 - dl0) * g0 * p.scale;
+        ds1 = p1 * (dp1 - dl1) * g1 * p.scale;
+    } else {
+        const float s0 = a0 * p.scale, s1 = a1 * p.scale;
+        float g0, g1;
+        if constexpr (MODE == kAttnSigmoidB3) {
+            float d0, d1;
+            b3_lane<true>(rbf(s0), p0, d0);
+            b3_lane<true>(rbf(s1), p1, d1);
+            if constexpr (GRAD == kGradDirect) {
+                g0 = rbf(d0);
+                g1 = rbf(d1);
+            } else {
+                g0 = p0 * (1.0f - p0);
+                g1 = p1 * (1.0f - p1);
+            }
+        } else if constexpr (MODE == kAttnSigmoidB3D2) {
+            b3_d2_lane(rbf(s0), p0, g0);
+            b3_d2_lane(rbf(s1), p1, g1);
+        } else if constexpr (MODE >= kAttnSigmoidD3 && MODE <= kAttnSigmoidD6) {
+            BF16Prog<kSigmoid, kFwd, MODE - kAttnSigmoidD3 + 3>::eval2(pack_bf(s0 + p.sig_bias, s1 + p.sig_bias),
+                                                                       p0, p1);
+            g0 = p0 * (1.0f - p0);
+            g1 = p1 * (1.0f - p1);
+        } else {
+            p0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(s0 + p.sig_bias) * kLog2e));
+            p1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(s1 + p.sig_bias) * kLog2e));
+            g0 = p0 * (1.0f - p0);
+            g1 = p1 * (1.0f - p1);
+        }
+        ds0 = dp0 * g0 * p.scale;
+        ds1 = dp1 * g1 * p.scale;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// delta: D[b, h, s] = sum_d dO[b, s, h, d] * O[b, s, h, d]; 16 lanes per row
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256) attn_delta_kernel(const uint16_t* __restrict__ out,
+                                                         const uint16_t* __restrict__ dout,
+                                                         float* __restrict__ delta, AttnStrides os,
+                                                         AttnStrides dos, int64_t hq, int64_t seq,
+                                                         int64_t rows) {
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int c = threadIdx.x & 15;
+    float acc = 0.0f;
+    if (row < rows) {
+        const int64_t s = row % seq, bh = row / seq, h = bh % hq, b = bh / hq;
+        const u32x4_t o = *reinterpret_cast<const u32x4_t*>(out + b * os.b + h * os.h + s * os.s + c * 8);
+        const u32x4_t g = *reinterpret_cast<const u32x4_t*>(dout + b * dos.b + h * dos.h + s * dos.s + c * 8);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc = __builtin_fmaf(bf_lo(o[j]), bf_lo(g[j]), acc);
+            acc = __builtin_fmaf(bf_hi(o[j]), bf_hi(g[j]), acc);
+        }
+    }
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+    if (row < rows && c == 0) delta[row] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// staging of a 32-row tile: row-major copy and transposed copy.  Thread
+// (pair pr = tid / 16, chunk dc = tid % 16) holds rows 2 pr, 2 pr + 1,
+// BF16 elements 8 dc .. 8 dc + 7.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void store_rows(uint16_t* rows, int pr, int dc, const u32x4_t& a, const u32x4_t& b) {
+    *reinterpret_cast<u32x4_t*>(rows + (2 * pr) * kRowStride + dc * 8) = a;
+    *reinterpret_cast<u32x4_t*>(rows + (2 * pr + 1) * kRowStride + dc * 8) = b;
+}
+
+__device__ __forceinline__ void store_transposed(uint16_t* t, int pr, int dc, const u32x4_t& a, const u32x4_t& b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        // (row 2pr, row 2pr+1) of columns d = 8 dc + 2j and 8 dc + 2j + 1
+        *reinterpret_cast<uint32_t*>(t + (dc * 8 + 2 * j) * kTStride + 2 * pr) =
+            __builtin_amdgcn_perm(b[j], a[j], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(t + (dc * 8 + 2 * j + 1) * kTStride + 2 * pr) =
+            __builtin_amdgcn_perm(b[j], a[j], 0x07060302u);
+    }
+}
+
+// A fragment of a transposed tile: row `row`, the eight k slots of lane half
+// h in accumulator order (columns 16 cc + 4h .. +3 and 16 cc + 8 + 4h .. +3).
+__device__ __forceinline__ bf16x8_t frag_t(const uint16_t* t, int row, int cc, int h) {
+    const uint16_t* r = t + row * kTStride + 16 * cc + 4 * h;
+    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r);
+    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + 8);
+    const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
+    return __builtin_bit_cast(bf16x8_t, w);
+}
+
+__device__ __forceinline__ bf16x8_t to_frag(const float (&x)[16], int cc) {
+    bf16x8_t f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (__bf16)x[8 * cc + e];
+    return f;
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV
+// ---------------------------------------------------------------------------
+
+struct BwdQTile {
+    uint16_t q[kBwdTile * kRowStride];
+    uint16_t qt[kHeadDim * kTStride];
+    uint16_t dout[kBwdTile * kRowStride];
+    uint16_t doutt[kHeadDim * kTStride];
+    float lse2[kBwdTile];
+    float delta[kBwdTile];
+};
+
+template <int MODE, int GRAD, int ROUTE>
+__global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p) {
+    constexpr bool kSigmoid = attn_is_sigmoid(MODE);
+    __shared__ __align__(16) BwdQTile tiles[2];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, c32 = lane & 31;
+    const int pr = tid >> 4, dc = tid & 15;
+    const int64_t kvh = blockIdx.x, kb = blockIdx.y, b = blockIdx.z;
+    const int64_t group = p.hq / p.hkv;
+    const int64_t key0 = kb * 128 + wave * 32;  // first key of this wave
+    const int64_t key = key0 + c32;             // this lane's key
+    const float inv_cap = 1.0f / p.cap;
+    const bool poly_key = ROUTE == kRouteRuntime && key % p.route < 4;
+
+    bf16x8_t kf[8], vf[8];
+    {
+        const uint16_t* kr = p.k + b * p.ks.b + kvh * p.ks.h + key * p.ks.s;
+        const uint16_t* vr = p.v + b * p.vs.b + kvh * p.vs.h + key * p.vs.s;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            kf[c] = *reinterpret_cast<const bf16x8_t*>(kr + c * 16 + h * 8);
+            vf[c] = *reinterpret_cast<const bf16x8_t*>(vr + c * 16 + h * 8);
+        }
+    }
+    f32x16_t dkacc[4], dvacc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) dkacc[dt] = dvacc[dt] = (f32x16_t){};
+
+    // query tiles: every head of the group, from the block's first key on
+    // under the causal mask
+    const int64_t qt0 = p.causal ? kb * (128 / kBwdTile) : 0;
+    const int64_t nqt = p.seq / kBwdTile - qt0;
+    const int64_t nit = group * nqt;
+
+    u32x4_t qa, qb, da, db;
+    float lse_r = 0.0f, del_r = 0.0f;
+    auto load = [&](int64_t it) {
+        const int64_t head = kvh * group + it / nqt;
+        const int64_t q0 = (qt0 + it % nqt) * kBwdTile;
+        const uint16_t* qr = p.q + b * p.qs.b + head * p.qs.h + (q0 + 2 * pr) * p.qs.s + dc * 8;
+        const uint16_t* dr = p.dout + b * p.dos.b + head * p.dos.h + (q0 + 2 * pr) * p.dos.s + dc * 8;
+        qa = *reinterpret_cast<const u32x4_t*>(qr);
+        qb = *reinterpret_cast<const u32x4_t*>(qr + p.qs.s);
+        da = *reinterpret_cast<const u32x4_t*>(dr);
+        db = *reinterpret_cast<const u32x4_t*>(dr + p.dos.s);
+        if constexpr (!kSigmoid) {
+            if (tid < kBwdTile) {
+                const int64_t i = (b * p.hq + head) * p.seq + q0 + tid;
+                lse_r = p.lse[i] * kLog2e;
+                del_r = p.delta[i];
+            }
+        }
+    };
+    auto store = [&](int buf) {
+        BwdQTile& t = tiles[buf];
+        store_rows(t.q, pr, dc, qa, qb);
+        store_transposed(t.qt, pr, dc, qa, qb);
+        store_rows(t.dout, pr, dc, da, db);
+        store_transposed(t.doutt, pr, dc, da, db);
+        if constexpr (!kSigmoid) {
+            if (tid < kBwdTile) {
+                t.lse2[tid] = lse_r;
+                t.delta[tid] = del_r;
+            }
+        }
+    };
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int64_t it = 0; it < nit; ++it) {
+        const int buf = (int)(it & 1);
+        const bool more = it + 1 < nit;
+        if (more) load(it + 1);
+        const int64_t q0 = (qt0 + it % nqt) * kBwdTile;
+        if (!p.causal || q0 + kBwdTile - 1 >= key0) {  // some query of the tile sees a key of the wave
+            const BwdQTile& t = tiles[buf];
+            f32x16_t sacc = {}, pacc = {};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const bf16x8_t aq = *reinterpret_cast<const bf16x8_t*>(t.q + c32 * kRowStride + 16 * c + 8 * h);
+                sacc = mfma32(aq, kf[c], sacc);
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const bf16x8_t ad = *reinterpret_cast<const bf16x8_t*>(t.dout + c32 * kRowStride + 16 * c + 8 * h);
+                pacc = mfma32(ad, vf[c], pacc);
+            }
+            // register r: query q0 + 8 (r/4) + 4h + r%4 of this lane's key
+            float lse[16], del[16];
+            if constexpr (!kSigmoid) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(t.lse2 + 8 * j + 4 * h);
+                    const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(t.delta + 8 * j + 4 * h);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        lse[4 * j + i] = l4[i];
+                        del[4 * j + i] = d4[i];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) lse[r] = del[r] = 0.0f;
+            }
+            const bool need_mask = p.causal && q0 < key0 + 31;
+            const int diag = (int)(key - q0) - 4 * h;  // masked when diag > 8 (r/4) + r%4
+            float pr_[16], ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[r], sacc[r + 1], pacc[r], pacc[r + 1], lse[r],
+                                               lse[r + 1], del[r], del[r + 1], poly_key, poly_key, pr_[r],
+                                               pr_[r + 1], ds[r], ds[r + 1]);
+            }
+            if (need_mask) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (diag > 8 * (r >> 2) + (r & 3)) pr_[r] = ds[r] = 0.0f;
+            }
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const bf16x8_t pf = to_frag(pr_, cc), sf = to_frag(ds, cc);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    dvacc[dt] = mfma32(frag_t(t.doutt, dt * 32 + c32, cc, h), pf, dvacc[dt]);
+                    dkacc[dt] = mfma32(frag_t(t.qt, dt * 32 + c32, cc, h), sf, dkacc[dt]);
+                }
+            }
+        }
+        if (more) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    // dK^T / dV^T: register r of dt holds d = 32 dt + 8 (r/4) + 4h + r%4 of key c32
+    uint16_t* dkr = p.dk + b * p.dks.b + kvh * p.dks.h + key * p.dks.s;
+    uint16_t* dvr = p.dv + b * p.dvs.b + kvh * p.dvs.h + key * p.dvs.s;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = dt * 32 + 8 * g + 4 * h;
+            const u32x2_t wk = {pack_bf(dkacc[dt][4 * g], dkacc[dt][4 * g + 1]),
+                                pack_bf(dkacc[dt][4 * g + 2], dkacc[dt][4 * g + 3])};
+            const u32x2_t wv = {pack_bf(dvacc[dt][4 * g], dvacc[dt][4 * g + 1]),
+                                pack_bf(dvacc[dt][4 * g + 2], dvacc[dt][4 * g + 3])};
+            *reinterpret_cast<u32x2_t*>(dkr + d) = wk;
+            *reinterpret_cast<u32x2_t*>(dvr + d) = wv;
+        }
+}
+
+// ---------------------------------------------------------------------------
+// dQ
+// ---------------------------------------------------------------------------
+
+struct BwdKTile {
+    uint16_t k[kBwdTile * kRowStride];
+    uint16_t kt[kHeadDim * kTStride];
+    uint16_t v[kBwdTile * kRowStride];
+};
+
+template <int MODE, int GRAD, int ROUTE>
+__global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
+    constexpr bool kSigmoid = attn_is_sigmoid(MODE);
+    __shared__ __align__(16) BwdKTile tiles[2];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, c32 = lane & 31;
+    const int pr = tid >> 4, dc = tid & 15;
+    const int64_t nqb = p.seq / kAttnBlockQ;
+    const int64_t head = blockIdx.x, b = blockIdx.z;
+    const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
+    const int64_t kvh = head / (p.hq / p.hkv);
+    const int64_t q0 = qb * kAttnBlockQ + wave * 32;
+    const int64_t qrow = q0 + c32;
+    const float inv_cap = 1.0f / p.cap;
+
+    bf16x8_t qf[8], df[8];
+    {
+        const uint16_t* qr = p.q + b * p.qs.b + head * p.qs.h + qrow * p.qs.s;
+        const uint16_t* dr = p.dout + b * p.dos.b + head * p.dos.h + qrow * p.dos.s;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            qf[c] = *reinterpret_cast<const bf16x8_t*>(qr + c * 16 + h * 8);
+            df[c] = *reinterpret_cast<const bf16x8_t*>(dr + c * 16 + h * 8);
+        }
+    }
+    float lse2 = 0.0f, dl = 0.0f;
+    if constexpr (!kSigmoid) {
+        const int64_t i = (b * p.hq + head) * p.seq + qrow;
+        lse2 = p.lse[i] * kLog2e;
+        dl = p.delta[i];
+    }
+    f32x16_t dqacc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) dqacc[dt] = (f32x16_t){};
+
+    const uint16_t* kp = p.k + b * p.ks.b + kvh * p.ks.h;
+    const uint16_t* vp = p.v + b * p.vs.b + kvh * p.vs.h;
+    u32x4_t ka, kb2, va, vb;
+    auto load = [&](int64_t k0) {
+        const uint16_t* kr = kp + (k0 + 2 * pr) * p.ks.s + dc * 8;
+        const uint16_t* vr = vp + (k0 + 2 * pr) * p.vs.s + dc * 8;
+        ka = *reinterpret_cast<const u32x4_t*>(kr);
+        kb2 = *reinterpret_cast<const u32x4_t*>(kr + p.ks.s);
+        va = *reinterpret_cast<const u32x4_t*>(vr);
+        vb = *reinterpret_cast<const u32x4_t*>(vr + p.vs.s);
+    };
+    auto store = [&](int buf) {
+        BwdKTile& t = tiles[buf];
+        store_rows(t.k, pr, dc, ka, kb2);
+        store_transposed(t.kt, pr, dc, ka, kb2);
+        store_rows(t.v, pr, dc, va, vb);
+    };
+
+    const int64_t nkt = p.causal ? (qb + 1) * (kAttnBlockQ / kBwdTile) : p.seq / kBwdTile;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int64_t kt = 0; kt < nkt; ++kt) {
+        const int buf = (int)(kt & 1);
+        const int64_t k0 = kt * kBwdTile;
+        const bool more = kt + 1 < nkt;
+        if (more) load(k0 + kBwdTile);
+        if (!p.causal || k0 <= q0 + 31) {
+            const BwdKTile& t = tiles[buf];
+            f32x16_t sacc = {}, pacc = {};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const bf16x8_t ak = *reinterpret_cast<const bf16x8_t*>(t.k + c32 * kRowStride + 16 * c + 8 * h);
+                sacc = mfma32(ak, qf[c], sacc);
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(t.v + c32 * kRowStride + 16 * c + 8 * h);
+                pacc = mfma32(av, df[c], pacc);
+            }
+            // register r: key k0 + 8 (r/4) + 4h + r%4 of this lane's query
+            const bool need_mask = p.causal && k0 + 31 > q0;
+            const int diag = (int)(k0 - qrow) + 4 * h;  // masked when diag + 8 (r/4) + r%4 > 0
+            float pr_[16], ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                bool poly0 = false, poly1 = false;
+                if constexpr (ROUTE == kRouteRuntime) {
+                    const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    poly0 = key % p.route < 4;
+                    poly1 = (key + 1) % p.route < 4;
+                }
+                score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[r], sacc[r + 1], pacc[r], pacc[r + 1], lse2,
+                                               lse2, dl, dl, poly0, poly1, pr_[r], pr_[r + 1], ds[r],
+                                               ds[r + 1]);
+            }
+            if (need_mask) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (diag + 8 * (r >> 2) + (r & 3) > 0) ds[r] = 0.0f;
+            }
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const bf16x8_t sf = to_frag(ds, cc);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) dqacc[dt] = mfma32(frag_t(t.kt, dt * 32 + c32, cc, h), sf, dqacc[dt]);
+            }
+        }
+        if (more) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    uint16_t* dqr = p.dq + b * p.dqs.b + head * p.dqs.h + qrow * p.dqs.s;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = dt * 32 + 8 * g + 4 * h;
+            const u32x2_t w = {pack_bf(dqacc[dt][4 * g], dqacc[dt][4 * g + 1]),
+                               pack_bf(dqacc[dt][4 * g + 2], dqacc[dt][4 * g + 3])};
+            *reinterpret_cast<u32x2_t*>(dqr + d) = w;
+        }
+}
+
+}  // namespace pt
+
+using namespace pt;
+
+namespace {
+
+template <int MODE, int GRAD, int ROUTE>
+void launch_bwd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
+    const dim3 gkv((unsigned)prm.hkv, (unsigned)(prm.seq / 128), (unsigned)batch);
+    const dim3 gq((unsigned)prm.hq, (unsigned)(prm.seq / kAttnBlockQ), (unsigned)batch);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE>), gkv, dim3(256), 0, st, prm);
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE>), gq, dim3(256), 0, st, prm);
+}
+
+template <int MODE>
+void launch_bwd_routed(const AttnBwdParams& prm, int64_t batch, hipStream_t st, int route) {
+    if (route == 0) launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, st);
+    else if (route == 4) launch_bwd<MODE, kGradNatural, 4>(prm, batch, st);
+    else launch_bwd<MODE, kGradNatural, kRouteRuntime>(prm, batch, st);
+}
+
+bool bwd_stride_ok(const AttnStrides& t) {
+    return t.b >= 0 && t.h >= 0 && t.s >= 0 && t.s % 8 == 0 && t.h % 8 == 0 && t.b % 8 == 0;
+}
+
+}  // namespace
+
+extern "C" int launch_flash_attention_bwd_strided_bf16(
+    void* dq, void* dk, void* dv, float* delta, const void* q, const void* k, const void* v,
+    const void* out, const void* dout, const float* lse, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t seq, int64_t head_dim, const int64_t* strides, int mode, int grad,
+    int exp2_route, int causal, float scale, float cap, float sigmoid_bias, void* stream) {
+    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || head_dim != kHeadDim || !strides)
+        return hipErrorInvalidValue;
+    if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
+        return hipErrorInvalidValue;
+    if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f)) return hipErrorInvalidValue;
+    if ((mode == kAttnSigmoidB3 || mode == kAttnSigmoidB3D2) && seq != 4096) return hipErrorInvalidValue;
+    // derivative programs: softcap D4 takes analytical / ste / 1 - T^2, B3
+    // algebraic / direct, every other mode its natural one
+    const bool grad_ok = mode == kAttnSoftcapD4 ? (grad >= kGradAnalytical && grad <= kGradExact1mt2)
+                         : mode == kAttnSigmoidB3 ? (grad == kGradAlgebraic || grad == kGradDirect)
+                                                  : grad == kGradNatural;
+    if (!grad_ok) return hipErrorInvalidValue;
+    if (attn_has_exp2_program(mode) && !(exp2_route == 0 || exp2_route == 4 || exp2_route == 6 ||
+                                         exp2_route == 8 || exp2_route == 10 || exp2_route == 12 ||
+                                         exp2_route == 16 || exp2_route == 20 || exp2_route == 24 ||
+                                         exp2_route == 32))
+        return hipErrorInvalidValue;
+    AttnStrides st[8];
+    for (int i = 0; i < 8; ++i) {
+        st[i] = {strides[3 * i], strides[3 * i + 1], strides[3 * i + 2]};
+        if (!bwd_stride_ok(st[i])) return hipErrorInvalidValue;
+    }
+    if (batch == 0 || seq == 0) return hipSuccess;
+    for (const void* ptr : {(const void*)dq, (const void*)dk, (const void*)dv, q, k, v, dout})
+        if (!ptr || !aligned16(ptr)) return hipErrorInvalidValue;
+    const bool sig = attn_is_sigmoid(mode);
+    if (!sig && (!out || !aligned16(out) || !lse || !delta || (reinterpret_cast<uintptr_t>(lse) & 3) ||
+                 (reinterpret_cast<uintptr_t>(delta) & 3)))
+        return hipErrorInvalidValue;
+    if (batch > 65535 || seq / 128 > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
+    hipStream_t hst = hs(stream);
+    if (!sig) {
+        const int64_t rows = batch * q_heads * seq;
+        hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, hst,
+                           (const uint16_t*)out, (const uint16_t*)dout, delta, st[3], st[4], q_heads,
+                           seq, rows);
+    }
+    AttnBwdParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
+                      sig ? nullptr : lse, sig ? nullptr : delta, (uint16_t*)dq, (uint16_t*)dk,
+                      (uint16_t*)dv, st[0], st[1], st[2], st[4], st[5], st[6], st[7], q_heads, kv_heads,
+                      seq, scale, cap > 0.0f ? cap : 1.0f, sigmoid_bias, exp2_route > 0 ? exp2_route : 4,
+                      causal != 0};
+    switch (mode) {
+        case kAttnSoftmaxNative: launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSoftmaxExp2D2: launch_bwd_routed<kAttnSoftmaxExp2D2>(prm, batch, hst, exp2_route); break;
+        case kAttnSoftmaxExp2D3: launch_bwd_routed<kAttnSoftmaxExp2D3>(prm, batch, hst, exp2_route); break;
+        case kAttnSoftmaxExp2Pwl2: launch_bwd_routed<kAttnSoftmaxExp2Pwl2>(prm, batch, hst, exp2_route); break;
+        case kAttnSoftcapNative: launch_bwd<kAttnSoftcapNative, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSoftcapD4:
+            if (grad == kGradAnalytical) launch_bwd<kAttnSoftcapD4, kGradAnalytical, 0>(prm, batch, hst);
+            else if (grad == kGradSte) launch_bwd<kAttnSoftcapD4, kGradSte, 0>(prm, batch, hst);
+            else launch_bwd<kAttnSoftcapD4, kGradExact1mt2, 0>(prm, batch, hst);
+            break;
+        case kAttnSigmoidNative: launch_bwd<kAttnSigmoidNative, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSigmoidB3:
+            if (grad == kGradDirect) launch_bwd<kAttnSigmoidB3, kGradDirect, 0>(prm, batch, hst);
+            else launch_bwd<kAttnSigmoidB3, kGradAlgebraic, 0>(prm, batch, hst);
+            break;
+        case kAttnSigmoidB3D2: launch_bwd<kAttnSigmoidB3D2, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSigmoidD3: launch_bwd<kAttnSigmoidD3, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSigmoidD3 + 1: launch_bwd<kAttnSigmoidD3 + 1, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSigmoidD3 + 2: launch_bwd<kAttnSigmoidD3 + 2, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSigmoidD6: launch_bwd<kAttnSigmoidD6, kGradNatural, 0>(prm, batch, hst); break;
+    }
+    return hipGetLastError();
+}

@@ -96,6 +96,14 @@ struct SoftcapConsts {
     static constexpr float d2 = bf16_value(3.0f * bf16_value(T::P.c[3]));
     static constexpr float d3 = bf16_value(4.0f * bf16_value(T::P.c[4]));
     static constexpr float t_sat = 2.609375f;
+
+    // D(t) at t = |u| (a BF16 magnitude); NaN magnitudes fail t < t_sat.
+    __device__ __forceinline__ static float deriv(float t) {
+        float r = bfma(t, d3, d2);
+        r = bfma(t, r, d1);
+        r = bfma(t, r, d0);
+        return t < t_sat ? r : 0.0f;
+    }
 };
 
 // ---------------------------------------------------------------------------
@@ -104,11 +112,14 @@ struct SoftcapConsts {
 // p = polynomial 2^f on [0, 1); result bits = (n << 23) + bits(p).
 // D2 "safe" fraction p = 1 + a f + (1 - a) f^2, a = 0.6602339719
 // (extras/paper/manuscript/appendix_exp2.tex:29-32; sampled-minimax fit),
-// keeps p(0) = 1 and p(1) = 2.  D3 is FA4's e2e_asm2 fraction.
+// keeps p(0) = 1 and p(1) = 2.  D3 is FA4's e2e_asm2 fraction.  PWL2 is
+// the continuous two-piece FP32 fraction of the full-range benchmark
+// (autonumerics_zero/cuda_benchmarks/benchmark_exp2_pwl2.cu:126-170):
+// p = 0.98946118 + 0.82085252 f + 0.34246066 max(f - 0.5, 0).
 // Defined for x < 128 (softmax exponents are <= 0); -inf and NaN give +0.
 // ---------------------------------------------------------------------------
 
-enum Exp2Kind : int { kExp2D2 = 0, kExp2D3 = 1, kExp2Native = 2 };
+enum Exp2Kind : int { kExp2D2 = 0, kExp2D3 = 1, kExp2Native = 2, kExp2Pwl2 = 3 };
 
 template <int KIND>
 __device__ __forceinline__ float exp2_lane(float x) {
@@ -122,6 +133,9 @@ __device__ __forceinline__ float exp2_lane(float x) {
         if constexpr (KIND == kExp2D2) {
             p = __builtin_fmaf(f, 0.33976602809999057f, 0.6602339719000094f);
             p = __builtin_fmaf(p, f, 1.0f);
+        } else if constexpr (KIND == kExp2Pwl2) {
+            p = __builtin_fmaf(f, 0.820852518081665f, 0.9894611835479736f);
+            p = __builtin_fmaf(__builtin_fmaxf(f - 0.5f, 0.0f), 0.34246066212654114f, p);
         } else {
             p = __builtin_fmaf(f, 0.077119089663028717041015625f, 0.227564394474029541015625f);
             p = __builtin_fmaf(p, f, 0.695146143436431884765625f);

@@ -443,6 +443,48 @@ int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k, con
                                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
                                     int64_t head_dim, int mode, int causal, float scale, float cap,
                                     void* stream);
+/* General form, the runtime behind the FA4 interface (the flash_attn_fwd that
+ * src/sfu_repro/fa4.py:356-428 calls).  strides: 12 element strides, (batch,
+ * head, sequence) of q, k, v and out in that order, each a multiple of 8; the
+ * head dimension (128) is contiguous, so [B, S, H, 128] (FA4's layout) and
+ * [B, H, S, 128] both work.  lse: null, or float [B, Hq, S] receiving
+ * ln sum_k exp(s'_k) (s' the scaled, capped score) for the softmax modes;
+ * sigmoid modes leave it untouched.  Extra modes:
+ *   7 sigmoid attention with the B3-D2 exp2 program (fitted for S = 4096)
+ *   8..11 sigmoid attention with the BF16 sigmoid D3..D6 program on
+ *     bf16(s + sigmoid_bias)          12 softmax, PWL2 hinge exp2.
+ * sigmoid_bias: the bias of the hardware and D3..D6 sigmoid modes.
+ * exp2_route (modes 1, 2, 12): of every exp2_route exponents of a query row,
+ * four take the polynomial and the rest v_exp_f32; one of 4 (all), 6, 8, 10,
+ * 12, 16, 20, 24, 32 (FA4's exp2_emu_freq, src/sfu_repro/fa4.py:223-231). */
+int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q, const void* k,
+                                            const void* v, int64_t batch, int64_t q_heads,
+                                            int64_t kv_heads, int64_t seq, int64_t head_dim,
+                                            const int64_t* strides, int mode, int exp2_route,
+                                            int causal, float scale, float cap, float sigmoid_bias,
+                                            void* stream);
+/* Backward of the same attention (the runtime behind FA4's flash_attn_bwd,
+ * src/sfu_repro/fa4.py:430-461): dq [B, S, Hq, 128], dk and dv [B, S, Hkv, 128]
+ * BF16 from q, k, v, out, dout (BF16) and the forward's lse (softmax modes).
+ * strides: 24 element strides, (batch, head, sequence) of q, k, v, out, dout,
+ * dq, dk, dv.  delta: caller-provided float [B, Hq, S] workspace receiving
+ * rowsum(dout * out) (softmax modes; unused for sigmoid modes, where out, lse
+ * and delta may be null).  grad, the derivative of the score program:
+ *   0 the mode's own (softmax, softcap 1 - tanh^2, sigmoid p (1 - p))
+ *   1 / 2 / 3  mode 4 only: the D4 derivative polynomial (FA4 "analytical") /
+ *              straight-through (ste) / 1 - T(u)^2 (exact_1mt2)
+ *   4 / 5      mode 6 only: y (1 - y) (algebraic) / the B3 factored D4
+ *              derivative (direct).
+ * exp2_route (modes 1, 2, 12): 0 hardware exp2, 4 the polynomial everywhere,
+ * 6..32 the polynomial for keys with key % exp2_route < 4 (FA4's
+ * exp2_emu_freq_bwd). */
+int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float* delta,
+                                            const void* q, const void* k, const void* v,
+                                            const void* out, const void* dout, const float* lse,
+                                            int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                            int64_t seq, int64_t head_dim, const int64_t* strides,
+                                            int mode, int grad, int exp2_route, int causal,
+                                            float scale, float cap, float sigmoid_bias, void* stream);
 
 /* ---- device/launch introspection --------------------------------------- */
 /* Number of compute units of the current device and the grid the

@@ -725,6 +725,9 @@ static float exp2_prog(int kind, float x) {
     if (kind == 0) { /* D2 safe: appendix_exp2.tex:29-32 */
         p = fmaf(fr, 0.33976602809999057f, 0.6602339719000094f);
         p = fmaf(p, fr, 1.0f);
+    } else if (kind == 2) { /* two-piece hinge, benchmark_exp2_pwl2.cu:126-170 */
+        p = fmaf(fr, 0.820852518081665f, 0.9894611835479736f);           /* 0x3F522364, 0x3F7D4D54 */
+        p = fmaf(fmaxf(fr - 0.5f, 0.0f), 0.34246066212654114f, p);       /* 0x3EAF5701 */
     } else {         /* FA4 D3 */
         p = fmaf(fr, 0.077119089663028717041015625f, 0.227564394474029541015625f);
         p = fmaf(p, fr, 0.695146143436431884765625f);
@@ -738,10 +741,10 @@ static float exp2_prog(int kind, float x) {
     return r;
 }
 
-/* kind: 0 = D2 safe, 1 = FA4 D3.  out_bf16: BF16 bits into y16, else FP32
- * into y32. */
+/* kind: 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge.  out_bf16: BF16 bits into
+ * y16, else FP32 into y32. */
 int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n) {
-    if (n < 0 || (kind != 0 && kind != 1)) return -1;
+    if (n < 0 || kind < 0 || kind > 2) return -1;
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
         float r = exp2_prog(kind, x[i]);

@@ -89,7 +89,7 @@ int orc_b3_exp2_d2_bf16(const uint16_t* x, uint16_t* y, uint16_t* dy, int64_t n,
 int orc_softcap_fwd_bf16(const uint16_t* s, uint16_t* y, int64_t n, float cap);
 int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int64_t n, float cap);
 
-/* ---- B5 exp2: kind 0 = D2 safe, 1 = FA4 D3 -------------------------------- */
+/* ---- B5 exp2: kind 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge ----------------- */
 int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n);
 
 /* ---- paired sin/cos: prog 0 BF16 D3/D4, 1 BF16 D5/D6, 2 FP16 D3/D4,

@@ -1,0 +1,290 @@
+"""GPU parity of the fused attention in FA4's layout ([B, S, H, 128]): the
+strided forward with its log-sum-exp output, and the backward (dQ, dK, dV)
+of every score mode and derivative program, through the C ABI.
+
+The backward is checked in isolation: it receives the forward's out and lse
+and is compared with a float32 CPU evaluation of the same formulas
+(P from the saved lse through the same exp2 program, the oracle's softcap /
+B3 / sigmoid programs, dS = P (dP - D) g or dP g, dq.k = dS * scale).  An
+end-to-end test compares the hardware-softmax forward + backward with torch
+autograd of exact attention in float64.  Tolerances cover the BF16 rounding
+of P and dS before the MFMA products and of the outputs."""
+
+import ctypes
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+M = {"softmax_native": 0, "softmax_d2": 1, "softmax_d3": 2, "softcap_native": 3, "softcap_d4": 4,
+     "sigmoid_native": 5, "sigmoid_b3": 6, "sigmoid_b3_d2": 7, "sigmoid_d3": 8, "sigmoid_d4": 9,
+     "sigmoid_d5": 10, "sigmoid_d6": 11, "softmax_pwl2": 12}
+EXP2_KIND = {"softmax_d2": 0, "softmax_d3": 1, "softmax_pwl2": 2}
+LOG2E = 1.4426950408889634
+
+
+def _inputs(b, hq, hkv, s, seed, qmul=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(b, s, hq, 128, generator=g) * qmul).bfloat16()
+    k = torch.randn(b, s, hkv, 128, generator=g).bfloat16()
+    v = torch.randn(b, s, hkv, 128, generator=g).bfloat16()
+    do = torch.randn(b, s, hq, 128, generator=g).bfloat16()
+    return q, k, v, do
+
+
+def _strides(*ts):
+    vals = []
+    for t in ts:
+        vals += [t.stride(0), t.stride(2), t.stride(1)]
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
+def _bias(mode, s):
+    return -math.log(s) if mode in ("sigmoid_native",) or mode.startswith("sigmoid_d") else 0.0
+
+
+def fwd(capi, cuda, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=None):
+    b, s, hq, _ = q.shape
+    hkv = k.shape[2]
+    qd, kd, vd = q.to(cuda), k.to(cuda), v.to(cuda)
+    out = torch.empty(b, s, hq, 128, dtype=torch.bfloat16, device=cuda)
+    lse = torch.zeros(b, hq, s, dtype=torch.float32, device=cuda)
+    bias = _bias(mode, s) if bias is None else bias
+    rc = capi.launch_flash_attention_fwd_strided_bf16(
+        capi.ptr(out), capi.ptr(lse), capi.ptr(qd), capi.ptr(kd), capi.ptr(vd), ctypes.c_int64(b),
+        ctypes.c_int64(hq), ctypes.c_int64(hkv), ctypes.c_int64(s), ctypes.c_int64(128),
+        _strides(qd, kd, vd, out), ctypes.c_int(M[mode]), ctypes.c_int(route), ctypes.c_int(int(causal)),
+        ctypes.c_float(scale), ctypes.c_float(cap), ctypes.c_float(bias), capi.stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def bwd(capi, cuda, q, k, v, out, do, lse, mode, grad, causal, scale, cap=30.0, route=0, bias=None):
+    b, s, hq, _ = q.shape
+    hkv = k.shape[2]
+    qd, kd, vd, dod = q.to(cuda), k.to(cuda), v.to(cuda), do.to(cuda)
+    dq = torch.empty_like(qd)
+    dk = torch.empty_like(kd)
+    dv = torch.empty_like(vd)
+    delta = torch.empty(b, hq, s, dtype=torch.float32, device=cuda)
+    bias = _bias(mode, s) if bias is None else bias
+    rc = capi.launch_flash_attention_bwd_strided_bf16(
+        capi.ptr(dq), capi.ptr(dk), capi.ptr(dv), capi.ptr(delta), capi.ptr(qd), capi.ptr(kd),
+        capi.ptr(vd), capi.ptr(out), capi.ptr(dod), capi.ptr(lse), ctypes.c_int64(b), ctypes.c_int64(hq),
+        ctypes.c_int64(hkv), ctypes.c_int64(s), ctypes.c_int64(128),
+        _strides(qd, kd, vd, out, dod, dq, dk, dv), ctypes.c_int(M[mode]), ctypes.c_int(grad),
+        ctypes.c_int(route), ctypes.c_int(int(causal)), ctypes.c_float(scale), ctypes.c_float(cap),
+        ctypes.c_float(bias), capi.stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    return dq.cpu().float(), dk.cpu().float(), dv.cpu().float(), delta.cpu()
+
+
+def _bf(oracle, x):
+    return torch.from_numpy(oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(x.numpy().reshape(-1)))).reshape(x.shape)
+
+
+def _b3_d2_coeffs():
+    with open(os.path.join(os.path.dirname(__file__), "golden", "b3_d2_coefficients.json")) as f:
+        return json.load(f)["coefficients_float32"]
+
+
+def probs_and_grad(oracle, a, mode, grad, scale, cap, bias, lse2, route):
+    """P and the derivative factor g of raw dot products a [B, H, Sq, Sk]
+    (float32), as the kernel evaluates them."""
+    shape = a.shape
+    if mode in ("softmax_native", "softmax_d2", "softmax_d3", "softmax_pwl2"):
+        x = a * np.float32(scale * LOG2E) - lse2[..., None]
+        p = torch.exp2(x.double()).float()
+        if mode in EXP2_KIND and route:
+            pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], x.numpy().reshape(-1), out_bf16=False)).reshape(shape)
+            keys = torch.arange(shape[-1])
+            sel = (keys % route) < 4
+            p = torch.where(sel, pp, p)
+        return p, torch.ones_like(p)
+    if mode == "softcap_native":
+        th = torch.tanh((a * np.float32(scale / cap)).double())
+        p = torch.exp2((cap * th * LOG2E).float() - lse2[..., None])
+        return p, (1 - th * th).float()
+    if mode == "softcap_d4":
+        sb = oracle.f32_to_bf16_bits((a * np.float32(scale)).numpy().reshape(-1))
+        y = torch.from_numpy(oracle.bf16_bits_to_f32(oracle.softcap_fwd_bf16(sb, cap)).reshape(shape))
+        p = torch.exp2(y * np.float32(LOG2E) - lse2[..., None])
+        if grad == 1:
+            one = np.full(sb.shape, 0x3F80, dtype=np.uint16)
+            g = torch.from_numpy(oracle.bf16_bits_to_f32(oracle.softcap_bwd_bf16(one, sb, cap)).reshape(shape))
+        elif grad == 2:
+            g = torch.ones_like(p)
+        else:
+            # 1 - T^2 with T the program's BF16 output before the cap product
+            tb = oracle.f32_to_bf16_bits((a * np.float32(scale)).numpy().reshape(-1))
+            u = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(oracle.bf16_bits_to_f32(tb) * np.float32(1.0 / cap)))
+            tt = oracle.bf16_bits_to_f32(oracle.activation("tanh", 0, 4, "bf16", oracle.f32_to_bf16_bits(u)))
+            g = torch.from_numpy(1 - tt * tt).reshape(shape)
+        return p, g
+    s = (a * np.float32(scale)).numpy().reshape(-1)
+    if mode == "sigmoid_native":
+        p = torch.sigmoid(torch.from_numpy(s).double() + bias).float().reshape(shape)
+        return p, p * (1 - p)
+    if mode == "sigmoid_b3":
+        y, dy = oracle.b3_direct_f32(s)
+        p = torch.from_numpy(oracle.bf16_bits_to_f32(y)).reshape(shape)
+        if grad == 5:
+            return p, torch.from_numpy(oracle.bf16_bits_to_f32(dy)).reshape(shape)
+        return p, p * (1 - p)
+    if mode == "sigmoid_b3_d2":
+        y, dy = oracle.b3_exp2_d2_bf16(oracle.f32_to_bf16_bits(s), _b3_d2_coeffs())
+        return (torch.from_numpy(oracle.bf16_bits_to_f32(y)).reshape(shape),
+                torch.from_numpy(oracle.bf16_bits_to_f32(dy)).reshape(shape))
+    deg = int(mode[-1])
+    u = oracle.f32_to_bf16_bits((s + np.float32(bias)).astype(np.float32))
+    p = torch.from_numpy(oracle.bf16_bits_to_f32(oracle.activation("sigmoid", 0, deg, "bf16", u))).reshape(shape)
+    return p, p * (1 - p)
+
+
+def reference_bwd(oracle, q, k, v, out, do, lse, mode, grad, causal, scale, cap, route, bias):
+    """float32 CPU gradients [B, S, H, 128] given the forward's out and lse."""
+    hq, hkv = q.shape[2], k.shape[2]
+    rep = hq // hkv
+    qf = q.float().transpose(1, 2)
+    kf = k.float().transpose(1, 2).repeat_interleave(rep, dim=1)
+    vf = v.float().transpose(1, 2).repeat_interleave(rep, dim=1)
+    dof = do.float().transpose(1, 2)
+    of = out.cpu().float().transpose(1, 2)
+    a = qf @ kf.transpose(-1, -2)
+    n = a.shape[-1]
+    lse2 = lse.cpu() * np.float32(LOG2E)
+    p, g = probs_and_grad(oracle, a, mode, grad, scale, cap, bias, lse2, route)
+    mask = torch.ones(n, n, dtype=torch.bool).triu(1) if causal else torch.zeros(n, n, dtype=torch.bool)
+    p = p.masked_fill(mask, 0.0)
+    dp = dof @ vf.transpose(-1, -2)
+    if mode.startswith("sigmoid"):
+        ds = dp * g * scale
+    else:
+        dl = (dof * of).sum(-1, keepdim=True)
+        ds = p * (dp - dl) * g * scale
+    ds = ds.masked_fill(mask, 0.0)
+    dq = ds @ kf
+    dk = (ds.transpose(-1, -2) @ qf)
+    dv = (p.transpose(-1, -2) @ dof)
+    b, _, s, d = dk.shape
+    dk = dk.reshape(b, hkv, rep, s, d).sum(2)
+    dv = dv.reshape(b, hkv, rep, s, d).sum(2)
+    return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2)
+
+
+def _close(got, ref, rel=2.5e-2):
+    err = (got - ref).abs().max().item()
+    tol = rel * ref.abs().max().item() + 1e-3
+    return err <= tol, (err, tol)
+
+
+CASES = [
+    ("softmax_native", 0, 0), ("softmax_d2", 0, 4), ("softmax_d2", 0, 32), ("softmax_d3", 0, 4),
+    ("softmax_d3", 0, 12), ("softmax_pwl2", 0, 4), ("softcap_native", 0, 0), ("softcap_d4", 1, 0),
+    ("softcap_d4", 2, 0), ("softcap_d4", 3, 0), ("sigmoid_native", 0, 0), ("sigmoid_d3", 0, 0),
+    ("sigmoid_d6", 0, 0),
+]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("mode,grad,route", CASES)
+def test_backward_matches_reference(capi, oracle, cuda, mode, grad, route, causal):
+    seed = 100 + M[mode] * 7 + grad + route
+    q, k, v, do = _inputs(1, 4, 2, 256, seed, qmul=6.0 if mode.startswith("softcap") else 1.0)
+    scale = 1 / math.sqrt(128)
+    fwd_route = route if route else 4
+    out, lse = fwd(capi, cuda, q, k, v, mode, causal, scale, route=fwd_route)
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, mode, grad, causal, scale, route=route)
+    bias = _bias(mode, 256)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, mode, grad, causal, scale, 30.0, route, bias)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert torch.isfinite(got).all(), name
+        ok, info = _close(got, ref)
+        assert ok, (mode, grad, route, causal, name, info)
+
+
+@pytest.mark.parametrize("grad", [4, 5])
+def test_backward_b3_at_its_fitted_length(capi, oracle, cuda, grad):
+    q, k, v, do = _inputs(1, 2, 1, 4096, 300 + grad)
+    scale = 1 / math.sqrt(128)
+    out, lse = fwd(capi, cuda, q, k, v, "sigmoid_b3", True, scale)
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, "sigmoid_b3", grad, True, scale)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, "sigmoid_b3", grad, True, scale, 30.0, 0, 0.0)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        ok, info = _close(got, ref)
+        assert ok, (grad, name, info)
+
+
+def test_backward_b3_d2_at_its_fitted_length(capi, oracle, cuda):
+    q, k, v, do = _inputs(1, 2, 1, 4096, 310)
+    scale = 1 / math.sqrt(128)
+    out, lse = fwd(capi, cuda, q, k, v, "sigmoid_b3_d2", True, scale)
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, "sigmoid_b3_d2", 0, True, scale)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, "sigmoid_b3_d2", 0, True, scale, 30.0, 0, 0.0)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        ok, info = _close(got, ref)
+        assert ok, (name, info)
+
+
+def test_forward_fa4_layout_and_lse(capi, oracle, cuda):
+    """[B, S, H, D] operands, lse = ln sum exp(s) per query."""
+    q, k, v, _ = _inputs(2, 4, 1, 256, 7)
+    scale = 1 / math.sqrt(128)
+    out, lse = fwd(capi, cuda, q, k, v, "softmax_native", True, scale)
+    qf = q.double().transpose(1, 2)
+    kf = k.double().transpose(1, 2).repeat_interleave(4, dim=1)
+    vf = v.double().transpose(1, 2).repeat_interleave(4, dim=1)
+    s = (qf @ kf.transpose(-1, -2)) * scale
+    s = s.masked_fill(torch.ones(256, 256, dtype=torch.bool).triu(1), -math.inf)
+    ref_lse = torch.logsumexp(s, -1)
+    ref = (torch.softmax(s, -1) @ vf).transpose(1, 2)
+    assert (lse.cpu().double() - ref_lse).abs().max().item() < 1e-3
+    assert (out.cpu().double() - ref).abs().max().item() < 1.5e-2 * ref.abs().max().item() + 2e-3
+
+
+def test_end_to_end_matches_exact_autograd(capi, cuda):
+    """Hardware-softmax forward + backward against exact float64 attention."""
+    q, k, v, do = _inputs(1, 4, 2, 384, 11)
+    scale = 1 / math.sqrt(128)
+    out, lse = fwd(capi, cuda, q, k, v, "softmax_native", True, scale)
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, "softmax_native", 0, True, scale)
+    qd = q.double().requires_grad_()
+    kd = k.double().requires_grad_()
+    vd = v.double().requires_grad_()
+    o = torch.nn.functional.scaled_dot_product_attention(
+        qd.transpose(1, 2), kd.transpose(1, 2).repeat_interleave(2, dim=1),
+        vd.transpose(1, 2).repeat_interleave(2, dim=1), is_causal=True, scale=scale).transpose(1, 2)
+    o.backward(do.double())
+    for name, got, ref in (("dq", dq, qd.grad), ("dk", dk, kd.grad), ("dv", dv, vd.grad)):
+        ok, info = _close(got.double(), ref, rel=3e-2)
+        assert ok, (name, info)
+
+
+def test_rejected_backward_arguments(capi, cuda):
+    q = torch.zeros(1, 128, 2, 128, dtype=torch.bfloat16, device=cuda)
+    lse = torch.zeros(1, 2, 128, dtype=torch.float32, device=cuda)
+    delta = torch.zeros_like(lse)
+
+    def call(mode, grad, route=0, seq=128, cap=30.0):
+        return capi.launch_flash_attention_bwd_strided_bf16(
+            capi.ptr(q), capi.ptr(q), capi.ptr(q), capi.ptr(delta), capi.ptr(q), capi.ptr(q), capi.ptr(q),
+            capi.ptr(q), capi.ptr(q), capi.ptr(lse), ctypes.c_int64(1), ctypes.c_int64(2), ctypes.c_int64(2),
+            ctypes.c_int64(seq), ctypes.c_int64(128), _strides(*([q] * 8)), ctypes.c_int(mode),
+            ctypes.c_int(grad), ctypes.c_int(route), ctypes.c_int(1), ctypes.c_float(0.1),
+            ctypes.c_float(cap), ctypes.c_float(0.0), capi.stream())
+
+    assert call(4, 0) != 0          # softcap D4 needs a derivative program
+    assert call(0, 1) != 0          # analytical only for softcap D4
+    assert call(6, 4) != 0          # B3 outside its fitted length
+    assert call(1, 0, route=7) != 0  # unsupported routing
+    assert call(4, 1, cap=0.0) != 0
+    assert call(13, 0) != 0
+    assert call(0, 0) == 0
+    torch.cuda.synchronize()

@@ -175,6 +175,35 @@ def test_exp2_d2_invariants_and_fit(oracle):
     assert oracle.exp2(0, np.array([-np.inf, -127.0, -1000.0], dtype=np.float32), False).tolist() == [0.0, 0.0, 0.0]
 
 
+def _full_f32_error_input():
+    """make_full_f32(1 << 20) of autonumerics_zero/cuda_benchmarks/
+    benchmark_exp2_pwl2.cu:335-343: pairs (-16 u, -16 v), u = (2i mod
+    1048573) / 1048573, v = (2i + 1 mod 1048573) / 1048573, FP32 arithmetic."""
+    i = np.arange(1 << 20, dtype=np.int64)
+    u = ((2 * i) % 1048573).astype(np.float32) / np.float32(1048573.0)
+    v = ((2 * i + 1) % 1048573).astype(np.float32) / np.float32(1048573.0)
+    return np.stack([np.float32(-16.0) * u, np.float32(-16.0) * v], axis=1).reshape(-1)
+
+
+@pytest.mark.parametrize("kind,golden", [
+    # evidence/report-data/exp2_pwl2_isolated_gb200.json "errors", domain full_f32
+    (1, (8.51484986e-05, 8.76867888e-05, 1.26746955e-05)),   # variant degree3
+    (2, (0.0105388165, 0.0105388165, 0.000954319254)),       # variant pwl2_hinge
+])
+def test_exp2_full_range_errors_match_published_metrics(oracle, kind, golden):
+    """max_abs, max_rel and rmse against exp2 in double over the reference
+    benchmark's input set (ErrorMetrics, benchmark_exp2_pwl2.cu:306-323),
+    reproduced to the printed precision: a dropped term, a wrong coefficient
+    or reduction would move them."""
+    x = _full_f32_error_input()
+    y = oracle.exp2(kind, x, False).astype(np.float64)
+    ref = np.exp2(x.astype(np.float64))
+    a = np.abs(y - ref)
+    got = (a.max(), (a / np.abs(ref)).max(), np.sqrt((a * a).mean()))
+    for g, want in zip(got, golden):
+        assert abs(g - want) <= 2e-8 * max(1.0, want / 1e-4) + 1e-6 * want, (got, golden)
+
+
 # ---- sin/cos and RoPE -------------------------------------------------------------
 
 @pytest.mark.parametrize("prog,bound", [(0, 1.3e-2), (1, 9e-3), (2, 1e-2), (3, 1.5e-3), (4, 1.2e-3), (5, 1.2e-3)])
