@@ -79,10 +79,12 @@ __device__ __forceinline__ void softmax_exponents(const f32x16_t& acc, float sca
     }
 }
 
-// exp2 of a softmax exponent (x <= 8 under the lazy rescale).  Of every
-// ROUTE consecutive exponents of a lane, the first four take the mode's
-// polynomial and the rest v_exp_f32 (FA4's routed exp2, four lanes per group
-// of exp2_emu_freq, src/sfu_repro/fa4.py:313-353); ROUTE 4 routes all.
+// exp2 of a softmax exponent (x <= 8 under the lazy rescale).  Exponent
+// slot i (kt * 16 + r) takes the mode's polynomial when i % ROUTE < 4, the
+// rest v_exp_f32: four of every ROUTE (FA4's routed exp2, four lanes per
+// group of exp2_emu_freq, src/sfu_repro/fa4.py:313-353); ROUTE 4 routes all.
+// The slot is a function of the key index alone (16 bit5 + 4 bits3..4 +
+// bits0..1), which the backward evaluates to route the same keys.
 template <int MODE, int ROUTE>
 __device__ __forceinline__ float softmax_exp2(float x, int i) {
     if (ROUTE >= 4 && i % ROUTE < 4) {

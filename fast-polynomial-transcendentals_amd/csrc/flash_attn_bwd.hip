@@ -55,9 +55,17 @@ struct AttnBwdParams {
     AttnStrides qs, ks, vs, dos, dqs, dks, dvs;
     int64_t hq, hkv, seq;
     float scale, cap, sig_bias;
-    int route;  // routed exp2: a key takes the polynomial when key % route < 4
+    int route;  // routed exp2: a key takes the polynomial when route_slot(key) % route < 4
     int causal;
 };
+
+// Routing slot of a key: the position of its exponent among the 32 a lane
+// of the forward kernel holds per 64-key tile (kt * 16 + r).  The forward
+// routes slot % route < 4 to the polynomial; the backward uses the same
+// function of the key, so all three kernels route the same exponents.
+__device__ __forceinline__ int route_slot(int64_t key) {
+    return 16 * (int)((key >> 5) & 1) + 4 * (int)((key >> 3) & 3) + (int)(key & 3);
+}
 
 template <int MODE>
 constexpr int exp2_kind() {
@@ -237,7 +245,7 @@ __global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p)
     const int64_t key0 = kb * 128 + wave * 32;  // first key of this wave
     const int64_t key = key0 + c32;             // this lane's key
     const float inv_cap = 1.0f / p.cap;
-    const bool poly_key = ROUTE == kRouteRuntime && key % p.route < 4;
+    const bool poly_key = ROUTE == kRouteRuntime && route_slot(key) % p.route < 4;
 
     bf16x8_t kf[8], vf[8];
     {
@@ -471,8 +479,8 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
                 bool poly0 = false, poly1 = false;
                 if constexpr (ROUTE == kRouteRuntime) {
                     const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    poly0 = key % p.route < 4;
-                    poly1 = (key + 1) % p.route < 4;
+                    poly0 = route_slot(key) % p.route < 4;
+                    poly1 = route_slot(key + 1) % p.route < 4;
                 }
                 score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[r], sacc[r + 1], pacc[r], pacc[r + 1], lse2,
                                                lse2, dl, dl, poly0, poly1, pr_[r], pr_[r + 1], ds[r],

@@ -1,0 +1,342 @@
+"""The FA4 runtime of this build: the fused attention kernels for gfx950.
+
+The reference binds its FA4 configuration layer (``src/sfu_repro/fa4.py``)
+to a patched FlashAttention-4 checkout that is not part of its tree
+(``_load_fa4_runtime``, ``fa4.py:419-451``).  This module provides the same
+runtime mapping -- ``flash_attn_fwd``, ``flash_attn_bwd``, the coefficient
+audits and the softcap score-mod factories -- over the HIP kernels of
+``flash_attn.hip`` / ``flash_attn_bwd.hip`` (through the ``spline_ops``
+extension), so ``sfu_repro.fa4`` resolves against it unchanged.
+
+Operands use FA4's layout: q [B, S, Hq, 128], k and v [B, S, Hkv, 128], BF16;
+``lse`` is float32 [B, Hq, S].  The score program is chosen from the same
+keyword arguments the reference passes (``fa4.py:356-428,430-461``):
+
+* softmax: ``exp2_emu_freq`` 0 or ``None`` -> hardware exp2 (v_exp_f32; on
+  MI355X the automatic route keeps the hardware unit, which issues faster
+  than any polynomial fraction); otherwise four of every ``exp2_emu_freq``
+  exponents take the ``exp2_emu_backend`` program (``d3``: FA4 D3,
+  ``d2_safe``: the B5 D2 fraction, ``pwl2``: the two-piece hinge), key j
+  when slot(j) % freq < 4 with slot(j) = 16 bit5(j) + 4 bits3..4(j) +
+  bits0..1(j), in the forward and the backward alike;
+* softcap: ``softcap > 0`` with no score_mod -> FP32 hardware tanh; a
+  score_mod from ``create_softcap_scoremod_backend`` -> the D4 BF16 program
+  (B2), its backward per ``backward_mode``;
+* sigmoid attention: SFU route -> hardware sigmoid; polynomial route ->
+  the B3 direct D3 program (degree 3, no bias, device backend; S = 4096),
+  the B3-D2 exp2 program (degree 2, no bias; S = 4096) or the BF16 sigmoid
+  D3..D6 programs on ``s + bias`` (``bias`` defaults to ``-ln S``).
+
+Combinations whose programs are not part of the reference tree (the FP16 /
+BF16 / PWL1 exp2 variants, Sollya attention fits, mixed SFU/polynomial
+sigmoid lanes) raise ``NotImplementedError`` naming what is missing.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from functools import lru_cache
+
+import torch
+
+FLASH_SIGMOID_DIRECT_SEQUENCE_LENGTH = 4096
+
+# kernel score modes (AttnMode in flash_attn.hpp)
+MODE_SOFTMAX_NATIVE = 0
+MODE_SOFTMAX_D2 = 1
+MODE_SOFTMAX_D3 = 2
+MODE_SOFTCAP_NATIVE = 3
+MODE_SOFTCAP_D4 = 4
+MODE_SIGMOID_NATIVE = 5
+MODE_SIGMOID_B3 = 6
+MODE_SIGMOID_B3_D2 = 7
+MODE_SIGMOID_D3 = 8  # 8..11: D3..D6
+MODE_SOFTMAX_PWL2 = 12
+
+# derivative programs (AttnGrad in flash_attn_bwd.hip)
+GRAD_NATURAL = 0
+GRAD_ANALYTICAL = 1
+GRAD_STE = 2
+GRAD_EXACT_1MT2 = 3
+GRAD_ALGEBRAIC = 4
+GRAD_DIRECT = 5
+
+BUILT_EXP2_BACKENDS = {"d3": MODE_SOFTMAX_D3, "d2_safe": MODE_SOFTMAX_D2, "pwl2": MODE_SOFTMAX_PWL2}
+SUPPORTED_ROUTES = (0, 4, 6, 8, 10, 12, 16, 20, 24, 32)
+_SOFTCAP_BWD = {"analytical": GRAD_ANALYTICAL, "ste": GRAD_STE, "exact_1mt2": GRAD_EXACT_1MT2}
+
+
+@lru_cache(maxsize=1)
+def _ops():
+    """The compiled extension; fails loudly when it is missing."""
+    try:
+        import spline_ops
+    except (ImportError, OSError) as error:
+        raise RuntimeError(
+            "The compiled spline_ops extension (libspline_hip.so) is unavailable. Build it with "
+            "`python fast-polynomial-transcendentals_amd/build.py`.") from error
+    return spline_ops
+
+
+# ---------------------------------------------------------------------------
+# softcap score-mod objects (FA4's create_softcap_scoremod_backend pair)
+# ---------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class SoftcapScoreMod:
+    """The B2 softcap program cap * tanh(s / cap) with the D4 BF16 tanh, as
+    a score modifier of the fused attention.  Calling it applies the same
+    program to a BF16 tensor of scores (the elementwise kernel)."""
+
+    softcap: float
+    degree: int = 4
+    backend: str = "device"
+    coeff_source: str = "current"
+
+    def __call__(self, scores: torch.Tensor) -> torch.Tensor:
+        return _ops().softcap_tanh_fwd_bf16(scores.contiguous(), float(self.softcap))
+
+
+@dataclass(frozen=True)
+class SoftcapScoreModBwd:
+    """Backward of :class:`SoftcapScoreMod`: ``backward_mode`` selects the
+    derivative the attention backward multiplies into dS."""
+
+    softcap: float
+    degree: int = 4
+    backend: str = "device"
+    backward_mode: str = "analytical"
+    coeff_source: str = "current"
+
+    def __call__(self, grad_out: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
+        if self.backward_mode != "analytical":
+            raise NotImplementedError("the elementwise softcap backward is the analytical D4 derivative")
+        return _ops().softcap_tanh_bwd_bf16(grad_out.contiguous(), scores.contiguous(), float(self.softcap))
+
+
+def _check_softcap_program(softcap: float, degree: int, backend: str, coeff_source: str) -> None:
+    if not softcap > 0:
+        raise ValueError("softcap must be positive")
+    if backend not in ("cute", "device"):
+        raise ValueError(f"unsupported softcap backend {backend!r}")
+    if int(degree) != 4:
+        raise NotImplementedError(
+            f"softcap degree {degree}: only the D4 BF16 tanh (spline_structs_odd_bf16.cuh:153-179) "
+            "is part of the reference tree")
+    if coeff_source != "current":
+        raise NotImplementedError("Sollya softcap fits are not part of the reference tree")
+
+
+def create_softcap_scoremod_backend(softcap: float, degree: int = 4, backend: str = "device",
+                                    coeff_source: str = "current") -> SoftcapScoreMod:
+    _check_softcap_program(softcap, degree, backend, coeff_source)
+    return SoftcapScoreMod(float(softcap), int(degree), backend, coeff_source)
+
+
+def create_softcap_scoremod_bwd_backend(softcap: float, degree: int = 4, backend: str = "device",
+                                        backward_mode: str = "analytical",
+                                        coeff_source: str = "current") -> SoftcapScoreModBwd:
+    _check_softcap_program(softcap, degree, backend, coeff_source)
+    if backward_mode not in _SOFTCAP_BWD:
+        raise ValueError(f"unsupported softcap backward mode {backward_mode!r}")
+    return SoftcapScoreModBwd(float(softcap), int(degree), backend, backward_mode, coeff_source)
+
+
+# ---------------------------------------------------------------------------
+# coefficient audits (FA4's polynomial_manifest / utils audit hooks)
+# ---------------------------------------------------------------------------
+
+# (family, degree, coefficient source) -> where the program lives in this build
+_BUILT_PROGRAMS = {
+    ("tanh_fwd", 4, "current"): "SoftcapConsts / TANH_FWD_D4_ODD_BF16 (score_programs.hpp)",
+    ("tanh_grad_analytical", 4, "current"): "SoftcapConsts::deriv (score_programs.hpp)",
+    ("flash_sigmoid_direct", 3, "current"): "b3_lane (score_programs.hpp)",
+    ("flash_sigmoid_direct_with_grad", 4, "current"): "b3_lane<true> (score_programs.hpp)",
+    ("sigmoid_bwd", 4, "current"): "b3_lane<true>, the B3 factored D4 derivative (score_programs.hpp)",
+    ("flash_sigmoid_exp2", 2, "current"): "b3_d2_lane (score_programs.hpp)",
+    **{("sigmoid_fwd", d, "current"): f"SIGMOID_FWD_D{d}_ODD_BF16 (programs.hpp)" for d in (3, 4, 5, 6)},
+}
+
+
+def run_polynomial_coefficient_audit() -> tuple:
+    """Names of the attention programs compiled into the HIP library.  The
+    constants themselves are pinned by the oracle tests (B3 manifest rows,
+    D4 tanh, B5 exp2 metrics); this check makes sure the library loads."""
+    _ops()
+    return ("b2_tanh_d4_bf16", "b3_direct_d3_d4_bf16", "b3_exp2_d2", "b5_exp2_d2_safe", "b5_exp2_d3",
+            "exp2_pwl2_hinge")
+
+
+def audit_polynomial_selection(selections) -> tuple:
+    out = []
+    for family, degree, source in selections:
+        key = (family, int(degree), source)
+        if key not in _BUILT_PROGRAMS:
+            raise NotImplementedError(f"no {family} D{degree} {source} program in this build")
+        out.append(f"{family} D{int(degree)} {source}")
+    return tuple(out)
+
+
+def audit_attention_handwritten_fast_path(family: str, degree: int, source: str) -> str:
+    key = (family, int(degree), source)
+    if key not in _BUILT_PROGRAMS:
+        raise NotImplementedError(f"no fused {family} D{degree} {source} program in this build")
+    return f"device {family} D{int(degree)} {source} -> {_BUILT_PROGRAMS[key]}"
+
+
+# ---------------------------------------------------------------------------
+# program selection (pure: testable without a GPU)
+# ---------------------------------------------------------------------------
+
+
+def select_forward(*, seqlen: int, softcap: float = 0.0, score_mod=None, sigmoid_attention: bool = False,
+                   sigmoid_sfu_freq: int = 16, sigmoid_sfu_res: int = 0, sigmoid_bias=None,
+                   sigmoid_poly_backend: str = "cute", sigmoid_degree: int = 3,
+                   sigmoid_coeff_source: str = "current", exp2_emu_backend: str = "d3",
+                   exp2_emu_freq=None) -> tuple:
+    """(mode, exp2_route, cap, sigmoid_bias) of the kernel for FA4's
+    forward keyword arguments."""
+    if sigmoid_attention:
+        default_bias = -math.log(seqlen) if seqlen > 0 else 0.0
+        bias = default_bias if sigmoid_bias is None else float(sigmoid_bias)
+        if sigmoid_sfu_res == sigmoid_sfu_freq:
+            return MODE_SIGMOID_NATIVE, 4, 1.0, bias
+        if sigmoid_sfu_res != 0:
+            raise NotImplementedError("mixed SFU / polynomial sigmoid lanes are not built")
+        if sigmoid_coeff_source != "current":
+            raise NotImplementedError("Sollya sigmoid-attention fits are not part of the reference tree")
+        degree = int(sigmoid_degree)
+        if sigmoid_bias is None and sigmoid_poly_backend == "device" and degree in (2, 3):
+            if seqlen != FLASH_SIGMOID_DIRECT_SEQUENCE_LENGTH:
+                raise ValueError(
+                    "direct FlashSigmoid programs are fitted for sequence length "
+                    f"{FLASH_SIGMOID_DIRECT_SEQUENCE_LENGTH}, got {seqlen}")
+            return (MODE_SIGMOID_B3 if degree == 3 else MODE_SIGMOID_B3_D2), 4, 1.0, 0.0
+        if degree not in (3, 4, 5, 6):
+            raise NotImplementedError(f"no BF16 sigmoid D{degree} program")
+        return MODE_SIGMOID_D3 + degree - 3, 4, 1.0, bias
+    if score_mod is not None:
+        if not isinstance(score_mod, SoftcapScoreMod):
+            raise NotImplementedError("only the softcap score_mod of create_softcap_scoremod_backend is fused")
+        return MODE_SOFTCAP_D4, 4, float(score_mod.softcap), 0.0
+    if softcap and softcap > 0:
+        return MODE_SOFTCAP_NATIVE, 4, float(softcap), 0.0
+    if exp2_emu_freq is None or int(exp2_emu_freq) == 0:
+        return MODE_SOFTMAX_NATIVE, 4, 1.0, 0.0
+    if exp2_emu_backend not in BUILT_EXP2_BACKENDS:
+        raise NotImplementedError(
+            f"exp2 backend {exp2_emu_backend!r} is not part of the reference tree; built: "
+            f"{sorted(BUILT_EXP2_BACKENDS)}")
+    route = int(exp2_emu_freq)
+    if route not in SUPPORTED_ROUTES:
+        raise NotImplementedError(f"exp2 routing frequency {route} is not built; built: {SUPPORTED_ROUTES[1:]}")
+    return BUILT_EXP2_BACKENDS[exp2_emu_backend], route, 1.0, 0.0
+
+
+def select_backward(*, seqlen: int, softcap: float = 0.0, score_mod=None, score_mod_bwd=None,
+                    sigmoid_attention: bool = False, sigmoid_bias=None, sigmoid_sfu_freq: int = 16,
+                    sigmoid_sfu_res: int = 0, sigmoid_use_direct_bwd_poly: bool = False,
+                    sigmoid_poly_backend: str = "cute", sigmoid_degree: int = 3,
+                    sigmoid_gradient_degree=None, sigmoid_coeff_source: str = "current",
+                    exp2_emu_backend: str = "d3", exp2_emu_freq: int = 0) -> tuple:
+    """(mode, grad, exp2_route, cap, sigmoid_bias) of the backward kernels
+    for FA4's backward keyword arguments."""
+    if sigmoid_attention:
+        mode, _, cap, bias = select_forward(
+            seqlen=seqlen, sigmoid_attention=True, sigmoid_sfu_freq=sigmoid_sfu_freq,
+            sigmoid_sfu_res=sigmoid_sfu_res, sigmoid_bias=sigmoid_bias,
+            sigmoid_poly_backend=sigmoid_poly_backend, sigmoid_degree=sigmoid_degree,
+            sigmoid_coeff_source=sigmoid_coeff_source)
+        grad = GRAD_NATURAL
+        if mode == MODE_SIGMOID_B3:
+            if sigmoid_use_direct_bwd_poly:
+                if sigmoid_gradient_degree not in (None, 4):
+                    raise NotImplementedError("the B3 direct gradient is the factored D4 program")
+                grad = GRAD_DIRECT
+            else:
+                grad = GRAD_ALGEBRAIC
+        elif sigmoid_use_direct_bwd_poly and mode != MODE_SIGMOID_NATIVE:
+            raise NotImplementedError("direct sigmoid gradient polynomials are built for B3 only")
+        return mode, grad, 0, cap, bias
+    if score_mod is not None:
+        mode, _, cap, _ = select_forward(seqlen=seqlen, score_mod=score_mod)
+        bwd_mode = getattr(score_mod_bwd, "backward_mode", "analytical")
+        if bwd_mode not in _SOFTCAP_BWD:
+            raise NotImplementedError(f"softcap backward mode {bwd_mode!r}")
+        return mode, _SOFTCAP_BWD[bwd_mode], 0, cap, 0.0
+    if softcap and softcap > 0:
+        return MODE_SOFTCAP_NATIVE, GRAD_NATURAL, 0, float(softcap), 0.0
+    route = int(exp2_emu_freq or 0)
+    if route == 0:
+        return MODE_SOFTMAX_NATIVE, GRAD_NATURAL, 0, 1.0, 0.0
+    mode, route, _, _ = select_forward(seqlen=seqlen, exp2_emu_backend=exp2_emu_backend, exp2_emu_freq=route)
+    return mode, GRAD_NATURAL, route, 1.0, 0.0
+
+
+# ---------------------------------------------------------------------------
+# kernels
+# ---------------------------------------------------------------------------
+
+
+def _check_operands(q, k, v):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16 (the fused attention computes BF16 products), got {t.dtype}")
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be [batch, seqlen, heads, head_dim]")
+
+
+def flash_attn_fwd(q, k, v, softmax_scale=None, causal=False, softcap=0.0, score_mod=None,
+                   sigmoid_attention=False, sigmoid_sfu_freq=16, sigmoid_sfu_res=0, sigmoid_bias=None,
+                   sigmoid_poly_backend="cute", sigmoid_degree=3, sigmoid_coeff_source="current",
+                   exp2_emu_backend="d3", exp2_emu_freq=None, **unused):
+    """FA4's forward: returns (out [B, S, Hq, D], lse [B, Hq, S])."""
+    if unused:
+        raise TypeError("unsupported flash_attn_fwd arguments: " + ", ".join(sorted(unused)))
+    _check_operands(q, k, v)
+    scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
+    mode, route, cap, bias = select_forward(
+        seqlen=q.shape[1], softcap=softcap, score_mod=score_mod, sigmoid_attention=sigmoid_attention,
+        sigmoid_sfu_freq=sigmoid_sfu_freq, sigmoid_sfu_res=sigmoid_sfu_res, sigmoid_bias=sigmoid_bias,
+        sigmoid_poly_backend=sigmoid_poly_backend, sigmoid_degree=sigmoid_degree,
+        sigmoid_coeff_source=sigmoid_coeff_source, exp2_emu_backend=exp2_emu_backend,
+        exp2_emu_freq=exp2_emu_freq)
+    out, lse = _ops().flash_attn_fwd_bf16(q, k, v, mode, route, bool(causal), scale, cap, bias)
+    return out, lse
+
+
+def flash_attn_bwd(q, k, v, out, dout, lse, softmax_scale=None, causal=False, softcap=0.0,
+                   score_mod=None, score_mod_bwd=None, sigmoid_attention=False, sigmoid_bias=None,
+                   sigmoid_sfu_freq=16, sigmoid_sfu_res=0, sigmoid_use_direct_bwd_poly=False,
+                   sigmoid_poly_backend="cute", sigmoid_degree=3, sigmoid_gradient_degree=None,
+                   sigmoid_coeff_source="current", exp2_emu_backend="d3", exp2_emu_freq=0, **unused):
+    """FA4's backward: returns (dq, dk, dv) in the operands' shapes."""
+    if unused:
+        raise TypeError("unsupported flash_attn_bwd arguments: " + ", ".join(sorted(unused)))
+    _check_operands(q, k, v)
+    scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
+    mode, grad, route, cap, bias = select_backward(
+        seqlen=q.shape[1], softcap=softcap, score_mod=score_mod, score_mod_bwd=score_mod_bwd,
+        sigmoid_attention=sigmoid_attention, sigmoid_bias=sigmoid_bias, sigmoid_sfu_freq=sigmoid_sfu_freq,
+        sigmoid_sfu_res=sigmoid_sfu_res, sigmoid_use_direct_bwd_poly=sigmoid_use_direct_bwd_poly,
+        sigmoid_poly_backend=sigmoid_poly_backend, sigmoid_degree=sigmoid_degree,
+        sigmoid_gradient_degree=sigmoid_gradient_degree, sigmoid_coeff_source=sigmoid_coeff_source,
+        exp2_emu_backend=exp2_emu_backend, exp2_emu_freq=exp2_emu_freq)
+    dq, dk, dv = _ops().flash_attn_bwd_bf16(q, k, v, out, dout, lse, mode, grad, route, bool(causal),
+                                           scale, cap, bias)
+    return dq, dk, dv
+
+
+def runtime() -> dict:
+    """The mapping ``sfu_repro.fa4`` resolves configurations against."""
+    return {
+        "flash_attn_fwd": flash_attn_fwd,
+        "flash_attn_bwd": flash_attn_bwd,
+        "run_polynomial_coefficient_audit": run_polynomial_coefficient_audit,
+        "audit_polynomial_selection": audit_polynomial_selection,
+        "audit_attention_handwritten_fast_path": audit_attention_handwritten_fast_path,
+        "create_softcap_scoremod_backend": create_softcap_scoremod_backend,
+        "create_softcap_scoremod_bwd_backend": create_softcap_scoremod_bwd_backend,
+    }

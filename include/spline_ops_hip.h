@@ -454,9 +454,12 @@ int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k, con
  *   8..11 sigmoid attention with the BF16 sigmoid D3..D6 program on
  *     bf16(s + sigmoid_bias)          12 softmax, PWL2 hinge exp2.
  * sigmoid_bias: the bias of the hardware and D3..D6 sigmoid modes.
- * exp2_route (modes 1, 2, 12): of every exp2_route exponents of a query row,
- * four take the polynomial and the rest v_exp_f32; one of 4 (all), 6, 8, 10,
- * 12, 16, 20, 24, 32 (FA4's exp2_emu_freq, src/sfu_repro/fa4.py:223-231). */
+ * exp2_route (modes 1, 2, 12): key j of a query row takes the polynomial when
+ * slot(j) % exp2_route < 4, else v_exp_f32, with slot(j) = 16 bit5(j) +
+ * 4 bits3..4(j) + bits0..1(j) (the slot of j's exponent in the kernel's
+ * registers), so four of every exp2_route exponents are routed; one of 4
+ * (all), 6, 8, 10, 12, 16, 20, 24, 32 (FA4's exp2_emu_freq,
+ * src/sfu_repro/fa4.py:223-231). */
 int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q, const void* k,
                                             const void* v, int64_t batch, int64_t q_heads,
                                             int64_t kv_heads, int64_t seq, int64_t head_dim,
@@ -476,8 +479,8 @@ int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q
  *   4 / 5      mode 6 only: y (1 - y) (algebraic) / the B3 factored D4
  *              derivative (direct).
  * exp2_route (modes 1, 2, 12): 0 hardware exp2, 4 the polynomial everywhere,
- * 6..32 the polynomial for keys with key % exp2_route < 4 (FA4's
- * exp2_emu_freq_bwd). */
+ * 6..32 the polynomial for the keys the forward routes with that value
+ * (FA4's exp2_emu_freq_bwd). */
 int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float* delta,
                                             const void* q, const void* k, const void* v,
                                             const void* out, const void* dout, const float* lse,
