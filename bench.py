@@ -162,6 +162,9 @@ def make_unary(lib, name, out, x):
         if rc != 0:
             raise RuntimeError(f"{name} failed with {rc}")
 
+    # the closure holds raw device pointers: keep the tensors alive with it
+    # (graph capture empties torch's allocator cache, which unmaps freed memory)
+    launch.tensors = (out, x)
     return launch
 
 
@@ -285,14 +288,18 @@ ATTN_SHAPE = (1, 32, 8, 4096, 128)  # B, Hq, Hkv, S, D
 
 
 def attention_rows(lib, reps: int, eager_launches: int = 0):
-    """The attention programs inside the fused forward at the reference's
-    component shape (causal GQA, B=1, S=4096, Hq=32, Hkv=8, D=128): B5
-    softmax with the D2 / D3 exp2 against hardware exp2, B2 softcap 30
-    with the D4 tanh against hardware tanh, B3 sigmoid attention with the
-    direct D3 program against hardware exp/rcp.  Causal FLOPs are
-    4 B Hq S^2 D / 2 (the two products over the lower triangle); the bound
-    is the dense BF16 MFMA peak.  With eager_launches > 0 each mode is only
-    launched that many times (a counter pass) and nothing is timed."""
+    """The attention programs inside the fused forward and backward at the
+    reference's component shape (causal GQA, B=1, S=4096, Hq=32, Hkv=8,
+    D=128): B5 softmax with the D2 / D3 exp2 (every exponent, and the B5
+    schedule: four of every 12 forward, 32 backward) against hardware exp2,
+    B2 softcap 30 with the D4 tanh (analytical backward) against hardware
+    tanh, B3 sigmoid attention with the direct D3 / D4 programs against
+    hardware exp/rcp.  Causal FLOPs: forward 4 B Hq S^2 D / 2 (two products
+    over the lower triangle), backward 2.5x that (five products, the usual
+    FlashAttention count; the kernels recompute S and dP once more, so they
+    issue 7/5 of it).  The bound is the dense BF16 MFMA peak.  With
+    eager_launches > 0 each case is only launched that many times (a counter
+    pass) and nothing is timed."""
     import ctypes
     import math
 
@@ -304,21 +311,53 @@ def attention_rows(lib, reps: int, eager_launches: int = 0):
     q = torch.randn(b, hq, s, d, device=dev, generator=g).bfloat16()
     k = torch.randn(b, hkv, s, d, device=dev, generator=g).bfloat16()
     v = torch.randn(b, hkv, s, d, device=dev, generator=g).bfloat16()
+    do = torch.randn(b, hq, s, d, device=dev, generator=g).bfloat16()
     # scores spread as after QK-norm with a learnt scale: s = q.k / sqrt(d) * 4
     qs = (q.float() * 4).bfloat16()
     o = torch.empty_like(q)
     scale = 1.0 / math.sqrt(d)
     flops = 4 * b * hq * s * s * d / 2
+    sigmoid_bias = -math.log(s)
 
-    def fa(mode, qq):
-        return _launcher(lib, "launch_flash_attention_fwd_bf16", o, qq, k, v, b, hq, hkv, s, d,
-                         ctypes.c_int(mode), ctypes.c_int(1), ctypes.c_float(scale), ctypes.c_float(30.0))
+    def strides(*ts):
+        vals = []
+        for t in ts:  # [B, H, S, D]: (batch, head, sequence)
+            vals += [t.stride(0), t.stride(1), t.stride(2)]
+        return (ctypes.c_int64 * len(vals))(*vals)
 
-    groups = [("B5 softmax exp2", [("poly_d2", fa(1, q)), ("poly_d3", fa(2, q)), ("native", fa(0, q))]),
-              ("B2 softcap 30", [("poly_d4", fa(4, qs)), ("native", fa(3, qs))]),
-              ("B3 sigmoid attention", [("poly_b3", fa(6, q)), ("native", fa(5, q))])]
+    def fa(mode, qq, route=4, out=o, lse=None):
+        lse_arg = lse if lse is not None else ctypes.c_void_p(0)
+        return _launcher(lib, "launch_flash_attention_fwd_strided_bf16", out, lse_arg, qq, k, v, b, hq, hkv, s,
+                         d, strides(qq, k, v, out), ctypes.c_int(mode), ctypes.c_int(route), ctypes.c_int(1),
+                         ctypes.c_float(scale), ctypes.c_float(30.0), ctypes.c_float(sigmoid_bias))
+
+    def fa_bwd(mode, grad, qq, route_fwd=4, route_bwd=0):
+        # out and lse of the same forward, then the backward on them
+        out = torch.empty_like(qq)
+        lse = torch.zeros(b, hq, s, dtype=torch.float32, device=dev)
+        fa(mode, qq, route_fwd, out, lse)()
+        torch.cuda.synchronize()
+        dq, dk, dv = torch.empty_like(qq), torch.empty_like(k), torch.empty_like(v)
+        delta = torch.empty(b, hq, s, dtype=torch.float32, device=dev)
+        ws = torch.empty(2, b, hq, s, d, dtype=torch.float32, device=dev)
+        return _launcher(lib, "launch_flash_attention_bwd_strided_bf16", dq, dk, dv, delta, ws, qq, k, v, out, do,
+                         lse, b, hq, hkv, s, d, strides(qq, k, v, out, do, dq, dk, dv), ctypes.c_int(mode),
+                         ctypes.c_int(grad), ctypes.c_int(route_bwd), ctypes.c_int(1), ctypes.c_float(scale),
+                         ctypes.c_float(30.0), ctypes.c_float(sigmoid_bias))
+
+    groups = [("fwd", "B5 softmax exp2", flops,
+               [("poly_d2", fa(1, q)), ("poly_d3", fa(2, q)), ("poly_d2_route12", fa(1, q, 12)),
+                ("native", fa(0, q))]),
+              ("fwd", "B2 softcap 30", flops, [("poly_d4", fa(4, qs)), ("native", fa(3, qs))]),
+              ("fwd", "B3 sigmoid attention", flops, [("poly_b3", fa(6, q)), ("native", fa(5, q))]),
+              ("bwd", "B5 softmax exp2", 2.5 * flops,
+               [("poly_d2_route32", fa_bwd(1, 0, q, 12, 32)), ("native", fa_bwd(0, 0, q))]),
+              ("bwd", "B2 softcap 30", 2.5 * flops,
+               [("poly_d4_analytical", fa_bwd(4, 1, qs)), ("native", fa_bwd(3, 0, qs))]),
+              ("bwd", "B3 sigmoid attention", 2.5 * flops,
+               [("poly_b3_direct", fa_bwd(6, 5, q)), ("native", fa_bwd(5, 0, q))])]
     rows = []
-    for function, launches in groups:
+    for direction, function, fl, launches in groups:
         if eager_launches:
             for _, fn in launches:
                 for _ in range(eager_launches):
@@ -326,12 +365,12 @@ def attention_rows(lib, reps: int, eager_launches: int = 0):
             torch.cuda.synchronize()
             continue
         times = time_graphs_alternating([fn for _, fn in launches], max(5, reps // 10))
-        row = {"function": f"attention_fwd {function}", "dtype": "bf16",
-               "config": f"causal GQA B={b} S={s} Hq={hq} Hkv={hkv} D={d}", "flops": flops}
+        row = {"function": f"attention_{direction} {function}", "dtype": "bf16",
+               "config": f"causal GQA B={b} S={s} Hq={hq} Hkv={hkv} D={d}", "flops": fl}
         for (label, _), ms in zip(launches, times):
             row[f"{label}_us"] = round(ms * 1e3, 2)
-            row[f"{label}_tflops"] = round(flops / ms / 1e9, 1)
-            row[f"{label}_frac_mfma_peak"] = round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)
+            row[f"{label}_tflops"] = round(fl / ms / 1e9, 1)
+            row[f"{label}_frac_mfma_peak"] = round(fl / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)
         for label, _ in launches[:-1]:
             row[f"{label}_speedup"] = round(row["native_us"] / row[f"{label}_us"], 3)
         rows.append(row)
@@ -471,7 +510,7 @@ def _launcher(lib, name, *args):
     fn.restype = ctypes.c_int
     conv = []
     for a in args:
-        if isinstance(a, ctypes._SimpleCData):
+        if isinstance(a, (ctypes._SimpleCData, ctypes.Array)):
             conv.append(a)
         elif isinstance(a, torch.Tensor):
             conv.append(_vp(a))
@@ -485,6 +524,9 @@ def _launcher(lib, name, *args):
         if rc != 0:
             raise RuntimeError(f"{name} failed with {rc}")
 
+    # the closure holds raw device pointers: keep the tensors alive with it
+    # (graph capture empties torch's allocator cache, which unmaps freed memory)
+    launch.tensors = tuple(a for a in args if isinstance(a, torch.Tensor))
     return launch
 
 

@@ -707,6 +707,8 @@ std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     at::Tensor dk = at::empty({b, sq, hkv, 128}, q.options());
     at::Tensor dv = at::empty({b, sq, hkv, 128}, q.options());
     at::Tensor delta = at::empty({b, hq, sq}, q.options().dtype(at::kFloat));
+    at::Tensor dkv_ws = hq != hkv ? at::empty({2, b, hq, sq, 128}, q.options().dtype(at::kFloat))
+                                  : at::Tensor();
     const int64_t strides[24] = {q.stride(0),    q.stride(2),    q.stride(1),    k.stride(0),
                                  k.stride(2),    k.stride(1),    v.stride(0),    v.stride(2),
                                  v.stride(1),    out.stride(0),  out.stride(2),  out.stride(1),
@@ -716,7 +718,7 @@ std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     void* s = current_stream(q);
     check_launch(launch_flash_attention_bwd_strided_bf16(
                      dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr<float>(),
-                     q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
+                     hq != hkv ? dkv_ws.data_ptr<float>() : nullptr, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
                      lse.data_ptr<float>(), b, hq, hkv, sq, 128, strides, (int)mode, (int)grad,
                      (int)exp2_route, causal ? 1 : 0, (float)softmax_scale, (float)softcap,
                      (float)sigmoid_bias, s),

@@ -3,10 +3,12 @@
 // FA4 integration site (src/sfu_repro/fa4.py:430-461 calls flash_attn_bwd;
 // the FA4 kernel itself is not part of the reference tree).
 //
-// Three kernels, no atomics:
+// Three kernels (four with grouped heads), no atomics:
 //  * delta: D[q] = sum_d dO[q][d] O[q][d] (FP32), for the softmax modes;
-//  * dK/dV: a block owns 128 keys (32 per wave, K and V held in registers)
-//    and streams 32-query tiles of Q, Q^T, dO, dO^T (+ lse, D) through LDS;
+//  * dK/dV: a block owns 128 keys of one query head (32 per wave, K and V
+//    held in registers) and streams 32-query tiles of Q, Q^T, dO, dO^T
+//    (+ lse, D) through LDS; with grouped-query heads each block writes FP32
+//    partials and a reduction kernel sums the group (deterministically);
 //    S = Q K^T and dP = dO V^T come out with one key per lane, so P and dS
 //    are ready-made B fragments of dV^T += dO^T P and dK^T += Q^T dS (the
 //    k index numbered in accumulator order, as in the forward);
@@ -52,6 +54,7 @@ struct AttnBwdParams {
     uint16_t* dq;
     uint16_t* dk;
     uint16_t* dv;
+    float* dkv_ws;  // grouped heads: per-query-head dK, dV partials [2][B, Hq, S, 128]
     AttnStrides qs, ks, vs, dos, dqs, dks, dvs;
     int64_t hq, hkv, seq;
     float scale, cap, sig_bias;
@@ -240,8 +243,12 @@ __global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p)
     const int wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, c32 = lane & 31;
     const int pr = tid >> 4, dc = tid & 15;
-    const int64_t kvh = blockIdx.x, kb = blockIdx.y, b = blockIdx.z;
+    // one block per (query head, 128-key block): grouped heads write FP32
+    // partials that attn_dkv_reduce_kernel sums, so the causal work per block
+    // stays within one head's query range
+    const int64_t head = blockIdx.x, kb = blockIdx.y, b = blockIdx.z;
     const int64_t group = p.hq / p.hkv;
+    const int64_t kvh = head / group;
     const int64_t key0 = kb * 128 + wave * 32;  // first key of this wave
     const int64_t key = key0 + c32;             // this lane's key
     const float inv_cap = 1.0f / p.cap;
@@ -261,17 +268,15 @@ __global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p)
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) dkacc[dt] = dvacc[dt] = (f32x16_t){};
 
-    // query tiles: every head of the group, from the block's first key on
-    // under the causal mask
+    // query tiles of this head, from the block's first key on under the
+    // causal mask
     const int64_t qt0 = p.causal ? kb * (128 / kBwdTile) : 0;
-    const int64_t nqt = p.seq / kBwdTile - qt0;
-    const int64_t nit = group * nqt;
+    const int64_t nit = p.seq / kBwdTile - qt0;
 
     u32x4_t qa, qb, da, db;
     float lse_r = 0.0f, del_r = 0.0f;
     auto load = [&](int64_t it) {
-        const int64_t head = kvh * group + it / nqt;
-        const int64_t q0 = (qt0 + it % nqt) * kBwdTile;
+        const int64_t q0 = (qt0 + it) * kBwdTile;
         const uint16_t* qr = p.q + b * p.qs.b + head * p.qs.h + (q0 + 2 * pr) * p.qs.s + dc * 8;
         const uint16_t* dr = p.dout + b * p.dos.b + head * p.dos.h + (q0 + 2 * pr) * p.dos.s + dc * 8;
         qa = *reinterpret_cast<const u32x4_t*>(qr);
@@ -307,7 +312,7 @@ __global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p)
         const int buf = (int)(it & 1);
         const bool more = it + 1 < nit;
         if (more) load(it + 1);
-        const int64_t q0 = (qt0 + it % nqt) * kBwdTile;
+        const int64_t q0 = (qt0 + it) * kBwdTile;
         if (!p.causal || q0 + kBwdTile - 1 >= key0) {  // some query of the tile sees a key of the wave
             const BwdQTile& t = tiles[buf];
             f32x16_t sacc = {}, pacc = {};
@@ -367,6 +372,22 @@ __global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p)
     }
 
     // dK^T / dV^T: register r of dt holds d = 32 dt + 8 (r/4) + 4h + r%4 of key c32
+    if (p.dkv_ws != nullptr) {
+        const int64_t plane = p.hq * p.seq * kHeadDim * (int64_t)gridDim.z;
+        float* wk = p.dkv_ws + ((b * p.hq + head) * p.seq + key) * kHeadDim;
+        float* wv = wk + plane;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = dt * 32 + 8 * g + 4 * h;
+                *reinterpret_cast<f32x4_t*>(wk + d) = (f32x4_t){dkacc[dt][4 * g], dkacc[dt][4 * g + 1],
+                                                               dkacc[dt][4 * g + 2], dkacc[dt][4 * g + 3]};
+                *reinterpret_cast<f32x4_t*>(wv + d) = (f32x4_t){dvacc[dt][4 * g], dvacc[dt][4 * g + 1],
+                                                               dvacc[dt][4 * g + 2], dvacc[dt][4 * g + 3]};
+            }
+        return;
+    }
     uint16_t* dkr = p.dk + b * p.dks.b + kvh * p.dks.h + key * p.dks.s;
     uint16_t* dvr = p.dv + b * p.dvs.b + kvh * p.dvs.h + key * p.dvs.s;
 #pragma unroll
@@ -381,6 +402,36 @@ __global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p)
             *reinterpret_cast<u32x2_t*>(dkr + d) = wk;
             *reinterpret_cast<u32x2_t*>(dvr + d) = wv;
         }
+}
+
+// dK, dV of grouped heads: the sum over the group's query heads of the FP32
+// partials, rounded once to BF16.  Thread = 8 head-dim elements of one key.
+__global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(const float* __restrict__ ws,
+                                                              uint16_t* __restrict__ dk,
+                                                              uint16_t* __restrict__ dv, AttnStrides dks,
+                                                              AttnStrides dvs, int64_t batch, int64_t hq,
+                                                              int64_t hkv, int64_t seq) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (b, kvh, key, chunk)
+    const int64_t total = batch * hkv * seq * (kHeadDim / 8);
+    if (i >= total) return;
+    const int c = (int)(i % (kHeadDim / 8));
+    const int64_t key = (i / (kHeadDim / 8)) % seq;
+    const int64_t bh = i / ((kHeadDim / 8) * seq);
+    const int64_t kvh = bh % hkv, b = bh / hkv;
+    const int64_t group = hq / hkv;
+    const int64_t plane = batch * hq * seq * kHeadDim;
+    f32x4_t k0 = {}, k1 = {}, v0 = {}, v1 = {};
+    for (int64_t g = 0; g < group; ++g) {
+        const float* w = ws + ((b * hq + kvh * group + g) * seq + key) * kHeadDim + c * 8;
+        k0 += *reinterpret_cast<const f32x4_t*>(w);
+        k1 += *reinterpret_cast<const f32x4_t*>(w + 4);
+        v0 += *reinterpret_cast<const f32x4_t*>(w + plane);
+        v1 += *reinterpret_cast<const f32x4_t*>(w + plane + 4);
+    }
+    const u32x4_t ok = {pack_bf(k0[0], k0[1]), pack_bf(k0[2], k0[3]), pack_bf(k1[0], k1[1]), pack_bf(k1[2], k1[3])};
+    const u32x4_t ov = {pack_bf(v0[0], v0[1]), pack_bf(v0[2], v0[3]), pack_bf(v1[0], v1[1]), pack_bf(v1[2], v1[3])};
+    *reinterpret_cast<u32x4_t*>(dk + b * dks.b + kvh * dks.h + key * dks.s + c * 8) = ok;
+    *reinterpret_cast<u32x4_t*>(dv + b * dvs.b + kvh * dvs.h + key * dvs.s + c * 8) = ov;
 }
 
 // ---------------------------------------------------------------------------
@@ -522,10 +573,15 @@ namespace {
 
 template <int MODE, int GRAD, int ROUTE>
 void launch_bwd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
-    const dim3 gkv((unsigned)prm.hkv, (unsigned)(prm.seq / 128), (unsigned)batch);
-    const dim3 gq((unsigned)prm.hq, (unsigned)(prm.seq / kAttnBlockQ), (unsigned)batch);
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE>), gkv, dim3(256), 0, st, prm);
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE>), gq, dim3(256), 0, st, prm);
+    const dim3 grid((unsigned)prm.hq, (unsigned)(prm.seq / 128), (unsigned)batch);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE>), grid, dim3(256), 0, st, prm);
+    if (prm.dkv_ws != nullptr) {
+        const int64_t n = batch * prm.hkv * prm.seq * (kHeadDim / 8);
+        hipLaunchKernelGGL(attn_dkv_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           (const float*)prm.dkv_ws, prm.dk, prm.dv, prm.dks, prm.dvs, batch, prm.hq,
+                           prm.hkv, prm.seq);
+    }
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE>), grid, dim3(256), 0, st, prm);
 }
 
 template <int MODE>
@@ -542,7 +598,7 @@ bool bwd_stride_ok(const AttnStrides& t) {
 }  // namespace
 
 extern "C" int launch_flash_attention_bwd_strided_bf16(
-    void* dq, void* dk, void* dv, float* delta, const void* q, const void* k, const void* v,
+    void* dq, void* dk, void* dv, float* delta, float* dkv_workspace, const void* q, const void* k, const void* v,
     const void* out, const void* dout, const float* lse, int64_t batch, int64_t q_heads,
     int64_t kv_heads, int64_t seq, int64_t head_dim, const int64_t* strides, int mode, int grad,
     int exp2_route, int causal, float scale, float cap, float sigmoid_bias, void* stream) {
@@ -576,6 +632,11 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
                  (reinterpret_cast<uintptr_t>(delta) & 3)))
         return hipErrorInvalidValue;
     if (batch > 65535 || seq / 128 > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
+    const bool grouped = q_heads != kv_heads;
+    if (grouped && (!dkv_workspace || (reinterpret_cast<uintptr_t>(dkv_workspace) & 15)))
+        return hipErrorInvalidValue;
+    // 2 * B * Hq * S * 128 floats must stay addressable
+    if (grouped && batch * q_heads * seq > (int64_t(1) << 52) / kHeadDim) return hipErrorInvalidValue;
     hipStream_t hst = hs(stream);
     if (!sig) {
         const int64_t rows = batch * q_heads * seq;
@@ -585,7 +646,7 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
     }
     AttnBwdParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
                       sig ? nullptr : lse, sig ? nullptr : delta, (uint16_t*)dq, (uint16_t*)dk,
-                      (uint16_t*)dv, st[0], st[1], st[2], st[4], st[5], st[6], st[7], q_heads, kv_heads,
+                      (uint16_t*)dv, grouped ? dkv_workspace : nullptr, st[0], st[1], st[2], st[4], st[5], st[6], st[7], q_heads, kv_heads,
                       seq, scale, cap > 0.0f ? cap : 1.0f, sigmoid_bias, exp2_route > 0 ? exp2_route : 4,
                       causal != 0};
     switch (mode) {

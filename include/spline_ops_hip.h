@@ -472,7 +472,10 @@ int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q
  * strides: 24 element strides, (batch, head, sequence) of q, k, v, out, dout,
  * dq, dk, dv.  delta: caller-provided float [B, Hq, S] workspace receiving
  * rowsum(dout * out) (softmax modes; unused for sigmoid modes, where out, lse
- * and delta may be null).  grad, the derivative of the score program:
+ * and delta may be null).  dkv_workspace: with grouped-query heads (Hq > Hkv)
+ * a caller-provided, 16-byte aligned float workspace of 2 * B * Hq * S * 128
+ * elements (per-query-head dK / dV partials, summed deterministically into
+ * dk / dv); null otherwise.  grad, the derivative of the score program:
  *   0 the mode's own (softmax, softcap 1 - tanh^2, sigmoid p (1 - p))
  *   1 / 2 / 3  mode 4 only: the D4 derivative polynomial (FA4 "analytical") /
  *              straight-through (ste) / 1 - T(u)^2 (exact_1mt2)
@@ -482,7 +485,7 @@ int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q
  * 6..32 the polynomial for the keys the forward routes with that value
  * (FA4's exp2_emu_freq_bwd). */
 int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float* delta,
-                                            const void* q, const void* k, const void* v,
+                                            float* dkv_workspace, const void* q, const void* k, const void* v,
                                             const void* out, const void* dout, const float* lse,
                                             int64_t batch, int64_t q_heads, int64_t kv_heads,
                                             int64_t seq, int64_t head_dim, const int64_t* strides,

@@ -63,9 +63,11 @@ def bwd(capi, cuda, q, k, v, out, do, lse, mode, grad, causal, scale, cap=30.0, 
     dk = torch.empty_like(kd)
     dv = torch.empty_like(vd)
     delta = torch.empty(b, hq, s, dtype=torch.float32, device=cuda)
+    ws = torch.empty(2, b, hq, s, 128, dtype=torch.float32, device=cuda) if hq != hkv else None
     bias = _bias(mode, s) if bias is None else bias
     rc = capi.launch_flash_attention_bwd_strided_bf16(
-        capi.ptr(dq), capi.ptr(dk), capi.ptr(dv), capi.ptr(delta), capi.ptr(qd), capi.ptr(kd),
+        capi.ptr(dq), capi.ptr(dk), capi.ptr(dv), capi.ptr(delta),
+        capi.ptr(ws) if ws is not None else ctypes.c_void_p(0), capi.ptr(qd), capi.ptr(kd),
         capi.ptr(vd), capi.ptr(out), capi.ptr(dod), capi.ptr(lse), ctypes.c_int64(b), ctypes.c_int64(hq),
         ctypes.c_int64(hkv), ctypes.c_int64(s), ctypes.c_int64(128),
         _strides(qd, kd, vd, out, dod, dq, dk, dv), ctypes.c_int(M[mode]), ctypes.c_int(grad),
@@ -171,7 +173,8 @@ def test_rejected_backward_arguments(capi, cuda):
 
     def call(mode, grad, route=0, seq=128, cap=30.0):
         return capi.launch_flash_attention_bwd_strided_bf16(
-            capi.ptr(q), capi.ptr(q), capi.ptr(q), capi.ptr(delta), capi.ptr(q), capi.ptr(q), capi.ptr(q),
+            capi.ptr(q), capi.ptr(q), capi.ptr(q), capi.ptr(delta), ctypes.c_void_p(0), capi.ptr(q),
+            capi.ptr(q), capi.ptr(q),
             capi.ptr(q), capi.ptr(q), capi.ptr(lse), ctypes.c_int64(1), ctypes.c_int64(2), ctypes.c_int64(2),
             ctypes.c_int64(seq), ctypes.c_int64(128), _strides(*([q] * 8)), ctypes.c_int(mode),
             ctypes.c_int(grad), ctypes.c_int(route), ctypes.c_int(1), ctypes.c_float(0.1),
@@ -184,4 +187,24 @@ def test_rejected_backward_arguments(capi, cuda):
     assert call(4, 1, cap=0.0) != 0
     assert call(13, 0) != 0
     assert call(0, 0) == 0
+    torch.cuda.synchronize()
+
+
+def test_grouped_heads_need_the_partials_workspace(capi, cuda):
+    q = torch.zeros(1, 128, 4, 128, dtype=torch.bfloat16, device=cuda)
+    kv = torch.zeros(1, 128, 2, 128, dtype=torch.bfloat16, device=cuda)
+    lse = torch.zeros(1, 4, 128, dtype=torch.float32, device=cuda)
+    delta = torch.zeros_like(lse)
+    ws = torch.zeros(2, 1, 4, 128, 128, dtype=torch.float32, device=cuda)
+
+    def call(wsp):
+        return capi.launch_flash_attention_bwd_strided_bf16(
+            capi.ptr(q), capi.ptr(kv), capi.ptr(kv), capi.ptr(delta), wsp, capi.ptr(q), capi.ptr(kv),
+            capi.ptr(kv), capi.ptr(q), capi.ptr(q), capi.ptr(lse), ctypes.c_int64(1), ctypes.c_int64(4),
+            ctypes.c_int64(2), ctypes.c_int64(128), ctypes.c_int64(128), _strides(q, kv, kv, q, q, q, kv, kv),
+            ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(1), ctypes.c_float(0.1),
+            ctypes.c_float(30.0), ctypes.c_float(0.0), capi.stream())
+
+    assert call(ctypes.c_void_p(0)) != 0
+    assert call(capi.ptr(ws)) == 0
     torch.cuda.synchronize()
