@@ -5,13 +5,14 @@
 //
 // Three kernels (four with grouped heads), no atomics:
 //  * delta: D[q] = sum_d dO[q][d] O[q][d] (FP32), for the softmax modes;
-//  * dK/dV: a block owns 128 keys of one query head (32 per wave, K and V
-//    held in registers) and streams 32-query tiles of Q, Q^T, dO, dO^T
-//    (+ lse, D) through LDS; with grouped-query heads each block writes FP32
-//    partials and a reduction kernel sums the group (deterministically);
-//    S = Q K^T and dP = dO V^T come out with one key per lane, so P and dS
-//    are ready-made B fragments of dV^T += dO^T P and dK^T += Q^T dS (the
-//    k index numbered in accumulator order, as in the forward);
+//  * dK/dV: a block of 8 waves owns 128 keys of one query head (16 per
+//    wave, K and V held in registers, 16x16x32 MFMA) and streams 32-query
+//    tiles of Q, Q^T, dO, dO^T (+ lse, D) through LDS; with grouped-query
+//    heads each block writes FP32 partials and a reduction kernel sums the
+//    group (deterministically); S = Q K^T and dP = dO V^T come out with one
+//    key per lane, so P and dS are ready-made B fragments of dV^T += dO^T P
+//    and dK^T += Q^T dS (the k index numbered in accumulator order, as in the
+//    forward);
 //  * dQ: a block owns 128 queries (32 per wave, Q and dO in registers) and
 //    streams 32-key tiles of K, K^T and V: S^T = K Q^T and dP^T = V dO^T have
 //    one query per lane, dQ^T += K^T dS^T.
@@ -234,74 +235,94 @@ struct BwdQTile {
     float delta[kBwdTile];
 };
 
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4v_t mfma16(bf16x8_t a, bf16x8_t b, f32x4v_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// A fragment (16x16x32) of a transposed tile: row `row`, the eight k slots
+// of lane group g in accumulator order (columns 4g .. 4g+3 and 16+4g .. +3).
+__device__ __forceinline__ bf16x8_t frag_t16(const uint16_t* t, int row, int g) {
+    const uint16_t* r = t + row * kTStride + 4 * g;
+    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r);
+    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + 16);
+    const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
+    return __builtin_bit_cast(bf16x8_t, w);
+}
+
+// One block = 8 waves = 128 keys of one query head, 16 keys per wave, all
+// products on v_mfma_f32_16x16x32_bf16 (A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
+// C register r -> row 4(l/16) + r, column l%16):
+//  * S = Q K^T and dP = dO V^T per 16-query row block rb: lane (g = l/16,
+//    key l%16) holds queries 16 rb + 4g + r;
+//  * dV^T += dO^T P and dK^T += Q^T dS take P / dS as B fragments with
+//    k slot 8g + e <-> query 16 (e/4) + 4g + e%4, the accumulator order;
+//  * per wave: K, V fragments 32 VGPRs, dK^T / dV^T accumulators 64, so two
+//    waves share a SIMD.
 template <int MODE, int GRAD, int ROUTE>
-__global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p) {
+__global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     __shared__ __align__(16) BwdQTile tiles[2];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int h = lane >> 5, c32 = lane & 31;
-    const int pr = tid >> 4, dc = tid & 15;
+    const int g = lane >> 4, kl = lane & 15;
+    // staging: threads 0..255 move Q, 256..511 dO (row pair pr, chunk dc)
+    const int half = tid >> 8, st = tid & 255;
+    const int pr = st >> 4, dc = st & 15;
     // one block per (query head, 128-key block): grouped heads write FP32
     // partials that attn_dkv_reduce_kernel sums, so the causal work per block
     // stays within one head's query range
     const int64_t head = blockIdx.x, kb = blockIdx.y, b = blockIdx.z;
     const int64_t group = p.hq / p.hkv;
     const int64_t kvh = head / group;
-    const int64_t key0 = kb * 128 + wave * 32;  // first key of this wave
-    const int64_t key = key0 + c32;             // this lane's key
+    const int64_t key0 = kb * 128 + wave * 16;  // first key of this wave
+    const int64_t key = key0 + kl;              // this lane's key
     const float inv_cap = 1.0f / p.cap;
     const bool poly_key = ROUTE == kRouteRuntime && route_slot(key) % p.route < 4;
 
-    bf16x8_t kf[8], vf[8];
+    bf16x8_t kf[4], vf[4];
     {
         const uint16_t* kr = p.k + b * p.ks.b + kvh * p.ks.h + key * p.ks.s;
         const uint16_t* vr = p.v + b * p.vs.b + kvh * p.vs.h + key * p.vs.s;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            kf[c] = *reinterpret_cast<const bf16x8_t*>(kr + c * 16 + h * 8);
-            vf[c] = *reinterpret_cast<const bf16x8_t*>(vr + c * 16 + h * 8);
+        for (int c = 0; c < 4; ++c) {
+            kf[c] = *reinterpret_cast<const bf16x8_t*>(kr + c * 32 + g * 8);
+            vf[c] = *reinterpret_cast<const bf16x8_t*>(vr + c * 32 + g * 8);
         }
     }
-    f32x16_t dkacc[4], dvacc[4];
+    f32x4v_t dkacc[8], dvacc[8];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) dkacc[dt] = dvacc[dt] = (f32x16_t){};
+    for (int dt = 0; dt < 8; ++dt) dkacc[dt] = dvacc[dt] = (f32x4v_t){};
 
     // query tiles of this head, from the block's first key on under the
     // causal mask
     const int64_t qt0 = p.causal ? kb * (128 / kBwdTile) : 0;
     const int64_t nit = p.seq / kBwdTile - qt0;
 
-    u32x4_t qa, qb, da, db;
-    float lse_r = 0.0f, del_r = 0.0f;
+    const uint16_t* src = half ? p.dout + b * p.dos.b + head * p.dos.h : p.q + b * p.qs.b + head * p.qs.h;
+    const int64_t src_s = half ? p.dos.s : p.qs.s;
+    u32x4_t ra, rb2;
+    float row_r = 0.0f;
     auto load = [&](int64_t it) {
         const int64_t q0 = (qt0 + it) * kBwdTile;
-        const uint16_t* qr = p.q + b * p.qs.b + head * p.qs.h + (q0 + 2 * pr) * p.qs.s + dc * 8;
-        const uint16_t* dr = p.dout + b * p.dos.b + head * p.dos.h + (q0 + 2 * pr) * p.dos.s + dc * 8;
-        qa = *reinterpret_cast<const u32x4_t*>(qr);
-        qb = *reinterpret_cast<const u32x4_t*>(qr + p.qs.s);
-        da = *reinterpret_cast<const u32x4_t*>(dr);
-        db = *reinterpret_cast<const u32x4_t*>(dr + p.dos.s);
+        const uint16_t* r = src + (q0 + 2 * pr) * src_s + dc * 8;
+        ra = *reinterpret_cast<const u32x4_t*>(r);
+        rb2 = *reinterpret_cast<const u32x4_t*>(r + src_s);
         if constexpr (!kSigmoid) {
-            if (tid < kBwdTile) {
-                const int64_t i = (b * p.hq + head) * p.seq + q0 + tid;
-                lse_r = p.lse[i] * kLog2e;
-                del_r = p.delta[i];
+            if (st < kBwdTile) {
+                const int64_t i = (b * p.hq + head) * p.seq + q0 + st;
+                row_r = half ? p.delta[i] : p.lse[i] * kLog2e;
             }
         }
     };
     auto store = [&](int buf) {
         BwdQTile& t = tiles[buf];
-        store_rows(t.q, pr, dc, qa, qb);
-        store_transposed(t.qt, pr, dc, qa, qb);
-        store_rows(t.dout, pr, dc, da, db);
-        store_transposed(t.doutt, pr, dc, da, db);
+        store_rows(half ? t.dout : t.q, pr, dc, ra, rb2);
+        store_transposed(half ? t.doutt : t.qt, pr, dc, ra, rb2);
         if constexpr (!kSigmoid) {
-            if (tid < kBwdTile) {
-                t.lse2[tid] = lse_r;
-                t.delta[tid] = del_r;
-            }
+            if (st < kBwdTile) (half ? t.delta : t.lse2)[st] = row_r;
         }
     };
 
@@ -315,93 +336,89 @@ __global__ void __launch_bounds__(256, 1) flash_bwd_dkdv_kernel(AttnBwdParams p)
         const int64_t q0 = (qt0 + it) * kBwdTile;
         if (!p.causal || q0 + kBwdTile - 1 >= key0) {  // some query of the tile sees a key of the wave
             const BwdQTile& t = tiles[buf];
-            f32x16_t sacc = {}, pacc = {};
+            f32x4v_t sacc[2], pacc[2];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const bf16x8_t aq = *reinterpret_cast<const bf16x8_t*>(t.q + c32 * kRowStride + 16 * c + 8 * h);
-                sacc = mfma32(aq, kf[c], sacc);
-            }
+            for (int rb = 0; rb < 2; ++rb) {
+                sacc[rb] = pacc[rb] = (f32x4v_t){};
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const bf16x8_t ad = *reinterpret_cast<const bf16x8_t*>(t.dout + c32 * kRowStride + 16 * c + 8 * h);
-                pacc = mfma32(ad, vf[c], pacc);
+                for (int c = 0; c < 4; ++c) {
+                    const int off = (16 * rb + kl) * kRowStride + 32 * c + 8 * g;
+                    sacc[rb] = mfma16(*reinterpret_cast<const bf16x8_t*>(t.q + off), kf[c], sacc[rb]);
+                    pacc[rb] = mfma16(*reinterpret_cast<const bf16x8_t*>(t.dout + off), vf[c], pacc[rb]);
+                }
             }
-            // register r: query q0 + 8 (r/4) + 4h + r%4 of this lane's key
-            float lse[16], del[16];
+            // register (rb, r): query q0 + 16 rb + 4g + r of this lane's key
+            float lse[8], del[8];
             if constexpr (!kSigmoid) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(t.lse2 + 8 * j + 4 * h);
-                    const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(t.delta + 8 * j + 4 * h);
+                for (int rb = 0; rb < 2; ++rb) {
+                    const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(t.lse2 + 16 * rb + 4 * g);
+                    const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(t.delta + 16 * rb + 4 * g);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        lse[4 * j + i] = l4[i];
-                        del[4 * j + i] = d4[i];
+                    for (int r = 0; r < 4; ++r) {
+                        lse[4 * rb + r] = l4[r];
+                        del[4 * rb + r] = d4[r];
                     }
                 }
             } else {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) lse[r] = del[r] = 0.0f;
+                for (int e = 0; e < 8; ++e) lse[e] = del[e] = 0.0f;
             }
-            const bool need_mask = p.causal && q0 < key0 + 31;
-            const int diag = (int)(key - q0) - 4 * h;  // masked when diag > 8 (r/4) + r%4
-            float pr_[16], ds[16];
+            float pr_[8], ds[8];
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[r], sacc[r + 1], pacc[r], pacc[r + 1], lse[r],
-                                               lse[r + 1], del[r], del[r + 1], poly_key, poly_key, pr_[r],
-                                               pr_[r + 1], ds[r], ds[r + 1]);
-            }
-            if (need_mask) {
+            for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (diag > 8 * (r >> 2) + (r & 3)) pr_[r] = ds[r] = 0.0f;
-            }
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const bf16x8_t pf = to_frag(pr_, cc), sf = to_frag(ds, cc);
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
-                    dvacc[dt] = mfma32(frag_t(t.doutt, dt * 32 + c32, cc, h), pf, dvacc[dt]);
-                    dkacc[dt] = mfma32(frag_t(t.qt, dt * 32 + c32, cc, h), sf, dkacc[dt]);
+                for (int r = 0; r < 4; r += 2) {
+                    const int e = 4 * rb + r;
+                    score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[rb][r], sacc[rb][r + 1], pacc[rb][r],
+                                                   pacc[rb][r + 1], lse[e], lse[e + 1], del[e], del[e + 1],
+                                                   poly_key, poly_key, pr_[e], pr_[e + 1], ds[e], ds[e + 1]);
                 }
+            if (p.causal && q0 < key0 + 15) {
+                const int diag = (int)(key - q0) - 4 * g;  // masked when diag > 16 rb + r
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (diag > 16 * (e >> 2) + (e & 3)) pr_[e] = ds[e] = 0.0f;
+            }
+            bf16x8_t pf, sf;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                pf[e] = (__bf16)pr_[e];
+                sf[e] = (__bf16)ds[e];
+            }
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                dvacc[dt] = mfma16(frag_t16(t.doutt, dt * 16 + kl, g), pf, dvacc[dt]);
+                dkacc[dt] = mfma16(frag_t16(t.qt, dt * 16 + kl, g), sf, dkacc[dt]);
             }
         }
         if (more) store(buf ^ 1);
         __syncthreads();
     }
 
-    // dK^T / dV^T: register r of dt holds d = 32 dt + 8 (r/4) + 4h + r%4 of key c32
+    // dK^T / dV^T: register r of dt holds d = 16 dt + 4g + r of key kl
     if (p.dkv_ws != nullptr) {
         const int64_t plane = p.hq * p.seq * kHeadDim * (int64_t)gridDim.z;
         float* wk = p.dkv_ws + ((b * p.hq + head) * p.seq + key) * kHeadDim;
         float* wv = wk + plane;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d = dt * 32 + 8 * g + 4 * h;
-                *reinterpret_cast<f32x4_t*>(wk + d) = (f32x4_t){dkacc[dt][4 * g], dkacc[dt][4 * g + 1],
-                                                               dkacc[dt][4 * g + 2], dkacc[dt][4 * g + 3]};
-                *reinterpret_cast<f32x4_t*>(wv + d) = (f32x4_t){dvacc[dt][4 * g], dvacc[dt][4 * g + 1],
-                                                               dvacc[dt][4 * g + 2], dvacc[dt][4 * g + 3]};
-            }
+        for (int dt = 0; dt < 8; ++dt) {
+            const int d = dt * 16 + 4 * g;
+            *reinterpret_cast<f32x4_t*>(wk + d) = (f32x4_t){dkacc[dt][0], dkacc[dt][1], dkacc[dt][2], dkacc[dt][3]};
+            *reinterpret_cast<f32x4_t*>(wv + d) = (f32x4_t){dvacc[dt][0], dvacc[dt][1], dvacc[dt][2], dvacc[dt][3]};
+        }
         return;
     }
     uint16_t* dkr = p.dk + b * p.dks.b + kvh * p.dks.h + key * p.dks.s;
     uint16_t* dvr = p.dv + b * p.dvs.b + kvh * p.dvs.h + key * p.dvs.s;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d = dt * 32 + 8 * g + 4 * h;
-            const u32x2_t wk = {pack_bf(dkacc[dt][4 * g], dkacc[dt][4 * g + 1]),
-                                pack_bf(dkacc[dt][4 * g + 2], dkacc[dt][4 * g + 3])};
-            const u32x2_t wv = {pack_bf(dvacc[dt][4 * g], dvacc[dt][4 * g + 1]),
-                                pack_bf(dvacc[dt][4 * g + 2], dvacc[dt][4 * g + 3])};
-            *reinterpret_cast<u32x2_t*>(dkr + d) = wk;
-            *reinterpret_cast<u32x2_t*>(dvr + d) = wv;
-        }
+    for (int dt = 0; dt < 8; ++dt) {
+        const int d = dt * 16 + 4 * g;
+        *reinterpret_cast<u32x2_t*>(dkr + d) = (u32x2_t){pack_bf(dkacc[dt][0], dkacc[dt][1]),
+                                                         pack_bf(dkacc[dt][2], dkacc[dt][3])};
+        *reinterpret_cast<u32x2_t*>(dvr + d) = (u32x2_t){pack_bf(dvacc[dt][0], dvacc[dt][1]),
+                                                         pack_bf(dvacc[dt][2], dvacc[dt][3])};
+    }
 }
 
 // dK, dV of grouped heads: the sum over the group's query heads of the FP32
@@ -574,7 +591,7 @@ namespace {
 template <int MODE, int GRAD, int ROUTE>
 void launch_bwd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
     const dim3 grid((unsigned)prm.hq, (unsigned)(prm.seq / 128), (unsigned)batch);
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE>), grid, dim3(256), 0, st, prm);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE>), grid, dim3(512), 0, st, prm);
     if (prm.dkv_ws != nullptr) {
         const int64_t n = batch * prm.hkv * prm.seq * (kHeadDim / 8);
         hipLaunchKernelGGL(attn_dkv_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
