@@ -131,38 +131,30 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr bool kPlain = attn_is_plain_softmax(MODE);
     // ---- S^T = K Q^T for two 32-key tiles ----
-    f32x16_t sacc[2];
+    // two independent accumulation chains, interleaved
+    f32x16_t sacc[2] = {(f32x16_t){}, (f32x16_t){}};
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-        sacc[kt] = (f32x16_t){};
+    for (int c = 0; c < 8; ++c)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int kt = 0; kt < 2; ++kt) {
             const bf16x8_t a =
                 *reinterpret_cast<const bf16x8_t*>(ks + (kt * 32 + c32) * kKStride + c * 16 + h * 8);
             sacc[kt] = mfma32(a, qf[c], sacc[kt]);
         }
-    }
     // accumulator register r of tile kt holds key k0 + kt*32 + 8*(r/4) + 4h + r%4;
     // diag = k0 + 4h - query, so the key is masked when diag + offset > 0
     auto masked = [&](int kt, int r) {
         return MASKED && diag + kt * 32 + 8 * (r >> 2) + (r & 3) > 0;
     };
-    float prob[2][16];
-    if constexpr (kSigmoid) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                float p0, p1;
-                sigmoid_prob2<MODE>(sacc[kt][r] * p.scale, sacc[kt][r + 1] * p.scale, p.sig_bias, p0, p1);
-                prob[kt][r] = masked(kt, r) ? 0.0f : p0;
-                prob[kt][r + 1] = masked(kt, r + 1) ? 0.0f : p1;
-            }
-    } else {
+    // probabilities are produced eight at a time right before the O^T MFMAs
+    // that consume them, so the exponentials of one group issue while the
+    // previous group's MFMAs run; max and sum use four independent chains
+    float x[2][16];
+    float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    [[maybe_unused]] const float sl = kPlain ? p.scale * kLog2e : 1.0f;
+    if constexpr (!kSigmoid) {
         // exponents: plain softmax keeps the raw dot products and folds the
         // scale into the exp2 argument; softcap modes transform first
-        float x[2][16];
-        const float sl = kPlain ? p.scale * kLog2e : 1.0f;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             if constexpr (kPlain) {
@@ -172,14 +164,15 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
                 softmax_exponents<MODE>(sacc[kt], p.scale, p.cap, inv_cap, x[kt]);
             }
         }
-        float mt = -__builtin_inff();
+        float mx[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 if (masked(kt, r)) x[kt][r] = -__builtin_inff();
-                mt = __builtin_fmaxf(mt, x[kt][r]);
+                mx[r & 3] = __builtin_fmaxf(mx[r & 3], x[kt][r]);
             }
+        float mt = __builtin_fmaxf(__builtin_fmaxf(mx[0], mx[1]), __builtin_fmaxf(mx[2], mx[3]));
         mt = __builtin_fmaxf(mt, __shfl_xor(mt, 32)) * sl;
         // lanes c and c + 32 hold the same query and take the same decision
         const bool move = mt > m + kRescaleThreshold;
@@ -191,26 +184,35 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
         }
-        float ls = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = softmax_exp2<MODE, ROUTE>(__builtin_fmaf(x[kt][r], sl, -m), kt * 16 + r);
-                // v_exp_f32(-inf) is 0; the polynomial programs clamp at -127
-                prob[kt][r] = (attn_has_exp2_program(MODE) && masked(kt, r)) ? 0.0f : e;
-                ls += prob[kt][r];
-            }
-        l += ls;
     }
-    // ---- O^T += V^T P^T ----
+    // ---- P, then O^T += V^T P^T, eight keys at a time ----
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
+            float pr[8];
+            if constexpr (kSigmoid) {
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const int r = 8 * cc + e;
+                    sigmoid_prob2<MODE>(sacc[kt][r] * p.scale, sacc[kt][r + 1] * p.scale, p.sig_bias, pr[e],
+                                        pr[e + 1]);
+                    pr[e] = masked(kt, r) ? 0.0f : pr[e];
+                    pr[e + 1] = masked(kt, r + 1) ? 0.0f : pr[e + 1];
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int r = 8 * cc + e;
+                    const float ev = softmax_exp2<MODE, ROUTE>(__builtin_fmaf(x[kt][r], sl, -m), kt * 16 + r);
+                    // v_exp_f32(-inf) is 0; the polynomial programs clamp at -127
+                    pr[e] = (attn_has_exp2_program(MODE) && masked(kt, r)) ? 0.0f : ev;
+                    ls[e & 3] += pr[e];
+                }
+            }
             bf16x8_t pf;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) pf[e] = (__bf16)prob[kt][8 * cc + e];
+            for (int e = 0; e < 8; ++e) pf[e] = (__bf16)pr[e];
             const int kbase = kt * 32 + cc * 16 + 4 * h;
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
@@ -221,6 +223,7 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
                 oacc[dt] = mfma32(__builtin_bit_cast(bf16x8_t, w), pf, oacc[dt]);
             }
         }
+    if constexpr (!kSigmoid) l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 }
 
 // Grid (q_heads, S / 128, batch): blockIdx.y runs over query blocks, heaviest

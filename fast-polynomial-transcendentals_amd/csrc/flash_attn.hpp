@@ -42,7 +42,9 @@ constexpr int kHeadDim = 128;
 constexpr int kAttnBlockQ = 128;  // 4 waves x 32 queries
 constexpr int kAttnBlockK = 64;   // keys per staged tile
 constexpr int kKStride = kHeadDim + 8;    // BF16 elements per LDS K row
-constexpr int kVStride = kAttnBlockK + 8;  // BF16 elements per LDS V^T row
+// BF16 elements per LDS V^T row: 34 words, so the 8-byte fragment reads of
+// 32 consecutive rows fall on distinct banks
+constexpr int kVStride = kAttnBlockK + 4;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kLn2 = 0.69314718055994530942f;
 

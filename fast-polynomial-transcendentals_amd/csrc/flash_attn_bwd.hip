@@ -194,13 +194,22 @@ __device__ __forceinline__ void store_rows(uint16_t* rows, int pr, int dc, const
     *reinterpret_cast<u32x4_t*>(rows + (2 * pr + 1) * kRowStride + dc * 8) = b;
 }
 
+// Transposed tiles [128][36] are swizzled: column group c (4 BF16 elements,
+// 8 bytes) of row d lives at group c ^ ((d >> 4) & 7).  The staging stores
+// of one instruction then cover all 32 banks (without it, 16 threads with
+// rows 8 apart share 4 banks), and fragment reads keep 8-byte groups whole.
+__device__ __forceinline__ int tcol(int row, int col) {
+    return ((((col >> 2) ^ (row >> 4)) & 7) << 2) | (col & 3);
+}
+
 __device__ __forceinline__ void store_transposed(uint16_t* t, int pr, int dc, const u32x4_t& a, const u32x4_t& b) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         // (row 2pr, row 2pr+1) of columns d = 8 dc + 2j and 8 dc + 2j + 1
-        *reinterpret_cast<uint32_t*>(t + (dc * 8 + 2 * j) * kTStride + 2 * pr) =
+        const int d = dc * 8 + 2 * j;
+        *reinterpret_cast<uint32_t*>(t + d * kTStride + tcol(d, 2 * pr)) =
             __builtin_amdgcn_perm(b[j], a[j], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(t + (dc * 8 + 2 * j + 1) * kTStride + 2 * pr) =
+        *reinterpret_cast<uint32_t*>(t + (d + 1) * kTStride + tcol(d + 1, 2 * pr)) =
             __builtin_amdgcn_perm(b[j], a[j], 0x07060302u);
     }
 }
@@ -208,9 +217,9 @@ __device__ __forceinline__ void store_transposed(uint16_t* t, int pr, int dc, co
 // A fragment of a transposed tile: row `row`, the eight k slots of lane half
 // h in accumulator order (columns 16 cc + 4h .. +3 and 16 cc + 8 + 4h .. +3).
 __device__ __forceinline__ bf16x8_t frag_t(const uint16_t* t, int row, int cc, int h) {
-    const uint16_t* r = t + row * kTStride + 16 * cc + 4 * h;
-    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r);
-    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + 8);
+    const uint16_t* r = t + row * kTStride;
+    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r + tcol(row, 16 * cc + 4 * h));
+    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + tcol(row, 16 * cc + 8 + 4 * h));
     const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
     return __builtin_bit_cast(bf16x8_t, w);
 }
@@ -244,9 +253,9 @@ __device__ __forceinline__ f32x4v_t mfma16(bf16x8_t a, bf16x8_t b, f32x4v_t c) {
 // A fragment (16x16x32) of a transposed tile: row `row`, the eight k slots
 // of lane group g in accumulator order (columns 4g .. 4g+3 and 16+4g .. +3).
 __device__ __forceinline__ bf16x8_t frag_t16(const uint16_t* t, int row, int g) {
-    const uint16_t* r = t + row * kTStride + 4 * g;
-    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r);
-    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + 16);
+    const uint16_t* r = t + row * kTStride;
+    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r + tcol(row, 4 * g));
+    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + tcol(row, 16 + 4 * g));
     const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
     return __builtin_bit_cast(bf16x8_t, w);
 }
