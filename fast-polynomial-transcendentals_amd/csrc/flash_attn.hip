@@ -132,7 +132,10 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
     constexpr bool kPlain = attn_is_plain_softmax(MODE);
     // ---- S^T = K Q^T for two 32-key tiles ----
     // two independent accumulation chains, interleaved
+    // (raised wave priority while this wave only issues MFMA: the other wave
+    // of the SIMD keeps the VALU busy meanwhile)
     f32x16_t sacc[2] = {(f32x16_t){}, (f32x16_t){}};
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int c = 0; c < 8; ++c)
 #pragma unroll
@@ -141,6 +144,7 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
                 *reinterpret_cast<const bf16x8_t*>(ks + (kt * 32 + c32) * kKStride + c * 16 + h * 8);
             sacc[kt] = mfma32(a, qf[c], sacc[kt]);
         }
+    __builtin_amdgcn_s_setprio(0);
     // accumulator register r of tile kt holds key k0 + kt*32 + 8*(r/4) + 4h + r%4;
     // diag = k0 + 4h - query, so the key is masked when diag + offset > 0
     auto masked = [&](int kt, int r) {
