@@ -60,6 +60,10 @@ def parse():
                         "component shape launched 3 times")
     p.add_argument("--attention-only", action="store_true",
                    help="time only the attention forward rows")
+    p.add_argument("--open-weights", action="store_true",
+                   help="model-level rows: prefill of randomly initialised Transformers models "
+                        "(Llama-3-8B dims, GLM-4 MoE-lite dims, Gemma2 with head_dim 128; 2 layers) "
+                        "unpatched and patched with each sfu_repro.open_weights family")
     p.add_argument("--pmc-sweep", action="store_true",
                    help="issue-rate counter pass: 3 eager launches of each polynomial, "
                         "native and copy kernel of the sweep at 2^20, 2^22 and 2^24 "
@@ -377,6 +381,49 @@ def attention_rows(lib, reps: int, eager_launches: int = 0):
     return rows
 
 
+def open_weights_rows(seq_len: int = 2048, steps: int = 5):
+    """Prefill (one forward of `seq_len` tokens, batch 1, BF16) of randomly
+    initialised 2-layer models at the dims of the reference's open-weight
+    models, unpatched ("native") and with each patch family of
+    sfu_repro.open_weights (scripts/benchmark_open_weights.py's protocol:
+    CUDA events around model(...), mean of `steps` after 2 warm-ups).
+    Gemma2 "native" is the eager attention; the fused-attention variants
+    replace it with the fused kernel, so they also change the attention
+    algorithm (noted in the row)."""
+    import torch
+
+    from sfu_repro import open_weights as ow
+
+    dev = torch.device("cuda:0")
+    cases = [
+        ("llama3-8b-2l", None, ["native", "spline_silu_d3_current", "fused_swiglu_d3_current"]),
+        ("glm4-moe-lite-2l", "batched_mm",
+         ["native", "fused_swiglu_d3_current", "spline_router_sigmoid_d3_current"]),
+        ("gemma2-d128-2l", None, ["native", "gemma_tanh_current", "gemma_fa4_tanh_native",
+                                  "gemma_fa4_tanh_d4_current"]),
+    ]
+    rows = []
+    for preset, experts, variants in cases:
+        model = ow.build_model(preset, dtype=torch.bfloat16, device=dev, experts_implementation=experts)
+        slots = ow.collect_slots(model)
+        tokens = ow.make_tokens(batch_size=1, seq_len=seq_len,
+                                vocab_size=int(model.get_input_embeddings().num_embeddings), device=dev, seed=0)
+        row = {"model": preset, "config": f"batch 1, {seq_len} tokens, BF16, random weights, 2 layers"}
+        for variant in variants:
+            res = ow.run_variant(model, slots, ow.parse_variant(variant), tokens, model_id=preset, mode="prefill",
+                                 warmup=2, steps=steps, decode_steps=0, seed=0)
+            row[f"{variant}_ms"] = round(res.prefill_ms, 3)
+            row[f"{variant}_tokens_s"] = round(res.prefill_tokens_per_s, 1)
+        ow.restore_gemma_attention()
+        base = row["native_ms"]
+        for variant in variants[1:]:
+            row[f"{variant}_speedup"] = round(base / row[f"{variant}_ms"], 3)
+        rows.append(row)
+        del model, slots
+        torch.cuda.empty_cache()
+    return rows
+
+
 PROBE_ITERS = 32
 
 
@@ -687,6 +734,9 @@ def main():
         return
     if args.attention_only:
         print(json.dumps({"functions": attention_rows(lib, args.sweep_reps)}), flush=True)
+        return
+    if args.open_weights:
+        print(json.dumps({"models": open_weights_rows()}), flush=True)
         return
 
     # Synthetic B1 gate activations [8192, 14336] ~ N(0, 2^2), FP16, in HBM.
