@@ -288,13 +288,22 @@ def sweep(lib, reps: int):
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-ATTN_SHAPE = (1, 32, 8, 4096, 128)  # B, Hq, Hkv, S, D
+# B, Hq, Hkv, S, D: the reference's component shape, and its Llama 1B
+# training model's attention (head_dim 64)
+ATTN_SHAPES = ((1, 32, 8, 4096, 128), (1, 32, 8, 4096, 64))
 
 
 def attention_rows(lib, reps: int, eager_launches: int = 0):
+    rows = []
+    for shape in ATTN_SHAPES:
+        rows.extend(attention_rows_at(lib, reps, shape, eager_launches))
+    return rows
+
+
+def attention_rows_at(lib, reps: int, shape, eager_launches: int = 0):
     """The attention programs inside the fused forward and backward at the
     reference's component shape (causal GQA, B=1, S=4096, Hq=32, Hkv=8,
-    D=128): B5 softmax with the D2 / D3 exp2 (every exponent, and the B5
+    D=128; and D=64, its Llama 1B training model's head size): B5 softmax with the D2 / D3 exp2 (every exponent, and the B5
     schedule: four of every 12 forward, 32 backward) against hardware exp2,
     B2 softcap 30 with the D4 tanh (analytical backward) against hardware
     tanh, B3 sigmoid attention with the direct D3 / D4 programs against
@@ -310,7 +319,7 @@ def attention_rows(lib, reps: int, eager_launches: int = 0):
     import torch
 
     dev = torch.device("cuda:0")
-    b, hq, hkv, s, d = ATTN_SHAPE
+    b, hq, hkv, s, d = shape
     g = torch.Generator(device=dev).manual_seed(30)
     q = torch.randn(b, hq, s, d, device=dev, generator=g).bfloat16()
     k = torch.randn(b, hkv, s, d, device=dev, generator=g).bfloat16()

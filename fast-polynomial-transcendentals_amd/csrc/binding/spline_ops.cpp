@@ -662,13 +662,14 @@ std::vector<at::Tensor> flash_attn_fwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     TORCH_CHECK(k.sizes() == v.sizes(), "k and v must have the same shape");
     TORCH_CHECK(q.size(0) == k.size(0) && q.size(1) == k.size(1) && q.size(3) == k.size(3),
                 "q, k and v must agree in batch, seqlen and head_dim");
-    TORCH_CHECK(q.size(3) == 128, "head_dim must be 128, got ", q.size(3));
+    TORCH_CHECK(q.size(3) == 64 || q.size(3) == 128, "head_dim must be 64 or 128, got ", q.size(3));
     TORCH_CHECK(q.size(2) % k.size(2) == 0, "q heads (", q.size(2),
                 ") must be a multiple of kv heads (", k.size(2), ")");
     TORCH_CHECK(q.size(1) % 128 == 0, "seqlen must be a multiple of 128, got ", q.size(1));
     c10::OptionalDeviceGuard guard(q.device());
     const int64_t b = q.size(0), sq = q.size(1), hq = q.size(2), hkv = k.size(2);
-    at::Tensor out = at::empty({b, sq, hq, 128}, q.options());
+    const int64_t d = q.size(3);
+    at::Tensor out = at::empty({b, sq, hq, d}, q.options());
     at::Tensor lse = at::zeros({b, hq, sq}, q.options().dtype(at::kFloat));
     const int64_t strides[12] = {q.stride(0), q.stride(2), q.stride(1), k.stride(0), k.stride(2),
                                  k.stride(1), v.stride(0), v.stride(2), v.stride(1), out.stride(0),
@@ -676,7 +677,7 @@ std::vector<at::Tensor> flash_attn_fwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     void* s = current_stream(q);
     check_launch(launch_flash_attention_fwd_strided_bf16(
                      out.data_ptr(), lse.data_ptr<float>(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                     b, hq, hkv, sq, 128, strides, (int)mode, (int)exp2_route, causal ? 1 : 0,
+                     b, hq, hkv, sq, d, strides, (int)mode, (int)exp2_route, causal ? 1 : 0,
                      (float)softmax_scale, (float)softcap, (float)sigmoid_bias, s),
                  s);
     return {out, lse};
@@ -695,7 +696,7 @@ std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     TORCH_CHECK(out.sizes() == q.sizes() && dout.sizes() == q.sizes(), "out and dout must have q's shape");
     TORCH_CHECK(q.size(0) == k.size(0) && q.size(1) == k.size(1) && q.size(3) == k.size(3),
                 "q, k and v must agree in batch, seqlen and head_dim");
-    TORCH_CHECK(q.size(3) == 128, "head_dim must be 128, got ", q.size(3));
+    TORCH_CHECK(q.size(3) == 64 || q.size(3) == 128, "head_dim must be 64 or 128, got ", q.size(3));
     TORCH_CHECK(q.size(2) % k.size(2) == 0, "q heads must be a multiple of kv heads");
     TORCH_CHECK(q.size(1) % 128 == 0, "seqlen must be a multiple of 128, got ", q.size(1));
     const int64_t b = q.size(0), sq = q.size(1), hq = q.size(2), hkv = k.size(2);
@@ -703,11 +704,12 @@ std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tens
                     lse.dim() == 3 && lse.size(0) == b && lse.size(1) == hq && lse.size(2) == sq,
                 "lse must be a contiguous float32 CUDA tensor [batch, heads, seqlen]");
     c10::OptionalDeviceGuard guard(q.device());
-    at::Tensor dq = at::empty({b, sq, hq, 128}, q.options());
-    at::Tensor dk = at::empty({b, sq, hkv, 128}, q.options());
-    at::Tensor dv = at::empty({b, sq, hkv, 128}, q.options());
+    const int64_t d = q.size(3);
+    at::Tensor dq = at::empty({b, sq, hq, d}, q.options());
+    at::Tensor dk = at::empty({b, sq, hkv, d}, q.options());
+    at::Tensor dv = at::empty({b, sq, hkv, d}, q.options());
     at::Tensor delta = at::empty({b, hq, sq}, q.options().dtype(at::kFloat));
-    at::Tensor dkv_ws = hq != hkv ? at::empty({2, b, hq, sq, 128}, q.options().dtype(at::kFloat))
+    at::Tensor dkv_ws = hq != hkv ? at::empty({2, b, hq, sq, d}, q.options().dtype(at::kFloat))
                                   : at::Tensor();
     const int64_t strides[24] = {q.stride(0),    q.stride(2),    q.stride(1),    k.stride(0),
                                  k.stride(2),    k.stride(1),    v.stride(0),    v.stride(2),
@@ -719,7 +721,7 @@ std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     check_launch(launch_flash_attention_bwd_strided_bf16(
                      dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr<float>(),
                      hq != hkv ? dkv_ws.data_ptr<float>() : nullptr, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
-                     lse.data_ptr<float>(), b, hq, hkv, sq, 128, strides, (int)mode, (int)grad,
+                     lse.data_ptr<float>(), b, hq, hkv, sq, d, strides, (int)mode, (int)grad,
                      (int)exp2_route, causal ? 1 : 0, (float)softmax_scale, (float)softcap,
                      (float)sigmoid_bias, s),
                  s);

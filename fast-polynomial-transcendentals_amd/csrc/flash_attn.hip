@@ -123,11 +123,12 @@ constexpr float kRescaleThreshold = 8.0f;
 // One 64-key tile for one wave: S^T = K Q^T, the score program, the online
 // softmax (or sigmoid) and O^T += V^T P^T.  MASKED: the tile crosses the
 // causal diagonal of this wave's 32 queries.
-template <int MODE, int ROUTE, bool MASKED>
+template <int MODE, int ROUTE, bool MASKED, int HD>
 __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t* __restrict__ ks,
-                                            const uint16_t* __restrict__ vt, const bf16x8_t (&qf)[8],
-                                            f32x16_t (&oacc)[4], float& m, float& l, int diag,
+                                            const uint16_t* __restrict__ vt, const bf16x8_t (&qf)[HD / 16],
+                                            f32x16_t (&oacc)[HD / 32], float& m, float& l, int diag,
                                             int h, int c32, float inv_cap) {
+    constexpr int kKStr = HD + 8;  // BF16 elements per LDS K row
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr bool kPlain = attn_is_plain_softmax(MODE);
     // ---- S^T = K Q^T for two 32-key tiles ----
@@ -137,11 +138,11 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
     f32x16_t sacc[2] = {(f32x16_t){}, (f32x16_t){}};
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < HD / 16; ++c)
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const bf16x8_t a =
-                *reinterpret_cast<const bf16x8_t*>(ks + (kt * 32 + c32) * kKStride + c * 16 + h * 8);
+                *reinterpret_cast<const bf16x8_t*>(ks + (kt * 32 + c32) * kKStr + c * 16 + h * 8);
             sacc[kt] = mfma32(a, qf[c], sacc[kt]);
         }
     __builtin_amdgcn_s_setprio(0);
@@ -186,7 +187,7 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
             m = m_use;
             l *= alpha;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+            for (int dt = 0; dt < HD / 32; ++dt) oacc[dt] *= alpha;
         }
     }
     // ---- P, then O^T += V^T P^T, eight keys at a time ----
@@ -219,7 +220,7 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
             for (int e = 0; e < 8; ++e) pf[e] = (__bf16)pr[e];
             const int kbase = kt * 32 + cc * 16 + 4 * h;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
+            for (int dt = 0; dt < HD / 32; ++dt) {
                 const uint16_t* row = vt + (dt * 32 + c32) * kVStride + kbase;
                 const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
                 const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 8);
@@ -233,12 +234,13 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
 // Grid (q_heads, S / 128, batch): blockIdx.y runs over query blocks, heaviest
 // first under the causal mask, and the head index varies fastest, so the
 // first wave of resident blocks takes the longest query blocks of every head.
-template <int MODE, int ROUTE>
+template <int MODE, int ROUTE, int HD>
 __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
+    constexpr int kKStr = HD + 8;
     // two buffers: the next tile is written while the current one is read
-    __shared__ __align__(16) uint16_t ks[2][kAttnBlockK * kKStride];
-    __shared__ __align__(16) uint16_t vt[2][kHeadDim * kVStride];
+    __shared__ __align__(16) uint16_t ks[2][kAttnBlockK * kKStr];
+    __shared__ __align__(16) uint16_t vt[2][HD * kVStride];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -254,38 +256,42 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     const int64_t q0 = qb * kAttnBlockQ + wave * 32;  // first query of this wave
     const int64_t qrow = q0 + c32;                     // this lane's query
 
-    bf16x8_t qf[8];
+    bf16x8_t qf[HD / 16];
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < HD / 16; ++c)
         qf[c] = *reinterpret_cast<const bf16x8_t*>(qp + qrow * p.qs.s + c * 16 + h * 8);
 
-    f32x16_t oacc[4];
+    f32x16_t oacc[HD / 32];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) oacc[dt] = (f32x16_t){};
+    for (int dt = 0; dt < HD / 32; ++dt) oacc[dt] = (f32x16_t){};
     float m = -__builtin_inff(), l = 0.0f;
     const float inv_cap = 1.0f / p.cap;
 
-    // staging: K rows krow + 16 j (16 bytes at kcol); V rows vkey, vkey + 1
-    // (16 bytes at vd + 64 r), transposed into V^T while written to LDS
-    const int krow = tid >> 4, kcol = (tid & 15) * 8;
+    // staging: K rows krow + kRowsPass j (16 bytes at kcol); V rows vkey,
+    // vkey + 1 (16 bytes at vd + 64 r), transposed into V^T while written
+    constexpr int kChunks = HD / 8;                   // 16-byte chunks per row
+    constexpr int kRowsPass = 256 / kChunks;          // K rows per pass
+    constexpr int kKPasses = kAttnBlockK / kRowsPass;
+    constexpr int kVPasses = HD / 64;
+    const int krow = tid / kChunks, kcol = (tid % kChunks) * 8;
     const int vkey = 2 * (tid & 31), vd = (tid >> 5) * 8;
-    u32x4_t kr[4], va[2], vc[2];
+    u32x4_t kr[kKPasses], va[kVPasses], vc[kVPasses];
     auto load = [&](int64_t k0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (k0 + krow + 16 * j) * kss + kcol);
+        for (int j = 0; j < kKPasses; ++j)
+            kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (k0 + krow + kRowsPass * j) * kss + kcol);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < kVPasses; ++r) {
             va[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey) * vss + vd + 64 * r);
             vc[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey + 1) * vss + vd + 64 * r);
         }
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<u32x4_t*>(&ks[buf][(krow + 16 * j) * kKStride + kcol]) = kr[j];
+        for (int j = 0; j < kKPasses; ++j)
+            *reinterpret_cast<u32x4_t*>(&ks[buf][(krow + kRowsPass * j) * kKStr + kcol]) = kr[j];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < kVPasses; ++r) {
             const int d0 = vd + 64 * r;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -310,9 +316,9 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
         if (!p.causal || k0 <= q0 + 31) {  // wave-uniform: some key of the tile is visible
             const int diag = (int)(k0 - qrow) + 4 * h;
             if (p.causal && k0 + kAttnBlockK - 1 > q0)
-                attend_tile<MODE, ROUTE, true>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
+                attend_tile<MODE, ROUTE, true, HD>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
             else
-                attend_tile<MODE, ROUTE, false>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
+                attend_tile<MODE, ROUTE, false, HD>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
         }
         if (more) store(buf ^ 1);
         __syncthreads();
@@ -330,7 +336,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     }
     uint16_t* orow = p.o + b * p.os.b + head * p.os.h + qrow * p.os.s;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d = dt * 32 + 8 * g + 4 * h;
@@ -355,22 +361,23 @@ bool route_supported(int route) {
 }
 
 template <int MODE, int ROUTE>
-void launch_fwd(const AttnParams& prm, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE>), grid, dim3(256), 0, st, prm);
+void launch_fwd(const AttnParams& prm, dim3 grid, hipStream_t st, int hd) {
+    if (hd == 64) hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 64>), grid, dim3(256), 0, st, prm);
+    else hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 128>), grid, dim3(256), 0, st, prm);
 }
 
 template <int MODE>
-void launch_routed(const AttnParams& prm, dim3 grid, hipStream_t st, int route) {
+void launch_routed(const AttnParams& prm, dim3 grid, hipStream_t st, int route, int hd) {
     switch (route) {
-        case 6: launch_fwd<MODE, 6>(prm, grid, st); break;
-        case 8: launch_fwd<MODE, 8>(prm, grid, st); break;
-        case 10: launch_fwd<MODE, 10>(prm, grid, st); break;
-        case 12: launch_fwd<MODE, 12>(prm, grid, st); break;
-        case 16: launch_fwd<MODE, 16>(prm, grid, st); break;
-        case 20: launch_fwd<MODE, 20>(prm, grid, st); break;
-        case 24: launch_fwd<MODE, 24>(prm, grid, st); break;
-        case 32: launch_fwd<MODE, 32>(prm, grid, st); break;
-        default: launch_fwd<MODE, 4>(prm, grid, st); break;
+        case 6: launch_fwd<MODE, 6>(prm, grid, st, hd); break;
+        case 8: launch_fwd<MODE, 8>(prm, grid, st, hd); break;
+        case 10: launch_fwd<MODE, 10>(prm, grid, st, hd); break;
+        case 12: launch_fwd<MODE, 12>(prm, grid, st, hd); break;
+        case 16: launch_fwd<MODE, 16>(prm, grid, st, hd); break;
+        case 20: launch_fwd<MODE, 20>(prm, grid, st, hd); break;
+        case 24: launch_fwd<MODE, 24>(prm, grid, st, hd); break;
+        case 32: launch_fwd<MODE, 32>(prm, grid, st, hd); break;
+        default: launch_fwd<MODE, 4>(prm, grid, st, hd); break;
     }
 }
 
@@ -385,13 +392,14 @@ extern "C" int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, co
                                                        int mode, int exp2_route, int causal,
                                                        float scale, float cap, float sigmoid_bias,
                                                        void* stream) {
-    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || head_dim != kHeadDim || !strides)
+    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || (head_dim != 64 && head_dim != 128) || !strides)
         return hipErrorInvalidValue;
     if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
         return hipErrorInvalidValue;
     if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f))
         return hipErrorInvalidValue;
     if (attn_has_exp2_program(mode) && !route_supported(exp2_route)) return hipErrorInvalidValue;
+    const int hd = (int)head_dim;
     // the B3 programs are fitted for n = 4096 (src/sfu_repro/fa4.py:404-413;
     // autonumerics_zero/evolution/fit_flash_sigmoid_exp2_d2.py)
     if ((mode == kAttnSigmoidB3 || mode == kAttnSigmoidB3D2) && seq != 4096) return hipErrorInvalidValue;
@@ -411,19 +419,19 @@ extern "C" int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, co
     const dim3 grid((unsigned)q_heads, (unsigned)(seq / kAttnBlockQ), (unsigned)batch);
     hipStream_t hst = hs(stream);
     switch (mode) {
-        case kAttnSoftmaxNative: launch_fwd<kAttnSoftmaxNative, 0>(prm, grid, hst); break;
-        case kAttnSoftmaxExp2D2: launch_routed<kAttnSoftmaxExp2D2>(prm, grid, hst, exp2_route); break;
-        case kAttnSoftmaxExp2D3: launch_routed<kAttnSoftmaxExp2D3>(prm, grid, hst, exp2_route); break;
-        case kAttnSoftmaxExp2Pwl2: launch_routed<kAttnSoftmaxExp2Pwl2>(prm, grid, hst, exp2_route); break;
-        case kAttnSoftcapNative: launch_fwd<kAttnSoftcapNative, 0>(prm, grid, hst); break;
-        case kAttnSoftcapD4: launch_fwd<kAttnSoftcapD4, 0>(prm, grid, hst); break;
-        case kAttnSigmoidNative: launch_fwd<kAttnSigmoidNative, 0>(prm, grid, hst); break;
-        case kAttnSigmoidB3: launch_fwd<kAttnSigmoidB3, 0>(prm, grid, hst); break;
-        case kAttnSigmoidB3D2: launch_fwd<kAttnSigmoidB3D2, 0>(prm, grid, hst); break;
-        case kAttnSigmoidD3: launch_fwd<kAttnSigmoidD3, 0>(prm, grid, hst); break;
-        case kAttnSigmoidD3 + 1: launch_fwd<kAttnSigmoidD3 + 1, 0>(prm, grid, hst); break;
-        case kAttnSigmoidD3 + 2: launch_fwd<kAttnSigmoidD3 + 2, 0>(prm, grid, hst); break;
-        case kAttnSigmoidD6: launch_fwd<kAttnSigmoidD6, 0>(prm, grid, hst); break;
+        case kAttnSoftmaxNative: launch_fwd<kAttnSoftmaxNative, 0>(prm, grid, hst, hd); break;
+        case kAttnSoftmaxExp2D2: launch_routed<kAttnSoftmaxExp2D2>(prm, grid, hst, exp2_route, hd); break;
+        case kAttnSoftmaxExp2D3: launch_routed<kAttnSoftmaxExp2D3>(prm, grid, hst, exp2_route, hd); break;
+        case kAttnSoftmaxExp2Pwl2: launch_routed<kAttnSoftmaxExp2Pwl2>(prm, grid, hst, exp2_route, hd); break;
+        case kAttnSoftcapNative: launch_fwd<kAttnSoftcapNative, 0>(prm, grid, hst, hd); break;
+        case kAttnSoftcapD4: launch_fwd<kAttnSoftcapD4, 0>(prm, grid, hst, hd); break;
+        case kAttnSigmoidNative: launch_fwd<kAttnSigmoidNative, 0>(prm, grid, hst, hd); break;
+        case kAttnSigmoidB3: launch_fwd<kAttnSigmoidB3, 0>(prm, grid, hst, hd); break;
+        case kAttnSigmoidB3D2: launch_fwd<kAttnSigmoidB3D2, 0>(prm, grid, hst, hd); break;
+        case kAttnSigmoidD3: launch_fwd<kAttnSigmoidD3, 0>(prm, grid, hst, hd); break;
+        case kAttnSigmoidD3 + 1: launch_fwd<kAttnSigmoidD3 + 1, 0>(prm, grid, hst, hd); break;
+        case kAttnSigmoidD3 + 2: launch_fwd<kAttnSigmoidD3 + 2, 0>(prm, grid, hst, hd); break;
+        case kAttnSigmoidD6: launch_fwd<kAttnSigmoidD6, 0>(prm, grid, hst, hd); break;
     }
     return hipGetLastError();
 }
@@ -434,9 +442,9 @@ extern "C" int launch_flash_attention_fwd_bf16(void* out, const void* q, const v
                                                int mode, int causal, float scale, float cap,
                                                void* stream) {
     if (mode < 0 || mode > kAttnSigmoidB3) return hipErrorInvalidValue;
-    const int64_t qh = seq * kHeadDim, kh = seq * kHeadDim;
-    const int64_t strides[12] = {q_heads * qh, qh, kHeadDim, kv_heads * kh, kh, kHeadDim,
-                                 kv_heads * kh, kh, kHeadDim, q_heads * qh, qh, kHeadDim};
+    const int64_t hs_ = seq * head_dim;  // [B, H, S, D] contiguous
+    const int64_t strides[12] = {q_heads * hs_, hs_, head_dim, kv_heads * hs_, hs_, head_dim,
+                                 kv_heads * hs_, hs_, head_dim, q_heads * hs_, hs_, head_dim};
     return launch_flash_attention_fwd_strided_bf16(out, nullptr, q, k, v, batch, q_heads, kv_heads,
                                                    seq, head_dim, strides, mode, 4, causal, scale,
                                                    cap, -__builtin_logf((float)seq), stream);

@@ -41,7 +41,6 @@ enum AttnGrad : int {
 };
 
 constexpr int kBwdTile = 32;              // queries (dK/dV) or keys (dQ) per staged tile
-constexpr int kRowStride = kHeadDim + 8;  // row-major tile rows in LDS (BF16 elements)
 constexpr int kTStride = kBwdTile + 4;    // transposed tile rows [128][36]
 constexpr int kRouteRuntime = -1;
 
@@ -157,16 +156,18 @@ __device__ __forceinline__ void score_grad2(const AttnBwdParams& p, float inv_ca
 }
 
 // ---------------------------------------------------------------------------
-// delta: D[b, h, s] = sum_d dO[b, s, h, d] * O[b, s, h, d]; 16 lanes per row
+// delta: D[b, h, s] = sum_d dO[b, s, h, d] * O[b, s, h, d]; HD / 8 lanes per row
 // ---------------------------------------------------------------------------
 
+template <int HD>
 __global__ void __launch_bounds__(256) attn_delta_kernel(const uint16_t* __restrict__ out,
                                                          const uint16_t* __restrict__ dout,
                                                          float* __restrict__ delta, AttnStrides os,
                                                          AttnStrides dos, int64_t hq, int64_t seq,
                                                          int64_t rows) {
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int c = threadIdx.x & 15;
+    constexpr int kLanes = HD / 8;
+    const int64_t row = (int64_t)blockIdx.x * (256 / kLanes) + (threadIdx.x / kLanes);
+    const int c = threadIdx.x % kLanes;
     float acc = 0.0f;
     if (row < rows) {
         const int64_t s = row % seq, bh = row / seq, h = bh % hq, b = bh / hq;
@@ -179,19 +180,23 @@ __global__ void __launch_bounds__(256) attn_delta_kernel(const uint16_t* __restr
         }
     }
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+    for (int m = kLanes / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
     if (row < rows && c == 0) delta[row] = acc;
 }
 
 // ---------------------------------------------------------------------------
 // staging of a 32-row tile: row-major copy and transposed copy.  Thread
-// (pair pr = tid / 16, chunk dc = tid % 16) holds rows 2 pr, 2 pr + 1,
-// BF16 elements 8 dc .. 8 dc + 7.
+// (pair pr, chunk dc) holds rows 2 pr, 2 pr + 1, BF16 elements
+// 8 dc .. 8 dc + 7; 16 x HD / 8 threads move a tile.
 // ---------------------------------------------------------------------------
 
+template <int HD>
+constexpr int row_stride() { return HD + 8; }  // BF16 elements per LDS row
+
+template <int HD>
 __device__ __forceinline__ void store_rows(uint16_t* rows, int pr, int dc, const u32x4_t& a, const u32x4_t& b) {
-    *reinterpret_cast<u32x4_t*>(rows + (2 * pr) * kRowStride + dc * 8) = a;
-    *reinterpret_cast<u32x4_t*>(rows + (2 * pr + 1) * kRowStride + dc * 8) = b;
+    *reinterpret_cast<u32x4_t*>(rows + (2 * pr) * row_stride<HD>() + dc * 8) = a;
+    *reinterpret_cast<u32x4_t*>(rows + (2 * pr + 1) * row_stride<HD>() + dc * 8) = b;
 }
 
 // Transposed tiles [128][36] are swizzled: column group c (4 BF16 elements,
@@ -235,11 +240,12 @@ __device__ __forceinline__ bf16x8_t to_frag(const float (&x)[16], int cc) {
 // dK / dV
 // ---------------------------------------------------------------------------
 
+template <int HD>
 struct BwdQTile {
-    uint16_t q[kBwdTile * kRowStride];
-    uint16_t qt[kHeadDim * kTStride];
-    uint16_t dout[kBwdTile * kRowStride];
-    uint16_t doutt[kHeadDim * kTStride];
+    uint16_t q[kBwdTile * row_stride<HD>()];
+    uint16_t qt[HD * kTStride];
+    uint16_t dout[kBwdTile * row_stride<HD>()];
+    uint16_t doutt[HD * kTStride];
     float lse2[kBwdTile];
     float delta[kBwdTile];
 };
@@ -269,17 +275,20 @@ __device__ __forceinline__ bf16x8_t frag_t16(const uint16_t* t, int row, int g) 
 //    k slot 8g + e <-> query 16 (e/4) + 4g + e%4, the accumulator order;
 //  * per wave: K, V fragments 32 VGPRs, dK^T / dV^T accumulators 64, so two
 //    waves share a SIMD.
-template <int MODE, int GRAD, int ROUTE>
+template <int MODE, int GRAD, int ROUTE, int HD>
 __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
-    __shared__ __align__(16) BwdQTile tiles[2];
+    constexpr int kRS = row_stride<HD>(), kChunks = HD / 8;
+    __shared__ __align__(16) BwdQTile<HD> tiles[2];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, kl = lane & 15;
-    // staging: threads 0..255 move Q, 256..511 dO (row pair pr, chunk dc)
+    // staging: threads 0..255 move Q, 256..511 dO (row pair pr, chunk dc);
+    // 16 x HD / 8 of each half are active
     const int half = tid >> 8, st = tid & 255;
-    const int pr = st >> 4, dc = st & 15;
+    const int pr = st / kChunks, dc = st % kChunks;
+    const bool stager = st < 16 * kChunks;
     // one block per (query head, 128-key block): grouped heads write FP32
     // partials that attn_dkv_reduce_kernel sums, so the causal work per block
     // stays within one head's query range
@@ -291,19 +300,19 @@ __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
     const float inv_cap = 1.0f / p.cap;
     const bool poly_key = ROUTE == kRouteRuntime && route_slot(key) % p.route < 4;
 
-    bf16x8_t kf[4], vf[4];
+    bf16x8_t kf[HD / 32], vf[HD / 32];
     {
         const uint16_t* kr = p.k + b * p.ks.b + kvh * p.ks.h + key * p.ks.s;
         const uint16_t* vr = p.v + b * p.vs.b + kvh * p.vs.h + key * p.vs.s;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < HD / 32; ++c) {
             kf[c] = *reinterpret_cast<const bf16x8_t*>(kr + c * 32 + g * 8);
             vf[c] = *reinterpret_cast<const bf16x8_t*>(vr + c * 32 + g * 8);
         }
     }
-    f32x4v_t dkacc[8], dvacc[8];
+    f32x4v_t dkacc[HD / 16], dvacc[HD / 16];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) dkacc[dt] = dvacc[dt] = (f32x4v_t){};
+    for (int dt = 0; dt < HD / 16; ++dt) dkacc[dt] = dvacc[dt] = (f32x4v_t){};
 
     // query tiles of this head, from the block's first key on under the
     // causal mask
@@ -316,9 +325,11 @@ __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
     float row_r = 0.0f;
     auto load = [&](int64_t it) {
         const int64_t q0 = (qt0 + it) * kBwdTile;
-        const uint16_t* r = src + (q0 + 2 * pr) * src_s + dc * 8;
-        ra = *reinterpret_cast<const u32x4_t*>(r);
-        rb2 = *reinterpret_cast<const u32x4_t*>(r + src_s);
+        if (stager) {
+            const uint16_t* r = src + (q0 + 2 * pr) * src_s + dc * 8;
+            ra = *reinterpret_cast<const u32x4_t*>(r);
+            rb2 = *reinterpret_cast<const u32x4_t*>(r + src_s);
+        }
         if constexpr (!kSigmoid) {
             if (st < kBwdTile) {
                 const int64_t i = (b * p.hq + head) * p.seq + q0 + st;
@@ -327,9 +338,11 @@ __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
         }
     };
     auto store = [&](int buf) {
-        BwdQTile& t = tiles[buf];
-        store_rows(half ? t.dout : t.q, pr, dc, ra, rb2);
-        store_transposed(half ? t.doutt : t.qt, pr, dc, ra, rb2);
+        BwdQTile<HD>& t = tiles[buf];
+        if (stager) {
+            store_rows<HD>(half ? t.dout : t.q, pr, dc, ra, rb2);
+            store_transposed(half ? t.doutt : t.qt, pr, dc, ra, rb2);
+        }
         if constexpr (!kSigmoid) {
             if (st < kBwdTile) (half ? t.delta : t.lse2)[st] = row_r;
         }
@@ -344,14 +357,14 @@ __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
         if (more) load(it + 1);
         const int64_t q0 = (qt0 + it) * kBwdTile;
         if (!p.causal || q0 + kBwdTile - 1 >= key0) {  // some query of the tile sees a key of the wave
-            const BwdQTile& t = tiles[buf];
+            const BwdQTile<HD>& t = tiles[buf];
             f32x4v_t sacc[2], pacc[2];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
                 sacc[rb] = pacc[rb] = (f32x4v_t){};
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int off = (16 * rb + kl) * kRowStride + 32 * c + 8 * g;
+                for (int c = 0; c < HD / 32; ++c) {
+                    const int off = (16 * rb + kl) * kRS + 32 * c + 8 * g;
                     sacc[rb] = mfma16(*reinterpret_cast<const bf16x8_t*>(t.q + off), kf[c], sacc[rb]);
                     pacc[rb] = mfma16(*reinterpret_cast<const bf16x8_t*>(t.dout + off), vf[c], pacc[rb]);
                 }
@@ -396,7 +409,7 @@ __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
                 sf[e] = (__bf16)ds[e];
             }
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
+            for (int dt = 0; dt < HD / 16; ++dt) {
                 dvacc[dt] = mfma16(frag_t16(t.doutt, dt * 16 + kl, g), pf, dvacc[dt]);
                 dkacc[dt] = mfma16(frag_t16(t.qt, dt * 16 + kl, g), sf, dkacc[dt]);
             }
@@ -407,11 +420,11 @@ __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
 
     // dK^T / dV^T: register r of dt holds d = 16 dt + 4g + r of key kl
     if (p.dkv_ws != nullptr) {
-        const int64_t plane = p.hq * p.seq * kHeadDim * (int64_t)gridDim.z;
-        float* wk = p.dkv_ws + ((b * p.hq + head) * p.seq + key) * kHeadDim;
+        const int64_t plane = p.hq * p.seq * HD * (int64_t)gridDim.z;
+        float* wk = p.dkv_ws + ((b * p.hq + head) * p.seq + key) * HD;
         float* wv = wk + plane;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
+        for (int dt = 0; dt < HD / 16; ++dt) {
             const int d = dt * 16 + 4 * g;
             *reinterpret_cast<f32x4_t*>(wk + d) = (f32x4_t){dkacc[dt][0], dkacc[dt][1], dkacc[dt][2], dkacc[dt][3]};
             *reinterpret_cast<f32x4_t*>(wv + d) = (f32x4_t){dvacc[dt][0], dvacc[dt][1], dvacc[dt][2], dvacc[dt][3]};
@@ -421,7 +434,7 @@ __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
     uint16_t* dkr = p.dk + b * p.dks.b + kvh * p.dks.h + key * p.dks.s;
     uint16_t* dvr = p.dv + b * p.dvs.b + kvh * p.dvs.h + key * p.dvs.s;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < HD / 16; ++dt) {
         const int d = dt * 16 + 4 * g;
         *reinterpret_cast<u32x2_t*>(dkr + d) = (u32x2_t){pack_bf(dkacc[dt][0], dkacc[dt][1]),
                                                          pack_bf(dkacc[dt][2], dkacc[dt][3])};
@@ -432,23 +445,24 @@ __global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
 
 // dK, dV of grouped heads: the sum over the group's query heads of the FP32
 // partials, rounded once to BF16.  Thread = 8 head-dim elements of one key.
+template <int HD>
 __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(const float* __restrict__ ws,
                                                               uint16_t* __restrict__ dk,
                                                               uint16_t* __restrict__ dv, AttnStrides dks,
                                                               AttnStrides dvs, int64_t batch, int64_t hq,
                                                               int64_t hkv, int64_t seq) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (b, kvh, key, chunk)
-    const int64_t total = batch * hkv * seq * (kHeadDim / 8);
+    const int64_t total = batch * hkv * seq * (HD / 8);
     if (i >= total) return;
-    const int c = (int)(i % (kHeadDim / 8));
-    const int64_t key = (i / (kHeadDim / 8)) % seq;
-    const int64_t bh = i / ((kHeadDim / 8) * seq);
+    const int c = (int)(i % (HD / 8));
+    const int64_t key = (i / (HD / 8)) % seq;
+    const int64_t bh = i / ((HD / 8) * seq);
     const int64_t kvh = bh % hkv, b = bh / hkv;
     const int64_t group = hq / hkv;
-    const int64_t plane = batch * hq * seq * kHeadDim;
+    const int64_t plane = batch * hq * seq * HD;
     f32x4_t k0 = {}, k1 = {}, v0 = {}, v1 = {};
     for (int64_t g = 0; g < group; ++g) {
-        const float* w = ws + ((b * hq + kvh * group + g) * seq + key) * kHeadDim + c * 8;
+        const float* w = ws + ((b * hq + kvh * group + g) * seq + key) * HD + c * 8;
         k0 += *reinterpret_cast<const f32x4_t*>(w);
         k1 += *reinterpret_cast<const f32x4_t*>(w + 4);
         v0 += *reinterpret_cast<const f32x4_t*>(w + plane);
@@ -464,21 +478,24 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(const float* __res
 // dQ
 // ---------------------------------------------------------------------------
 
+template <int HD>
 struct BwdKTile {
-    uint16_t k[kBwdTile * kRowStride];
-    uint16_t kt[kHeadDim * kTStride];
-    uint16_t v[kBwdTile * kRowStride];
+    uint16_t k[kBwdTile * row_stride<HD>()];
+    uint16_t kt[HD * kTStride];
+    uint16_t v[kBwdTile * row_stride<HD>()];
 };
 
-template <int MODE, int GRAD, int ROUTE>
+template <int MODE, int GRAD, int ROUTE, int HD>
 __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
-    __shared__ __align__(16) BwdKTile tiles[2];
+    constexpr int kRS = row_stride<HD>(), kChunks = HD / 8;
+    __shared__ __align__(16) BwdKTile<HD> tiles[2];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, c32 = lane & 31;
-    const int pr = tid >> 4, dc = tid & 15;
+    const int pr = tid / kChunks, dc = tid % kChunks;
+    const bool stager = tid < 16 * kChunks;
     const int64_t nqb = p.seq / kAttnBlockQ;
     const int64_t head = blockIdx.x, b = blockIdx.z;
     const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
@@ -487,12 +504,12 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
     const int64_t qrow = q0 + c32;
     const float inv_cap = 1.0f / p.cap;
 
-    bf16x8_t qf[8], df[8];
+    bf16x8_t qf[HD / 16], df[HD / 16];
     {
         const uint16_t* qr = p.q + b * p.qs.b + head * p.qs.h + qrow * p.qs.s;
         const uint16_t* dr = p.dout + b * p.dos.b + head * p.dos.h + qrow * p.dos.s;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < HD / 16; ++c) {
             qf[c] = *reinterpret_cast<const bf16x8_t*>(qr + c * 16 + h * 8);
             df[c] = *reinterpret_cast<const bf16x8_t*>(dr + c * 16 + h * 8);
         }
@@ -503,14 +520,15 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
         lse2 = p.lse[i] * kLog2e;
         dl = p.delta[i];
     }
-    f32x16_t dqacc[4];
+    f32x16_t dqacc[HD / 32];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) dqacc[dt] = (f32x16_t){};
+    for (int dt = 0; dt < HD / 32; ++dt) dqacc[dt] = (f32x16_t){};
 
     const uint16_t* kp = p.k + b * p.ks.b + kvh * p.ks.h;
     const uint16_t* vp = p.v + b * p.vs.b + kvh * p.vs.h;
     u32x4_t ka, kb2, va, vb;
     auto load = [&](int64_t k0) {
+        if (!stager) return;
         const uint16_t* kr = kp + (k0 + 2 * pr) * p.ks.s + dc * 8;
         const uint16_t* vr = vp + (k0 + 2 * pr) * p.vs.s + dc * 8;
         ka = *reinterpret_cast<const u32x4_t*>(kr);
@@ -519,10 +537,11 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
         vb = *reinterpret_cast<const u32x4_t*>(vr + p.vs.s);
     };
     auto store = [&](int buf) {
-        BwdKTile& t = tiles[buf];
-        store_rows(t.k, pr, dc, ka, kb2);
+        if (!stager) return;
+        BwdKTile<HD>& t = tiles[buf];
+        store_rows<HD>(t.k, pr, dc, ka, kb2);
         store_transposed(t.kt, pr, dc, ka, kb2);
-        store_rows(t.v, pr, dc, va, vb);
+        store_rows<HD>(t.v, pr, dc, va, vb);
     };
 
     const int64_t nkt = p.causal ? (qb + 1) * (kAttnBlockQ / kBwdTile) : p.seq / kBwdTile;
@@ -535,16 +554,16 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
         const bool more = kt + 1 < nkt;
         if (more) load(k0 + kBwdTile);
         if (!p.causal || k0 <= q0 + 31) {
-            const BwdKTile& t = tiles[buf];
+            const BwdKTile<HD>& t = tiles[buf];
             f32x16_t sacc = {}, pacc = {};
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const bf16x8_t ak = *reinterpret_cast<const bf16x8_t*>(t.k + c32 * kRowStride + 16 * c + 8 * h);
+            for (int c = 0; c < HD / 16; ++c) {
+                const bf16x8_t ak = *reinterpret_cast<const bf16x8_t*>(t.k + c32 * kRS + 16 * c + 8 * h);
                 sacc = mfma32(ak, qf[c], sacc);
             }
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(t.v + c32 * kRowStride + 16 * c + 8 * h);
+            for (int c = 0; c < HD / 16; ++c) {
+                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(t.v + c32 * kRS + 16 * c + 8 * h);
                 pacc = mfma32(av, df[c], pacc);
             }
             // register r: key k0 + 8 (r/4) + 4h + r%4 of this lane's query
@@ -572,7 +591,8 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
             for (int cc = 0; cc < 2; ++cc) {
                 const bf16x8_t sf = to_frag(ds, cc);
 #pragma unroll
-                for (int dt = 0; dt < 4; ++dt) dqacc[dt] = mfma32(frag_t(t.kt, dt * 32 + c32, cc, h), sf, dqacc[dt]);
+                for (int dt = 0; dt < HD / 32; ++dt)
+                    dqacc[dt] = mfma32(frag_t(t.kt, dt * 32 + c32, cc, h), sf, dqacc[dt]);
             }
         }
         if (more) store(buf ^ 1);
@@ -581,7 +601,7 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
 
     uint16_t* dqr = p.dq + b * p.dqs.b + head * p.dqs.h + qrow * p.dqs.s;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d = dt * 32 + 8 * g + 4 * h;
@@ -597,24 +617,30 @@ using namespace pt;
 
 namespace {
 
-template <int MODE, int GRAD, int ROUTE>
-void launch_bwd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
+template <int MODE, int GRAD, int ROUTE, int HD>
+void launch_bwd_hd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
     const dim3 grid((unsigned)prm.hq, (unsigned)(prm.seq / 128), (unsigned)batch);
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE>), grid, dim3(512), 0, st, prm);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE, HD>), grid, dim3(512), 0, st, prm);
     if (prm.dkv_ws != nullptr) {
-        const int64_t n = batch * prm.hkv * prm.seq * (kHeadDim / 8);
-        hipLaunchKernelGGL(attn_dkv_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+        const int64_t n = batch * prm.hkv * prm.seq * (HD / 8);
+        hipLaunchKernelGGL((attn_dkv_reduce_kernel<HD>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                            (const float*)prm.dkv_ws, prm.dk, prm.dv, prm.dks, prm.dvs, batch, prm.hq,
                            prm.hkv, prm.seq);
     }
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE>), grid, dim3(256), 0, st, prm);
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD>), grid, dim3(256), 0, st, prm);
+}
+
+template <int MODE, int GRAD, int ROUTE>
+void launch_bwd(const AttnBwdParams& prm, int64_t batch, hipStream_t st, int hd) {
+    if (hd == 64) launch_bwd_hd<MODE, GRAD, ROUTE, 64>(prm, batch, st);
+    else launch_bwd_hd<MODE, GRAD, ROUTE, 128>(prm, batch, st);
 }
 
 template <int MODE>
-void launch_bwd_routed(const AttnBwdParams& prm, int64_t batch, hipStream_t st, int route) {
-    if (route == 0) launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, st);
-    else if (route == 4) launch_bwd<MODE, kGradNatural, 4>(prm, batch, st);
-    else launch_bwd<MODE, kGradNatural, kRouteRuntime>(prm, batch, st);
+void launch_bwd_routed(const AttnBwdParams& prm, int64_t batch, hipStream_t st, int route, int hd) {
+    if (route == 0) launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, st, hd);
+    else if (route == 4) launch_bwd<MODE, kGradNatural, 4>(prm, batch, st, hd);
+    else launch_bwd<MODE, kGradNatural, kRouteRuntime>(prm, batch, st, hd);
 }
 
 bool bwd_stride_ok(const AttnStrides& t) {
@@ -628,8 +654,9 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
     const void* out, const void* dout, const float* lse, int64_t batch, int64_t q_heads,
     int64_t kv_heads, int64_t seq, int64_t head_dim, const int64_t* strides, int mode, int grad,
     int exp2_route, int causal, float scale, float cap, float sigmoid_bias, void* stream) {
-    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || head_dim != kHeadDim || !strides)
+    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || (head_dim != 64 && head_dim != 128) || !strides)
         return hipErrorInvalidValue;
+    const int hd = (int)head_dim;
     if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
         return hipErrorInvalidValue;
     if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f)) return hipErrorInvalidValue;
@@ -662,13 +689,18 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
     if (grouped && (!dkv_workspace || (reinterpret_cast<uintptr_t>(dkv_workspace) & 15)))
         return hipErrorInvalidValue;
     // 2 * B * Hq * S * 128 floats must stay addressable
-    if (grouped && batch * q_heads * seq > (int64_t(1) << 52) / kHeadDim) return hipErrorInvalidValue;
+    if (grouped && batch * q_heads * seq > (int64_t(1) << 52) / head_dim) return hipErrorInvalidValue;
     hipStream_t hst = hs(stream);
     if (!sig) {
         const int64_t rows = batch * q_heads * seq;
-        hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, hst,
-                           (const uint16_t*)out, (const uint16_t*)dout, delta, st[3], st[4], q_heads,
-                           seq, rows);
+        if (hd == 64)
+            hipLaunchKernelGGL((attn_delta_kernel<64>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, hst,
+                               (const uint16_t*)out, (const uint16_t*)dout, delta, st[3], st[4], q_heads, seq,
+                               rows);
+        else
+            hipLaunchKernelGGL((attn_delta_kernel<128>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, hst,
+                               (const uint16_t*)out, (const uint16_t*)dout, delta, st[3], st[4], q_heads, seq,
+                               rows);
     }
     AttnBwdParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
                       sig ? nullptr : lse, sig ? nullptr : delta, (uint16_t*)dq, (uint16_t*)dk,
@@ -676,26 +708,26 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
                       seq, scale, cap > 0.0f ? cap : 1.0f, sigmoid_bias, exp2_route > 0 ? exp2_route : 4,
                       causal != 0};
     switch (mode) {
-        case kAttnSoftmaxNative: launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, hst); break;
-        case kAttnSoftmaxExp2D2: launch_bwd_routed<kAttnSoftmaxExp2D2>(prm, batch, hst, exp2_route); break;
-        case kAttnSoftmaxExp2D3: launch_bwd_routed<kAttnSoftmaxExp2D3>(prm, batch, hst, exp2_route); break;
-        case kAttnSoftmaxExp2Pwl2: launch_bwd_routed<kAttnSoftmaxExp2Pwl2>(prm, batch, hst, exp2_route); break;
-        case kAttnSoftcapNative: launch_bwd<kAttnSoftcapNative, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSoftmaxNative: launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, hst, hd); break;
+        case kAttnSoftmaxExp2D2: launch_bwd_routed<kAttnSoftmaxExp2D2>(prm, batch, hst, exp2_route, hd); break;
+        case kAttnSoftmaxExp2D3: launch_bwd_routed<kAttnSoftmaxExp2D3>(prm, batch, hst, exp2_route, hd); break;
+        case kAttnSoftmaxExp2Pwl2: launch_bwd_routed<kAttnSoftmaxExp2Pwl2>(prm, batch, hst, exp2_route, hd); break;
+        case kAttnSoftcapNative: launch_bwd<kAttnSoftcapNative, kGradNatural, 0>(prm, batch, hst, hd); break;
         case kAttnSoftcapD4:
-            if (grad == kGradAnalytical) launch_bwd<kAttnSoftcapD4, kGradAnalytical, 0>(prm, batch, hst);
-            else if (grad == kGradSte) launch_bwd<kAttnSoftcapD4, kGradSte, 0>(prm, batch, hst);
-            else launch_bwd<kAttnSoftcapD4, kGradExact1mt2, 0>(prm, batch, hst);
+            if (grad == kGradAnalytical) launch_bwd<kAttnSoftcapD4, kGradAnalytical, 0>(prm, batch, hst, hd);
+            else if (grad == kGradSte) launch_bwd<kAttnSoftcapD4, kGradSte, 0>(prm, batch, hst, hd);
+            else launch_bwd<kAttnSoftcapD4, kGradExact1mt2, 0>(prm, batch, hst, hd);
             break;
-        case kAttnSigmoidNative: launch_bwd<kAttnSigmoidNative, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSigmoidNative: launch_bwd<kAttnSigmoidNative, kGradNatural, 0>(prm, batch, hst, hd); break;
         case kAttnSigmoidB3:
-            if (grad == kGradDirect) launch_bwd<kAttnSigmoidB3, kGradDirect, 0>(prm, batch, hst);
-            else launch_bwd<kAttnSigmoidB3, kGradAlgebraic, 0>(prm, batch, hst);
+            if (grad == kGradDirect) launch_bwd<kAttnSigmoidB3, kGradDirect, 0>(prm, batch, hst, hd);
+            else launch_bwd<kAttnSigmoidB3, kGradAlgebraic, 0>(prm, batch, hst, hd);
             break;
-        case kAttnSigmoidB3D2: launch_bwd<kAttnSigmoidB3D2, kGradNatural, 0>(prm, batch, hst); break;
-        case kAttnSigmoidD3: launch_bwd<kAttnSigmoidD3, kGradNatural, 0>(prm, batch, hst); break;
-        case kAttnSigmoidD3 + 1: launch_bwd<kAttnSigmoidD3 + 1, kGradNatural, 0>(prm, batch, hst); break;
-        case kAttnSigmoidD3 + 2: launch_bwd<kAttnSigmoidD3 + 2, kGradNatural, 0>(prm, batch, hst); break;
-        case kAttnSigmoidD6: launch_bwd<kAttnSigmoidD6, kGradNatural, 0>(prm, batch, hst); break;
+        case kAttnSigmoidB3D2: launch_bwd<kAttnSigmoidB3D2, kGradNatural, 0>(prm, batch, hst, hd); break;
+        case kAttnSigmoidD3: launch_bwd<kAttnSigmoidD3, kGradNatural, 0>(prm, batch, hst, hd); break;
+        case kAttnSigmoidD3 + 1: launch_bwd<kAttnSigmoidD3 + 1, kGradNatural, 0>(prm, batch, hst, hd); break;
+        case kAttnSigmoidD3 + 2: launch_bwd<kAttnSigmoidD3 + 2, kGradNatural, 0>(prm, batch, hst, hd); break;
+        case kAttnSigmoidD6: launch_bwd<kAttnSigmoidD6, kGradNatural, 0>(prm, batch, hst, hd); break;
     }
     return hipGetLastError();
 }

@@ -428,8 +428,8 @@ int launch_evaluate_reduced_sincos(void* sin_out, void* cos_out, const void* red
  * softcap, B3 sigmoid attention, B5 exp2) run inside a FlashAttention-4 fork
  * that is not part of the reference tree (src/sfu_repro/fa4.py:454-752 selects
  * them; extras/paper/manuscript/main.tex:483-509 describes the fusion).
- * q [B, Hq, S, 128], k and v [B, Hkv, S, 128] -> out [B, Hq, S, 128], BF16;
- * Hq a multiple of Hkv (grouped-query), S a multiple of 128, head_dim 128,
+ * q [B, Hq, S, D], k and v [B, Hkv, S, D] -> out [B, Hq, S, D], BF16;
+ * Hq a multiple of Hkv (grouped-query), S a multiple of 128, head_dim D 64 or 128,
  * every pointer 16-byte aligned; s = q.k * scale.  mode:
  *   0 softmax, hardware exp2 (v_exp_f32)      1 softmax, B5 D2 "safe" exp2
  *   2 softmax, FA4 D3 exp2                     3 softcap cap*tanh(s/cap), FP32
@@ -446,8 +446,8 @@ int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k, con
 /* General form, the runtime behind the FA4 interface (the flash_attn_fwd that
  * src/sfu_repro/fa4.py:356-428 calls).  strides: 12 element strides, (batch,
  * head, sequence) of q, k, v and out in that order, each a multiple of 8; the
- * head dimension (128) is contiguous, so [B, S, H, 128] (FA4's layout) and
- * [B, H, S, 128] both work.  lse: null, or float [B, Hq, S] receiving
+ * head dimension D (64 or 128) is contiguous, so [B, S, H, D] (FA4's layout)
+ * and [B, H, S, D] both work.  lse: null, or float [B, Hq, S] receiving
  * ln sum_k exp(s'_k) (s' the scaled, capped score) for the softmax modes;
  * sigmoid modes leave it untouched.  Extra modes:
  *   7 sigmoid attention with the B3-D2 exp2 program (fitted for S = 4096)
@@ -467,13 +467,13 @@ int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q
                                             int causal, float scale, float cap, float sigmoid_bias,
                                             void* stream);
 /* Backward of the same attention (the runtime behind FA4's flash_attn_bwd,
- * src/sfu_repro/fa4.py:430-461): dq [B, S, Hq, 128], dk and dv [B, S, Hkv, 128]
+ * src/sfu_repro/fa4.py:430-461): dq [B, S, Hq, D], dk and dv [B, S, Hkv, D]
  * BF16 from q, k, v, out, dout (BF16) and the forward's lse (softmax modes).
  * strides: 24 element strides, (batch, head, sequence) of q, k, v, out, dout,
  * dq, dk, dv.  delta: caller-provided float [B, Hq, S] workspace receiving
  * rowsum(dout * out) (softmax modes; unused for sigmoid modes, where out, lse
  * and delta may be null).  dkv_workspace: with grouped-query heads (Hq > Hkv)
- * a caller-provided, 16-byte aligned float workspace of 2 * B * Hq * S * 128
+ * a caller-provided, 16-byte aligned float workspace of 2 * B * Hq * S * D
  * elements (per-query-head dK / dV partials, summed deterministically into
  * dk / dv); null otherwise.  grad, the derivative of the score program:
  *   0 the mode's own (softmax, softcap 1 - tanh^2, sigmoid p (1 - p))

@@ -1,4 +1,4 @@
-"""CPU references of the fused attention in FA4's layout ([B, S, H, 128]),
+"""CPU references of the fused attention in FA4's layout ([B, S, H, D]),
 shared by the GPU parity tests: the forward (with routed exp2, softcap and
 sigmoid programs through the oracle) and the backward formulas given the
 forward's out and lse."""
@@ -84,7 +84,7 @@ def probs_and_grad(oracle, a, mode, grad, scale, cap, bias, lse2, route):
 
 
 def reference_bwd(oracle, q, k, v, out, do, lse, mode, grad, causal, scale, cap, route, bias):
-    """float32 CPU gradients [B, S, H, 128] given the forward's out and lse."""
+    """float32 CPU gradients [B, S, H, D] given the forward's out and lse."""
     hq, hkv = q.shape[2], k.shape[2]
     rep = hq // hkv
     qf = q.float().transpose(1, 2)
@@ -123,7 +123,7 @@ def _heads(q, k, v):
 
 
 def reference_fwd(oracle, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=None):
-    """(out [B, S, H, 128], lse [B, H, S]) in float32; lse is None for the
+    """(out [B, S, H, D], lse [B, H, S]) in float32; lse is None for the
     sigmoid modes.  Softmax exponents are taken relative to the row maximum;
     routed keys (route_slot % route < 4) take the mode's exp2 program."""
     qf, kf, vf = _heads(q, k, v)

@@ -22,12 +22,12 @@ pytestmark = pytest.mark.gpu
 
 
 
-def _inputs(b, hq, hkv, s, seed, qmul=1.0):
+def _inputs(b, hq, hkv, s, seed, qmul=1.0, d=128):
     g = torch.Generator().manual_seed(seed)
-    q = (torch.randn(b, s, hq, 128, generator=g) * qmul).bfloat16()
-    k = torch.randn(b, s, hkv, 128, generator=g).bfloat16()
-    v = torch.randn(b, s, hkv, 128, generator=g).bfloat16()
-    do = torch.randn(b, s, hq, 128, generator=g).bfloat16()
+    q = (torch.randn(b, s, hq, d, generator=g) * qmul).bfloat16()
+    k = torch.randn(b, s, hkv, d, generator=g).bfloat16()
+    v = torch.randn(b, s, hkv, d, generator=g).bfloat16()
+    do = torch.randn(b, s, hq, d, generator=g).bfloat16()
     return q, k, v, do
 
 
@@ -39,15 +39,15 @@ def _strides(*ts):
 
 
 def fwd(capi, cuda, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=None):
-    b, s, hq, _ = q.shape
+    b, s, hq, d = q.shape
     hkv = k.shape[2]
     qd, kd, vd = q.to(cuda), k.to(cuda), v.to(cuda)
-    out = torch.empty(b, s, hq, 128, dtype=torch.bfloat16, device=cuda)
+    out = torch.empty(b, s, hq, d, dtype=torch.bfloat16, device=cuda)
     lse = torch.zeros(b, hq, s, dtype=torch.float32, device=cuda)
     bias = _bias(mode, s) if bias is None else bias
     rc = capi.launch_flash_attention_fwd_strided_bf16(
         capi.ptr(out), capi.ptr(lse), capi.ptr(qd), capi.ptr(kd), capi.ptr(vd), ctypes.c_int64(b),
-        ctypes.c_int64(hq), ctypes.c_int64(hkv), ctypes.c_int64(s), ctypes.c_int64(128),
+        ctypes.c_int64(hq), ctypes.c_int64(hkv), ctypes.c_int64(s), ctypes.c_int64(d),
         _strides(qd, kd, vd, out), ctypes.c_int(M[mode]), ctypes.c_int(route), ctypes.c_int(int(causal)),
         ctypes.c_float(scale), ctypes.c_float(cap), ctypes.c_float(bias), capi.stream())
     assert rc == 0
@@ -56,20 +56,20 @@ def fwd(capi, cuda, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=None):
 
 
 def bwd(capi, cuda, q, k, v, out, do, lse, mode, grad, causal, scale, cap=30.0, route=0, bias=None):
-    b, s, hq, _ = q.shape
+    b, s, hq, d = q.shape
     hkv = k.shape[2]
     qd, kd, vd, dod = q.to(cuda), k.to(cuda), v.to(cuda), do.to(cuda)
     dq = torch.empty_like(qd)
     dk = torch.empty_like(kd)
     dv = torch.empty_like(vd)
     delta = torch.empty(b, hq, s, dtype=torch.float32, device=cuda)
-    ws = torch.empty(2, b, hq, s, 128, dtype=torch.float32, device=cuda) if hq != hkv else None
+    ws = torch.empty(2, b, hq, s, d, dtype=torch.float32, device=cuda) if hq != hkv else None
     bias = _bias(mode, s) if bias is None else bias
     rc = capi.launch_flash_attention_bwd_strided_bf16(
         capi.ptr(dq), capi.ptr(dk), capi.ptr(dv), capi.ptr(delta),
         capi.ptr(ws) if ws is not None else ctypes.c_void_p(0), capi.ptr(qd), capi.ptr(kd),
         capi.ptr(vd), capi.ptr(out), capi.ptr(dod), capi.ptr(lse), ctypes.c_int64(b), ctypes.c_int64(hq),
-        ctypes.c_int64(hkv), ctypes.c_int64(s), ctypes.c_int64(128),
+        ctypes.c_int64(hkv), ctypes.c_int64(s), ctypes.c_int64(d),
         _strides(qd, kd, vd, out, dod, dq, dk, dv), ctypes.c_int(M[mode]), ctypes.c_int(grad),
         ctypes.c_int(route), ctypes.c_int(int(causal)), ctypes.c_float(scale), ctypes.c_float(cap),
         ctypes.c_float(bias), capi.stream())
@@ -107,6 +107,31 @@ def test_backward_matches_reference(capi, oracle, cuda, mode, grad, route, causa
         assert torch.isfinite(got).all(), name
         ok, info = _close(got, ref)
         assert ok, (mode, grad, route, causal, name, info)
+
+
+D64_CASES = [("softmax_native", 0, 0), ("softmax_d2", 0, 32), ("softcap_d4", 1, 0), ("sigmoid_native", 0, 0)]
+
+
+@pytest.mark.parametrize("mode,grad,route", D64_CASES)
+def test_head_dim_64(capi, oracle, cuda, mode, grad, route):
+    """Forward (with lse) and backward at head_dim 64 (the reference's
+    Llama 1B training model), grouped heads, causal."""
+    q, k, v, do = _inputs(1, 4, 2, 256, 200 + M[mode], qmul=6.0 if mode.startswith("softcap") else 1.0, d=64)
+    scale = 1 / math.sqrt(64)
+    out, lse = fwd(capi, cuda, q, k, v, mode, True, scale, route=route if route else 4)
+    from attention_reference import reference_fwd
+
+    ref_out, ref_lse = reference_fwd(oracle, q, k, v, mode, True, scale, 30.0, route if route else 4)
+    ok, info = _close(out.cpu().float(), ref_out, rel=1.5e-2)
+    assert ok, ("out", info)
+    if ref_lse is not None:
+        assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, mode, grad, True, scale, route=route)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, mode, grad, True, scale, 30.0, route,
+                               _bias(mode, 256))
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        ok, info = _close(got, ref)
+        assert ok, (mode, name, info)
 
 
 @pytest.mark.parametrize("grad", [4, 5])

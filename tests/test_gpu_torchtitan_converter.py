@@ -54,6 +54,22 @@ def test_b1_fused_mlp_and_fa4_softmax(cuda, variant, tol):
     assert all(torch.isfinite(p.grad).all() for p in model.parameters() if p.grad is not None)
 
 
+def test_b1_at_head_dim_64(cuda):
+    """The reference's training model has head_dim 64 (Llama 1B: dim 2048,
+    32 heads); a model with that head size converts and trains."""
+    torch.manual_seed(0)
+    base = Transformer(dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv_heads=2).to(cuda, torch.bfloat16)
+    model = copy.deepcopy(base)
+    assert _convert(model, "b1", "polynomial") == {"attention": 2, "activation": 2}
+    x = torch.randn(1, 256, 512, device=cuda, dtype=torch.bfloat16, requires_grad=True)
+    with torch.no_grad():
+        ref = base(x)
+    out = model(x)
+    assert _rel(out, ref) < 0.05
+    out.float().square().mean().backward()
+    assert torch.isfinite(x.grad).all()
+
+
 def test_b2_softcap_variants_agree(cuda):
     outs = {}
     x = torch.randn(1, 256, 512, device=cuda, dtype=torch.bfloat16) * 4
