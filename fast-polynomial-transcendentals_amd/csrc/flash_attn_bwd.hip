@@ -273,10 +273,14 @@ __device__ __forceinline__ bf16x8_t frag_t16(const uint16_t* t, int row, int g) 
 //    key l%16) holds queries 16 rb + 4g + r;
 //  * dV^T += dO^T P and dK^T += Q^T dS take P / dS as B fragments with
 //    k slot 8g + e <-> query 16 (e/4) + 4g + e%4, the accumulator order;
-//  * per wave: K, V fragments 32 VGPRs, dK^T / dV^T accumulators 64, so two
-//    waves share a SIMD.
+//  * per wave (head_dim 128): K, V fragments 32 VGPRs, dK^T / dV^T
+//    accumulators 64, so two waves share a SIMD; with head_dim 64 the kernel
+//    is held to 128 VGPRs, so two blocks (four waves per SIMD) share a CU
+//    (measured on MI355X: 1.14-1.22x on the softmax and softcap modes, a
+//    few spilled registers included).
 template <int MODE, int GRAD, int ROUTE, int HD>
-__global__ void __launch_bounds__(512) flash_bwd_dkdv_kernel(AttnBwdParams p) {
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2)))
+flash_bwd_dkdv_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kRS = row_stride<HD>(), kChunks = HD / 8;
     __shared__ __align__(16) BwdQTile<HD> tiles[2];
