@@ -17,16 +17,17 @@
 // Design (all-transposed MFMA formulation, v_mfma_f32_32x32x16_bf16):
 //  * a block of 4 waves owns 128 queries; each wave owns 32 queries, held
 //    as the B operand Q^T (8 fragments of 8 BF16 per lane, loaded once);
-//  * the block stages 64-key tiles of K (row-major, 16-byte padded rows) and
-//    V^T (transposed while staging) in LDS;
+//  * the block stages 64-key tiles of K and V in LDS, both row-major as they
+//    arrive (16-byte stores, padded rows);
 //  * S^T = K Q^T: lane (h, c) of a wave accumulates 16 keys x query c for
 //    each 32-key tile, so every per-query reduction is lane-local plus one
 //    exchange with lane c + 32;
 //  * O^T = V^T P^T: the S^T accumulator registers become the P^T fragments
 //    with no data movement by numbering the MFMA k index in the order the
-//    accumulator holds the keys; the V^T fragments are read from LDS in the
-//    same order (two 8-byte reads per fragment), and O^T keeps each lane on
-//    its own query, so the online-softmax rescale is lane-local too;
+//    accumulator holds the keys; the V^T fragments come from the row-major V
+//    tile in the same order through gfx950's transposing LDS reads
+//    (ds_read_b64_tr_b16, two per fragment), and O^T keeps each lane on its
+//    own query, so the online-softmax rescale is lane-local too;
 //  * the next K / V tile is loaded into registers while the current one is
 //    used and written to the second LDS buffer afterwards (one barrier per
 //    tile);
@@ -125,7 +126,7 @@ constexpr float kRescaleThreshold = 8.0f;
 // causal diagonal of this wave's 32 queries.
 template <int MODE, int ROUTE, bool MASKED, int HD>
 __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t* __restrict__ ks,
-                                            const uint16_t* __restrict__ vt, const bf16x8_t (&qf)[HD / 16],
+                                            const uint16_t* __restrict__ vrow, const bf16x8_t (&qf)[HD / 16],
                                             f32x16_t (&oacc)[HD / 32], float& m, float& l, int diag,
                                             int h, int c32, float inv_cap) {
     constexpr int kKStr = HD + 8;  // BF16 elements per LDS K row
@@ -218,13 +219,16 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
             bf16x8_t pf;
 #pragma unroll
             for (int e = 0; e < 8; ++e) pf[e] = (__bf16)pr[e];
-            const int kbase = kt * 32 + cc * 16 + 4 * h;
+                // V^T fragment of dims dt*32 + (lane % 32), keys kt*32 + cc*16 + 4h
+            // + {0..3, 8..11}: two transposing reads of the row-major V tile
+            // (vrow points at this lane's source chunk of the first)
 #pragma unroll
             for (int dt = 0; dt < HD / 32; ++dt) {
-                const uint16_t* row = vt + (dt * 32 + c32) * kVStride + kbase;
-                const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
-                const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 8);
-                const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
+                const uint16_t* src = vrow + (kt * 32 + cc * 16) * kVRowStr<HD>() + dt * 32;
+                const v4i16_t lo = lds_read_tr16(src);
+                const v4i16_t hi = lds_read_tr16(src + 8 * kVRowStr<HD>());
+                const u32x4_t w = {__builtin_bit_cast(u32x2_t, lo).x, __builtin_bit_cast(u32x2_t, lo).y,
+                                   __builtin_bit_cast(u32x2_t, hi).x, __builtin_bit_cast(u32x2_t, hi).y};
                 oacc[dt] = mfma32(__builtin_bit_cast(bf16x8_t, w), pf, oacc[dt]);
             }
         }
@@ -238,9 +242,10 @@ template <int MODE, int ROUTE, int HD>
 __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kKStr = HD + 8;
-    // two buffers: the next tile is written while the current one is read
+    // two buffers: the next tile is written while the current one is read;
+    // K and V are both row-major (V^T fragments come from transposing reads)
     __shared__ __align__(16) uint16_t ks[2][kAttnBlockK * kKStr];
-    __shared__ __align__(16) uint16_t vt[2][HD * kVStride];
+    __shared__ __align__(16) uint16_t vs[2][kAttnBlockK * kVRowStr<HD>()];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -267,42 +272,29 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     float m = -__builtin_inff(), l = 0.0f;
     const float inv_cap = 1.0f / p.cap;
 
-    // staging: K rows krow + kRowsPass j (16 bytes at kcol); V rows vkey,
-    // vkey + 1 (16 bytes at vd + 64 r), transposed into V^T while written
+    // staging: K and V rows krow + kRowsPass j, 16 bytes at kcol
     constexpr int kChunks = HD / 8;                   // 16-byte chunks per row
-    constexpr int kRowsPass = 256 / kChunks;          // K rows per pass
-    constexpr int kKPasses = kAttnBlockK / kRowsPass;
-    constexpr int kVPasses = HD / 64;
+    constexpr int kRowsPass = 256 / kChunks;          // rows per pass
+    constexpr int kPasses = kAttnBlockK / kRowsPass;
     const int krow = tid / kChunks, kcol = (tid % kChunks) * 8;
-    const int vkey = 2 * (tid & 31), vd = (tid >> 5) * 8;
-    u32x4_t kr[kKPasses], va[kVPasses], vc[kVPasses];
+    u32x4_t kr[kPasses], vr[kPasses];
     auto load = [&](int64_t k0) {
 #pragma unroll
-        for (int j = 0; j < kKPasses; ++j)
+        for (int j = 0; j < kPasses; ++j) {
             kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (k0 + krow + kRowsPass * j) * kss + kcol);
-#pragma unroll
-        for (int r = 0; r < kVPasses; ++r) {
-            va[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey) * vss + vd + 64 * r);
-            vc[r] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + vkey + 1) * vss + vd + 64 * r);
+            vr[j] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + krow + kRowsPass * j) * vss + kcol);
         }
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < kKPasses; ++j)
+        for (int j = 0; j < kPasses; ++j) {
             *reinterpret_cast<u32x4_t*>(&ks[buf][(krow + kRowsPass * j) * kKStr + kcol]) = kr[j];
-#pragma unroll
-        for (int r = 0; r < kVPasses; ++r) {
-            const int d0 = vd + 64 * r;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // (V[key][d], V[key+1][d]) for d = d0 + 2j and d0 + 2j + 1
-                *reinterpret_cast<uint32_t*>(&vt[buf][(d0 + 2 * j) * kVStride + vkey]) =
-                    __builtin_amdgcn_perm(vc[r][j], va[r][j], 0x05040100u);
-                *reinterpret_cast<uint32_t*>(&vt[buf][(d0 + 2 * j + 1) * kVStride + vkey]) =
-                    __builtin_amdgcn_perm(vc[r][j], va[r][j], 0x07060302u);
-            }
+            *reinterpret_cast<u32x4_t*>(&vs[buf][(krow + kRowsPass * j) * kVRowStr<HD>() + kcol]) = vr[j];
         }
     };
+    // this lane's source chunk of the transposing V reads: key (lane % 16) / 4
+    // + 4h, dims 16 ((lane / 16) % 2) + 4 (lane % 4) of a 32-dim slice
+    const int vlane = (((lane & 15) >> 2) + 4 * h) * kVRowStr<HD>() + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     const int64_t nkb = p.causal ? (qb + 1) * (kAttnBlockQ / kAttnBlockK) : p.seq / kAttnBlockK;
     load(0);
@@ -316,9 +308,9 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
         if (!p.causal || k0 <= q0 + 31) {  // wave-uniform: some key of the tile is visible
             const int diag = (int)(k0 - qrow) + 4 * h;
             if (p.causal && k0 + kAttnBlockK - 1 > q0)
-                attend_tile<MODE, ROUTE, true, HD>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
+                attend_tile<MODE, ROUTE, true, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap);
             else
-                attend_tile<MODE, ROUTE, false, HD>(p, ks[buf], vt[buf], qf, oacc, m, l, diag, h, c32, inv_cap);
+                attend_tile<MODE, ROUTE, false, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap);
         }
         if (more) store(buf ^ 1);
         __syncthreads();

@@ -42,9 +42,6 @@ constexpr int kHeadDim = 128;
 constexpr int kAttnBlockQ = 128;  // 4 waves x 32 queries
 constexpr int kAttnBlockK = 64;   // keys per staged tile
 constexpr int kKStride = kHeadDim + 8;    // BF16 elements per LDS K row
-// BF16 elements per LDS V^T row: 34 words, so the 8-byte fragment reads of
-// 32 consecutive rows fall on distinct banks
-constexpr int kVStride = kAttnBlockK + 4;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kLn2 = 0.69314718055994530942f;
 
@@ -56,6 +53,25 @@ struct AttnStrides {
 
 __device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// BF16 elements per row of the row-major V tile read by transposing loads:
+// one wave's read covers 8 rows x 64 bytes, and a row stride of 64 bytes
+// modulo 256 puts four consecutive rows on disjoint banks (measured on
+// MI355X against paddings of 0-40 elements: 1.5-7 % faster forward than 8).
+template <int HD>
+constexpr int kVRowStr() { return HD + 32; }
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 (gfx950): each lane names an 8-byte chunk (4 BF16) of
+// LDS; within every group of 16 lanes, lane i receives element i % 4 of the
+// chunks of lanes 4s + i / 4, s = 0..3.  With lane j of a group pointing at
+// row r0 + j / 4, columns c0 + 4 (j % 4) of a row-major tile, lane i gets
+// column c0 + i of rows r0 .. r0 + 3: a 4 x 16 block, transposed (layout
+// measured on MI355X).
+__device__ __forceinline__ v4i16_t lds_read_tr16(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)(p));
 }
 
 }  // namespace pt

@@ -7,15 +7,17 @@
 //  * delta: D[q] = sum_d dO[q][d] O[q][d] (FP32), for the softmax modes;
 //  * dK/dV: a block of 8 waves owns 128 keys of one query head (16 per
 //    wave, K and V held in registers, 16x16x32 MFMA) and streams 32-query
-//    tiles of Q, Q^T, dO, dO^T (+ lse, D) through LDS; with grouped-query
+//    tiles of Q and dO (+ lse, D) through LDS; with grouped-query
 //    heads each block writes FP32 partials and a reduction kernel sums the
 //    group (deterministically); S = Q K^T and dP = dO V^T come out with one
 //    key per lane, so P and dS are ready-made B fragments of dV^T += dO^T P
 //    and dK^T += Q^T dS (the k index numbered in accumulator order, as in the
 //    forward);
 //  * dQ: a block owns 128 queries (32 per wave, Q and dO in registers) and
-//    streams 32-key tiles of K, K^T and V: S^T = K Q^T and dP^T = V dO^T have
+//    streams 32-key tiles of K and V: S^T = K Q^T and dP^T = V dO^T have
 //    one query per lane, dQ^T += K^T dS^T.
+// Tiles are staged row-major; the transposed operands Q^T, dO^T and K^T are
+// read from the same rows with transposing LDS loads (ds_read_b64_tr_b16).
 // P is recomputed from the saved log-sum-exp (softmax) or directly (sigmoid
 // attention); the score program's derivative enters dS:
 //   softmax        dS = P (dP - D)
@@ -41,7 +43,6 @@ enum AttnGrad : int {
 };
 
 constexpr int kBwdTile = 32;              // queries (dK/dV) or keys (dQ) per staged tile
-constexpr int kTStride = kBwdTile + 4;    // transposed tile rows [128][36]
 constexpr int kRouteRuntime = -1;
 
 struct AttnBwdParams {
@@ -185,9 +186,10 @@ __global__ void __launch_bounds__(256) attn_delta_kernel(const uint16_t* __restr
 }
 
 // ---------------------------------------------------------------------------
-// staging of a 32-row tile: row-major copy and transposed copy.  Thread
-// (pair pr, chunk dc) holds rows 2 pr, 2 pr + 1, BF16 elements
-// 8 dc .. 8 dc + 7; 16 x HD / 8 threads move a tile.
+// staging of a 32-row tile, row-major as it arrives.  Thread (pair pr, chunk
+// dc) holds rows 2 pr, 2 pr + 1, BF16 elements 8 dc .. 8 dc + 7; 16 x HD / 8
+// threads move a tile.  The transposed operands (Q^T, dO^T, K^T) are read
+// from the same rows with gfx950's transposing LDS loads.
 // ---------------------------------------------------------------------------
 
 template <int HD>
@@ -197,36 +199,6 @@ template <int HD>
 __device__ __forceinline__ void store_rows(uint16_t* rows, int pr, int dc, const u32x4_t& a, const u32x4_t& b) {
     *reinterpret_cast<u32x4_t*>(rows + (2 * pr) * row_stride<HD>() + dc * 8) = a;
     *reinterpret_cast<u32x4_t*>(rows + (2 * pr + 1) * row_stride<HD>() + dc * 8) = b;
-}
-
-// Transposed tiles [128][36] are swizzled: column group c (4 BF16 elements,
-// 8 bytes) of row d lives at group c ^ ((d >> 4) & 7).  The staging stores
-// of one instruction then cover all 32 banks (without it, 16 threads with
-// rows 8 apart share 4 banks), and fragment reads keep 8-byte groups whole.
-__device__ __forceinline__ int tcol(int row, int col) {
-    return ((((col >> 2) ^ (row >> 4)) & 7) << 2) | (col & 3);
-}
-
-__device__ __forceinline__ void store_transposed(uint16_t* t, int pr, int dc, const u32x4_t& a, const u32x4_t& b) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        // (row 2pr, row 2pr+1) of columns d = 8 dc + 2j and 8 dc + 2j + 1
-        const int d = dc * 8 + 2 * j;
-        *reinterpret_cast<uint32_t*>(t + d * kTStride + tcol(d, 2 * pr)) =
-            __builtin_amdgcn_perm(b[j], a[j], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(t + (d + 1) * kTStride + tcol(d + 1, 2 * pr)) =
-            __builtin_amdgcn_perm(b[j], a[j], 0x07060302u);
-    }
-}
-
-// A fragment of a transposed tile: row `row`, the eight k slots of lane half
-// h in accumulator order (columns 16 cc + 4h .. +3 and 16 cc + 8 + 4h .. +3).
-__device__ __forceinline__ bf16x8_t frag_t(const uint16_t* t, int row, int cc, int h) {
-    const uint16_t* r = t + row * kTStride;
-    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r + tcol(row, 16 * cc + 4 * h));
-    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + tcol(row, 16 * cc + 8 + 4 * h));
-    const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
-    return __builtin_bit_cast(bf16x8_t, w);
 }
 
 __device__ __forceinline__ bf16x8_t to_frag(const float (&x)[16], int cc) {
@@ -243,9 +215,7 @@ __device__ __forceinline__ bf16x8_t to_frag(const float (&x)[16], int cc) {
 template <int HD>
 struct BwdQTile {
     uint16_t q[kBwdTile * row_stride<HD>()];
-    uint16_t qt[HD * kTStride];
     uint16_t dout[kBwdTile * row_stride<HD>()];
-    uint16_t doutt[HD * kTStride];
     float lse2[kBwdTile];
     float delta[kBwdTile];
 };
@@ -256,13 +226,32 @@ __device__ __forceinline__ f32x4v_t mfma16(bf16x8_t a, bf16x8_t b, f32x4v_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// A fragment (16x16x32) of a transposed tile: row `row`, the eight k slots
-// of lane group g in accumulator order (columns 4g .. 4g+3 and 16+4g .. +3).
-__device__ __forceinline__ bf16x8_t frag_t16(const uint16_t* t, int row, int g) {
-    const uint16_t* r = t + row * kTStride;
-    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r + tcol(row, 4 * g));
-    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + tcol(row, 16 + 4 * g));
-    const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
+// A fragment (16x16x32) of X^T for a row-major 32-row tile X (rows =
+// queries): dims 16 dt + (lane % 16), the eight k slots of lane group
+// g = lane / 16 in accumulator order (rows 4g .. 4g+3 and 16+4g .. +3).
+// `src` is the tile plus this lane's source chunk, (4g + (lane % 16) / 4)
+// rows and 4 (lane % 4) columns in.
+template <int HD>
+__device__ __forceinline__ bf16x8_t frag_tr16(const uint16_t* src, int dt) {
+    const v4i16_t lo = lds_read_tr16(src + 16 * dt);
+    const v4i16_t hi = lds_read_tr16(src + 16 * row_stride<HD>() + 16 * dt);
+    const u32x2_t a = __builtin_bit_cast(u32x2_t, lo), b = __builtin_bit_cast(u32x2_t, hi);
+    const u32x4_t w = {a.x, a.y, b.x, b.y};
+    return __builtin_bit_cast(bf16x8_t, w);
+}
+
+// A fragment (32x32x16) of X^T for a row-major 32-row tile X (rows = keys):
+// dims 32 dt + (lane % 32), the eight k slots of lane half h = lane / 32 in
+// accumulator order (rows 16 cc + 4h .. +3 and 16 cc + 8 + 4h .. +3).  `src`
+// is the tile plus this lane's source chunk, (4h + (lane % 16) / 4) rows and
+// 16 ((lane / 16) % 2) + 4 (lane % 4) columns in.
+template <int HD>
+__device__ __forceinline__ bf16x8_t frag_tr32(const uint16_t* src, int dt, int cc) {
+    const uint16_t* r = src + 16 * cc * row_stride<HD>() + 32 * dt;
+    const v4i16_t lo = lds_read_tr16(r);
+    const v4i16_t hi = lds_read_tr16(r + 8 * row_stride<HD>());
+    const u32x2_t a = __builtin_bit_cast(u32x2_t, lo), b = __builtin_bit_cast(u32x2_t, hi);
+    const u32x4_t w = {a.x, a.y, b.x, b.y};
     return __builtin_bit_cast(bf16x8_t, w);
 }
 
@@ -343,10 +332,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     };
     auto store = [&](int buf) {
         BwdQTile<HD>& t = tiles[buf];
-        if (stager) {
-            store_rows<HD>(half ? t.dout : t.q, pr, dc, ra, rb2);
-            store_transposed(half ? t.doutt : t.qt, pr, dc, ra, rb2);
-        }
+        if (stager) store_rows<HD>(half ? t.dout : t.q, pr, dc, ra, rb2);
         if constexpr (!kSigmoid) {
             if (st < kBwdTile) (half ? t.delta : t.lse2)[st] = row_r;
         }
@@ -412,10 +398,11 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
                 pf[e] = (__bf16)pr_[e];
                 sf[e] = (__bf16)ds[e];
             }
+            const int tr_off = (4 * g + (kl >> 2)) * kRS + 4 * (kl & 3);
 #pragma unroll
             for (int dt = 0; dt < HD / 16; ++dt) {
-                dvacc[dt] = mfma16(frag_t16(t.doutt, dt * 16 + kl, g), pf, dvacc[dt]);
-                dkacc[dt] = mfma16(frag_t16(t.qt, dt * 16 + kl, g), sf, dkacc[dt]);
+                dvacc[dt] = mfma16(frag_tr16<HD>(t.dout + tr_off, dt), pf, dvacc[dt]);
+                dkacc[dt] = mfma16(frag_tr16<HD>(t.q + tr_off, dt), sf, dkacc[dt]);
             }
         }
         if (more) store(buf ^ 1);
@@ -485,7 +472,6 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(const float* __res
 template <int HD>
 struct BwdKTile {
     uint16_t k[kBwdTile * row_stride<HD>()];
-    uint16_t kt[HD * kTStride];
     uint16_t v[kBwdTile * row_stride<HD>()];
 };
 
@@ -544,7 +530,6 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
         if (!stager) return;
         BwdKTile<HD>& t = tiles[buf];
         store_rows<HD>(t.k, pr, dc, ka, kb2);
-        store_transposed(t.kt, pr, dc, ka, kb2);
         store_rows<HD>(t.v, pr, dc, va, vb);
     };
 
@@ -591,12 +576,13 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
                 for (int r = 0; r < 16; ++r)
                     if (diag + 8 * (r >> 2) + (r & 3) > 0) ds[r] = 0.0f;
             }
+            const int tr_off = (4 * h + ((lane & 15) >> 2)) * kRS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const bf16x8_t sf = to_frag(ds, cc);
 #pragma unroll
                 for (int dt = 0; dt < HD / 32; ++dt)
-                    dqacc[dt] = mfma32(frag_t(t.kt, dt * 32 + c32, cc, h), sf, dqacc[dt]);
+                    dqacc[dt] = mfma32(frag_tr32<HD>(t.k + tr_off, dt, cc), sf, dqacc[dt]);
             }
         }
         if (more) store(buf ^ 1);
