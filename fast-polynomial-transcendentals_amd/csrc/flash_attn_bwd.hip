@@ -192,13 +192,19 @@ __global__ void __launch_bounds__(256) attn_delta_kernel(const uint16_t* __restr
 // from the same rows with gfx950's transposing LDS loads.
 // ---------------------------------------------------------------------------
 
+// BF16 elements per LDS row.  Each tile is read both by 16-byte row
+// fragments and by transposing loads, whose bank patterns differ; the
+// paddings were chosen with the bank-conflict counter on MI355X (dK/dV's Q
+// and dO tiles: none at +16; dQ's K and V tiles: fewest at +24).
 template <int HD>
-constexpr int row_stride() { return HD + 8; }  // BF16 elements per LDS row
+constexpr int q_row_stride() { return HD + 16; }
+template <int HD>
+constexpr int k_row_stride() { return HD + 24; }
 
-template <int HD>
+template <int RS>
 __device__ __forceinline__ void store_rows(uint16_t* rows, int pr, int dc, const u32x4_t& a, const u32x4_t& b) {
-    *reinterpret_cast<u32x4_t*>(rows + (2 * pr) * row_stride<HD>() + dc * 8) = a;
-    *reinterpret_cast<u32x4_t*>(rows + (2 * pr + 1) * row_stride<HD>() + dc * 8) = b;
+    *reinterpret_cast<u32x4_t*>(rows + (2 * pr) * RS + dc * 8) = a;
+    *reinterpret_cast<u32x4_t*>(rows + (2 * pr + 1) * RS + dc * 8) = b;
 }
 
 __device__ __forceinline__ bf16x8_t to_frag(const float (&x)[16], int cc) {
@@ -214,8 +220,8 @@ __device__ __forceinline__ bf16x8_t to_frag(const float (&x)[16], int cc) {
 
 template <int HD>
 struct BwdQTile {
-    uint16_t q[kBwdTile * row_stride<HD>()];
-    uint16_t dout[kBwdTile * row_stride<HD>()];
+    uint16_t q[kBwdTile * q_row_stride<HD>()];
+    uint16_t dout[kBwdTile * q_row_stride<HD>()];
     float lse2[kBwdTile];
     float delta[kBwdTile];
 };
@@ -234,7 +240,7 @@ __device__ __forceinline__ f32x4v_t mfma16(bf16x8_t a, bf16x8_t b, f32x4v_t c) {
 template <int HD>
 __device__ __forceinline__ bf16x8_t frag_tr16(const uint16_t* src, int dt) {
     const v4i16_t lo = lds_read_tr16(src + 16 * dt);
-    const v4i16_t hi = lds_read_tr16(src + 16 * row_stride<HD>() + 16 * dt);
+    const v4i16_t hi = lds_read_tr16(src + 16 * q_row_stride<HD>() + 16 * dt);
     const u32x2_t a = __builtin_bit_cast(u32x2_t, lo), b = __builtin_bit_cast(u32x2_t, hi);
     const u32x4_t w = {a.x, a.y, b.x, b.y};
     return __builtin_bit_cast(bf16x8_t, w);
@@ -247,9 +253,9 @@ __device__ __forceinline__ bf16x8_t frag_tr16(const uint16_t* src, int dt) {
 // 16 ((lane / 16) % 2) + 4 (lane % 4) columns in.
 template <int HD>
 __device__ __forceinline__ bf16x8_t frag_tr32(const uint16_t* src, int dt, int cc) {
-    const uint16_t* r = src + 16 * cc * row_stride<HD>() + 32 * dt;
+    const uint16_t* r = src + 16 * cc * k_row_stride<HD>() + 32 * dt;
     const v4i16_t lo = lds_read_tr16(r);
-    const v4i16_t hi = lds_read_tr16(r + 8 * row_stride<HD>());
+    const v4i16_t hi = lds_read_tr16(r + 8 * k_row_stride<HD>());
     const u32x2_t a = __builtin_bit_cast(u32x2_t, lo), b = __builtin_bit_cast(u32x2_t, hi);
     const u32x4_t w = {a.x, a.y, b.x, b.y};
     return __builtin_bit_cast(bf16x8_t, w);
@@ -271,7 +277,7 @@ template <int MODE, int GRAD, int ROUTE, int HD>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2)))
 flash_bwd_dkdv_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
-    constexpr int kRS = row_stride<HD>(), kChunks = HD / 8;
+    constexpr int kRS = q_row_stride<HD>(), kChunks = HD / 8;
     __shared__ __align__(16) BwdQTile<HD> tiles[2];
 
     const int tid = threadIdx.x;
@@ -332,7 +338,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     };
     auto store = [&](int buf) {
         BwdQTile<HD>& t = tiles[buf];
-        if (stager) store_rows<HD>(half ? t.dout : t.q, pr, dc, ra, rb2);
+        if (stager) store_rows<kRS>(half ? t.dout : t.q, pr, dc, ra, rb2);
         if constexpr (!kSigmoid) {
             if (st < kBwdTile) (half ? t.delta : t.lse2)[st] = row_r;
         }
@@ -471,14 +477,14 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(const float* __res
 
 template <int HD>
 struct BwdKTile {
-    uint16_t k[kBwdTile * row_stride<HD>()];
-    uint16_t v[kBwdTile * row_stride<HD>()];
+    uint16_t k[kBwdTile * k_row_stride<HD>()];
+    uint16_t v[kBwdTile * k_row_stride<HD>()];
 };
 
 template <int MODE, int GRAD, int ROUTE, int HD>
 __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
-    constexpr int kRS = row_stride<HD>(), kChunks = HD / 8;
+    constexpr int kRS = k_row_stride<HD>(), kChunks = HD / 8;
     __shared__ __align__(16) BwdKTile<HD> tiles[2];
 
     const int tid = threadIdx.x;
@@ -529,8 +535,8 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
     auto store = [&](int buf) {
         if (!stager) return;
         BwdKTile<HD>& t = tiles[buf];
-        store_rows<HD>(t.k, pr, dc, ka, kb2);
-        store_rows<HD>(t.v, pr, dc, va, vb);
+        store_rows<kRS>(t.k, pr, dc, ka, kb2);
+        store_rows<kRS>(t.v, pr, dc, va, vb);
     };
 
     const int64_t nkt = p.causal ? (qb + 1) * (kAttnBlockQ / kBwdTile) : p.seq / kBwdTile;
