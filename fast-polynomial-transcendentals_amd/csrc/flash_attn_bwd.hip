@@ -273,29 +273,25 @@ __device__ __forceinline__ bf16x8_t frag_tr32(const uint16_t* src, int dt, int c
 //    is held to 128 VGPRs, so two blocks (four waves per SIMD) share a CU
 //    (measured on MI355X: 1.14-1.22x on the softmax and softcap modes, a
 //    few spilled registers included).
-template <int MODE, int GRAD, int ROUTE, int HD>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2)))
+template <int MODE, int GRAD, int ROUTE, int HD, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2)))
 flash_bwd_dkdv_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kRS = q_row_stride<HD>(), kChunks = HD / 8;
+    constexpr int kThreads = 64 * W, kKeys = 16 * W;  // keys per block
     __shared__ __align__(16) BwdQTile<HD> tiles[2];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, kl = lane & 15;
-    // staging: threads 0..255 move Q, 256..511 dO (row pair pr, chunk dc);
-    // 16 x HD / 8 of each half are active
-    const int half = tid >> 8, st = tid & 255;
-    const int pr = st / kChunks, dc = st % kChunks;
-    const bool stager = st < 16 * kChunks;
-    // one block per (query head, 128-key block): grouped heads write FP32
+    // one block per (query head, kKeys-key block): grouped heads write FP32
     // partials that attn_dkv_reduce_kernel sums, so the causal work per block
     // stays within one head's query range
     const int64_t head = blockIdx.x, kb = blockIdx.y, b = blockIdx.z;
     const int64_t group = p.hq / p.hkv;
     const int64_t kvh = head / group;
-    const int64_t key0 = kb * 128 + wave * 16;  // first key of this wave
-    const int64_t key = key0 + kl;              // this lane's key
+    const int64_t key0 = kb * kKeys + wave * 16;  // first key of this wave
+    const int64_t key = key0 + kl;                // this lane's key
     const float inv_cap = 1.0f / p.cap;
     const bool poly_key = ROUTE == kRouteRuntime && route_slot(key) % p.route < 4;
 
@@ -315,32 +311,61 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
 
     // query tiles of this head, from the block's first key on under the
     // causal mask
-    const int64_t qt0 = p.causal ? kb * (128 / kBwdTile) : 0;
+    const int64_t qt0 = p.causal ? kb * (kKeys / kBwdTile) : 0;
     const int64_t nit = p.seq / kBwdTile - qt0;
 
-    const uint16_t* src = half ? p.dout + b * p.dos.b + head * p.dos.h : p.q + b * p.qs.b + head * p.qs.h;
-    const int64_t src_s = half ? p.dos.s : p.qs.s;
-    u32x4_t ra, rb2;
+    // staging: item i = (tensor, row pair pr, chunk dc) of a tile, tensor 0 =
+    // Q, 1 = dO; thread tid moves items tid + kThreads j (rows 2 pr, 2 pr + 1,
+    // 16 bytes at 8 dc); the first 32 threads of each half of the block load
+    // lse and D (two different waves)
+    constexpr int kItems = 2 * 16 * kChunks;
+    constexpr int kPasses = (kItems + kThreads - 1) / kThreads;
+    const uint16_t* sbase[kPasses];  // this thread's first source row of each pass
+    int64_t sstride[kPasses];
+    int shalf[kPasses], soff[kPasses];  // tensor and LDS offset of each pass
+#pragma unroll
+    for (int j = 0; j < kPasses; ++j) {
+        const int i = tid + kThreads * j;
+        const int half = i / (16 * kChunks), st = i % (16 * kChunks);
+        const int pr = st / kChunks, dc = st % kChunks;
+        sstride[j] = half ? p.dos.s : p.qs.s;
+        sbase[j] = (half ? p.dout + b * p.dos.b + head * p.dos.h : p.q + b * p.qs.b + head * p.qs.h) +
+                   (2 * pr) * sstride[j] + dc * 8;
+        shalf[j] = half;
+        soff[j] = 2 * pr * kRS + dc * 8;
+    }
+    auto active = [&](int j) { return kItems % kThreads == 0 || tid + kThreads * j < kItems; };
+    u32x4_t ra[kPasses], rb2[kPasses];
     float row_r = 0.0f;
     auto load = [&](int64_t it) {
         const int64_t q0 = (qt0 + it) * kBwdTile;
-        if (stager) {
-            const uint16_t* r = src + (q0 + 2 * pr) * src_s + dc * 8;
-            ra = *reinterpret_cast<const u32x4_t*>(r);
-            rb2 = *reinterpret_cast<const u32x4_t*>(r + src_s);
+#pragma unroll
+        for (int j = 0; j < kPasses; ++j) {
+            if (active(j)) {
+                const uint16_t* r = sbase[j] + q0 * sstride[j];
+                ra[j] = *reinterpret_cast<const u32x4_t*>(r);
+                rb2[j] = *reinterpret_cast<const u32x4_t*>(r + sstride[j]);
+            }
         }
         if constexpr (!kSigmoid) {
-            if (st < kBwdTile) {
-                const int64_t i = (b * p.hq + head) * p.seq + q0 + st;
-                row_r = half ? p.delta[i] : p.lse[i] * kLog2e;
+            if (tid % (kThreads / 2) < kBwdTile) {
+                const int64_t i = (b * p.hq + head) * p.seq + q0 + tid % (kThreads / 2);
+                row_r = tid >= kThreads / 2 ? p.delta[i] : p.lse[i] * kLog2e;
             }
         }
     };
     auto store = [&](int buf) {
         BwdQTile<HD>& t = tiles[buf];
-        if (stager) store_rows<kRS>(half ? t.dout : t.q, pr, dc, ra, rb2);
+#pragma unroll
+        for (int j = 0; j < kPasses; ++j) {
+            if (active(j)) {
+                uint16_t* dst = (shalf[j] ? t.dout : t.q) + soff[j];
+                *reinterpret_cast<u32x4_t*>(dst) = ra[j];
+                *reinterpret_cast<u32x4_t*>(dst + kRS) = rb2[j];
+            }
+        }
         if constexpr (!kSigmoid) {
-            if (st < kBwdTile) (half ? t.delta : t.lse2)[st] = row_r;
+            if (tid % (kThreads / 2) < kBwdTile) (tid >= kThreads / 2 ? t.delta : t.lse2)[tid % (kThreads / 2)] = row_r;
         }
     };
 
@@ -616,7 +641,12 @@ namespace {
 template <int MODE, int GRAD, int ROUTE, int HD>
 void launch_bwd_hd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
     const dim3 grid((unsigned)prm.hq, (unsigned)(prm.seq / 128), (unsigned)batch);
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE, HD>), grid, dim3(512), 0, st, prm);
+    // waves (16 keys each) per dK/dV block: the sigmoid modes run faster as
+    // independent 4-wave blocks, the softmax modes as 8-wave blocks that stage
+    // each query tile once per 128 keys (measured on MI355X)
+    constexpr int kW = attn_is_sigmoid(MODE) ? 4 : 8;
+    const dim3 kgrid((unsigned)prm.hq, (unsigned)(prm.seq / (16 * kW)), (unsigned)batch);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE, HD, kW>), kgrid, dim3(64 * kW), 0, st, prm);
     if (prm.dkv_ws != nullptr) {
         const int64_t n = batch * prm.hkv * prm.seq * (HD / 8);
         hipLaunchKernelGGL((attn_dkv_reduce_kernel<HD>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
