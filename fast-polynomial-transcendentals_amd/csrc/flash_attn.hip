@@ -15,7 +15,8 @@
 // optional causal mask.  s = q.k * scale.
 //
 // Design (all-transposed MFMA formulation, v_mfma_f32_32x32x16_bf16):
-//  * a block of 4 waves owns 128 queries; each wave owns 32 queries, held
+//  * a block of 4 or 8 waves owns 128 or 256 queries (launch_fwd picks by
+//    head_dim and mode); each wave owns 32 queries, held
 //    as the B operand Q^T (8 fragments of 8 BF16 per lane, loaded once);
 //  * the block stages 64-key tiles of K and V in LDS, both row-major as they
 //    arrive (16-byte stores, padded rows);
@@ -235,11 +236,13 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
     if constexpr (!kSigmoid) l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 }
 
-// Grid (q_heads, S / 128, batch): blockIdx.y runs over query blocks, heaviest
-// first under the causal mask, and the head index varies fastest, so the
-// first wave of resident blocks takes the longest query blocks of every head.
-template <int MODE, int ROUTE, int HD>
-__global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
+// Grid (q_heads, S / (32 W), batch), W waves of 32 queries per block:
+// blockIdx.y runs over query blocks, heaviest first under the causal mask,
+// and the head index varies fastest, so the first wave of resident blocks
+// takes the longest query blocks of every head.
+template <int MODE, int ROUTE, int HD, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) flash_fwd_kernel(AttnParams p) {
+    constexpr int kBlockQ = 32 * W;  // queries per block
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kKStr = HD + 8;
     // two buffers: the next tile is written while the current one is read;
@@ -250,7 +253,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, c32 = lane & 31;
-    const int64_t nqb = p.seq / kAttnBlockQ;
+    const int64_t nqb = p.seq / kBlockQ;
     const int64_t head = blockIdx.x, b = blockIdx.z;
     const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
     const int64_t kvh = head / (p.hq / p.hkv);
@@ -258,7 +261,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     const uint16_t* kp = p.k + b * p.ks.b + kvh * p.ks.h;
     const uint16_t* vp = p.v + b * p.vs.b + kvh * p.vs.h;
     const int64_t kss = p.ks.s, vss = p.vs.s;
-    const int64_t q0 = qb * kAttnBlockQ + wave * 32;  // first query of this wave
+    const int64_t q0 = qb * kBlockQ + wave * 32;  // first query of this wave
     const int64_t qrow = q0 + c32;                     // this lane's query
 
     bf16x8_t qf[HD / 16];
@@ -274,7 +277,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
 
     // staging: K and V rows krow + kRowsPass j, 16 bytes at kcol
     constexpr int kChunks = HD / 8;                   // 16-byte chunks per row
-    constexpr int kRowsPass = 256 / kChunks;          // rows per pass
+    constexpr int kRowsPass = 64 * W / kChunks;       // rows per pass
     constexpr int kPasses = kAttnBlockK / kRowsPass;
     const int krow = tid / kChunks, kcol = (tid % kChunks) * 8;
     u32x4_t kr[kPasses], vr[kPasses];
@@ -296,7 +299,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(AttnParams p) {
     // + 4h, dims 16 ((lane / 16) % 2) + 4 (lane % 4) of a 32-dim slice
     const int vlane = (((lane & 15) >> 2) + 4 * h) * kVRowStr<HD>() + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    const int64_t nkb = p.causal ? (qb + 1) * (kAttnBlockQ / kAttnBlockK) : p.seq / kAttnBlockK;
+    const int64_t nkb = p.causal ? (qb + 1) * (kBlockQ / kAttnBlockK) : p.seq / kAttnBlockK;
     load(0);
     store(0);
     __syncthreads();
@@ -352,10 +355,27 @@ bool route_supported(int route) {
     return false;
 }
 
+// Waves (32 queries each) per block.  head_dim 128 runs 8-wave blocks (each
+// staged K / V tile serves 256 queries; one block per CU) except the modes
+// whose score program dominates the tile (softcap D4, the sigmoid polynomials),
+// which keep two independent 4-wave blocks per CU; head_dim 64 fits three
+// 4-wave blocks per CU and keeps them (measured on MI355X: 1.03-1.11x for the
+// softmax and hardware modes at D 128, 0.81-0.96x for 8 waves at D 64).
+template <int MODE>
+constexpr bool fwd_program_heavy() {
+    return MODE == kAttnSoftcapD4 || (attn_is_sigmoid(MODE) && MODE != kAttnSigmoidNative);
+}
+
 template <int MODE, int ROUTE>
 void launch_fwd(const AttnParams& prm, dim3 grid, hipStream_t st, int hd) {
-    if (hd == 64) hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 64>), grid, dim3(256), 0, st, prm);
-    else hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 128>), grid, dim3(256), 0, st, prm);
+    if (hd == 128 && !fwd_program_heavy<MODE>() && prm.seq % 256 == 0) {
+        const dim3 g(grid.x, (unsigned)(prm.seq / 256), grid.z);
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 128, 8>), g, dim3(512), 0, st, prm);
+    } else if (hd == 64) {
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 64, 4>), grid, dim3(256), 0, st, prm);
+    } else {
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 128, 4>), grid, dim3(256), 0, st, prm);
+    }
 }
 
 template <int MODE>

@@ -76,10 +76,13 @@ def _run(capi, cuda, q, k, v, mode, causal, scale, cap):
     return out.cpu().float()
 
 
+# S = 384 runs 4-wave (128-query) blocks, S = 512 the 8-wave (256-query)
+# blocks the launcher picks at head_dim 128 for S a multiple of 256
+@pytest.mark.parametrize("seq", [384, 512])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("mode", [m for m in MODES if m != "sigmoid_b3"])
-def test_attention_modes_match_reference(capi, oracle, cuda, mode, causal):
-    q, k, v = _inputs(1, 4, 2, 384, seed=MODES[mode] + 10 * causal)
+def test_attention_modes_match_reference(capi, oracle, cuda, mode, causal, seq):
+    q, k, v = _inputs(1, 4, 2, seq, seed=MODES[mode] + 10 * causal)
     scale = 1 / math.sqrt(128)
     # softcap 30 on scaled scores: raise the score spread so the cap bites
     if mode.startswith("softcap"):
