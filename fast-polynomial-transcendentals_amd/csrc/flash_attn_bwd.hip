@@ -13,7 +13,7 @@
 //    key per lane, so P and dS are ready-made B fragments of dV^T += dO^T P
 //    and dK^T += Q^T dS (the k index numbered in accumulator order, as in the
 //    forward);
-//  * dQ: a block owns 128 queries (32 per wave, Q and dO in registers) and
+//  * dQ: a block owns 128 or 256 queries (32 per wave, Q and dO in registers) and
 //    streams 32-key tiles of K and V: S^T = K Q^T and dP^T = V dO^T have
 //    one query per lane, dQ^T += K^T dS^T.
 // Tiles are staged row-major; the transposed operands Q^T, dO^T and K^T are
@@ -506,22 +506,21 @@ struct BwdKTile {
     uint16_t v[kBwdTile * k_row_stride<HD>()];
 };
 
-template <int MODE, int GRAD, int ROUTE, int HD>
-__global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
+template <int MODE, int GRAD, int ROUTE, int HD, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) flash_bwd_dq_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kRS = k_row_stride<HD>(), kChunks = HD / 8;
+    constexpr int kThreads = 64 * W, kBlockQ = 32 * W;  // queries per block
     __shared__ __align__(16) BwdKTile<HD> tiles[2];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, c32 = lane & 31;
-    const int pr = tid / kChunks, dc = tid % kChunks;
-    const bool stager = tid < 16 * kChunks;
-    const int64_t nqb = p.seq / kAttnBlockQ;
+    const int64_t nqb = p.seq / kBlockQ;
     const int64_t head = blockIdx.x, b = blockIdx.z;
     const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
     const int64_t kvh = head / (p.hq / p.hkv);
-    const int64_t q0 = qb * kAttnBlockQ + wave * 32;
+    const int64_t q0 = qb * kBlockQ + wave * 32;
     const int64_t qrow = q0 + c32;
     const float inv_cap = 1.0f / p.cap;
 
@@ -545,26 +544,49 @@ __global__ void __launch_bounds__(256, 2) flash_bwd_dq_kernel(AttnBwdParams p) {
 #pragma unroll
     for (int dt = 0; dt < HD / 32; ++dt) dqacc[dt] = (f32x16_t){};
 
-    const uint16_t* kp = p.k + b * p.ks.b + kvh * p.ks.h;
-    const uint16_t* vp = p.v + b * p.vs.b + kvh * p.vs.h;
-    u32x4_t ka, kb2, va, vb;
+    // staging: item i = (tensor, row pair pr, chunk dc) of a 32-key tile,
+    // tensor 0 = K, 1 = V; thread tid moves items tid + kThreads j
+    constexpr int kItems = 2 * 16 * kChunks;
+    constexpr int kPasses = (kItems + kThreads - 1) / kThreads;
+    const uint16_t* sbase[kPasses];  // this thread's first source row of each pass
+    int64_t sstride[kPasses];
+    int shalf[kPasses], soff[kPasses];  // tensor and LDS offset of each pass
+#pragma unroll
+    for (int j = 0; j < kPasses; ++j) {
+        const int i = tid + kThreads * j;
+        const int half = i / (16 * kChunks), st = i % (16 * kChunks);
+        const int pr = st / kChunks, dc = st % kChunks;
+        sstride[j] = half ? p.vs.s : p.ks.s;
+        sbase[j] = (half ? p.v + b * p.vs.b + kvh * p.vs.h : p.k + b * p.ks.b + kvh * p.ks.h) +
+                   (2 * pr) * sstride[j] + dc * 8;
+        shalf[j] = half;
+        soff[j] = 2 * pr * kRS + dc * 8;
+    }
+    auto active = [&](int j) { return kItems % kThreads == 0 || tid + kThreads * j < kItems; };
+    u32x4_t ra[kPasses], rb2[kPasses];
     auto load = [&](int64_t k0) {
-        if (!stager) return;
-        const uint16_t* kr = kp + (k0 + 2 * pr) * p.ks.s + dc * 8;
-        const uint16_t* vr = vp + (k0 + 2 * pr) * p.vs.s + dc * 8;
-        ka = *reinterpret_cast<const u32x4_t*>(kr);
-        kb2 = *reinterpret_cast<const u32x4_t*>(kr + p.ks.s);
-        va = *reinterpret_cast<const u32x4_t*>(vr);
-        vb = *reinterpret_cast<const u32x4_t*>(vr + p.vs.s);
+#pragma unroll
+        for (int j = 0; j < kPasses; ++j) {
+            if (active(j)) {
+                const uint16_t* r = sbase[j] + k0 * sstride[j];
+                ra[j] = *reinterpret_cast<const u32x4_t*>(r);
+                rb2[j] = *reinterpret_cast<const u32x4_t*>(r + sstride[j]);
+            }
+        }
     };
     auto store = [&](int buf) {
-        if (!stager) return;
         BwdKTile<HD>& t = tiles[buf];
-        store_rows<kRS>(t.k, pr, dc, ka, kb2);
-        store_rows<kRS>(t.v, pr, dc, va, vb);
+#pragma unroll
+        for (int j = 0; j < kPasses; ++j) {
+            if (active(j)) {
+                uint16_t* dst = (shalf[j] ? t.v : t.k) + soff[j];
+                *reinterpret_cast<u32x4_t*>(dst) = ra[j];
+                *reinterpret_cast<u32x4_t*>(dst + kRS) = rb2[j];
+            }
+        }
     };
 
-    const int64_t nkt = p.causal ? (qb + 1) * (kAttnBlockQ / kBwdTile) : p.seq / kBwdTile;
+    const int64_t nkt = p.causal ? (qb + 1) * (kBlockQ / kBwdTile) : p.seq / kBwdTile;
     load(0);
     store(0);
     __syncthreads();
@@ -653,7 +675,16 @@ void launch_bwd_hd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
                            (const float*)prm.dkv_ws, prm.dk, prm.dv, prm.dks, prm.dvs, batch, prm.hq,
                            prm.hkv, prm.seq);
     }
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD>), grid, dim3(256), 0, st, prm);
+    // waves (32 queries each) per dQ block: 8 (each staged K / V tile serves
+    // 256 queries) for the hardware softmax and sigmoid modes at head_dim
+    // 128, 4 otherwise (measured on MI355X: +2-4 % and -1-3 % respectively)
+    constexpr int kQW = HD == 128 && (MODE == kAttnSoftmaxNative || MODE == kAttnSigmoidNative) ? 8 : 4;
+    if (prm.seq % (32 * kQW) == 0) {
+        const dim3 qgrid((unsigned)prm.hq, (unsigned)(prm.seq / (32 * kQW)), (unsigned)batch);
+        hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, kQW>), qgrid, dim3(64 * kQW), 0, st, prm);
+    } else {
+        hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, 4>), grid, dim3(256), 0, st, prm);
+    }
 }
 
 template <int MODE, int GRAD, int ROUTE>
