@@ -220,7 +220,7 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
             bf16x8_t pf;
 #pragma unroll
             for (int e = 0; e < 8; ++e) pf[e] = (__bf16)pr[e];
-                // V^T fragment of dims dt*32 + (lane % 32), keys kt*32 + cc*16 + 4h
+            // V^T fragment of dims dt*32 + (lane % 32), keys kt*32 + cc*16 + 4h
             // + {0..3, 8..11}: two transposing reads of the row-major V tile
             // (vrow points at this lane's source chunk of the first)
 #pragma unroll
