@@ -43,7 +43,6 @@ enum AttnGrad : int {
 };
 
 constexpr int kBwdTile = 32;              // queries (dK/dV) or keys (dQ) per staged tile
-constexpr int kRouteRuntime = -1;
 
 struct AttnBwdParams {
     const uint16_t* q;
@@ -59,7 +58,6 @@ struct AttnBwdParams {
     AttnStrides qs, ks, vs, dos, dqs, dks, dvs;
     int64_t hq, hkv, seq;
     float scale, cap, sig_bias;
-    int route;  // routed exp2: a key takes the polynomial when route_slot(key) % route < 4
     int causal;
 };
 
@@ -76,27 +74,36 @@ constexpr int exp2_kind() {
     return MODE == kAttnSoftmaxExp2D2 ? kExp2D2 : MODE == kAttnSoftmaxExp2D3 ? kExp2D3 : kExp2Pwl2;
 }
 
-// Probability and gradient w.r.t. the raw dot product (q.k) of two scores.
+// Probability and gradient w.r.t. the raw dot product (q.k) of two scores
+// (two queries of one key, or two keys whose routing slots share a group of
+// four, so one routing decision covers both).
 // a: raw dot products; dp: dO.v; lse2: log-sum-exp in log2 units; dl: D;
-// poly: the key takes the exp2 polynomial (routed modes).
+// poly: the key takes the exp2 polynomial (routed modes); any_poly: some
+// lane of the wave takes it (wave-uniform), otherwise only the hardware
+// exp2 is evaluated.
 template <int MODE, int GRAD, int ROUTE>
 __device__ __forceinline__ void score_grad2(const AttnBwdParams& p, float inv_cap, float a0, float a1,
                                             float dp0, float dp1, float lse0, float lse1, float dl0,
-                                            float dl1, bool poly0, bool poly1, float& p0, float& p1,
+                                            float dl1, bool poly, bool any_poly, float& p0, float& p1,
                                             float& ds0, float& ds1) {
-    auto ex2 = [&](float x, bool poly) {
-        if constexpr (attn_has_exp2_program(MODE) && ROUTE == 4) {
-            return exp2_lane<exp2_kind<MODE>()>(x);
-        } else if constexpr (attn_has_exp2_program(MODE) && ROUTE == kRouteRuntime) {
-            return poly ? exp2_lane<exp2_kind<MODE>()>(x) : __builtin_amdgcn_exp2f(x);
-        } else {
-            return __builtin_amdgcn_exp2f(x);
-        }
-    };
     if constexpr (attn_is_plain_softmax(MODE)) {
         const float sl = p.scale * kLog2e;
-        p0 = ex2(__builtin_fmaf(a0, sl, -lse0), poly0);
-        p1 = ex2(__builtin_fmaf(a1, sl, -lse1), poly1);
+        const float x0 = __builtin_fmaf(a0, sl, -lse0), x1 = __builtin_fmaf(a1, sl, -lse1);
+        if constexpr (attn_has_exp2_program(MODE) && ROUTE == 4) {
+            p0 = exp2_lane<exp2_kind<MODE>()>(x0);
+            p1 = exp2_lane<exp2_kind<MODE>()>(x1);
+        } else if constexpr (attn_has_exp2_program(MODE) && ROUTE > 4) {
+            if (any_poly) {
+                p0 = poly ? exp2_lane<exp2_kind<MODE>()>(x0) : __builtin_amdgcn_exp2f(x0);
+                p1 = poly ? exp2_lane<exp2_kind<MODE>()>(x1) : __builtin_amdgcn_exp2f(x1);
+            } else {
+                p0 = __builtin_amdgcn_exp2f(x0);
+                p1 = __builtin_amdgcn_exp2f(x1);
+            }
+        } else {
+            p0 = __builtin_amdgcn_exp2f(x0);
+            p1 = __builtin_amdgcn_exp2f(x1);
+        }
         ds0 = p0 * (dp0 - dl0) * p.scale;
         ds1 = p1 * (dp1 - dl1) * p.scale;
     } else if constexpr (MODE == kAttnSoftcapNative) {
@@ -290,10 +297,17 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     const int64_t head = blockIdx.x, kb = blockIdx.y, b = blockIdx.z;
     const int64_t group = p.hq / p.hkv;
     const int64_t kvh = head / group;
-    const int64_t key0 = kb * kKeys + wave * 16;  // first key of this wave
+    // first key of this wave: with 8 waves the 16-key groups are permuted
+    // (wave w -> group (w >> 1) | 4 (w & 1)) so that the two groups of a
+    // 128-key block whose keys take the routed exp2 at route 32 (the first of
+    // each 64) sit on different SIMDs
+    const int kgroup = W == 8 ? ((wave >> 1) | ((wave & 1) << 2)) : wave;
+    const int64_t key0 = kb * kKeys + kgroup * 16;
     const int64_t key = key0 + kl;                // this lane's key
     const float inv_cap = 1.0f / p.cap;
-    const bool poly_key = ROUTE == kRouteRuntime && route_slot(key) % p.route < 4;
+    const bool poly_key = ROUTE > 4 && route_slot(key) % ROUTE < 4;
+    // with route 32 three waves in four hold no routed key
+    const bool wave_poly = __builtin_amdgcn_ballot_w64(poly_key) != 0;
 
     bf16x8_t kf[HD / 32], vf[HD / 32];
     {
@@ -415,7 +429,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
                     const int e = 4 * rb + r;
                     score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[rb][r], sacc[rb][r + 1], pacc[rb][r],
                                                    pacc[rb][r + 1], lse[e], lse[e + 1], del[e], del[e + 1],
-                                                   poly_key, poly_key, pr_[e], pr_[e + 1], ds[e], ds[e + 1]);
+                                                   poly_key, wave_poly, pr_[e], pr_[e + 1], ds[e], ds[e + 1]);
                 }
             if (p.causal && q0 < key0 + 15) {
                 const int diag = (int)(key - q0) - 4 * g;  // masked when diag > 16 rb + r
@@ -612,18 +626,21 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
             const bool need_mask = p.causal && k0 + 31 > q0;
             const int diag = (int)(k0 - qrow) + 4 * h;  // masked when diag + 8 (r/4) + r%4 > 0
             float pr_[16], ds[16];
+            // keys k0 + 8 (r/4) + 4h + r%4 and the next: the routing slot
+            // 16 (bit 5) + 4 (bits 3-4) + bits 0-1 ignores key bit 2 (h) and
+            // the pair shares a group of four, so with the tile parity (key
+            // bit 5) fixed the decision is a compile-time constant per pair
+            auto scores = [&](auto par_c) {
+                constexpr int kPar = decltype(par_c)::value;
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                bool poly0 = false, poly1 = false;
-                if constexpr (ROUTE == kRouteRuntime) {
-                    const int64_t key = k0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    poly0 = route_slot(key) % p.route < 4;
-                    poly1 = route_slot(key + 1) % p.route < 4;
+                for (int r = 0; r < 16; r += 2) {
+                    const bool poly = ROUTE > 4 && (16 * kPar + 4 * (r >> 2) + (r & 3)) % (ROUTE > 4 ? ROUTE : 1) < 4;
+                    score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[r], sacc[r + 1], pacc[r], pacc[r + 1], lse2,
+                                                   lse2, dl, dl, poly, poly, pr_[r], pr_[r + 1], ds[r], ds[r + 1]);
                 }
-                score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[r], sacc[r + 1], pacc[r], pacc[r + 1], lse2,
-                                               lse2, dl, dl, poly0, poly1, pr_[r], pr_[r + 1], ds[r],
-                                               ds[r + 1]);
-            }
+            };
+            if (ROUTE > 4 && ((k0 >> 5) & 1)) scores(std::integral_constant<int, 1>{});
+            else scores(std::integral_constant<int, 0>{});
             if (need_mask) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
@@ -695,9 +712,18 @@ void launch_bwd(const AttnBwdParams& prm, int64_t batch, hipStream_t st, int hd)
 
 template <int MODE>
 void launch_bwd_routed(const AttnBwdParams& prm, int64_t batch, hipStream_t st, int route, int hd) {
-    if (route == 0) launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, st, hd);
-    else if (route == 4) launch_bwd<MODE, kGradNatural, 4>(prm, batch, st, hd);
-    else launch_bwd<MODE, kGradNatural, kRouteRuntime>(prm, batch, st, hd);
+    switch (route) {
+        case 0: launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, st, hd); break;
+        case 6: launch_bwd<MODE, kGradNatural, 6>(prm, batch, st, hd); break;
+        case 8: launch_bwd<MODE, kGradNatural, 8>(prm, batch, st, hd); break;
+        case 10: launch_bwd<MODE, kGradNatural, 10>(prm, batch, st, hd); break;
+        case 12: launch_bwd<MODE, kGradNatural, 12>(prm, batch, st, hd); break;
+        case 16: launch_bwd<MODE, kGradNatural, 16>(prm, batch, st, hd); break;
+        case 20: launch_bwd<MODE, kGradNatural, 20>(prm, batch, st, hd); break;
+        case 24: launch_bwd<MODE, kGradNatural, 24>(prm, batch, st, hd); break;
+        case 32: launch_bwd<MODE, kGradNatural, 32>(prm, batch, st, hd); break;
+        default: launch_bwd<MODE, kGradNatural, 4>(prm, batch, st, hd); break;
+    }
 }
 
 bool bwd_stride_ok(const AttnStrides& t) {
@@ -762,8 +788,7 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
     AttnBwdParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
                       sig ? nullptr : lse, sig ? nullptr : delta, (uint16_t*)dq, (uint16_t*)dk,
                       (uint16_t*)dv, grouped ? dkv_workspace : nullptr, st[0], st[1], st[2], st[4], st[5], st[6], st[7], q_heads, kv_heads,
-                      seq, scale, cap > 0.0f ? cap : 1.0f, sigmoid_bias, exp2_route > 0 ? exp2_route : 4,
-                      causal != 0};
+                      seq, scale, cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0};
     switch (mode) {
         case kAttnSoftmaxNative: launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, hst, hd); break;
         case kAttnSoftmaxExp2D2: launch_bwd_routed<kAttnSoftmaxExp2D2>(prm, batch, hst, exp2_route, hd); break;

@@ -86,7 +86,8 @@ def _close(got, ref, rel=2.5e-2):
 
 CASES = [
     ("softmax_native", 0, 0), ("softmax_d2", 0, 4), ("softmax_d2", 0, 32), ("softmax_d3", 0, 4),
-    ("softmax_d3", 0, 12), ("softmax_pwl2", 0, 4), ("softcap_native", 0, 0), ("softcap_d4", 1, 0),
+    ("softmax_d3", 0, 12), ("softmax_pwl2", 0, 4), ("softmax_d2", 0, 6), ("softmax_pwl2", 0, 10),
+    ("softcap_native", 0, 0), ("softcap_d4", 1, 0),
     ("softcap_d4", 2, 0), ("softcap_d4", 3, 0), ("sigmoid_native", 0, 0), ("sigmoid_d3", 0, 0),
     ("sigmoid_d6", 0, 0),
 ]
