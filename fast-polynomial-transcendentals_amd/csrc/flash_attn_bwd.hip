@@ -225,12 +225,19 @@ __device__ __forceinline__ bf16x8_t to_frag(const float (&x)[16], int cc) {
 // dK / dV
 // ---------------------------------------------------------------------------
 
-template <int HD>
+// QT queries per staged dK/dV tile (a multiple of 32, processed as 32-query
+// chunks): 64 for the softmax modes (half the barriers and staging rounds
+// per query; 1.01-1.04x), 32 for sigmoid attention, whose 4-wave blocks would
+// lose a resident block to the larger tile (measured on MI355X).
+template <int MODE>
+constexpr int dkdv_query_tile() { return attn_is_sigmoid(MODE) ? 32 : 64; }
+
+template <int HD, int QT>
 struct BwdQTile {
-    uint16_t q[kBwdTile * q_row_stride<HD>()];
-    uint16_t dout[kBwdTile * q_row_stride<HD>()];
-    float lse2[kBwdTile];
-    float delta[kBwdTile];
+    uint16_t q[QT * q_row_stride<HD>()];
+    uint16_t dout[QT * q_row_stride<HD>()];
+    float lse2[QT];
+    float delta[QT];
 };
 
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
@@ -286,7 +293,8 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kRS = q_row_stride<HD>(), kChunks = HD / 8;
     constexpr int kThreads = 64 * W, kKeys = 16 * W;  // keys per block
-    __shared__ __align__(16) BwdQTile<HD> tiles[2];
+    constexpr int kQT = dkdv_query_tile<MODE>();
+    __shared__ __align__(16) BwdQTile<HD, kQT> tiles[2];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -325,14 +333,14 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
 
     // query tiles of this head, from the block's first key on under the
     // causal mask
-    const int64_t qt0 = p.causal ? kb * (kKeys / kBwdTile) : 0;
-    const int64_t nit = p.seq / kBwdTile - qt0;
+    const int64_t qt0 = p.causal ? kb * kKeys / kQT : 0;
+    const int64_t nit = p.seq / kQT - qt0;
 
     // staging: item i = (tensor, row pair pr, chunk dc) of a tile, tensor 0 =
     // Q, 1 = dO; thread tid moves items tid + kThreads j (rows 2 pr, 2 pr + 1,
     // 16 bytes at 8 dc); the first 32 threads of each half of the block load
     // lse and D (two different waves)
-    constexpr int kItems = 2 * 16 * kChunks;
+    constexpr int kItems = 2 * (kQT / 2) * kChunks;
     constexpr int kPasses = (kItems + kThreads - 1) / kThreads;
     const uint16_t* sbase[kPasses];  // this thread's first source row of each pass
     int64_t sstride[kPasses];
@@ -340,7 +348,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
 #pragma unroll
     for (int j = 0; j < kPasses; ++j) {
         const int i = tid + kThreads * j;
-        const int half = i / (16 * kChunks), st = i % (16 * kChunks);
+        const int half = i / ((kQT / 2) * kChunks), st = i % ((kQT / 2) * kChunks);
         const int pr = st / kChunks, dc = st % kChunks;
         sstride[j] = half ? p.dos.s : p.qs.s;
         sbase[j] = (half ? p.dout + b * p.dos.b + head * p.dos.h : p.q + b * p.qs.b + head * p.qs.h) +
@@ -352,7 +360,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     u32x4_t ra[kPasses], rb2[kPasses];
     float row_r = 0.0f;
     auto load = [&](int64_t it) {
-        const int64_t q0 = (qt0 + it) * kBwdTile;
+        const int64_t q0 = (qt0 + it) * kQT;
 #pragma unroll
         for (int j = 0; j < kPasses; ++j) {
             if (active(j)) {
@@ -362,14 +370,14 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
             }
         }
         if constexpr (!kSigmoid) {
-            if (tid % (kThreads / 2) < kBwdTile) {
+            if (tid % (kThreads / 2) < kQT) {
                 const int64_t i = (b * p.hq + head) * p.seq + q0 + tid % (kThreads / 2);
                 row_r = tid >= kThreads / 2 ? p.delta[i] : p.lse[i] * kLog2e;
             }
         }
     };
     auto store = [&](int buf) {
-        BwdQTile<HD>& t = tiles[buf];
+        BwdQTile<HD, kQT>& t = tiles[buf];
 #pragma unroll
         for (int j = 0; j < kPasses; ++j) {
             if (active(j)) {
@@ -379,7 +387,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
             }
         }
         if constexpr (!kSigmoid) {
-            if (tid % (kThreads / 2) < kBwdTile) (tid >= kThreads / 2 ? t.delta : t.lse2)[tid % (kThreads / 2)] = row_r;
+            if (tid % (kThreads / 2) < kQT) (tid >= kThreads / 2 ? t.delta : t.lse2)[tid % (kThreads / 2)] = row_r;
         }
     };
 
@@ -390,16 +398,19 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
         const int buf = (int)(it & 1);
         const bool more = it + 1 < nit;
         if (more) load(it + 1);
-        const int64_t q0 = (qt0 + it) * kBwdTile;
-        if (!p.causal || q0 + kBwdTile - 1 >= key0) {  // some query of the tile sees a key of the wave
-            const BwdQTile<HD>& t = tiles[buf];
+        const BwdQTile<HD, kQT>& t = tiles[buf];
+        // the tile's 32-query chunks in turn (rows 32 sc ..)
+#pragma unroll
+        for (int sc = 0; sc < kQT / 32; ++sc) {
+        const int64_t q0 = (qt0 + it) * kQT + 32 * sc;
+        if (!p.causal || q0 + 31 >= key0) {  // some query of the chunk sees a key of the wave
             f32x4v_t sacc[2], pacc[2];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
                 sacc[rb] = pacc[rb] = (f32x4v_t){};
 #pragma unroll
                 for (int c = 0; c < HD / 32; ++c) {
-                    const int off = (16 * rb + kl) * kRS + 32 * c + 8 * g;
+                    const int off = (32 * sc + 16 * rb + kl) * kRS + 32 * c + 8 * g;
                     sacc[rb] = mfma16(*reinterpret_cast<const bf16x8_t*>(t.q + off), kf[c], sacc[rb]);
                     pacc[rb] = mfma16(*reinterpret_cast<const bf16x8_t*>(t.dout + off), vf[c], pacc[rb]);
                 }
@@ -409,8 +420,8 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
             if constexpr (!kSigmoid) {
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb) {
-                    const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(t.lse2 + 16 * rb + 4 * g);
-                    const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(t.delta + 16 * rb + 4 * g);
+                    const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(t.lse2 + 32 * sc + 16 * rb + 4 * g);
+                    const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(t.delta + 32 * sc + 16 * rb + 4 * g);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         lse[4 * rb + r] = l4[r];
@@ -443,12 +454,13 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
                 pf[e] = (__bf16)pr_[e];
                 sf[e] = (__bf16)ds[e];
             }
-            const int tr_off = (4 * g + (kl >> 2)) * kRS + 4 * (kl & 3);
+            const int tr_off = (32 * sc + 4 * g + (kl >> 2)) * kRS + 4 * (kl & 3);
 #pragma unroll
             for (int dt = 0; dt < HD / 16; ++dt) {
                 dvacc[dt] = mfma16(frag_tr16<HD>(t.dout + tr_off, dt), pf, dvacc[dt]);
                 dkacc[dt] = mfma16(frag_tr16<HD>(t.q + tr_off, dt), sf, dkacc[dt]);
             }
+        }
         }
         if (more) store(buf ^ 1);
         __syncthreads();
