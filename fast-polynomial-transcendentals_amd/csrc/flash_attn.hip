@@ -4,15 +4,18 @@
 // extras/paper/manuscript/main.tex:483-509), whose kernel is not part of the
 // reference tree.
 //
-// Modes (AttnMode): softmax with hardware exp2 (v_exp_f32), the B5 D2 "safe"
-// or FA4 D3 exp2 polynomial; tanh softcap (B2) cap*tanh(s/cap) with FP32
-// hardware tanh or the D4 BF16 program, followed by the hardware softmax;
-// sigmoid attention p = sigmoid(s - ln n) with hardware exp/rcp or the B3
-// direct D3 program (fitted for n = 4096), unnormalised O = P V.
+// Modes (AttnMode): softmax with hardware exp2 (v_exp_f32), the B5 D2 "safe",
+// FA4 D3 or PWL2 exp2 polynomial (every exponent, or four of every ROUTE);
+// tanh softcap (B2) cap*tanh(s/cap) with FP32 hardware tanh or the D4 BF16
+// program, followed by the hardware softmax; sigmoid attention
+// p = sigmoid(s + bias) with hardware exp/rcp, the B3 direct D3 or B3-D2
+// program (fitted for n = 4096) or the BF16 sigmoid D3-D6 programs,
+// unnormalised O = P V.
 //
-// Layout: Q [B, Hq, S, 128], K and V [B, Hkv, S, 128], O [B, Hq, S, 128],
-// BF16, grouped-query heads (Hq a multiple of Hkv), S a multiple of 128,
-// optional causal mask.  s = q.k * scale.
+// Layout: Q, O [B, Hq, S, D] and K, V [B, Hkv, S, D] at any element strides
+// with a contiguous head dimension (D 64 or 128), BF16, grouped-query heads
+// (Hq a multiple of Hkv), S a multiple of 128, optional causal mask.
+// s = q.k * scale.
 //
 // Design (all-transposed MFMA formulation, v_mfma_f32_32x32x16_bf16):
 //  * a block of 4 or 8 waves owns 128 or 256 queries (launch_fwd picks by

@@ -5,9 +5,9 @@
 //
 // Three kernels (four with grouped heads), no atomics:
 //  * delta: D[q] = sum_d dO[q][d] O[q][d] (FP32), for the softmax modes;
-//  * dK/dV: a block of 8 waves owns 128 keys of one query head (16 per
-//    wave, K and V held in registers, 16x16x32 MFMA) and streams 32-query
-//    tiles of Q and dO (+ lse, D) through LDS; with grouped-query
+//  * dK/dV: a block of 8 (4) waves owns 128 (64) keys of one query head (16
+//    per wave, K and V held in registers, 16x16x32 MFMA) and streams 64- (32-)
+//    query tiles of Q and dO (+ lse, D) through LDS; with grouped-query
 //    heads each block writes FP32 partials and a reduction kernel sums the
 //    group (deterministically); S = Q K^T and dP = dO V^T come out with one
 //    key per lane, so P and dS are ready-made B fragments of dV^T += dO^T P
@@ -275,9 +275,10 @@ __device__ __forceinline__ bf16x8_t frag_tr32(const uint16_t* src, int dt, int c
     return __builtin_bit_cast(bf16x8_t, w);
 }
 
-// One block = 8 waves = 128 keys of one query head, 16 keys per wave, all
-// products on v_mfma_f32_16x16x32_bf16 (A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
-// C register r -> row 4(l/16) + r, column l%16):
+// One block = W waves = 16 W keys of one query head, 16 keys per wave (8
+// waves for the softmax modes, 4 for sigmoid attention; the launcher picks),
+// all products on v_mfma_f32_16x16x32_bf16 (A[l%16][8(l/16)+e],
+// B[8(l/16)+e][l%16], C register r -> row 4(l/16) + r, column l%16):
 //  * S = Q K^T and dP = dO V^T per 16-query row block rb: lane (g = l/16,
 //    key l%16) holds queries 16 rb + 4g + r;
 //  * dV^T += dO^T P and dK^T += Q^T dS take P / dS as B fragments with
