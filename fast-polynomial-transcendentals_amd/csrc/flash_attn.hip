@@ -186,6 +186,11 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
         mt = __builtin_fmaxf(mt, __shfl_xor(mt, 32)) * sl;
         // lanes c and c + 32 hold the same query and take the same decision
         const bool move = mt > m + kRescaleThreshold;
+        // scheduling fences around the rare rescale: without them the
+        // scheduler interleaves it with the surrounding code and the register
+        // allocator then copies all of O on the common no-rescale path
+        // (head_dim 64: 34 moves per tile)
+        __builtin_amdgcn_sched_barrier(0);
         if (__any(move)) {
             const float m_use = move ? mt : m;
             const float alpha = __builtin_amdgcn_exp2f(m - m_use);
@@ -194,6 +199,7 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
 #pragma unroll
             for (int dt = 0; dt < HD / 32; ++dt) oacc[dt] *= alpha;
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
     // ---- P, then O^T += V^T P^T, eight keys at a time ----
 #pragma unroll
