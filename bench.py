@@ -721,7 +721,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the elementwise path needs no cross-GPU exchange; see DESIGN.md for sharding).",
+              "(the elementwise path needs no cross-GPU exchange: each GPU would run the same "
+              "kernel on its own contiguous shard).",
               file=sys.stderr)
         sys.exit(2)
 
