@@ -110,6 +110,23 @@ def test_backward_matches_reference(capi, oracle, cuda, mode, grad, route, causa
         assert ok, (mode, grad, route, causal, name, info)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("mode,route", [("softmax_native", 0), ("softmax_d2", 32)])
+def test_backward_batched_grouped(capi, oracle, cuda, mode, route, d):
+    """Two sequences, four query heads per KV head: the per-(batch, query
+    head) dK / dV partials and their group reduction."""
+    q, k, v, do = _inputs(2, 8, 2, 256, 400 + d + route, d=d)
+    scale = 1 / math.sqrt(d)
+    out, lse = fwd(capi, cuda, q, k, v, mode, True, scale, route=route if route else 4)
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, mode, 0, True, scale, route=route)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, mode, 0, True, scale, 30.0, route,
+                               _bias(mode, 256))
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert torch.isfinite(got).all(), name
+        ok, info = _close(got, ref)
+        assert ok, (mode, d, name, info)
+
+
 D64_CASES = [("softmax_native", 0, 0), ("softmax_d2", 0, 32), ("softcap_d4", 1, 0), ("sigmoid_native", 0, 0)]
 
 
