@@ -706,9 +706,11 @@ void launch_bwd_hd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
                            prm.hkv, prm.seq);
     }
     // waves (32 queries each) per dQ block: 8 (each staged K / V tile serves
-    // 256 queries) for the hardware softmax and sigmoid modes at head_dim
-    // 128, 4 otherwise (measured on MI355X: +2-4 % and -1-3 % respectively)
-    constexpr int kQW = HD == 128 && (MODE == kAttnSoftmaxNative || MODE == kAttnSigmoidNative) ? 8 : 4;
+    // 256 queries) for plain softmax (hardware or routed exp2) and hardware
+    // sigmoid at head_dim 128, 4 otherwise (measured on MI355X: +2-6 % for
+    // the dQ kernel of those modes, -1-3 % for softcap and the sigmoid
+    // polynomials)
+    constexpr int kQW = HD == 128 && (attn_is_plain_softmax(MODE) || MODE == kAttnSigmoidNative) ? 8 : 4;
     if (prm.seq % (32 * kQW) == 0) {
         const dim3 qgrid((unsigned)prm.hq, (unsigned)(prm.seq / (32 * kQW)), (unsigned)batch);
         hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, kQW>), qgrid, dim3(64 * kQW), 0, st, prm);
