@@ -89,3 +89,49 @@ struct CopyProg {
     __device__ __forceinline__ static uint32_t eval(uint32_t x) { return x; }
 };
 PT_UNARY(spline_hip_copy16, (CopyProg))
+
+// Read-only and write-only streams with the driver's launch shape (one
+// 16-byte vector per thread, 256-thread blocks, non-temporal): the two
+// one-directional ceilings that bracket a 1:1 read/write stream.  The read
+// kernel folds every word into an XOR and stores it only when it equals a
+// constant, so the loads cannot be removed and (almost) nothing is written.
+namespace {
+
+constexpr uint32_t kReadSinkKey = 0x9e3779b9u;
+
+__global__ void __launch_bounds__(kBlock) read16_kernel(const void* in, uint32_t* sink,
+                                                        int64_t n_vec) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    uint32_t acc = 0;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n_vec; i += stride) {
+        const Vec4 v = ld16<true>(in, i);
+        acc ^= v.w[0] ^ v.w[1] ^ v.w[2] ^ v.w[3];
+    }
+    if (acc == kReadSinkKey) sink[0] = acc;
+}
+
+__global__ void __launch_bounds__(kBlock) fill16_kernel(void* out, int64_t n_vec, uint32_t word) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n_vec; i += stride)
+        st16<true>(out, i, Vec4{{word, word, word, word}});
+}
+
+}  // namespace
+
+extern "C" int spline_hip_read16(void* sink, const void* in, int64_t size, void* stream) {
+    if (bad_args(size, {sink, in}) || !aligned16(in)) return hipErrorInvalidValue;
+    const int64_t n_vec = size >> 3;
+    if (n_vec == 0) return hipSuccess;
+    hipLaunchKernelGGL(read16_kernel, dim3((unsigned)grid_one_pass(n_vec)), dim3(kBlock), 0,
+                       hs(stream), in, (uint32_t*)sink, n_vec);
+    return hipGetLastError();
+}
+
+extern "C" int spline_hip_fill16(void* out, int64_t size, uint32_t word, void* stream) {
+    if (bad_args(size, {out}) || !aligned16(out)) return hipErrorInvalidValue;
+    const int64_t n_vec = size >> 3;
+    if (n_vec == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill16_kernel, dim3((unsigned)grid_one_pass(n_vec)), dim3(kBlock), 0,
+                       hs(stream), out, n_vec, word);
+    return hipGetLastError();
+}

@@ -34,6 +34,26 @@ struct B3FwdOp {
     }
 };
 
+// Hardware control of B3 (FA4's sigmoid_variant="sfu", the "native" B3
+// component config, src/sfu_repro/fa4.py:687-693): p = sigmoid(x - ln 4096)
+// = 1 / (1 + 2^(12 - x log2 e)) in FP32 with v_exp_f32 / v_rcp_f32,
+// dy = p (1 - p), each rounded once to BF16.
+struct B3NativeOp {
+    static constexpr int NIN = 1, NOUT = 2;
+    __device__ __forceinline__ static void lane(float x, float& y, float& dy) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(-x, 1.44269504088896340736f, 12.0f));
+        y = __builtin_amdgcn_rcpf(1.0f + e);
+        dy = __builtin_fmaf(-y, y, y);
+    }
+    __device__ __forceinline__ static void pair(const uint32_t (&a)[1], uint32_t (&b)[2]) {
+        float y0, y1, d0, d1;
+        lane(bf_lo(a[0]), y0, d0);
+        lane(bf_hi(a[0]), y1, d1);
+        b[0] = pack_bf(y0, y1);
+        b[1] = pack_bf(d0, d1);
+    }
+};
+
 struct B3D2Op {
     static constexpr int NIN = 1, NOUT = 2;
     __device__ __forceinline__ static void pair(const uint32_t (&a)[1], uint32_t (&b)[2]) {
@@ -76,15 +96,19 @@ b3_f32_kernel(const float* __restrict__ s, uint16_t* __restrict__ y, uint16_t* _
     }
 }
 
+// Forward on the magnitudes (SoftcapConsts::mag_open), the scores' sign bits
+// written into the packed result (whose sign bits are zero).  Measured on
+// MI355X at [4,32,2048,2048]: 323 us against 335 us for the same program
+// with the sign carried through the lanes (the packed 16-bit clamp, sign
+// merge and unpack of the signed form cost 10 VALU per pair against 8).
 struct SoftcapFwdOp {
     static constexpr int NIN = 1, NOUT = 1;
     static constexpr bool kParams = true;  // prm[0] = cap, prm[1] = 1/cap (FP32)
     __device__ __forceinline__ static void pair(const uint32_t (&a)[1], uint32_t (&b)[1],
                                                 const float (&prm)[2]) {
-        const uint32_t u = pack_bf(bf_lo(a[0]) * prm[1], bf_hi(a[0]) * prm[1]);
-        float t0, t1;
-        SoftcapConsts::T::eval2(u, t0, t1);
-        b[0] = pack_bf(t0 * prm[0], t1 * prm[0]);
+        const uint32_t m = pack_bf(SoftcapConsts::mag_open(bf_lo(a[0]), prm[1], prm[0]),
+                                   SoftcapConsts::mag_open(bf_hi(a[0]), prm[1], prm[0]));
+        b[0] = (a[0] & 0x80008000u) | m;
     }
 };
 
@@ -107,9 +131,10 @@ struct SoftcapBwdOp {
     __device__ __forceinline__ static float deriv(float t) { return SoftcapConsts::deriv(t); }
     __device__ __forceinline__ static void pair(const uint32_t (&a)[2], uint32_t (&b)[1],
                                                 const float (&prm)[2]) {
-        const uint32_t u = pack_bf(bf_lo(a[1]) * prm[1], bf_hi(a[1]) * prm[1]);
-        const uint32_t t2 = u & 0x7fff7fffu;  // |u|; NaN magnitudes fail t < t_sat
-        b[0] = pack_bf(bf_lo(a[0]) * deriv(bf_lo(t2)), bf_hi(a[0]) * deriv(bf_hi(t2)));
+        // |u| per lane; NaN magnitudes fail t < t_sat
+        const float t0 = SoftcapConsts::abs_u(bf_lo(a[1]), prm[1]);
+        const float t1 = SoftcapConsts::abs_u(bf_hi(a[1]), prm[1]);
+        b[0] = pack_bf(bf_lo(a[0]) * deriv(t0), bf_hi(a[0]) * deriv(t1));
     }
 };
 
@@ -192,6 +217,13 @@ extern "C" int launch_flash_sigmoid_direct_d3_d4_bf16(void* y, void* dy, const v
 extern "C" int launch_flash_sigmoid_direct_d3_bf16(void* y, const void* scores, int64_t size,
                                                    void* stream) {
     return run1<B3FwdOp>(y, scores, size, stream);
+}
+
+extern "C" int launch_flash_sigmoid_native_bf16(void* y, void* dy, const void* scores,
+                                                int64_t size, void* stream) {
+    if (bad_args(size, {y, dy, scores})) return hipErrorInvalidValue;
+    Streams<1, 2> s{{scores}, {y, dy}};
+    return launch_pairwise<B3NativeOp>(s, size, hs(stream));
 }
 
 extern "C" int launch_flash_sigmoid_direct_d3_d4_f32_bf16(void* y, void* dy, const void* scores,

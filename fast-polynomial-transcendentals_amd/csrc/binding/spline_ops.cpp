@@ -334,7 +334,9 @@ std::vector<at::Tensor> flash_sigmoid_direct_d3_d4(at::Tensor scores) {
     return {y, dy};
 }
 
-std::vector<at::Tensor> flash_sigmoid_exp2_d2(at::Tensor scores) {
+using B3PairLauncher = int (*)(void*, void*, const void*, int64_t, void*);
+
+std::vector<at::Tensor> flash_sigmoid_pair(at::Tensor scores, B3PairLauncher fn) {
     CHECK_CUDA(scores);
     CHECK_CONTIGUOUS(scores);
     TORCH_CHECK(scores.scalar_type() == at::kBFloat16, "scores must be bfloat16");
@@ -342,10 +344,16 @@ std::vector<at::Tensor> flash_sigmoid_exp2_d2(at::Tensor scores) {
     at::Tensor y = at::empty_like(scores);
     at::Tensor dy = at::empty_like(scores);
     void* s = current_stream(scores);
-    check_launch(launch_flash_sigmoid_exp2_d2_bf16(y.data_ptr(), dy.data_ptr(), scores.data_ptr(),
-                                                   scores.numel(), s),
-                 s);
+    check_launch(fn(y.data_ptr(), dy.data_ptr(), scores.data_ptr(), scores.numel(), s), s);
     return {y, dy};
+}
+
+std::vector<at::Tensor> flash_sigmoid_exp2_d2(at::Tensor scores) {
+    return flash_sigmoid_pair(scores, launch_flash_sigmoid_exp2_d2_bf16);
+}
+
+std::vector<at::Tensor> flash_sigmoid_native(at::Tensor scores) {
+    return flash_sigmoid_pair(scores, launch_flash_sigmoid_native_bf16);
 }
 
 at::Tensor flash_sigmoid_direct_d3(at::Tensor scores) {
@@ -1351,4 +1359,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "B3-D2 sigmoid via range-reduced degree-2 exp2 (probability, derivative), BF16");
     m.def("flash_sigmoid_direct_d3_bf16", &flash_sigmoid_direct_d3,
           "B3 deployed direct-D3 probability (BF16)");
+    m.def("flash_sigmoid_native_bf16", &flash_sigmoid_native,
+          "B3 hardware control: sigmoid(s - ln 4096) and p (1 - p) via v_exp_f32 / v_rcp_f32");
 }

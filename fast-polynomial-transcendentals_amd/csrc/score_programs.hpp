@@ -104,6 +104,27 @@ struct SoftcapConsts {
         r = bfma(t, r, d0);
         return t < t_sat ? r : 0.0f;
     }
+
+    // |u| = bf16(|s| * (1/cap)) for a score s (FP32 holding a BF16 value):
+    // RNE is odd-symmetric, so this is the magnitude of u = bf16(s * (1/cap)).
+    __device__ __forceinline__ static float abs_u(float s, float inv_cap) {
+        return rbf(__builtin_fabsf(s) * inv_cap);
+    }
+
+    // The forward program on the magnitude, before its last rounding:
+    // |y| = bf16(cap * bf16(min(t * H(t), 1))), t = min(|u|, Lc).  Equal to
+    // the signed program sign(s) * bf16(cap * bf16(clamp(ts * H(t), -1, 1)))
+    // because every step is odd-symmetric and t * H(t) >= 0 on [0, Lc]; the
+    // caller restores the sign of s on the packed result.  The clamp is an
+    // unsigned minimum on the FP32 bits of |u| (low half zero): integer order
+    // is numeric order for non-negative patterns, and a NaN magnitude selects
+    // Lc, the rule of the signed program's packed 16-bit minimum.
+    __device__ __forceinline__ static float mag_open(float s, float inv_cap, float cap) {
+        const uint32_t tb = as_u32(abs_u(s, inv_cap));
+        const uint32_t lc = as_u32(bf16_value(T::P.lc));
+        const float t = as_f32(tb < lc ? tb : lc);
+        return rbf(__builtin_fminf(t * T::odd_horner(t), 1.0f)) * cap;
+    }
 };
 
 // ---------------------------------------------------------------------------

@@ -255,6 +255,12 @@ int launch_flash_sigmoid_direct_d3_d4_f32_bf16(void* y, void* dy, const void* sc
 /* Forward only (the first listing, main.tex:1041-1070). */
 int launch_flash_sigmoid_direct_d3_bf16(void* y, const void* scores, int64_t size,
                                         void* stream);
+/* Hardware control of B3: FA4's SFU sigmoid (sigmoid_variant="sfu", the
+ * "native" entry of b3_component_configs, src/sfu_repro/fa4.py:687-693),
+ * y = bf16(sigmoid(s - ln 4096)) via v_exp_f32 / v_rcp_f32 in FP32 and
+ * dy = bf16(p (1 - p)) from the FP32 probability. */
+int launch_flash_sigmoid_native_bf16(void* y, void* dy, const void* scores, int64_t size,
+                                     void* stream);
 /* B3-D2 sigmoid via a range-reduced degree-2 exp2 (FA4 sigmoid_degree == 2,
  * src/sfu_repro/fa4.py:469-476; model and coefficients from
  * autonumerics_zero/evolution/fit_flash_sigmoid_exp2_d2.py:55-143):
@@ -503,6 +509,13 @@ int spline_hip_grid_for(int64_t size, int streams, int64_t* grid_out, int* cus_o
  * as the unary launchers above.  Its time is the achievable ceiling a
  * 1-read/1-write stream of that size reaches on this device. */
 int spline_hip_copy16(void* out, const void* in, int64_t size, void* stream);
+/* Measurement helpers, no counterpart in the reference: the read-only and
+ * write-only ceilings of the same launch shape (non-temporal, one 16-byte
+ * vector per thread) over the first size/8*8 16-bit elements.  read16 reads
+ * `in` (16-byte aligned) and writes at most 4 bytes to `sink`; fill16
+ * writes `word` to every 32-bit word of `out` (16-byte aligned). */
+int spline_hip_read16(void* sink, const void* in, int64_t size, void* stream);
+int spline_hip_fill16(void* out, int64_t size, uint32_t word, void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,9 @@ def _f32_inputs(seed, n=1 << 18):
     return x.astype(np.float32)
 
 
-@pytest.mark.parametrize("cap", [30.0, 50.0])
+# caps below 1 and far above the scores cover the saturated and the
+# near-linear ends; the magnitude form must match the signed program for all.
+@pytest.mark.parametrize("cap", [30.0, 50.0, 1.0, 0.3, 7.5, 1000.0])
 def test_softcap_forward_exhaustive(capi, oracle, cuda, cap):
     s = oracle.all_bits()
     sd = _dev(s, "bf16", cuda)
@@ -36,7 +38,8 @@ def test_softcap_forward_exhaustive(capi, oracle, cuda, cap):
     assert_bits_equal(_host(y), oracle.softcap_fwd_bf16(s, cap), "bf16", f"softcap cap={cap}")
 
 
-def test_softcap_backward(capi, oracle, cuda):
+@pytest.mark.parametrize("cap", [30.0, 0.3, 1000.0])
+def test_softcap_backward(capi, oracle, cuda, cap):
     rng = np.random.default_rng(5)
     s = np.tile(oracle.all_bits(), 2)
     go = oracle.f32_to_bf16_bits(rng.standard_normal(s.size).astype(np.float32))
@@ -44,11 +47,11 @@ def test_softcap_backward(capi, oracle, cuda):
     sd, god = _dev(s, "bf16", cuda), _dev(go, "bf16", cuda)
     g = torch.empty_like(sd)
     rc = capi.launch_softcap_tanh_d4_bwd_bf16(capi.ptr(g), capi.ptr(god), capi.ptr(sd),
-                                              ctypes.c_int64(s.size), ctypes.c_float(30.0),
+                                              ctypes.c_int64(s.size), ctypes.c_float(cap),
                                               capi.stream())
     assert rc == 0
     torch.cuda.synchronize()
-    assert_bits_equal(_host(g), oracle.softcap_bwd_bf16(go, s, 30.0), "bf16", "softcap bwd")
+    assert_bits_equal(_host(g), oracle.softcap_bwd_bf16(go, s, cap), "bf16", f"softcap bwd cap={cap}")
 
 
 def test_softcap_config3_distribution(spline_ops, cuda):
@@ -114,3 +117,40 @@ def test_b3_exp2_d2_exhaustive(capi, oracle, cuda):
     want_y, want_dy = oracle.b3_exp2_d2_bf16(s, coeffs)
     assert_bits_equal(_host(y), want_y, "bf16", "B3-D2 y")
     assert_bits_equal(_host(dy), want_dy, "bf16", "B3-D2 dy")
+
+
+def _ulps_bf16(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    """ULP distance of BF16 bit patterns (sign-magnitude -> ordered integers)."""
+    def key(b):
+        b = b.astype(np.int32)
+        return np.where(b & 0x8000, -(b & 0x7FFF), b)
+    return np.abs(key(got) - key(want))
+
+
+def test_b3_native_control(capi, oracle, cuda):
+    """The B3 hardware control (v_exp_f32 / v_rcp_f32 in FP32, one RNE per
+    output) on every BF16 score: within one BF16 ULP of sigmoid(s - ln 4096)
+    and of p (1 - p), both correctly rounded from float64."""
+    s = oracle.all_bits()
+    x = oracle.bf16_bits_to_f32(s).astype(np.float64)
+    fin = np.isfinite(x)
+    sd = _dev(s, "bf16", cuda)
+    y, dy = torch.empty_like(sd), torch.empty_like(sd)
+    capi.call("launch_flash_sigmoid_native_bf16", y, dy, sd, s.size)
+    torch.cuda.synchronize()
+    with np.errstate(over="ignore"):
+        p = 1.0 / (1.0 + np.exp(-(x - np.log(4096.0))))
+    want_y = oracle.f32_to_bf16_bits(p.astype(np.float32))
+    gy, gdy = _host(y), _host(dy)
+    # FP32 denormal results flush: ULPs are counted where p is a normal number
+    norm = fin & (p >= 2.0 ** -120)
+    assert _ulps_bf16(gy[norm], want_y[norm]).max() <= 1
+    assert (np.abs(oracle.bf16_bits_to_f32(gy[fin & ~norm])) <= 2.0 ** -120).all()
+    # p (1 - p) cancels near p = 1, where the FP32 p (v_exp_f32, v_rcp_f32:
+    # a few FP32 ULPs) carries up to ~2^-22 absolute error; elsewhere the
+    # BF16 rounding of dy dominates
+    err = np.abs(oracle.bf16_bits_to_f32(gdy[fin]).astype(np.float64) - (p * (1 - p))[fin])
+    tol = 2.0 ** -8 * np.abs(p * (1 - p))[fin] + 2.0 ** -21
+    assert (err <= tol).all()
+    nan = np.isnan(x)
+    assert np.isnan(oracle.bf16_bits_to_f32(gy[nan])).all()
