@@ -27,6 +27,8 @@
 // and dq.k = dS * scale.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "flash_attn.hpp"
 #include "spline_ops_hip.h"
 
@@ -827,4 +829,74 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
         case kAttnSigmoidD6: launch_bwd<kAttnSigmoidD6, kGradNatural, 0>(prm, batch, hst, hd); break;
     }
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free backward: the delta rows and the grouped-head dK / dV
+// partials live in a file-scope device array instead of caller workspaces.
+// Every GPU the library runs on holds its own copy of the array (at its own
+// address) until the process ends.  Neither workspace needs clearing: the
+// delta kernel writes every row and the dK / dV kernel writes every partial
+// before the reduction reads it.  Calls that overlap on one GPU share the
+// array and race.
+// ---------------------------------------------------------------------------
+
+static __device__ __align__(256) unsigned char scratch[SPLINE_HIP_BWD_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device
+
+// Device address of this library's `scratch` on `dev`, looked up once per
+// device with that device current (the host-side name is only a stand-in).
+hipError_t scratch_address(int dev, void** ptr) {
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int cur = -1;
+        hipError_t e = hipGetDevice(&cur);
+        if (e != hipSuccess) return e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) {
+            const hipError_t r = hipSetDevice(cur);
+            if (e == hipSuccess) e = r;
+        }
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int launch_flash_attention_bwd_strided_bf16_noalloc(
+    void* dq, void* dk, void* dv, const void* q, const void* k, const void* v, const void* out,
+    const void* dout, const float* lse, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
+    int64_t head_dim, const int64_t* strides, int mode, int grad, int exp2_route, int causal, float scale,
+    float cap, float sigmoid_bias, void* stream) {
+    if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || (head_dim != 64 && head_dim != 128))
+        return hipErrorInvalidValue;
+    // delta rows (256-byte aligned), then the FP32 partials of grouped heads
+    const unsigned __int128 rows = (unsigned __int128)batch * (unsigned __int128)q_heads * (unsigned __int128)seq;
+    const unsigned __int128 delta_bytes = (rows * 4 + 255) / 256 * 256;
+    const unsigned __int128 ws_bytes = q_heads != kv_heads ? rows * (unsigned __int128)head_dim * 8 : 0;
+    if (delta_bytes + ws_bytes > (unsigned __int128)SPLINE_HIP_BWD_SCRATCH_BYTES) return hipErrorOutOfMemory;
+    int dev = -1;
+    hipError_t e = stream != nullptr ? hipStreamGetDevice(hs(stream), &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    void* base = nullptr;
+    if ((e = scratch_address(dev, &base)) != hipSuccess) return e;
+    float* delta = static_cast<float*>(base);
+    float* ws = q_heads != kv_heads
+                    ? reinterpret_cast<float*>(static_cast<unsigned char*>(base) + (size_t)delta_bytes)
+                    : nullptr;
+    return launch_flash_attention_bwd_strided_bf16(dq, dk, dv, delta, ws, q, k, v, out, dout, lse, batch,
+                                                   q_heads, kv_heads, seq, head_dim, strides, mode, grad,
+                                                   exp2_route, causal, scale, cap, sigmoid_bias, stream);
 }

@@ -497,6 +497,27 @@ int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float*
                                             int64_t seq, int64_t head_dim, const int64_t* strides,
                                             int mode, int grad, int exp2_route, int causal,
                                             float scale, float cap, float sigmoid_bias, void* stream);
+/* Allocation-free form of launch_flash_attention_bwd_strided_bf16: no
+ * counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results without `delta` and
+ * `dkv_workspace`: both live in a device array inside the library
+ * (SPLINE_HIP_BWD_SCRATCH_BYTES per GPU, held until the process ends), laid
+ * out as delta [B, Hq, S] FP32 (padded to 256 bytes), then with grouped heads
+ * (Hq > Hkv) the 2 * B * Hq * S * D FP32 dK / dV partials.  Returns
+ * hipErrorOutOfMemory (2) when those exceed SPLINE_HIP_BWD_SCRATCH_BYTES:
+ * the limit is B * Hq * S <= 16,777,216 query rows without grouped heads,
+ * and <= 65,280 (D = 128) or <= 130,055 (D = 64) with them.  Calls no
+ * allocator.  Calls that overlap on one GPU share the array and race: order
+ * them on one stream. */
+#define SPLINE_HIP_BWD_SCRATCH_BYTES (64ll << 20)
+int launch_flash_attention_bwd_strided_bf16_noalloc(void* dq, void* dk, void* dv, const void* q,
+                                                    const void* k, const void* v, const void* out,
+                                                    const void* dout, const float* lse, int64_t batch,
+                                                    int64_t q_heads, int64_t kv_heads, int64_t seq,
+                                                    int64_t head_dim, const int64_t* strides, int mode,
+                                                    int grad, int exp2_route, int causal, float scale,
+                                                    float cap, float sigmoid_bias, void* stream);
 
 /* ---- device/launch introspection --------------------------------------- */
 /* Number of compute units of the current device and the grid the
