@@ -270,24 +270,32 @@ def _ordered16(t):
     return torch.where(b < 0, -(b & 0x7FFF), b)
 
 
-def numerics(out, ref):
+def numerics(out, ref, where=None):
     """Error of a 16-bit output against an FP32 (or FP64) reference over the
-    elements whose reference is finite: max and mean |out - ref|, and max
-    ULPs (of the output format) from the reference rounded to that format.
-    NaN outputs where the reference is finite count as an infinite error."""
+    elements whose reference is finite (and `where`, when given): max and
+    mean |out - ref|; max ULPs (of the output format) from the reference
+    rounded to that format and max relative error, both where
+    |ref| >= 2^-10 (below that the absolute error is the meaningful
+    figure).  NaN outputs where the reference is finite count as an
+    infinite error."""
     import torch
 
     out = out.reshape(-1)
     ref = ref.reshape(-1).float()
-    fin = torch.isfinite(ref)
-    d = (out.float() - ref).abs()[fin]
+    keep = torch.isfinite(ref)
+    if where is not None:
+        keep &= where.reshape(-1)
+    d = (out.float() - ref).abs()
     d = torch.where(torch.isnan(d), torch.full_like(d, float("inf")), d)
-    u = (_ordered16(out) - _ordered16(ref.to(out.dtype))).abs()[fin]
-    return {"max_abs": float(d.max()), "mean_abs": float(d.double().mean()), "max_ulp": int(u.max())}
+    u = (_ordered16(out) - _ordered16(ref.to(out.dtype))).abs()
+    sig = keep & (ref.abs() >= 2.0 ** -10)
+    return {"max_abs": float(d[keep].max()), "mean_abs": float(d[keep].double().mean()),
+            "max_ulp": int(u[sig].max()), "max_rel": float((d[sig] / ref.abs()[sig]).max())}
 
 
 def _numerics_short(nm):
-    return {"max_abs": float(f"{nm['max_abs']:.4g}"), "max_ulp": nm["max_ulp"]}
+    return {"max_abs": float(f"{nm['max_abs']:.4g}"), "max_ulp": nm["max_ulp"],
+            "max_rel": float(f"{nm['max_rel']:.3g}")}
 
 
 SWEEP_LOG2 = (16, 18, 20, 22, 24, 26, 28)
@@ -672,8 +680,8 @@ def _summary(row):
             round(row["poly_frac_hbm_peak"], 3)]
 
 
-def _with_numerics(row, label, out, ref):
-    row[f"{label}_numerics"] = _numerics_short(numerics(out, ref))
+def _with_numerics(row, label, out, ref, where=None):
+    row[f"{label}_numerics"] = _numerics_short(numerics(out, ref, where))
 
 
 C3_SHAPE = (4, 32, 2048, 2048)
@@ -740,10 +748,16 @@ def config_rows(lib, reps: int, emit, headline=None):
                [("poly", poly), ("native", nat), ("poly_exp2_d2", d2)], reps)
     ref_y = torch.sigmoid(s.float() - math.log(4096.0))
     ref_dy = ref_y * (1 - ref_y)
-    for label, fn in (("poly", poly), ("native", nat), ("poly_exp2_d2", d2)):
+    # each program also over its fitted domain: B3's clamp |s| <= 6, the
+    # B3-D2 fit interval |s| <= 7 (outside it the D2 model is e^s / 4096)
+    for label, fn, fit in (("poly", poly, 6.0), ("native", nat, None), ("poly_exp2_d2", d2, 7.0)):
         fn()
         _with_numerics(row, label, y, ref_y)
         _with_numerics(row, label + "_dy", dy, ref_dy)
+        if fit is not None:
+            inside = s.float().abs() <= fit
+            _with_numerics(row, label + "_in_fit", y, ref_y, inside)
+            _with_numerics(row, label + "_in_fit_dy", dy, ref_dy, inside)
     emit(row)
     summary["C1_b3"] = _summary(row)
     del s, y, dy, ref_y, ref_dy

@@ -1,0 +1,123 @@
+"""Routed exp2 (B5: four of every `route` keys take the polynomial) must
+route exactly the keys the reference routes.  The ordinary parity
+tolerances cannot see a misrouted key (the routed-vs-hardware difference is
+a fraction of a BF16 ULP per element), so these tests compare against three
+references at once -- the correct routing, hardware exp2 everywhere, and
+the routing shifted by four slots -- and require the kernel to be much
+closer to the first:
+
+* forward: the log-sum-exp is an FP32 output, so it resolves the routed
+  polynomial's error exactly; the inputs put every row's maximum in the
+  first key tile, so the kernel's online maximum never moves and its
+  exponents are the reference's;
+* backward: P is recomputed from the saved log-sum-exp, the reference does
+  the same, and the PWL2 program's error is large enough to stand out of
+  the BF16 rounding of dQ, dK, dV in an L2 norm over all elements.
+
+Also covers the S = 384 backward cases that reach the 4-wave dQ blocks at
+head_dim 128 (the 8-wave blocks need S a multiple of 256)."""
+
+import math
+
+import pytest
+import torch
+
+import attention_reference as AR
+from attention_reference import default_bias, reference_bwd, reference_fwd
+from test_gpu_flash_attention_bwd import _close, _inputs, bwd, fwd
+
+pytestmark = pytest.mark.gpu
+
+
+def _shifted_routing():
+    """Context: the reference with every key's routing slot moved by four."""
+    class Shift:
+        def __enter__(self):
+            self.orig = AR.route_slot
+            AR.route_slot = lambda keys: self.orig(keys) + 4
+
+        def __exit__(self, *exc):
+            AR.route_slot = self.orig
+    return Shift()
+
+
+def _max_in_first_tile(seed, s=256, d=128):
+    q, k, v, do = _inputs(1, 4, 2, s, seed, d=d)
+    kf = k.float()
+    kf[:, 64:] *= 0.25  # later keys score lower: no row maximum leaves tile 0
+    k = kf.bfloat16()
+    qf, kh, _ = AR._heads(q, k, v)
+    a = qf @ kh.transpose(-1, -2)
+    assert bool((a[..., :64].amax(-1) > a[..., 64:].amax(-1)).all()), "precondition: maxima in tile 0"
+    return q, k, v, do
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("mode,route", [("softmax_pwl2", 10), ("softmax_pwl2", 6), ("softmax_d2", 6),
+                                        ("softmax_d2", 12)])
+def test_forward_routing_is_exact(capi, oracle, cuda, mode, route, causal):
+    q, k, v, _ = _max_in_first_tile(700 + route + 3 * causal)
+    scale = 1 / math.sqrt(128)
+    out, lse = fwd(capi, cuda, q, k, v, mode, causal, scale, route=route)
+    out, lse = out.cpu().float(), lse.cpu()
+    o_r, l_r = reference_fwd(oracle, q, k, v, mode, causal, scale, route=route)
+    o_h, l_h = reference_fwd(oracle, q, k, v, "softmax_native", causal, scale)
+    with _shifted_routing():
+        o_w, l_w = reference_fwd(oracle, q, k, v, mode, causal, scale, route=route)
+    err = (lse - l_r).abs().mean().item()
+    gap = min((l_r - l_h).abs().mean().item(), (l_r - l_w).abs().mean().item())
+    print(f"{mode} route {route} causal {causal}: lse err {err:.3g}, gap {gap:.3g}", flush=True)
+    assert gap > 1e-5
+    assert err < 0.1 * gap, (err, gap)
+    if mode != "softmax_pwl2":
+        # D2 is continuous across integer exponents (p(0) = 1, p(1) = 2), so
+        # every row agrees; PWL2 jumps there (p(1-) = 1.98154 against
+        # 2 p(0) = 1.97892), and an exponent that the kernel's FP32 fma and
+        # the reference's two roundings put on opposite sides of an integer
+        # moves that row by up to 1.3e-3 of one probability
+        assert (lse - l_r).abs().max().item() < 0.25 * gap
+    # the BF16 output: within the usual tolerance of the routed reference
+    ok, info = _close(out, o_r, rel=1.5e-2)
+    assert ok, info
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("route", [6, 10])
+def test_backward_routing_is_exact(capi, oracle, cuda, route, causal):
+    mode = "softmax_pwl2"
+    q, k, v, do = _inputs(1, 4, 2, 256, 800 + route + causal)
+    scale = 1 / math.sqrt(128)
+    out, lse = fwd(capi, cuda, q, k, v, mode, causal, scale, route=route)
+    got = bwd(capi, cuda, q, k, v, out, do, lse, mode, 0, causal, scale, route=route)[:3]
+    args = (oracle, q, k, v, out, do, lse, mode, 0, causal, scale, 30.0)
+    ref_r = reference_bwd(*args, route, 0.0)
+    ref_h = reference_bwd(*args, 0, 0.0)
+    with _shifted_routing():
+        ref_w = reference_bwd(*args, route, 0.0)
+    flat = lambda ts: torch.cat([t.reshape(-1).double() for t in ts])
+    g, r, h, w = flat(got), flat(ref_r), flat(ref_h), flat(ref_w)
+    err = (g - r).norm().item()
+    gap_h, gap_w = (r - h).norm().item(), (r - w).norm().item()
+    print(f"route {route} causal {causal}: err {err:.4g}, gap hw {gap_h:.4g}, gap shifted {gap_w:.4g}", flush=True)
+    # a kernel routing like the alternative would sit about sqrt(err^2 + gap^2) away
+    assert err < 0.8 * gap_h, (err, gap_h)
+    assert err < 0.8 * gap_w, (err, gap_w)
+    assert (g - h).norm().item() > 1.2 * err
+    assert (g - w).norm().item() > 1.2 * err
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("mode,route", [("softmax_native", 0), ("softmax_d2", 12), ("sigmoid_native", 0)])
+def test_backward_seq_384_four_wave_dq(capi, oracle, cuda, mode, route, causal):
+    """S = 384 at head_dim 128: the dQ kernel falls back to 4-wave blocks for
+    the modes that otherwise run 8-wave blocks."""
+    q, k, v, do = _inputs(1, 4, 2, 384, 850 + AR.M[mode] + route + causal)
+    scale = 1 / math.sqrt(128)
+    out, lse = fwd(capi, cuda, q, k, v, mode, causal, scale, route=route if route else 4)
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, mode, 0, causal, scale, route=route)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, mode, 0, causal, scale, 30.0, route,
+                               default_bias(mode, 384))
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert torch.isfinite(got).all(), name
+        ok, info = _close(got, ref)
+        assert ok, (mode, route, causal, name, info)
