@@ -975,6 +975,14 @@ def pmc_pass(lib):
         torch.cuda.synchronize()
         plan.append({"tag": tag, "elements": elements, "launches": 4})
 
+    g = torch.Generator().manual_seed(0)
+    s = (torch.rand(1 << 20, generator=g) * 32 - 16).to(torch.bfloat16).to(dev)
+    y, dy = torch.empty_like(s), torch.empty_like(s)
+    for tag, name in (("C1 b3 direct", "launch_flash_sigmoid_direct_d3_d4_bf16"),
+                      ("C1 b3 native", "launch_flash_sigmoid_native_bf16"),
+                      ("C1 b3 exp2 d2", "launch_flash_sigmoid_exp2_d2_bf16")):
+        run(tag, _launcher(lib, name, y, dy, s, s.numel()), s.numel())
+    del s, y, dy
     sc = c3_scores(dev)
     out = torch.empty_like(sc)
     n = sc.numel()
