@@ -1011,6 +1011,67 @@ def pmc_pass(lib):
     print(json.dumps({"pmc_pass": plan}), flush=True)
 
 
+_WORKLOAD_KEYS = ("config", "dtype", "elements", "regime", "degree", "bytes_per_launch", "flops", "evaluations")
+
+
+def device_environment() -> dict:
+    """Environment block of the result envelope (needs the HIP device)."""
+    import platform
+
+    import numpy as np
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    name = torch.cuda.get_device_name(0)
+    return {"gpu": name, "device_name": name, "gcn_arch": getattr(props, "gcnArchName", None),
+            "python": platform.python_version(), "torch_version": torch.__version__,
+            "hip_version": torch.version.hip, "cuda_version": None,
+            "total_memory_bytes": int(props.total_memory), "host_cpu": _cpu_model(),
+            "packages": {"numpy": np.__version__}}
+
+
+def _git_revision():
+    import subprocess
+
+    try:
+        out = subprocess.run(["git", "-C", ROOT, "rev-parse", "HEAD"], stdout=subprocess.PIPE,
+                             stderr=subprocess.DEVNULL, text=True, timeout=10)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    rev = out.stdout.strip()
+    return rev if out.returncode == 0 and len(rev) == 40 else None
+
+
+def result_envelope(rows, headline, args, environment) -> dict:
+    """Every row of the run in the reference's version-1 result envelope
+    (src/sfu_repro/artifact.py): one observation per row, its identifying
+    fields under `workload` and its measurements under `metrics`; the
+    headline line is the first observation."""
+    from sfu_repro import artifact
+
+    results = [{"case": "headline", "variant": "poly", "workload": headline["config"],
+                "metrics": {k: v for k, v in headline.items() if k not in ("config", "configs")}}]
+    for row in rows:
+        results.append({
+            "case": row.get("function", "row"),
+            "variant": "poly-vs-native",
+            "workload": {k: row[k] for k in _WORKLOAD_KEYS if k in row},
+            "metrics": {k: v for k, v in row.items() if k not in _WORKLOAD_KEYS and k != "function"},
+        })
+    return artifact.make_result(
+        "mi355x-spline-ops-bench",
+        description="Polynomial vs hardware-transcendental kernels on one MI355X: BASELINE configurations "
+                    "C1..C5, the 2^16..2^28 sweep, sin/cos probes and attention rows",
+        command=[os.path.basename(sys.executable), "bench.py", *sys.argv[1:]],
+        source={"repository": "fast-polynomial-transcendentals_amd", "revision": _git_revision(), "dirty": None},
+        environment=environment,
+        measurement={"dtype": "bf16 (per row: fp16, bf16, f32->bf16)", "seed": 0, "warmup": args.warmup,
+                     "iterations": args.sweep_reps, "rounds": 9,
+                     "summary_statistic": "median of 9 graph replays (headline: mean of K launches)",
+                     "order_policy": "implementations interleaved, alternating order per round"},
+        results=results)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1138,8 +1199,9 @@ def main():
             for row in attention_rows(lib, args.sweep_reps):
                 emit(row)
     if args.rows_out:
+        doc = result_envelope(all_rows, line, args, device_environment())
         with open(args.rows_out, "w") as f:
-            json.dump(all_rows, f, indent=1)
+            json.dump(doc, f, indent=1)
     text = json.dumps(line, separators=(",", ":"))
     if len(text) > 2000:
         print(f"headline line is {len(text)} bytes", file=sys.stderr)
