@@ -125,8 +125,9 @@ def test_softcap_forward_error_bound(oracle):
     y = oracle.bf16_bits_to_f32(oracle.softcap_fwd_bf16(x, 30.0))[m]
     ref = 30.0 * np.tanh(s[m] / 30.0)
     # D4 tanh (max error 0.0133 on its fit range) scaled by cap, plus the BF16
-    # rounding of the input scale and of the output (|y| <= 30: half-ulp 0.0625)
-    assert np.abs(y - ref).max() < 30 * 0.0133 + 0.0625 + 0.2
+    # rounding of the input scale and of the output (|y| <= 30: half-ulp 0.0625);
+    # the exhaustive maximum is 0.4029
+    assert np.abs(y - ref).max() < 0.41
     assert np.all(np.abs(y) <= 30.0)
     # odd symmetry is exact (the program restores the sign by XOR)
     pos = x[(x < 0x7F80) & (x > 0)]
@@ -134,6 +135,25 @@ def test_softcap_forward_error_bound(oracle):
     yn = oracle.softcap_fwd_bf16(pos | np.uint16(0x8000), 30.0)
     assert np.array_equal(yn, yp ^ np.uint16(0x8000)) or np.array_equal(
         oracle.bf16_bits_to_f32(yn), -oracle.bf16_bits_to_f32(yp))
+
+
+@pytest.mark.parametrize("cap", [30.0, 7.5, 1.0, 0.3])
+def test_softcap_forward_is_the_pinned_tanh_program_between_two_roundings(oracle, cap):
+    """The softcap composition, step by step from independently pinned
+    parts: u = RNE_bf16(float32(s) * float32(1/cap)) with numpy's float32
+    product, T = the reference's TANH_FWD_D4_ODD_BF16 program (pinned by its
+    own tests), y = RNE_bf16(float32(T) * float32(cap)).  A dropped or moved
+    rounding in the oracle's softcap changes outputs: cap * T taken before T
+    is rounded differs on 9,734 of the 65,536 patterns at cap 30."""
+    x = _all(oracle)
+    s = oracle.bf16_bits_to_f32(x)
+    with np.errstate(invalid="ignore", over="ignore"):
+        u = oracle.f32_to_bf16_bits((s * np.float32(1.0 / np.float32(cap))).astype(np.float32))
+        t = oracle.activation("tanh", oracle.FWD, 4, "bf16", u)
+        y = oracle.f32_to_bf16_bits((oracle.bf16_bits_to_f32(t) * np.float32(cap)).astype(np.float32))
+    got = oracle.softcap_fwd_bf16(x, cap)
+    nan = ((got & 0x7F80) == 0x7F80) & ((got & 0x7F) != 0) & ((y & 0x7F80) == 0x7F80) & ((y & 0x7F) != 0)
+    assert np.array_equal(got[~nan], y[~nan])
 
 
 def test_softcap_backward_is_derivative_of_d4_program(oracle):
