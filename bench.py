@@ -63,9 +63,10 @@ def parse():
     p.add_argument("--rows-out", default=None,
                    help="also write every row (JSON list) to this file")
     p.add_argument("--pmc-pass", action="store_true",
-                   help="counter pass: 3 launches of each configuration's polynomial and native "
-                        "kernel (C1..C5 and the 2^28 sweep point) and 3 plain 256 MiB copies "
-                        "(torch copy_) as the byte-count calibration")
+                   help="counter pass: 4 launches each of the C1 B3 kernels (direct, hardware "
+                        "control, B3-D2), the C3 softcap (polynomial, hardware, copy) and the 2^28 "
+                        "sweep kernels, then 3 plain 256 MiB copies (torch copy_) as the "
+                        "byte-count calibration")
     p.add_argument("--pmc-probes", action="store_true",
                    help="counter pass over the sin/cos repeated-evaluation probes: each "
                         "polynomial and native probe of the bench launched 4 times")

@@ -2,9 +2,9 @@
 (launch_flash_attention_bwd_strided_bf16_noalloc) against the entry point it
 wraps (launch_flash_attention_bwd_strided_bf16 with caller workspaces),
 through the C ABI: identical dq, dk, dv bits on two calls in a row, the
-second with a smaller problem, and the size limit reported as an error.
-Both entry points run the same kernels, so the results must be equal bit
-for bit."""
+second with a smaller problem, the size limit reported as an error, and
+replays of a captured HIP graph.  Both entry points run the same kernels,
+so the results must be equal bit for bit."""
 
 import ctypes
 import math
@@ -81,3 +81,41 @@ def test_noalloc_rejects_problems_beyond_the_array(capi, cuda):
         ctypes.c_int(0), ctypes.c_int(1), ctypes.c_float(0.1), ctypes.c_float(30.0), ctypes.c_float(0.0),
         capi.stream())
     assert rc == 2  # hipErrorOutOfMemory
+
+
+def test_noalloc_under_graph_capture(capi, cuda):
+    """The reason for the entry point: a captured backward (grouped heads, so
+    both the delta rows and the dK / dV partials live in the library's array)
+    replays to the eager result every time, with eager work between replays."""
+    b, hq, hkv, s, d = 1, 4, 2, 256, 128
+    print("no-alloc backward under graph capture", flush=True)
+    q, k, v, do = _inputs(b, hq, hkv, s, 520, d=d)
+    scale = 1.0 / math.sqrt(d)
+    out, lse = fwd(capi, cuda, q, k, v, "softmax_native", True, scale)
+    want = bwd(capi, cuda, q, k, v, out, do, lse, "softmax_native", 0, True, scale)[:3]
+    qd, kd, vd, dod = q.to(cuda), k.to(cuda), v.to(cuda), do.to(cuda)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    strides = _strides(qd, kd, vd, out, dod, dq, dk, dv)
+
+    def launch():
+        rc = capi.launch_flash_attention_bwd_strided_bf16_noalloc(
+            capi.ptr(dq), capi.ptr(dk), capi.ptr(dv), capi.ptr(qd), capi.ptr(kd), capi.ptr(vd), capi.ptr(out),
+            capi.ptr(dod), capi.ptr(lse), ctypes.c_int64(b), ctypes.c_int64(hq), ctypes.c_int64(hkv),
+            ctypes.c_int64(s), ctypes.c_int64(d), strides, ctypes.c_int(M["softmax_native"]), ctypes.c_int(0),
+            ctypes.c_int(0), ctypes.c_int(1), ctypes.c_float(scale), ctypes.c_float(30.0), ctypes.c_float(0.0),
+            capi.stream())
+        assert rc == 0, rc
+
+    launch()  # first call on this device: the array's address is looked up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for _ in range(3):
+        for t in (dq, dk, dv):
+            t.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for name, got, w in zip(("dq", "dk", "dv"), (dq, dk, dv), want):
+            assert torch.equal(got.cpu().float().view(torch.int32), w.view(torch.int32)), name
