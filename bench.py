@@ -28,7 +28,8 @@ Every other row -- the per-function sweep over 2^16..2^28 elements (L2,
 MALL and HBM regimes), the full configuration rows with their numerics
 against FP32 torch, the sin/cos repeated-evaluation probes and the fused
 attention rows -- is printed to stderr, one JSON object per line, before
-the headline (and written to --rows-out when given).  Sweep and
+the headline (and written to --rows-out when given, as observations of the
+reference's version-1 result envelope).  Sweep and
 configuration rows use graph replay, median of 9 rounds, implementations
 interleaved.
 
@@ -61,7 +62,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--sweep-reps", type=int, default=100)
     p.add_argument("--rows-out", default=None,
-                   help="also write every row (JSON list) to this file")
+                   help="also write every row to this file, in the version-1 result envelope "
+                        "(sfu_repro.artifact)")
     p.add_argument("--pmc-pass", action="store_true",
                    help="counter pass: 4 launches each of the C1 B3 kernels (direct, hardware "
                         "control, B3-D2), the C3 softcap (polynomial, hardware, copy) and the 2^28 "
