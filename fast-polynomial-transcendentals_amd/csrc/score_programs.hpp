@@ -41,8 +41,12 @@ __device__ __forceinline__ void b3_lane(float x, float& y, float& dy) {
         __builtin_elementwise_maximum(x, -C::clamp), C::clamp);
     float f = bfma(xc, row ? C::r1[3] : C::r0[3], row ? C::r1[2] : C::r0[2]);
     f = bfma(xc, f, row ? C::r1[1] : C::r0[1]);
-    f = bfma(xc, f, row ? C::r1[0] : C::r0[0]);
-    y = f > 0.0f ? f : 0.0f;
+    // y = max(0, bf16(v)) taken as bf16(max(0, v)): RNE is monotone and maps
+    // 0 to +0, so both give +0 for v <= 0 (and for NaN) and bf16(v) for v > 0.
+    // The maximum then reads the FMA's own result, which needs no NaN
+    // quieting, instead of the bits of the packed rounding.
+    const float v = __builtin_fmaf(xc, f, row ? C::r1[0] : C::r0[0]);
+    y = rbf(v > 0.0f ? v : 0.0f);
     if constexpr (WITH_GRAD) {
         const float fac = bfma(xc, row ? C::g1[1] : C::g0[1], row ? C::g1[0] : C::g0[0]);
         dy = y * fac;  // rounded once by the final pack
