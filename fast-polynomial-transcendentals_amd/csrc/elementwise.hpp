@@ -204,8 +204,6 @@ inline int nt_mode(int64_t in_bytes, int64_t out_bytes) {
 // Blocks for a one-pass launch over `n_items` work items (1 per thread),
 // clamped to the grid limit (the kernels stride over any remainder).
 int64_t grid_one_pass(int64_t n_items);
-// Blocks for a persistent launch: at most `blocks_per_cu` per CU.
-int64_t grid_for_vectors(int64_t n_vec, int unroll, int blocks_per_cu);
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 

@@ -30,14 +30,6 @@ int64_t grid_one_pass(int64_t n_items) {
     return need < 1 ? 1 : (need > limit ? limit : need);
 }
 
-int64_t grid_for_vectors(int64_t n_vec, int unroll, int blocks_per_cu) {
-    const int64_t per_block = (int64_t)kBlock * unroll;
-    int64_t need = (n_vec + per_block - 1) / per_block;
-    const int64_t cap = (int64_t)device_shape().cus * blocks_per_cu;
-    if (need > cap) need = cap;
-    return need < 1 ? 1 : need;
-}
-
 }  // namespace pt
 
 extern "C" int spline_hip_grid_for(int64_t size, int streams, int64_t* grid_out, int* cus_out) {
