@@ -20,16 +20,19 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
   when slot(j) % freq < 4 with slot(j) = 16 bit5(j) + 4 bits3..4(j) +
   bits0..1(j), in the forward and the backward alike;
 * softcap: ``softcap > 0`` with no score_mod -> FP32 hardware tanh; a
-  score_mod from ``create_softcap_scoremod_backend`` -> the D4 BF16 program
-  (B2), its backward per ``backward_mode``;
-* sigmoid attention: SFU route -> hardware sigmoid; polynomial route ->
-  the B3 direct D3 program (degree 3, no bias, device backend; S = 4096),
-  the B3-D2 exp2 program (degree 2, no bias; S = 4096) or the BF16 sigmoid
-  D3..D6 programs on ``s + bias`` (``bias`` defaults to ``-ln S``).
+  score_mod from ``create_softcap_scoremod_backend(backend="device")`` ->
+  the D4 BF16 program (B2), its backward per ``backward_mode``;
+* sigmoid attention: SFU route -> hardware sigmoid; polynomial route with
+  ``sigmoid_poly_backend="device"`` -> the B3 direct D3 program (degree 3,
+  no bias; S = 4096), the B3-D2 exp2 program (degree 2, no bias; S = 4096)
+  or the BF16 sigmoid D3..D6 programs on ``s + bias`` (``bias`` defaults to
+  ``-ln S``).
 
 Combinations whose programs are not part of the reference tree (the FP16 /
 BF16 / PWL1 exp2 variants, Sollya attention fits, mixed SFU/polynomial
-sigmoid lanes) raise ``NotImplementedError`` naming what is missing.
+sigmoid lanes, and the ``cute`` backends -- FA4's CuTe FP32 score programs,
+whose coefficients live in FA4) raise ``NotImplementedError`` naming what is
+missing.
 """
 
 from __future__ import annotations
@@ -121,6 +124,10 @@ def _check_softcap_program(softcap: float, degree: int, backend: str, coeff_sour
         raise ValueError("softcap must be positive")
     if backend not in ("cute", "device"):
         raise ValueError(f"unsupported softcap backend {backend!r}")
+    if backend != "device":
+        raise NotImplementedError(
+            "softcap backend 'cute' is FA4's CuTe FP32 score_mod with FA4's own FP32 coefficients, which are not "
+            "part of the reference tree; backend='device' selects the deployed D4 BF16 program")
     if int(degree) != 4:
         raise NotImplementedError(
             f"softcap degree {degree}: only the D4 BF16 tanh (spline_structs_odd_bf16.cuh:153-179) "
@@ -207,8 +214,12 @@ def select_forward(*, seqlen: int, softcap: float = 0.0, score_mod=None, sigmoid
             raise NotImplementedError("mixed SFU / polynomial sigmoid lanes are not built")
         if sigmoid_coeff_source != "current":
             raise NotImplementedError("Sollya sigmoid-attention fits are not part of the reference tree")
+        if sigmoid_poly_backend != "device":
+            raise NotImplementedError(
+                f"sigmoid_poly_backend={sigmoid_poly_backend!r}: FA4's CuTe FP32 sigmoid polynomial is not part of "
+                "the reference tree; sigmoid_poly_backend='device' selects the deployed BF16 programs")
         degree = int(sigmoid_degree)
-        if sigmoid_bias is None and sigmoid_poly_backend == "device" and degree in (2, 3):
+        if sigmoid_bias is None and degree in (2, 3):
             if seqlen != FLASH_SIGMOID_DIRECT_SEQUENCE_LENGTH:
                 raise ValueError(
                     "direct FlashSigmoid programs are fitted for sequence length "

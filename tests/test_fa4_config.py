@@ -183,6 +183,13 @@ def test_forward_program_selection():
     assert (m, bias) == (rt.MODE_SIGMOID_D3 + 2, -3.0)
     with pytest.raises(NotImplementedError, match="mixed"):
         sel(seqlen=4096, sigmoid_attention=True, sigmoid_sfu_res=4)
+    # FA4's CuTe FP32 sigmoid polynomial (the runtime's default backend) is not built
+    with pytest.raises(NotImplementedError, match="CuTe FP32 sigmoid"):
+        sel(seqlen=4096, sigmoid_attention=True)
+    with pytest.raises(NotImplementedError, match="CuTe FP32 sigmoid"):
+        sel(seqlen=2048, sigmoid_attention=True, sigmoid_degree=5, sigmoid_bias=-3.0)
+    # the SFU route takes no polynomial, whatever the backend
+    assert sel(seqlen=4096, sigmoid_attention=True, sigmoid_sfu_res=16)[0] == rt.MODE_SIGMOID_NATIVE
 
 
 def test_backward_program_selection():
@@ -209,6 +216,12 @@ def test_softcap_factories_reject_unbuilt_programs():
         rt.create_softcap_scoremod_backend(30.0, degree=3)
     with pytest.raises(NotImplementedError, match="Sollya"):
         rt.create_softcap_scoremod_backend(30.0, coeff_source="sollya")
+    with pytest.raises(NotImplementedError, match="CuTe FP32"):
+        rt.create_softcap_scoremod_backend(30.0, backend="cute")
+    with pytest.raises(NotImplementedError, match="CuTe FP32"):
+        rt.create_softcap_scoremod_bwd_backend(30.0, backend="cute")
+    with pytest.raises(ValueError, match="unsupported softcap backend"):
+        rt.create_softcap_scoremod_backend(30.0, backend="ptx")
     with pytest.raises(ValueError, match="backward mode"):
         rt.create_softcap_scoremod_bwd_backend(30.0, backward_mode="native")
 
