@@ -5,7 +5,8 @@ CPU reference that evaluates the same score programs through the oracle.
 
 Two sequences, eight query heads over two KV heads (four per group), S =
 256: every block of the grid maps its own (batch, query head) to the right
-KV head.  The B3 programs, fitted for S = 4096, run at that length."""
+KV head.  The B3 programs, fitted for S = 4096, run at that length.  The
+backward of the programs not otherwise tested at head_dim 64 follows."""
 
 import math
 
@@ -54,3 +55,48 @@ def test_forward_b3_programs_at_4096(capi, oracle, cuda, mode, d):
     assert torch.isfinite(got).all()
     ok, info = _close(got, ref_out, rel=1.5e-2)
     assert ok, (mode, d, info)
+
+
+# backward at head_dim 64 for the programs that test_head_dim_64
+# (test_gpu_flash_attention_bwd.py) does not reach: routed D3 / PWL2,
+# hardware softcap, the STE and 1 - T^2 softcap derivatives, biased sigmoid
+# programs and the B3 programs; batched and grouped like the forward matrix
+BWD64 = [("softmax_d3", 0, 12), ("softmax_pwl2", 0, 10), ("softcap_native", 0, 0), ("softcap_d4", 2, 0),
+         ("softcap_d4", 3, 0), ("sigmoid_d3", 0, 0), ("sigmoid_d5", 0, 0)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("mode,grad,route", BWD64)
+def test_backward_head_dim_64_grouped(capi, oracle, cuda, mode, grad, route, causal):
+    from attention_reference import default_bias, reference_bwd
+    from test_gpu_flash_attention_bwd import bwd
+
+    seed = 1000 + 5 * M[mode] + grad + route + int(causal)
+    print(f"bwd d64 {mode} grad {grad} route {route} causal {causal} seed {seed}", flush=True)
+    q, k, v, do = _inputs(2, 8, 2, 256, seed, qmul=6.0 if mode.startswith("softcap") else 1.0, d=64)
+    scale = 1 / math.sqrt(64)
+    out, lse = fwd(capi, cuda, q, k, v, mode, causal, scale, route=route if route else 4)
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, mode, grad, causal, scale, route=route)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, mode, grad, causal, scale, 30.0, route,
+                               default_bias(mode, 256))
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert torch.isfinite(got).all(), name
+        ok, info = _close(got, ref)
+        assert ok, (mode, grad, route, causal, name, info)
+
+
+@pytest.mark.parametrize("mode,grad", [("sigmoid_b3", 4), ("sigmoid_b3", 5), ("sigmoid_b3_d2", 0)])
+def test_backward_b3_programs_head_dim_64(capi, oracle, cuda, mode, grad):
+    from attention_reference import reference_bwd
+    from test_gpu_flash_attention_bwd import bwd
+
+    print(f"bwd d64 {mode} grad {grad} S 4096", flush=True)
+    q, k, v, do = _inputs(1, 2, 1, 4096, 1100 + grad + M[mode], d=64)
+    scale = 1 / math.sqrt(64)
+    out, lse = fwd(capi, cuda, q, k, v, mode, True, scale)
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, mode, grad, True, scale)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, mode, grad, True, scale, 30.0, 0, 0.0)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert torch.isfinite(got).all(), name
+        ok, info = _close(got, ref)
+        assert ok, (mode, grad, name, info)
