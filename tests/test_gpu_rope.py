@@ -95,7 +95,8 @@ def _rope_reference(values, theta):
 
 
 @pytest.mark.parametrize("fmt,name", [(torch.float16, "fp16"), (torch.bfloat16, "bf16")])
-@pytest.mark.parametrize("shape", [(2, 64, 4, 2, 128), (1, 37, 9, 3, 64), (1, 4096, 1, 1, 128)])
+@pytest.mark.parametrize("shape", [(2, 64, 4, 2, 128), (1, 37, 9, 3, 64), (1, 4096, 1, 1, 128),
+                                   (3, 17, 2, 1, 8), (1, 33, 5, 5, 24), (1, 8, 16, 16, 256)])
 def test_rope_apply_parity(capi, oracle, cuda, fmt, name, shape):
     b, s, hq, hk, d = shape
     q, k = _rope_inputs(fmt, b, s, hq, hk, d, seed=sum(shape))
