@@ -120,7 +120,7 @@ def test_swish_mul_forward_and_backward(capi, oracle, cuda, degree, fmt):
 
 @pytest.mark.parametrize("fmt", ["f16", "bf16"])
 @pytest.mark.parametrize("degree", [3, 4, 5, 6, 0])
-@pytest.mark.parametrize("hidden", [2048, 520, 6])
+@pytest.mark.parametrize("hidden", [2048, 520, 6, 10, 1030])
 def test_packed_matches_separate(capi, cuda, degree, fmt, hidden):
     """Packed [rows, 2H] kernels equal the separate-tensor kernels bit for bit
     (reference test_spline_ops.py:190-204)."""
