@@ -937,18 +937,22 @@ def stream_ceiling(lib, x, y, steps: int, warmup: int):
     """Achievable HBM rates of plain streams over the 16-bit tensor `x`
     (and `y`, same size), timed like the headline (back-to-back launches,
     HIP events): the one-pass 1:1 copy of the kernels' own driver, the
-    read-only and write-only streams of the same launch shape, torch's
-    copy_ (the runtime's copy kernel) and zero_.  Fractions of 8 TB/s."""
+    read-only and write-only streams of the same launch shape, the 2:1
+    stream of the BF16 product a * b (the shape of the backward and SwiGLU
+    kernels), torch's copy_ (the runtime's copy kernel) and zero_.
+    Fractions of 8 TB/s."""
     import ctypes
 
     import torch
 
     n = x.numel()
     sink = torch.zeros(4, dtype=torch.int32, device=x.device)
+    z = torch.empty_like(x)
     cases = [
         ("copy", 4 * n, make_unary(lib, "spline_hip_copy16", y, x)),
         ("read", 2 * n, _launcher(lib, "spline_hip_read16", sink, x, n)),
         ("write", 2 * n, _launcher(lib, "spline_hip_fill16", y, n, ctypes.c_uint32(0x3F803F80))),
+        ("two_to_one", 6 * n, _launcher(lib, "launch_multiply_kernel_bf16", z, x, y, n)),
         ("torch_copy", 4 * n, lambda: y.copy_(x)),
         ("torch_zero", 2 * n, lambda: y.zero_()),
     ]
@@ -956,6 +960,7 @@ def stream_ceiling(lib, x, y, steps: int, warmup: int):
     for label, nbytes, fn in cases:
         ms = time_launches(fn, steps, warmup)
         out[label] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    del z
     return out
 
 
