@@ -28,9 +28,9 @@ struct B3FwdOp {
     static constexpr int NIN = 1, NOUT = 1;
     __device__ __forceinline__ static void pair(const uint32_t (&a)[1], uint32_t (&b)[1]) {
         float y0, y1, d;
-        b3_lane<false>(bf_lo(a[0]), y0, d);
-        b3_lane<false>(bf_hi(a[0]), y1, d);
-        b[0] = pack_exact_bf(y0, y1);
+        b3_lane<false, true>(bf_lo(a[0]), y0, d);
+        b3_lane<false, true>(bf_hi(a[0]), y1, d);
+        b[0] = pack_bf(y0, y1);  // the probability's final rounding
     }
 };
 

@@ -100,19 +100,21 @@ __device__ __forceinline__ float softmax_exp2(float x, int i) {
     return __builtin_amdgcn_exp2f(x);
 }
 
-// Sigmoid-attention probabilities of two scores.
+// Sigmoid-attention probabilities of two scores, before their rounding to
+// BF16: the only consumer is the conversion to the BF16 operand of the P V
+// product, which performs the programs' final rounding.
 template <int MODE>
 __device__ __forceinline__ void sigmoid_prob2(float s0, float s1, float bias, float& p0, float& p1) {
     if constexpr (MODE == kAttnSigmoidB3) {
         float dy;
-        b3_lane<false>(rbf(s0), p0, dy);
-        b3_lane<false>(rbf(s1), p1, dy);
+        b3_lane<false, true>(rbf(s0), p0, dy);
+        b3_lane<false, true>(rbf(s1), p1, dy);
     } else if constexpr (MODE == kAttnSigmoidB3D2) {
         float dy;
         b3_d2_lane(rbf(s0), p0, dy);
         b3_d2_lane(rbf(s1), p1, dy);
     } else if constexpr (MODE >= kAttnSigmoidD3 && MODE <= kAttnSigmoidD6) {
-        BF16Prog<kSigmoid, kFwd, MODE - kAttnSigmoidD3 + 3>::eval2(pack_bf(s0 + bias, s1 + bias), p0, p1);
+        BF16Prog<kSigmoid, kFwd, MODE - kAttnSigmoidD3 + 3>::open2(pack_bf(s0 + bias, s1 + bias), p0, p1);
     } else {
         p0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(s0 + bias) * kLog2e));
         p1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(s1 + bias) * kLog2e));

@@ -33,8 +33,12 @@ struct B3Consts {
 
 // One lane on a BF16 value held in FP32.  NaN follows the audit's Python
 // semantics: the clamp keeps NaN, max(0, NaN) gives 0, the derivative is NaN.
-template <bool WITH_GRAD>
+// OPEN_Y (probability only) returns y before its final rounding, for callers
+// whose conversion to BF16 is that rounding: RNE of an already rounded value
+// is the same value, so the converted bits are unchanged.
+template <bool WITH_GRAD, bool OPEN_Y = false>
 __device__ __forceinline__ void b3_lane(float x, float& y, float& dy) {
+    static_assert(!(WITH_GRAD && OPEN_Y), "the derivative multiplies the rounded probability");
     using C = B3Consts;
     const bool row = x >= C::split;
     const float xc = __builtin_elementwise_minimum(
@@ -46,7 +50,7 @@ __device__ __forceinline__ void b3_lane(float x, float& y, float& dy) {
     // The maximum then reads the FMA's own result, which needs no NaN
     // quieting, instead of the bits of the packed rounding.
     const float v = __builtin_fmaf(xc, f, row ? C::r1[0] : C::r0[0]);
-    y = rbf(v > 0.0f ? v : 0.0f);
+    y = OPEN_Y ? (v > 0.0f ? v : 0.0f) : rbf(v > 0.0f ? v : 0.0f);
     if constexpr (WITH_GRAD) {
         const float fac = bfma(xc, row ? C::g1[1] : C::g0[1], row ? C::g1[0] : C::g0[0]);
         dy = y * fac;  // rounded once by the final pack
