@@ -93,8 +93,19 @@ __device__ __forceinline__ void f16_sincos(float a_lo, float a_hi, uint32_t& cos
     f16_sincos_reduced<P>(r, (s_lo >> 16) | s_hi, cos2, sin2);
 }
 
-// BF16 half-turn program on one FP32 angle; results are FP32 values that hold
-// BF16 values (signs applied).
+// Horner in sq over n BF16 coefficients (highest power first), every step
+// rounded to BF16 except the last, which is returned before its rounding.
+__device__ __forceinline__ float bf16_horner_open(const float (&k)[4], int n, float sq) {
+    float h = bf16_value(k[0]);
+#pragma unroll
+    for (int i = 1; i < n - 1; ++i) h = bfma(h, sq, bf16_value(k[i]));
+    return __builtin_fmaf(h, sq, bf16_value(k[n - 1]));
+}
+
+// BF16 half-turn program on one FP32 angle; results are the FP32 values of
+// the last steps (signs applied) before their final rounding, which the
+// caller's pack to BF16 performs: RNE is odd-symmetric, so rounding after the
+// sign is applied gives the same bits.
 template <int P>
 __device__ __forceinline__ void bf16_sincos_lane(float angle, float& c, float& s) {
     constexpr SinCosProg Q = kSinCos[P];
@@ -103,15 +114,9 @@ __device__ __forceinline__ void bf16_sincos_lane(float angle, float& c, float& s
     reduce_half_turn(angle, r, sign);
     r = rbf(r);
     const float sq = rbf(r * r);
-    float sp = bfma(bf16_value(Q.s[0]), sq, bf16_value(Q.s[1]));
-#pragma unroll
-    for (int i = 2; i < Q.ns; ++i) sp = bfma(sp, sq, bf16_value(Q.s[i]));
-    const float sr = rbf(r * sp);
-    float cp = bfma(bf16_value(Q.c[0]), sq, bf16_value(Q.c[1]));
-#pragma unroll
-    for (int i = 2; i < Q.nc; ++i) cp = bfma(cp, sq, bf16_value(Q.c[i]));
-    s = as_f32(as_u32(sr) ^ sign);
-    c = as_f32(as_u32(cp) ^ sign);
+    const float sp = rbf(bf16_horner_open(Q.s, Q.ns, sq));
+    s = as_f32(as_u32(r * sp) ^ sign);
+    c = as_f32(as_u32(bf16_horner_open(Q.c, Q.nc, sq)) ^ sign);
 }
 
 // ---------------------------------------------------------------------------
@@ -311,15 +316,12 @@ __device__ __forceinline__ void f16_poly_pair(const SinCosProg& Q, h2_t r, uint3
 }
 
 // BF16 polynomial on one reduced lane (FP32 value holding a BF16 value);
-// results are FP32 values holding BF16 values.
+// results are the last steps' FP32 values before their final rounding, which
+// the caller's pack to BF16 performs.
 __device__ __forceinline__ void bf16_poly_lane(const SinCosProg& Q, float r, float& cr, float& sr) {
     const float sq = rbf(r * r);
-    float sp = bfma(bf16_value(Q.s[0]), sq, bf16_value(Q.s[1]));
-    for (int i = 2; i < Q.ns; ++i) sp = bfma(sp, sq, bf16_value(Q.s[i]));
-    float cp = bfma(bf16_value(Q.c[0]), sq, bf16_value(Q.c[1]));
-    for (int i = 2; i < Q.nc; ++i) cp = bfma(cp, sq, bf16_value(Q.c[i]));
-    sr = rbf(r * sp);
-    cr = cp;
+    sr = r * rbf(bf16_horner_open(Q.s, Q.ns, sq));
+    cr = bf16_horner_open(Q.c, Q.nc, sq);
 }
 
 // FP16 quarter-turn D3/D4 on two FP32 angles (PolynomialD3D4QuarterTurnFP16, :573-595).
@@ -353,8 +355,7 @@ __device__ __forceinline__ void bf16_sincos_quarter(float a_lo, float a_hi, uint
     float c_lo, s_lo, c_hi, s_hi;
     bf16_poly_lane(Q, rbf(r_lo), c_lo, s_lo);
     bf16_poly_lane(Q, rbf(r_hi), c_hi, s_hi);
-    restore_quadrant_pair(pack_exact_bf(s_lo, s_hi), pack_exact_bf(c_lo, c_hi), q_lo, q_hi, sin2,
-                          cos2);
+    restore_quadrant_pair(pack_bf(s_lo, s_hi), pack_bf(c_lo, c_hi), q_lo, q_hi, sin2, cos2);
 }
 
 // RoPE fixed-point phase, quarter turn (reduce_rope_phase_to_quarter_turn_q15
@@ -441,8 +442,8 @@ struct BF16HalfTurn {
         float c0, s0, c1, s1;
         bf16_sincos_lane<P>(a0, c0, s0);
         bf16_sincos_lane<P>(a1, c1, s1);
-        c = pack_exact_bf(c0, c1);
-        s = pack_exact_bf(s0, s1);
+        c = pack_bf(c0, c1);  // the programs' final roundings
+        s = pack_bf(s0, s1);
     }
 };
 
