@@ -75,6 +75,8 @@ def _declare(l: ctypes.CDLL) -> None:
     ip = ctypes.POINTER(ctypes.c_int)
     l.orc_program.argtypes = [ci, ci, ci, ci, ip, f32p, ip, f32p]
     l.orc_program.restype = ctypes.c_int
+    l.orc_sincos_coeffs.argtypes = [ci, ci, ip, f32p, ip, f32p]
+    l.orc_sincos_coeffs.restype = ctypes.c_int
     l.orc_activation_bwd_alg.argtypes = [ci, ci, u16p, u16p, u16p, i64]
     l.orc_swish_mul_fwd.argtypes = [ci, ci, ci, u16p, u16p, u16p, i64]
     l.orc_swish_mul_bwd.argtypes = [ci, ci, ci, u16p, u16p, u16p, u16p, u16p, i64]
@@ -156,6 +158,17 @@ def program(family, direction: int, degree: int, fmt):
     _check(lib().orc_program(family_id(family), direction, degree, fmt_id(fmt),
                              ctypes.byref(shape), ctypes.byref(lc), ctypes.byref(deg), c))
     return SHAPES[shape.value], lc.value, deg.value, [c[i] for i in range(deg.value + 1)]
+
+
+def sincos_coefficients(table: int, idx: int):
+    """(sin coefficients, cos coefficients) of a paired sin/cos program, as
+    float32 values, highest power of r^2 first: table 0 the 16-bit half-turn
+    programs, 1 the FP32 programs, 2 the 16-bit quarter-turn programs, 3 the
+    RoPE Q15 quarter-turn program."""
+    ns, nc = ctypes.c_int(), ctypes.c_int()
+    s, c = (ctypes.c_float * 4)(), (ctypes.c_float * 4)()
+    _check(lib().orc_sincos_coeffs(table, idx, ctypes.byref(ns), s, ctypes.byref(nc), c))
+    return [s[i] for i in range(ns.value)], [c[i] for i in range(nc.value)]
 
 
 def activation_bwd(family, degree: int, fmt, go: np.ndarray, x: np.ndarray,

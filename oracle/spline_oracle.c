@@ -1195,9 +1195,11 @@ int orc_sincos16(int prog, int out_fmt, int rnd, const float* angles, uint16_t* 
 
 /* RoPE Q0.32 phase, quarter turn (reduce_rope_phase_to_quarter_turn_q15 and
  * evaluate_quarter_turn_q15_d3_d4_fp16, :1242-1287). */
+static const sincos_t ROPE_Q15_QUARTER = {ORC_F16, 2, {-0.07763671875f, 0.78466796875f}, 3,
+                                          {0.01538848876953125f, -0.308349609375f, 1.0f}};
+
 static void rope_q15_quarter(uint32_t position, uint32_t inc, double* c, double* s) {
-    static const sincos_t Q = {ORC_F16, 2, {-0.07763671875f, 0.78466796875f}, 3,
-                               {0.01538848876953125f, -0.308349609375f, 1.0f}};
+    const sincos_t Q = ROPE_Q15_QUARTER;
     uint32_t phase = position * inc;
     uint32_t quadrant = (phase + 0x20000000u) >> 30;
     int32_t residual = (int32_t)(phase - (quadrant << 30));
@@ -1310,6 +1312,36 @@ int orc_b3_exp2_d2_bf16(const uint16_t* x, uint16_t* y, uint16_t* dy, int64_t n,
         float p = ldexpf(m, (int)fl - 12);
         y[i] = bits_fmt(rne_bf16_f32(p), &FMT_BF16);
         dy[i] = bits_fmt(rne_bf16_f32(fmaf(-p, p, p)), &FMT_BF16);
+    }
+    return 0;
+}
+
+/* The coefficient tables of the paired sin/cos programs (test access): table
+ * 0 the 16-bit half-turn programs (SINCOS), 1 the FP32 programs (SINCOS32),
+ * 2 the 16-bit quarter-turn programs (SINCOS_QUARTER), 3 the RoPE Q15
+ * quarter-turn program; highest power of sq first. */
+int orc_sincos_coeffs(int table, int idx, int* ns, float* s, int* nc, float* c) {
+    int i;
+    if (table == 1) {
+        if (idx < 0 || idx >= 7) return -1;
+        *ns = SINCOS32[idx].ns;
+        *nc = SINCOS32[idx].nc;
+        for (i = 0; i < 4; ++i) {
+            s[i] = SINCOS32[idx].s[i];
+            c[i] = SINCOS32[idx].c[i];
+        }
+        return 0;
+    }
+    const sincos_t* q;
+    if (table == 0 && idx >= 0 && idx < 7) q = &SINCOS[idx];
+    else if (table == 2 && idx >= 0 && idx < 3) q = &SINCOS_QUARTER[idx];
+    else if (table == 3 && idx == 0) q = &ROPE_Q15_QUARTER;
+    else return -1;
+    *ns = q->ns;
+    *nc = q->nc;
+    for (i = 0; i < 4; ++i) {
+        s[i] = q->s[i];
+        c[i] = q->c[i];
     }
     return 0;
 }

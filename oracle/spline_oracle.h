@@ -111,6 +111,9 @@ int orc_sincos_f32(int prog, const float* angles, float* cos_out, float* sin_out
 /* ---- every 16-bit sin/cos program: prog 0..5 as orc_sincos, 6 FP16 quarter
  * turn D3/D4, 7 BF16 quarter turn D3/D4, 8 BF16 Cody-Waite D3/D4; outputs in
  * out_fmt; iterations > 0: compute probe sums in out_fmt. */
+/* Coefficient tables of the paired sin/cos programs (0 half turn 16-bit,
+ * 1 FP32, 2 quarter turn 16-bit, 3 RoPE Q15 quarter turn). */
+int orc_sincos_coeffs(int table, int idx, int* ns, float* s, int* nc, float* c);
 int orc_sincos16(int prog, int out_fmt, int rnd, const float* angles, uint16_t* cos_out,
                  uint16_t* sin_out, int64_t n, int iterations);
 /* RoPE tables [2, seq, nfreq] FP16: kind 0 half-turn D5/D6, 1 quarter-turn
