@@ -35,6 +35,11 @@ def _all_inputs(fmt, cuda):
 
 
 def _key(t):
+    """Integers whose differences count ULPs of t's format (sign-magnitude
+    bit patterns mapped onto a monotone line)."""
+    if t.dtype == torch.float32:
+        b = t.view(torch.int32).to(torch.int64)
+        return torch.where(b < 0, -(b & 0x7FFFFFFF), b)
     b = t.view(torch.int16).to(torch.int32)
     return torch.where(b < 0, -(b & 0x7FFF), b)
 
@@ -149,8 +154,17 @@ def sincos_case(capi, cuda, name, dt):
     capi.call(name, out, a, a.numel())
     torch.cuda.synchronize()
     ad = a.double()
-    return {"cos_max_abs": float((out[0].double() - torch.cos(ad)).abs().max()),
-            "sin_max_abs": float((out[1].double() - torch.sin(ad)).abs().max())}
+    res = {}
+    for plane, fn, label in ((0, torch.cos, "cos"), (1, torch.sin, "sin")):
+        ref = fn(ad)
+        res[f"{label}_max_abs"] = float((out[plane].double() - ref).abs().max())
+        # ULPs of the output format where |ref| >= 1/2, the binade below 1
+        # (near the zeros of sin and cos, absolute errors of 1e-3..1e-2 move
+        # the result across many binades and the absolute figure is the
+        # meaningful one)
+        sig = ref.abs() >= 0.5
+        res[f"{label}_max_ulp"] = int((_key(out[plane]) - _key(ref.to(dt))).abs()[sig].max())
+    return res
 
 
 # Stated bounds: the measured figure rounded up (max_abs to 2 significant
@@ -202,16 +216,16 @@ BOUNDS = {
     "exp2 d2 f32->bf16": {'max_rel': 0.0062, 'max_ulp': 1},
     "exp2 d3 f32->bf16": {'max_rel': 0.004, 'max_ulp': 1},
     "exp2 native f32->bf16": {'max_rel': 0.0039, 'max_ulp': 1},
-    "sincos_d3_d4_half_turn_bf16": {'cos_max_abs': 0.0077, 'sin_max_abs': 0.012},
-    "sincos_d5_d6_half_turn_bf16": {'cos_max_abs': 0.0082, 'sin_max_abs': 0.0059},
-    "sincos_d3_d4_half_turn_fp16": {'cos_max_abs': 0.0022, 'sin_max_abs': 0.0093},
-    "sincos_d5_d6_half_turn_fp16": {'cos_max_abs': 0.0011, 'sin_max_abs': 0.00079},
-    "sincos_d7_d6_half_turn_fp16": {'cos_max_abs': 0.0011, 'sin_max_abs': 0.00085},
-    "sincos_native_bf16": {'cos_max_abs': 0.0021, 'sin_max_abs': 0.0021},
-    "sincos_native_fp16": {'cos_max_abs': 0.00044, 'sin_max_abs': 0.00045},
-    "sincos_d3_d4_f32": {'cos_max_abs': 0.00016, 'sin_max_abs': 0.00016},
-    "sincos_d7_d6_f32": {'cos_max_abs': 1.2e-07, 'sin_max_abs': 1.2e-07},
-    "sincos_native_f32": {'cos_max_abs': 0.00035, 'sin_max_abs': 0.00035},
+    "sincos_d3_d4_half_turn_bf16": {'cos_max_abs': 0.0077, 'cos_max_ulp': 2, 'sin_max_abs': 0.012, 'sin_max_ulp': 3},
+    "sincos_d5_d6_half_turn_bf16": {'cos_max_abs': 0.0082, 'cos_max_ulp': 2, 'sin_max_abs': 0.0059, 'sin_max_ulp': 1},
+    "sincos_d3_d4_half_turn_fp16": {'cos_max_abs': 0.0022, 'cos_max_ulp': 2, 'sin_max_abs': 0.0093, 'sin_max_ulp': 19},
+    "sincos_d5_d6_half_turn_fp16": {'cos_max_abs': 0.0011, 'cos_max_ulp': 2, 'sin_max_abs': 0.00079, 'sin_max_ulp': 2},
+    "sincos_d7_d6_half_turn_fp16": {'cos_max_abs': 0.0011, 'cos_max_ulp': 2, 'sin_max_abs': 0.00085, 'sin_max_ulp': 2},
+    "sincos_native_bf16": {'cos_max_abs': 0.0021, 'cos_max_ulp': 1, 'sin_max_abs': 0.0021, 'sin_max_ulp': 1},
+    "sincos_native_fp16": {'cos_max_abs': 0.00044, 'cos_max_ulp': 1, 'sin_max_abs': 0.00045, 'sin_max_ulp': 1},
+    "sincos_d3_d4_f32": {'cos_max_abs': 0.00016, 'cos_max_ulp': 2546, 'sin_max_abs': 0.00016, 'sin_max_ulp': 2546},
+    "sincos_d7_d6_f32": {'cos_max_abs': 1.2e-07, 'cos_max_ulp': 2, 'sin_max_abs': 1.2e-07, 'sin_max_ulp': 2},
+    "sincos_native_f32": {'cos_max_abs': 0.00035, 'cos_max_ulp': 4815, 'sin_max_abs': 0.00035, 'sin_max_ulp': 4785},
 }
 
 
