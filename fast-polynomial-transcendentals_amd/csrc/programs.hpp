@@ -47,6 +47,20 @@ __device__ __forceinline__ uint32_t umin16x2(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
+// Clamp both halves of a sign-magnitude pair (BF16 or FP16 bits) to
+// [-Lc, Lc], keeping each half's sign, for lc = bits of the positive Lc in
+// both halves: a signed 16-bit minimum with Lc clamps the non-negative
+// halves and leaves the negative ones (below zero as int16) alone, then an
+// unsigned minimum with -Lc clamps the negative halves and leaves the
+// non-negative ones (below 0x8000) alone.  Equal to min(|x|, Lc) | sign(x)
+// on every pattern: a NaN or infinite magnitude selects Lc.
+__device__ __forceinline__ uint32_t sclamp16x2(uint32_t x, uint32_t lc) {
+    typedef int16_t i16x2_t __attribute__((ext_vector_type(2)));
+    const i16x2_t p = __builtin_elementwise_min(__builtin_bit_cast(i16x2_t, x),
+                                                __builtin_bit_cast(i16x2_t, lc));
+    return umin16x2(__builtin_bit_cast(uint32_t, p), lc | 0x80008000u);
+}
+
 // FP32 lanes of a BF16 pair.
 __device__ __forceinline__ float bf_lo(uint32_t u) { return as_f32(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return as_f32(u & 0xffff0000u); }
@@ -410,12 +424,12 @@ struct BF16Prog {
             lo = __builtin_fmaf(__builtin_fabsf(xl), rbf(tl * odd_horner(tl)), rbf(0.5f * xl));
             hi = __builtin_fmaf(__builtin_fabsf(xh), rbf(th * odd_horner(th)), rbf(0.5f * xh));
         } else {
-            const uint32_t t2 = umin16x2(x & 0x7fff7fffu, bf16_pair_bits(P.lc));
             if constexpr (P.shape == kEven) {
+                const uint32_t t2 = umin16x2(x & 0x7fff7fffu, bf16_pair_bits(P.lc));
                 lo = even_open(bf_lo(t2));
                 hi = even_open(bf_hi(t2));
             } else {
-                const uint32_t ts = t2 | (x & 0x80008000u);
+                const uint32_t ts = sclamp16x2(x, bf16_pair_bits(P.lc));
                 lo = odd_signed_open(bf_lo(ts));
                 hi = odd_signed_open(bf_hi(ts));
                 if constexpr (P.shape == kXHalfOdd) {
