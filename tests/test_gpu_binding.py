@@ -3,7 +3,6 @@
 torch.compile and the resolver layer — restating the reference's GPU verify
 script (autonumerics_zero/spline_ops/test_spline_ops.py) as pytest."""
 
-import numpy as np
 import pytest
 import torch
 

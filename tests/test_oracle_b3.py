@@ -8,7 +8,6 @@ hand-written PTX immediates of extras/paper/manuscript/main.tex:1046-1111.
 import math
 
 import numpy as np
-import pytest
 
 
 def bf(oracle, values):
