@@ -1,13 +1,14 @@
-"""HIP-graph capture of the drop-in ops.
+"""HIP-graph capture of the drop-in ops, forward and backward.
 
 The reference's launchers are graph-capture-safe: they launch on the current
 stream, allocate nothing themselves and never synchronise
 (autonumerics_zero/spline_ops/spline_ops.cpp:314-323 syncs only under
 SPLINE_OPS_SYNC_DEBUG).  This build's launchers keep that contract, so a
-torch.cuda.CUDAGraph can hold the forward ops of every hot-path family.  The
-graph is replayed several times with new inputs copied in eagerly between the
-replays (and eager launches of the same ops in between), and every replay
-must equal the eager result on the same inputs bit for bit."""
+torch.cuda.CUDAGraph can hold the forward and derivative launches of every
+hot-path family.  The graph is replayed several times with new inputs
+copied in eagerly between the replays (and eager launches of the same ops in
+between), and every replay must equal the eager result on the same inputs
+bit for bit."""
 
 import pytest
 import torch
@@ -42,6 +43,9 @@ def _inputs(seed: int) -> dict:
         "q": torch.randn(1, S_ATTN, 4, 128, generator=g).to(torch.bfloat16),
         "k": torch.randn(1, S_ATTN, 2, 128, generator=g).to(torch.bfloat16),
         "v": torch.randn(1, S_ATTN, 2, 128, generator=g).to(torch.bfloat16),
+        "dout": torch.randn(1, S_ATTN, 4, 128, generator=g).to(torch.bfloat16),
+        "gx": torch.randn(n, generator=g).to(torch.bfloat16),
+        "gpacked": torch.randn(24, 520, generator=g).to(torch.bfloat16),
     }
 
 
@@ -63,25 +67,41 @@ def _run(spline_ops, t: dict) -> list:
     return outs
 
 
+def _run_backward(spline_ops, t: dict) -> list:
+    """The derivative launches: activation and SwiGLU programs, the softcap
+    gradient, and the attention backward (delta, dK/dV with the grouped-head
+    partials, their reduction, dQ) behind its own forward."""
+    outs = [
+        spline_ops.sigmoid_bwd_variant(t["gx"], t["xb"], 4, 0),
+        spline_ops.softcap_tanh_bwd_bf16(t["gx"], t["scores"], 30.0),
+        spline_ops.swish_mul_packed_bwd_variant(t["gpacked"], t["packed"], 3, 0),
+    ]
+    scale = 128 ** -0.5
+    out, lse = spline_ops.flash_attn_fwd_bf16(t["q"], t["k"], t["v"], 0, 4, True, scale)
+    outs += list(spline_ops.flash_attn_bwd_bf16(t["q"], t["k"], t["v"], out, t["dout"], lse, 0, 0, 0, True,
+                                                scale, 0.0, 0.0))
+    return outs
+
+
 def _bits(t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
 
 
-def test_graph_replays_match_eager(cuda):
+def _check_replays(run):
     import spline_ops
 
-    static = {k: v.to(cuda) for k, v in _inputs(0).items()}
+    static = {k: v.to("cuda:0") for k, v in _inputs(0).items()}
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for _ in range(2):
-            _run(spline_ops, static)
+            run(spline_ops, static)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
 
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        captured = _run(spline_ops, static)
+        captured = run(spline_ops, static)
 
     for seed in (1, 2, 3):
         fresh = _inputs(seed)
@@ -89,9 +109,17 @@ def test_graph_replays_match_eager(cuda):
             tensor.copy_(fresh[name])
         graph.replay()
         torch.cuda.synchronize()
-        eager = _run(spline_ops, static)
+        eager = run(spline_ops, static)
         torch.cuda.synchronize()
         assert len(captured) == len(eager)
         for i, (a, b) in enumerate(zip(captured, eager)):
             assert a.shape == b.shape and a.dtype == b.dtype, (seed, i)
             assert torch.equal(_bits(a), _bits(b)), f"replay {seed}: output {i} differs from eager"
+
+
+def test_graph_replays_match_eager(cuda):
+    _check_replays(_run)
+
+
+def test_backward_graph_replays_match_eager(cuda):
+    _check_replays(_run_backward)
