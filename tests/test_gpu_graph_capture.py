@@ -117,7 +117,12 @@ def _check_replays(run):
             assert torch.equal(_bits(a), _bits(b)), f"replay {seed}: output {i} differs from eager"
 
 
-def test_graph_replays_match_eager(cuda):
+@pytest.mark.parametrize("sync_debug", [False, True])
+def test_graph_replays_match_eager(cuda, monkeypatch, sync_debug):
+    # SPLINE_OPS_SYNC_DEBUG synchronises after every launch except while the
+    # stream is being captured, so capture works with it on too
+    if sync_debug:
+        monkeypatch.setenv("SPLINE_OPS_SYNC_DEBUG", "1")
     _check_replays(_run)
 
 
