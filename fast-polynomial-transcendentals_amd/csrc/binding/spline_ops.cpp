@@ -678,7 +678,12 @@ std::vector<at::Tensor> flash_attn_fwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     const int64_t b = q.size(0), sq = q.size(1), hq = q.size(2), hkv = k.size(2);
     const int64_t d = q.size(3);
     at::Tensor out = at::empty({b, sq, hq, d}, q.options());
-    at::Tensor lse = at::zeros({b, hq, sq}, q.options().dtype(at::kFloat));
+    // the softmax and softcap modes write every lse row; the sigmoid modes
+    // (5..11) have no partition function and leave it untouched, so only
+    // they need it cleared
+    const bool sigmoid_mode = mode >= 5 && mode <= 11;
+    at::Tensor lse = sigmoid_mode ? at::zeros({b, hq, sq}, q.options().dtype(at::kFloat))
+                                  : at::empty({b, hq, sq}, q.options().dtype(at::kFloat));
     const int64_t strides[12] = {q.stride(0), q.stride(2), q.stride(1), k.stride(0), k.stride(2),
                                  k.stride(1), v.stride(0), v.stride(2), v.stride(1), out.stride(0),
                                  out.stride(2), out.stride(1)};

@@ -179,6 +179,40 @@ def test_graph_capture_replays(spline_ops, cuda):
         _eq(y, eager)
 
 
+@pytest.mark.parametrize("mode", [0, 4, 5])
+def test_flash_attn_lse_rows(spline_ops, cuda, mode):
+    """flash_attn_fwd_bf16's lse: every row written for the softmax and
+    softcap modes (the binding does not clear it), zeros for sigmoid
+    attention, which has no partition function."""
+    b, s, hq, hkv, d = 1, 256, 4, 2, 128
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(b, s, hq, d, generator=g).to(torch.bfloat16).to(cuda)
+    k = torch.randn(b, s, hkv, d, generator=g).to(torch.bfloat16).to(cuda)
+    v = torch.randn(b, s, hkv, d, generator=g).to(torch.bfloat16).to(cuda)
+    scale, cap = d ** -0.5, 30.0
+    # leave NaNs in the allocator block the lse will reuse
+    junk = torch.full((b * hq * s,), float("nan"), device=cuda)
+    del junk
+    torch.cuda.synchronize()
+    _, lse = spline_ops.flash_attn_fwd_bf16(q, k, v, mode, 4, True, scale, cap if mode == 4 else 0.0,
+                                            -6.0 if mode == 5 else 0.0)
+    torch.cuda.synchronize()
+    assert lse.shape == (b, hq, s) and lse.dtype == torch.float32
+    if mode == 5:
+        assert torch.count_nonzero(lse) == 0
+        return
+    qf = q.float().transpose(1, 2)
+    kf = k.float().transpose(1, 2).repeat_interleave(hq // hkv, dim=1)
+    sc = (qf @ kf.transpose(-1, -2)) * scale
+    if mode == 4:
+        sc = cap * torch.tanh(sc / cap)
+    sc = sc.masked_fill(torch.ones(s, s, dtype=torch.bool, device=cuda).triu(1), float("-inf"))
+    want = torch.logsumexp(sc, dim=-1)
+    assert torch.isfinite(lse).all()
+    # the D4 softcap program departs from FP32 tanh by up to 0.41 per score
+    torch.testing.assert_close(lse, want, rtol=0.0, atol=0.45 if mode == 4 else 2e-3)
+
+
 def test_activation_resolver_layer(cuda):
     from sfu_repro import activations
 
