@@ -1,0 +1,153 @@
+"""AMD ISA audit of the built library, the gfx950 counterpart of the
+reference's SASS audit (autonumerics_zero/spline_ops/audit_sincos_sass.py
+greps the disassembled CUDA kernels for MUFU opcodes to show that the
+polynomial programs issue no hardware transcendental).  Here the gfx950 code
+objects embedded in libspline_hip.so (this build's own output) are
+disassembled with llvm-objdump and every kernel is classified by the program
+its name carries:
+
+* polynomial kernels issue no hardware transcendental: no v_exp, v_log,
+  v_sin, v_cos, v_sqrt or v_rsq, and, in the kernel families that do no
+  integer division, no v_rcp either (the compiler's 64-bit division
+  expansion uses v_rcp_f32 on converted integers, as in the packed SwiGLU
+  row / column split and the RoPE and attention index math);
+* the hardware baselines, the hybrid kernels' transcendental lanes and the
+  softmax attention issue theirs;
+* no kernel issues packed FP32 arithmetic (v_pk_fma_f32, v_pk_mul_f32,
+  v_pk_add_f32): the build turns the packed-fp32-ops target feature off.
+
+Runs on the CPU (no GPU, no compute)."""
+
+import collections
+import os
+import re
+import struct
+import subprocess
+import tempfile
+
+import pytest
+
+import capi_helpers
+
+OBJDUMP = "/opt/rocm/llvm/bin/llvm-objdump"
+OBJCOPY = "/opt/rocm/llvm/bin/llvm-objcopy"
+BUNDLE_MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+
+HARD_TRANS = re.compile(r"^v_(exp|log|sin|cos|sqrt|rsq)_")
+RCP = re.compile(r"^v_rcp_(f32|f16)")  # v_rcp_iflag_f32 (integer division) excluded
+PACKED_F32 = re.compile(r"^v_pk_(fma|mul|add)_f32")
+
+
+def _code_objects(lib_path: str, tmp: str) -> list:
+    """gfx950 code objects of every offload bundle in the library's
+    .hip_fatbin section (one bundle per translation unit)."""
+    fatbin = os.path.join(tmp, "fatbin")
+    subprocess.run([OBJCOPY, "--dump-section", f".hip_fatbin={fatbin}", lib_path, os.path.join(tmp, "stripped")],
+                   check=True, capture_output=True)
+    data = open(fatbin, "rb").read()
+    objects = []
+    for start in (m.start() for m in re.finditer(re.escape(BUNDLE_MAGIC), data)):
+        (entries,) = struct.unpack_from("<Q", data, start + len(BUNDLE_MAGIC))
+        p = start + len(BUNDLE_MAGIC) + 8
+        for _ in range(entries):
+            offset, size, triple_len = struct.unpack_from("<QQQ", data, p)
+            p += 24
+            triple = data[p:p + triple_len].decode()
+            p += triple_len
+            if triple.endswith("gfx950"):
+                path = os.path.join(tmp, f"co{len(objects)}.o")
+                with open(path, "wb") as f:
+                    f.write(data[start + offset:start + offset + size])
+                objects.append(path)
+    return objects
+
+
+@pytest.fixture(scope="module")
+def kernels():
+    """Demangled kernel name (without parameters) -> Counter of mnemonics."""
+    if not os.path.exists(OBJDUMP) or not os.path.exists(OBJCOPY):
+        pytest.skip("ROCm llvm-objdump / llvm-objcopy not found")
+    assert os.path.exists(capi_helpers.LIB), "build the library first (__graft_entry__.build())"
+    out = collections.defaultdict(collections.Counter)
+    with tempfile.TemporaryDirectory() as tmp:
+        objects = _code_objects(capi_helpers.LIB, tmp)
+        assert objects, "no gfx950 code object in the library"
+        for obj in objects:
+            text = subprocess.run([OBJDUMP, "-d", "-C", "--no-show-raw-insn", "--no-leading-addr", obj],
+                                  check=True, capture_output=True, text=True).stdout
+            name = None
+            for line in text.splitlines():
+                m = re.match(r"^<(.+)>:$", line)
+                if m:
+                    name = re.sub(r"\(.*", "", m.group(1))
+                    continue
+                if name and line.startswith("\t"):
+                    out[name][line.split()[0]] += 1
+    return out
+
+
+def _uses(counter, pattern) -> list:
+    return sorted(k for k in counter if pattern.match(k))
+
+
+NATIVE_OR_HYBRID = re.compile(r"Native|Hybrid|exp2_(bf16|f32)_kernel<2,")
+# families whose index math has no integer division
+NO_DIVISION = re.compile(r"pt::(pairwise_kernel|pairwise_element_kernel|sincos_table_kernel|"
+                         r"sincos_compute_kernel|sincos_f32_kernel|exp2_bf16_kernel|exp2_f32_kernel|b3_f32_kernel|"
+                         r"ref_sincos_kernel)\b")
+# sigmoid-attention modes with a score program: B3 (6), B3-D2 (7), BF16 D3-D6 (8-11)
+POLY_ATTENTION = re.compile(r"pt::flash_(fwd|bwd_dkdv|bwd_dq)_kernel<(6|7|8|9|10|11),")
+
+
+def _polynomial(name: str) -> bool:
+    if NATIVE_OR_HYBRID.search(name):
+        return False
+    if POLY_ATTENTION.search(name):
+        return True
+    return bool(re.search(r"Prog<|Alg<|Softcap(Fwd|Bwd)\w*Op|B3\w*Op|B3D2|HalfTurn|Quarter|PairLut|"
+                          r"RopeFixedPhase|RopeCachedTable|exp2_(bf16|f32)_kernel<[013],|b3_f32_kernel|ref_sincos_kernel",
+                          name))
+
+
+def test_audit_sees_every_family(kernels):
+    assert len(kernels) > 900
+    for family in ("pairwise_kernel", "packed_fwd_kernel", "sincos_compute_kernel", "rope_apply_kernel",
+                   "flash_fwd_kernel", "flash_bwd_dkdv_kernel", "flash_bwd_dq_kernel", "exp2_bf16_kernel"):
+        assert any(f"pt::{family}<" in k for k in kernels), family
+    poly = [k for k in kernels if _polynomial(k)]
+    assert len(poly) > 500
+
+
+def test_no_packed_fp32_arithmetic(kernels):
+    bad = {k: _uses(c, PACKED_F32) for k, c in kernels.items() if _uses(c, PACKED_F32)}
+    assert not bad, bad
+
+
+def test_polynomial_kernels_issue_no_transcendental(kernels):
+    bad = {}
+    for name, counter in kernels.items():
+        if not _polynomial(name):
+            continue
+        hits = _uses(counter, HARD_TRANS)
+        if NO_DIVISION.search(name):
+            hits += _uses(counter, RCP)
+        if hits:
+            bad[name] = hits
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("pattern,needed", [
+    (r"UnaryOp<pt::(F16|BF16)Native<", r"^v_exp_f32"),
+    (r"pt::(NativeSinCos|F32Native|PairNative|RopeNativeAngle)\b", r"^v_(sin|cos)_f32"),
+    (r"SoftcapNativeOp|B3NativeOp", r"^v_exp_f32"),
+    (r"exp2_(bf16|f32)_kernel<2,", r"^v_exp_f32"),
+    # the vector path (the element path is all polynomial: the transcendental
+    # lanes exist only for whole 16-byte vectors)
+    (r"pairwise_kernel<pt::Hybrid(Fwd|Bwd)Op", r"^v_exp_f32"),
+    (r"pt::flash_fwd_kernel<0,", r"^v_exp_f32"),
+])
+def test_hardware_baselines_issue_their_transcendental(kernels, pattern, needed):
+    matched = [k for k in kernels if re.search(pattern, k)]
+    assert matched, pattern
+    missing = [k for k in matched if not _uses(kernels[k], re.compile(needed))]
+    assert not missing, missing
