@@ -14,7 +14,9 @@ its name carries:
 * the hardware baselines, the hybrid kernels' transcendental lanes and the
   softmax attention issue theirs;
 * no kernel issues packed FP32 arithmetic (v_pk_fma_f32, v_pk_mul_f32,
-  v_pk_add_f32): the build turns the packed-fp32-ops target feature off.
+  v_pk_add_f32): the build turns the packed-fp32-ops target feature off;
+* no kernel spills registers to scratch memory (the code objects' AMDGPU
+  metadata), apart from one measured exception.
 
 Runs on the CPU (no GPU, no compute)."""
 
@@ -60,6 +62,42 @@ def _code_objects(lib_path: str, tmp: str) -> list:
                     f.write(data[start + offset:start + offset + size])
                 objects.append(path)
     return objects
+
+
+READELF = "/opt/rocm/llvm/bin/llvm-readelf"
+
+
+def _kernel_metadata(obj: str) -> list:
+    """(.name, .vgpr_spill_count, .private_segment_fixed_size) of every
+    kernel in one code object's AMDGPU metadata note."""
+    text = subprocess.run([READELF, "--notes", obj], check=True, capture_output=True, text=True).stdout
+    records, cur = [], {}
+    for line in text.splitlines():
+        m = re.match(r"\s*(-\s+)?\.(\w+):\s+(.*)$", line)
+        if not m:
+            continue
+        if m.group(1) and cur:  # a new list item starts a new kernel record
+            records.append(cur)
+            cur = {}
+        cur[m.group(2)] = m.group(3).strip()
+    if cur:
+        records.append(cur)
+    return [(r["name"], int(r.get("vgpr_spill_count", 0)), int(r.get("private_segment_fixed_size", 0)))
+            for r in records if "name" in r and "vgpr_spill_count" in r]
+
+
+@pytest.fixture(scope="module")
+def metadata():
+    if not os.path.exists(READELF) or not os.path.exists(OBJCOPY):
+        pytest.skip("ROCm llvm-readelf / llvm-objcopy not found")
+    assert os.path.exists(capi_helpers.LIB), "build the library first (__graft_entry__.build())"
+    with tempfile.TemporaryDirectory() as tmp:
+        rows = []
+        for obj in _code_objects(capi_helpers.LIB, tmp):
+            rows += _kernel_metadata(obj)
+    demangled = subprocess.run(["c++filt"], input="\n".join(r[0] for r in rows), check=True,
+                               capture_output=True, text=True).stdout.splitlines()
+    return [(re.sub(r"\(.*", "", d), spill, scratch) for d, (_, spill, scratch) in zip(demangled, rows)]
 
 
 @pytest.fixture(scope="module")
@@ -151,3 +189,15 @@ def test_hardware_baselines_issue_their_transcendental(kernels, pattern, needed)
     assert matched, pattern
     missing = [k for k in matched if not _uses(kernels[k], re.compile(needed))]
     assert not missing, missing
+
+
+def test_no_register_spills_outside_the_measured_exception(metadata):
+    """No kernel spills VGPRs to scratch memory, except the head_dim-64
+    dK/dV kernels of the softmax modes, which are held to 128 VGPRs for four
+    waves per SIMD and spill at most a few registers (measured faster than
+    the unspilled two-wave form)."""
+    assert len(metadata) > 900
+    allowed = re.compile(r"pt::flash_bwd_dkdv_kernel<(0|1|2|12), 0, \d+, 64, 8>$")
+    bad = [(n, spill, scratch) for n, spill, scratch in metadata
+           if (spill or scratch) and not (allowed.search(n) and spill <= 4 and scratch <= 16)]
+    assert not bad, bad
