@@ -17,6 +17,11 @@
  *
  * The B3 program follows scripts/audit_b3_deployed_fit.py:319-366 literally:
  * its BF16 FMA is round_bf16(float32(a*b + c)) computed in binary64.
+ *
+ * Parity unpinned (no reference arithmetic to check against; see
+ * spline_oracle.h): the B2 softcap composition and the 16-bit output
+ * rounding of the B5 exp2 programs, both of which live in the absent
+ * FlashAttention-4.
  */
 #include "spline_oracle.h"
 

@@ -85,11 +85,20 @@ int orc_b3_constants(uint16_t* fwd8, uint16_t* grad4, uint16_t* split_clamp2);
 int orc_b3_exp2_d2_bf16(const uint16_t* x, uint16_t* y, uint16_t* dy, int64_t n,
                         const float* coeffs3);
 
-/* ---- B2 softcap (BF16) --------------------------------------------------- */
+/* ---- B2 softcap (BF16) ---------------------------------------------------
+ * Parity unpinned against the reference: its softcap composition lives in
+ * FlashAttention-4, which is not part of the reference tree.  The steps are
+ * this build's (u = bf16(s * (1/cap)), the reference's TANH_FWD_D4_ODD_BF16,
+ * y = bf16(T * cap)); tests pin them step by step to that D4 program and
+ * bound the result against cap * tanh(s / cap). */
 int orc_softcap_fwd_bf16(const uint16_t* s, uint16_t* y, int64_t n, float cap);
 int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int64_t n, float cap);
 
-/* ---- B5 exp2: kind 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge ----------------- */
+/* ---- B5 exp2: kind 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge -----------------
+ * The FP32 programs are pinned (p(0) = 1, p(1) = 2, the published fit and
+ * error metrics); the deployed 16-bit output rounding is parity unpinned
+ * (it lives in the absent FlashAttention-4): here one RNE of the FP32
+ * result. */
 int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n);
 
 /* ---- paired sin/cos: prog 0 BF16 D3/D4, 1 BF16 D5/D6, 2 FP16 D3/D4,
