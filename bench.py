@@ -15,8 +15,8 @@ object (under 2 KB) carrying
   launch / average kernel time against the 8 TB/s HBM peak, the HBM
   traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
   profile of this kernel, and `stream_ceiling_frac`: plain copy, read-only,
-  write-only, torch copy_ and zero_ streams over the same tensor, as
-  fractions of 8 TB/s;
+  write-only, two-reads-per-write, torch copy_ and zero_ streams over the
+  same tensor, as fractions of 8 TB/s;
 * `numerics`: max |error| and max ULP (BF16) against FP32 torch
   30*tanh(s/30) on the whole tensor, for the polynomial and the native;
 * `cpu_baseline`: the CPU oracle (a C restatement of the same program, all
