@@ -145,7 +145,17 @@ struct SoftcapConsts {
 // the continuous two-piece FP32 fraction of the full-range benchmark
 // (autonumerics_zero/cuda_benchmarks/benchmark_exp2_pwl2.cu:126-170):
 // p = 0.98946118 + 0.82085252 f + 0.34246066 max(f - 0.5, 0).
-// Defined for x < 128 (softmax exponents are <= 0); -inf and NaN give +0.
+// Defined for x < 128 (softmax exponents are <= 0); -inf and NaN give +0
+// (D2, D3) or the value at the clamp (PWL2).
+//
+// The PWL2 fraction starts below one (p(0) = 0.98946), so at n = -127 the
+// exponent field of (n << 23) + bits(p) wraps below zero and the bits are a
+// NaN for x < -126.987: the reference's hinge clamps at -127 too
+// (benchmark_exp2_pwl2.cu:161-162), harmlessly on its benchmark domain
+// [-16, 0].  A softmax exponent takes any negative value (a key far below
+// the row maximum, or s - lse in the backward), so PWL2 is clamped at -126
+// here: from there on the result is positive and at most 2^-126, as 2^x is.
+// The programs agree with the reference's bit for bit on x >= -126.
 // ---------------------------------------------------------------------------
 
 enum Exp2Kind : int { kExp2D2 = 0, kExp2D3 = 1, kExp2Native = 2, kExp2Pwl2 = 3 };
@@ -155,7 +165,7 @@ __device__ __forceinline__ float exp2_lane(float x) {
     if constexpr (KIND == kExp2Native) {
         return __builtin_amdgcn_exp2f(x);
     } else {
-        x = __builtin_fmaxf(x, -127.0f);
+        x = __builtin_fmaxf(x, KIND == kExp2Pwl2 ? -126.0f : -127.0f);
         const float fl = __builtin_floorf(x);
         const float f = x - fl;
         float p;

@@ -31,6 +31,13 @@ def _b3_d2_coeffs():
         return json.load(f)["coefficients_float32"]
 
 
+def _exp2_arg(mode, x):
+    """The fused kernels clamp the PWL2 exponent at -126 (the reference's
+    hinge, clamped at -127, wraps into NaN bits below -126.987: its fraction
+    starts below one); the D2 / D3 programs take the reference's -127."""
+    return torch.clamp(x, min=-126.0) if mode == "softmax_pwl2" else x
+
+
 def probs_and_grad(oracle, a, mode, grad, scale, cap, bias, lse2, route):
     """P and the derivative factor g of raw dot products a [B, H, Sq, Sk]
     (float32), as the kernel evaluates them."""
@@ -39,7 +46,8 @@ def probs_and_grad(oracle, a, mode, grad, scale, cap, bias, lse2, route):
         x = a * np.float32(scale * LOG2E) - lse2[..., None]
         p = torch.exp2(x.double()).float()
         if mode in EXP2_KIND and route:
-            pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], x.numpy().reshape(-1), out_bf16=False)).reshape(shape)
+            pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], _exp2_arg(mode, x).numpy().reshape(-1),
+                                              out_bf16=False)).reshape(shape)
             sel = (route_slot(torch.arange(shape[-1])) % route) < 4
             p = torch.where(sel, pp, p)
         return p, torch.ones_like(p)
@@ -147,7 +155,8 @@ def reference_fwd(oracle, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=
     m = x.amax(-1, keepdim=True)
     e = torch.exp2((x - m).double()).float()
     if mode in EXP2_KIND:
-        pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], (x - m).numpy().reshape(-1), out_bf16=False)).reshape(x.shape)
+        pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], _exp2_arg(mode, x - m).numpy().reshape(-1),
+                                          out_bf16=False)).reshape(x.shape)
         sel = (route_slot(torch.arange(n)) % route) < 4
         e = torch.where(sel, pp, e).masked_fill(mask, 0.0)
     l = e.sum(-1, keepdim=True)

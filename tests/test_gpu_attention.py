@@ -19,7 +19,7 @@ def _f32_inputs(seed, n=1 << 18):
         -rng.random(n, dtype=np.float32) * 140.0,             # softmax exponents
         np.linspace(-3.0, 1.0, 4099, dtype=np.float32),
         np.array([0.0, -0.0, -1e-30, -1e-40, -126.5, -127.0, -127.25, -128.0,
-                  -np.inf, 0.999999, 1.5, 60.25], dtype=np.float32),
+                  -np.inf, np.nan, -np.nan, 0.999999, 1.5, 60.25], dtype=np.float32),
     ])
     return x.astype(np.float32)
 

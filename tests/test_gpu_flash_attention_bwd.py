@@ -251,3 +251,34 @@ def test_grouped_heads_need_the_partials_workspace(capi, cuda):
     assert call(ctypes.c_void_p(0)) != 0
     assert call(capi.ptr(ws)) == 0
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("mode,route", [("softmax_pwl2", 4), ("softmax_pwl2", 10), ("softmax_d2", 4),
+                                        ("softmax_d3", 4)])
+def test_wide_score_range(capi, oracle, cuda, mode, route):
+    """Scores spread over hundreds of log2 units, so many softmax exponents
+    (against the row maximum forward, against lse backward) fall below
+    -127: every program must give a probability that vanishes, never a NaN
+    (the PWL2 fraction starts below one, so its -127 clamp would wrap the
+    exponent field; the kernels clamp it at -126)."""
+    from attention_reference import reference_fwd
+
+    q, k, v, do = _inputs(1, 4, 2, 256, 900 + route + M[mode], qmul=30.0)
+    scale = 1 / math.sqrt(128)
+    out, lse = fwd(capi, cuda, q, k, v, mode, True, scale, route=route)
+    ro, rl = reference_fwd(oracle, q, k, v, mode, True, scale, route=route)
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    ok, info = _close(out.cpu().float(), ro)
+    assert ok, ("out", info)
+    # the kernel takes exponents against its lazily moved row maximum (up to
+    # 8 below the true one), the reference against the true maximum, so a
+    # routed exponent's program error (PWL2 up to 1.05 % relative) can differ
+    # by up to twice that between the two sums
+    bound = 2.5e-2 if mode == "softmax_pwl2" else 1e-2
+    assert (lse.cpu() - rl).abs().max().item() < bound
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, mode, 0, True, scale, route=route)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, mode, 0, True, scale, 30.0, route, 0.0)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert torch.isfinite(got).all(), name
+        ok, info = _close(got, ref)
+        assert ok, (mode, route, name, info)

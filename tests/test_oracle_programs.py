@@ -191,8 +191,21 @@ def test_exp2_d2_invariants_and_fit(oracle):
     assert 2.0e-3 < rel.max() < 2.8e-3        # appendix_exp2.tex: 2.679e-3
     rel3 = np.abs(oracle.exp2(1, x, False) / np.exp2(x.astype(np.float64)) - 1)
     assert rel3.max() < 1.0e-4                 # FA4 D3: 8.763e-5
-    # masking value and clamp
-    assert oracle.exp2(0, np.array([-np.inf, -127.0, -1000.0], dtype=np.float32), False).tolist() == [0.0, 0.0, 0.0]
+    # masking value and clamp; a NaN exponent takes the clamp (max(NaN, -127)
+    # is -127), so it gives +0 like a masked score
+    low = np.array([-np.inf, -127.0, -1000.0, np.nan, -np.nan], dtype=np.float32)
+    for kind in (0, 1):
+        got = oracle.exp2(kind, low, False)
+        assert got.view(np.uint32).tolist() == [0, 0, 0, 0, 0], (kind, got)
+    # the reference's PWL2 hinge starts below one (p(0) = 0.98946), so at its
+    # -127 clamp the exponent field wraps into NaN bits (the fused attention
+    # kernels clamp PWL2 at -126 for this reason); from -126 up it is positive
+    # and at most 2^-126
+    assert np.isnan(oracle.exp2(2, low, False)).all()
+    edge = np.array([-126.99, -126.98, -126.5, -126.0], dtype=np.float32)
+    assert np.isnan(oracle.exp2(2, edge[:1], False)).all()
+    tail = oracle.exp2(2, edge[1:], False)
+    assert (tail > 0).all() and (tail <= 2.0 ** -126).all()
 
 
 def _full_f32_error_input():
