@@ -257,14 +257,14 @@ extern "C" int launch_flash_sigmoid_direct_d3_d4_f32_bf16(void* y, void* dy, con
 
 extern "C" int launch_softcap_tanh_d4_bf16(void* out, const void* scores, int64_t size, float cap,
                                            void* stream) {
-    if (bad_args(size, {out, scores}) || !(cap > 0.0f)) return hipErrorInvalidValue;
+    if (bad_args(size, {out, scores}) || !(cap > 0.0f && cap <= __FLT_MAX__)) return hipErrorInvalidValue;
     Streams<1, 1> s{{scores}, {out}, {cap, 1.0f / cap}};
     return launch_pairwise<SoftcapFwdOp>(s, size, hs(stream));
 }
 
 extern "C" int launch_softcap_tanh_native_bf16(void* out, const void* scores, int64_t size,
                                                float cap, void* stream) {
-    if (bad_args(size, {out, scores}) || !(cap > 0.0f)) return hipErrorInvalidValue;
+    if (bad_args(size, {out, scores}) || !(cap > 0.0f && cap <= __FLT_MAX__)) return hipErrorInvalidValue;
     Streams<1, 1> s{{scores}, {out}, {cap, 1.0f / cap}};
     return launch_pairwise<SoftcapNativeOp>(s, size, hs(stream));
 }
@@ -272,7 +272,7 @@ extern "C" int launch_softcap_tanh_native_bf16(void* out, const void* scores, in
 extern "C" int launch_softcap_tanh_d4_bwd_bf16(void* grad_scores, const void* grad_out,
                                                const void* scores, int64_t size, float cap,
                                                void* stream) {
-    if (bad_args(size, {grad_scores, grad_out, scores}) || !(cap > 0.0f))
+    if (bad_args(size, {grad_scores, grad_out, scores}) || !(cap > 0.0f && cap <= __FLT_MAX__))
         return hipErrorInvalidValue;
     Streams<2, 1> s{{grad_out, scores}, {grad_scores}, {cap, 1.0f / cap}};
     return launch_pairwise<SoftcapBwdOp>(s, size, hs(stream));

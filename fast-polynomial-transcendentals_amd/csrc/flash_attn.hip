@@ -455,7 +455,7 @@ extern "C" int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, co
         return hipErrorInvalidValue;
     if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
         return hipErrorInvalidValue;
-    if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f))
+    if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f && cap <= __FLT_MAX__))
         return hipErrorInvalidValue;
     if (attn_has_exp2_program(mode) && !route_supported(exp2_route)) return hipErrorInvalidValue;
     const int hd = (int)head_dim;

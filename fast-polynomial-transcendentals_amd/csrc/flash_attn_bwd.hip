@@ -759,7 +759,8 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
     const int hd = (int)head_dim;
     if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
         return hipErrorInvalidValue;
-    if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f)) return hipErrorInvalidValue;
+    if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f && cap <= __FLT_MAX__))
+        return hipErrorInvalidValue;
     if ((mode == kAttnSigmoidB3 || mode == kAttnSigmoidB3D2) && seq != 4096) return hipErrorInvalidValue;
     // derivative programs: softcap D4 takes analytical / ste / 1 - T^2, B3
     // algebraic / direct, every other mode its natural one

@@ -276,7 +276,9 @@ int launch_flash_sigmoid_exp2_d2_bf16(void* y, void* dy, const void* scores, int
  * lives in the absent FA4 kernel.  Forward: u = bf16(s * (1/cap)),
  * out = bf16(cap * TANH_FWD_D4_ODD_BF16(u)).  Backward: grad_scores =
  * bf16(grad_out * T'(u)) with the differentiated D4 polynomial (the scale
- * cancels, extras/paper/manuscript/main.tex:443-449, 754-758). */
+ * cancels, extras/paper/manuscript/main.tex:443-449, 754-758).  cap must be
+ * positive and finite (hipErrorInvalidValue otherwise), here and in the
+ * attention softcap modes. */
 int launch_softcap_tanh_d4_bf16(void* out, const void* scores, int64_t size, float cap,
                                 void* stream);
 int launch_softcap_tanh_d4_bwd_bf16(void* grad_scores, const void* grad_out, const void* scores,

@@ -209,6 +209,26 @@ def test_zero_size_and_bad_args(capi, cuda):
     rc = capi.launch_swish_fwd_d3_kernel(ctypes.c_void_p(0), ctypes.c_void_p(0), ctypes.c_int64(-1),
                                          capi.stream())
     assert rc != 0
+    # softcap: cap must be positive and finite; nothing is launched otherwise
+    s = torch.zeros(64, dtype=torch.bfloat16, device=cuda)
+    for cap in (0.0, -30.0, float("inf"), float("nan")):
+        for name in ("launch_softcap_tanh_d4_bf16", "launch_softcap_tanh_native_bf16"):
+            rc = getattr(capi, name)(capi.ptr(s), capi.ptr(s), ctypes.c_int64(64), ctypes.c_float(cap),
+                                     capi.stream())
+            assert rc != 0, (name, cap)
+        rc = capi.launch_softcap_tanh_d4_bwd_bf16(capi.ptr(s), capi.ptr(s), capi.ptr(s), ctypes.c_int64(64),
+                                                  ctypes.c_float(cap), capi.stream())
+        assert rc != 0, cap
+    # the attention softcap modes check cap before an empty batch returns
+    strides = (ctypes.c_int64 * 12)(*([128 * 128, 128 * 128, 128] * 4))
+    null = ctypes.c_void_p(0)
+    for mode in (3, 4):
+        for cap, ok in ((30.0, True), (float("inf"), False), (0.0, False)):
+            rc = capi.launch_flash_attention_fwd_strided_bf16(
+                null, null, null, null, null, ctypes.c_int64(0), ctypes.c_int64(1), ctypes.c_int64(1),
+                ctypes.c_int64(128), ctypes.c_int64(128), strides, ctypes.c_int(mode), ctypes.c_int(4),
+                ctypes.c_int(0), ctypes.c_float(1.0), ctypes.c_float(cap), ctypes.c_float(0.0), capi.stream())
+            assert (rc == 0) == ok, (mode, cap, rc)
 
 
 @pytest.mark.parametrize("reps", [1024, 2056])
