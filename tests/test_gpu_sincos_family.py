@@ -38,12 +38,14 @@ TABLES16 = [
 
 def _angles(ragged, n_random=1 << 18):
     rng = np.random.default_rng(3)
+    # special angles first: the length is cut to whole vectors at the end
     a = np.concatenate([
+        np.array([0.0, -0.0, 1e-30, -1e-30, 1e-40, 4095.0, 3e7, -1e10,
+                  np.inf, -np.inf, np.nan, -np.nan, 3.4e38, -3.4e38], dtype=np.float32),
+        (np.arange(-16, 17) * (math.pi / 4)).astype(np.float32),
         rng.uniform(-200.0, 200.0, n_random).astype(np.float32),
         rng.uniform(-2e5, 2e5, 4096).astype(np.float32),
         np.linspace(-4 * math.pi, 4 * math.pi, 8197, dtype=np.float32),
-        (np.arange(-16, 17) * (math.pi / 4)).astype(np.float32),
-        np.array([0.0, -0.0, 1e-30, -1e-30, 1e-40, 4095.0, 3e7, -1e10], dtype=np.float32),
     ])
     n = (a.size // 8) * 8
     return np.ascontiguousarray(a[: n - 3] if ragged else a[:n])
