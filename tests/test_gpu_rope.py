@@ -24,11 +24,13 @@ TABLES = [
 
 def _angles(ragged, n_random=1 << 18):
     rng = np.random.default_rng(2)
+    # special angles first: the length is cut to whole vectors at the end
     a = np.concatenate([
+        np.array([0.0, -0.0, 1e-30, math.pi / 2, math.pi, 4095.0, np.inf, -np.inf, np.nan, 3e7,
+                  -1e10], dtype=np.float32),
         rng.uniform(-100.0, 100.0, n_random).astype(np.float32),
         np.linspace(-4 * math.pi, 4 * math.pi, 8197, dtype=np.float32),
         np.arange(4096, dtype=np.float32) * np.float32(0.0157),
-        np.array([0.0, -0.0, 1e-30, math.pi / 2, math.pi, 4095.0], dtype=np.float32),
     ])
     n = (a.size // 8) * 8
     return np.ascontiguousarray(a[: n - 3] if ragged else a[:n])
