@@ -126,6 +126,36 @@ def test_autograd_functions(spline_ops, cuda):
     _eq(x.grad, spline_ops.swish_bwd_d5(torch.ones_like(y), x.detach()))
 
 
+def test_bf16_swish_tails(spline_ops, cuda):
+    """test_spline_ops.py:159-166: the BF16 SwiGLU tails are exact."""
+    x = torch.tensor([-100.0, -20.0, 20.0, 100.0], device=cuda, dtype=torch.bfloat16)
+    expected = torch.tensor([0.0, 0.0, 20.0, 100.0], device=cuda, dtype=torch.bfloat16)
+    for degree in (3, 4, 5, 6):
+        _eq(spline_ops.swish_mul_fwd_variant(x, torch.ones_like(x), degree, 0), expected)
+
+
+def test_bf16_sollya_variants(spline_ops, cuda):
+    """test_spline_ops.py:169-204: the Sollya coefficients through the unary,
+    fused and packed paths."""
+    x = torch.linspace(-8.0, 8.0, 16384, device=cuda, dtype=torch.bfloat16)
+    up = torch.linspace(-1.0, 1.0, x.numel(), device=cuda, dtype=torch.bfloat16)
+    grad_out = torch.linspace(1.0, -1.0, x.numel(), device=cuda, dtype=torch.bfloat16)
+    sigmoid = spline_ops.sigmoid_fwd_variant(x, 4, 1)
+    torch.testing.assert_close(sigmoid.float(), torch.sigmoid(x).float(), rtol=0.0, atol=0.0078125)
+    sigmoid_grad = spline_ops.sigmoid_bwd_variant(grad_out, x, 4, 1)
+    ref = torch.sigmoid(x.float())
+    torch.testing.assert_close(sigmoid_grad.float(), grad_out.float() * ref * (1.0 - ref), rtol=0.0, atol=0.0082)
+    fused = spline_ops.swish_mul_fwd_variant(x, up, 4, 1)
+    _eq(fused, spline_ops.swish_fwd_variant(x, 4, 1) * up)
+    packed = torch.cat((x.reshape(8, -1), up.reshape(8, -1)), dim=-1)
+    _eq(spline_ops.swish_mul_packed_fwd_variant(packed, 4, 1).reshape(-1), fused)
+    grad_gate, grad_up = spline_ops.swish_mul_bwd_variant(grad_out, x, up, 4, 1)
+    packed_grad = spline_ops.swish_mul_packed_bwd_variant(grad_out.reshape(8, -1), packed, 4, 1)
+    split = packed.shape[-1] // 2
+    _eq(packed_grad[..., :split].reshape(-1), grad_gate)
+    _eq(packed_grad[..., split:].reshape(-1), grad_up)
+
+
 def test_fp16_sigmoid_d3_error(spline_ops, cuda):
     """test_spline_ops.py:249-259."""
     x = torch.randn(1 << 24, device=cuda, dtype=torch.float16) * 3
