@@ -110,6 +110,40 @@ def test_packed_native_backward(cuda):
                                rtol=0.01, atol=0.0078125)
 
 
+def _bf16_ulps(a, b):
+    ka = a.view(torch.int16).to(torch.int32)
+    kb = b.view(torch.int16).to(torch.int32)
+    ka = torch.where(ka < 0, -(ka & 0x7FFF), ka)
+    kb = torch.where(kb < 0, -(kb & 0x7FFF), kb)
+    return (ka - kb).abs()
+
+
+def test_compiled_packed_native_swiglu(cuda):
+    """test_spline_ops.py:115-138 (verify_compiled_packed_native_swiglu):
+    the packed hardware-transcendental SwiGLU and its gradients against
+    torch's silu(gate) * up.  The reference asserts equality; its native
+    program is x / (1 + __expf(-x)) under --use_fast_math, this build's
+    v_exp_f32 / v_rcp_f32, torch's an accurate exp and division, so the
+    BF16 results may differ by one ULP where the FP32 value sits next to a
+    rounding boundary (13 of 4096 outputs here)."""
+    from spline_compile import make_native_silu_packed
+
+    packed = (torch.linspace(-12.0, 12.0, 8192, device=cuda, dtype=torch.bfloat16)
+              .reshape(2, 4096).requires_grad_(True))
+    grad_out = torch.linspace(1.0, -1.0, 4096, device=cuda, dtype=torch.bfloat16).reshape(2, 2048)
+    native_packed = packed.detach().clone().requires_grad_(True)
+    native_gate, native_up = native_packed.chunk(2, dim=-1)
+    expected = torch.nn.functional.silu(native_gate) * native_up
+    expected.backward(grad_out)
+    activation = torch.compile(make_native_silu_packed(), fullgraph=True)
+    actual = activation(packed)
+    actual.backward(grad_out)
+    fwd = _bf16_ulps(actual.detach(), expected.detach())
+    bwd = _bf16_ulps(packed.grad, native_packed.grad)
+    assert fwd.max() <= 1 and (fwd > 0).sum() <= 32, (fwd.max(), (fwd > 0).sum())
+    assert bwd.max() <= 1 and (bwd > 0).sum() <= 32, (bwd.max(), (bwd > 0).sum())
+
+
 def test_autograd_functions(spline_ops, cuda):
     x = torch.linspace(-6, 6, 2049, device=cuda, dtype=torch.float16).requires_grad_(True)
     y = spline_ops.sigmoid_ag(x)
