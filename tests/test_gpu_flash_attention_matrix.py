@@ -100,3 +100,51 @@ def test_backward_b3_programs_head_dim_64(capi, oracle, cuda, mode, grad):
         assert torch.isfinite(got).all(), name
         ok, info = _close(got, ref)
         assert ok, (mode, grad, name, info)
+
+
+@pytest.mark.parametrize("mode,mode_id,grad,cap", [("softmax_native", 0, 0, 0.0), ("softmax_d2", 1, 0, 0.0),
+                                                   ("softcap_d4", 4, 1, 30.0), ("sigmoid_b3", 6, 5, 0.0)])
+def test_fused_qkv_views_match_contiguous(spline_ops, cuda, mode, mode_id, grad, cap):
+    """Q, K and V as views of one fused [B, S, 3, H, D] projection (head
+    stride D, sequence stride 3 H D): the kernels take any element strides
+    with a contiguous head dimension, so the result must equal the
+    contiguous operands' bit for bit, forward and backward."""
+    s = 4096 if mode == "sigmoid_b3" else 384
+    g = torch.Generator().manual_seed(77 + mode_id)
+    qkv = (torch.randn(1, s, 3, 4, 128, generator=g) * (4.0 if cap else 1.0)).bfloat16().to(cuda)
+    do = torch.randn(1, s, 4, 128, generator=g).bfloat16().to(cuda)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    assert not q.is_contiguous() and q.stride() == (s * 3 * 4 * 128, 3 * 4 * 128, 128, 1)
+    scale, bias = 128 ** -0.5, 0.0
+    args = (mode_id, 4, True, scale, cap, bias)
+    out_v, lse_v = spline_ops.flash_attn_fwd_bf16(q, k, v, *args)
+    out_c, lse_c = spline_ops.flash_attn_fwd_bf16(q.contiguous(), k.contiguous(), v.contiguous(), *args)
+    assert torch.equal(out_v.view(torch.int16), out_c.view(torch.int16))
+    assert torch.equal(lse_v, lse_c)
+    grads_v = spline_ops.flash_attn_bwd_bf16(q, k, v, out_v, do, lse_v, mode_id, grad, 0, True, scale, cap,
+                                             bias)
+    grads_c = spline_ops.flash_attn_bwd_bf16(q.contiguous(), k.contiguous(), v.contiguous(), out_c, do, lse_c,
+                                             mode_id, grad, 0, True, scale, cap, bias)
+    for name, a, b in zip(("dq", "dk", "dv"), grads_v, grads_c):
+        assert torch.isfinite(a.float()).all(), name
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), name
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_shortest_sequence(capi, oracle, cuda, causal):
+    """S = 128, one query block: the smallest length the kernels take."""
+    from attention_reference import reference_bwd
+    from test_gpu_flash_attention_bwd import bwd
+
+    q, k, v, do = _inputs(1, 4, 2, 128, 1300 + int(causal))
+    scale = 128 ** -0.5
+    out, lse = fwd(capi, cuda, q, k, v, "softmax_native", causal, scale)
+    ref_out, ref_lse = reference_fwd(oracle, q, k, v, "softmax_native", causal, scale, 30.0, 4)
+    ok, info = _close(out.cpu().float(), ref_out, rel=1.5e-2)
+    assert ok, info
+    assert (lse.cpu() - ref_lse).abs().max().item() < 1e-3
+    dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, "softmax_native", 0, causal, scale)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, "softmax_native", 0, causal, scale, 30.0, 0, 0.0)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        ok, info = _close(got, ref)
+        assert ok, (name, info)
