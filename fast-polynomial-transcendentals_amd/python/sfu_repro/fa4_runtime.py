@@ -28,6 +28,12 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
   or the BF16 sigmoid D3..D6 programs on ``s + bias`` (``bias`` defaults to
   ``-ln S``).
 
+Sequence lengths: the kernels work on whole 128-row query blocks.  Causal
+attention of any length is padded at the end to the next multiple of 128
+(zero rows: a padded key comes after every real query, so the mask hides it;
+a padded query's zero output gradient gives it no share of dK / dV) and the
+outputs are cut back; non-causal attention needs a multiple of 128.
+
 Combinations whose programs are not part of the reference tree (the FP16 /
 BF16 / PWL1 exp2 variants, Sollya attention fits, mixed SFU/polynomial
 sigmoid lanes, and the ``cute`` backends -- FA4's CuTe FP32 score programs,
@@ -299,6 +305,28 @@ def _check_operands(q, k, v):
             raise ValueError(f"{name} must be [batch, seqlen, heads, head_dim]")
 
 
+_BLOCK = 128  # query / key rows per kernel block
+
+
+def _padded_length(seqlen: int, causal: bool) -> int:
+    """The length the kernels run at: seqlen itself, or for causal attention
+    the next multiple of 128."""
+    if seqlen % _BLOCK == 0:
+        return seqlen
+    if not causal:
+        raise ValueError(f"non-causal attention needs seqlen a multiple of {_BLOCK}, got {seqlen} "
+                         "(causal attention of any length is padded)")
+    return (seqlen + _BLOCK - 1) // _BLOCK * _BLOCK
+
+
+def _pad_rows(t, length: int, value: float = 0.0):
+    """t [B, S, ...] padded along S to `length` (a new tensor)."""
+    pad = length - t.shape[1]
+    if pad == 0:
+        return t
+    return torch.cat((t, t.new_full((t.shape[0], pad, *t.shape[2:]), value)), dim=1)
+
+
 def flash_attn_fwd(q, k, v, softmax_scale=None, causal=False, softcap=0.0, score_mod=None,
                    sigmoid_attention=False, sigmoid_sfu_freq=16, sigmoid_sfu_res=0, sigmoid_bias=None,
                    sigmoid_poly_backend="cute", sigmoid_degree=3, sigmoid_coeff_source="current",
@@ -314,7 +342,13 @@ def flash_attn_fwd(q, k, v, softmax_scale=None, causal=False, softcap=0.0, score
         sigmoid_poly_backend=sigmoid_poly_backend, sigmoid_degree=sigmoid_degree,
         sigmoid_coeff_source=sigmoid_coeff_source, exp2_emu_backend=exp2_emu_backend,
         exp2_emu_freq=exp2_emu_freq)
+    seqlen = q.shape[1]
+    padded = _padded_length(seqlen, bool(causal))
+    if padded != seqlen:
+        q, k, v = (_pad_rows(t, padded) for t in (q, k, v))
     out, lse = _ops().flash_attn_fwd_bf16(q, k, v, mode, route, bool(causal), scale, cap, bias)
+    if padded != seqlen:
+        out, lse = out[:, :seqlen].contiguous(), lse[:, :, :seqlen].contiguous()
     return out, lse
 
 
@@ -335,8 +369,17 @@ def flash_attn_bwd(q, k, v, out, dout, lse, softmax_scale=None, causal=False, so
         sigmoid_poly_backend=sigmoid_poly_backend, sigmoid_degree=sigmoid_degree,
         sigmoid_gradient_degree=sigmoid_gradient_degree, sigmoid_coeff_source=sigmoid_coeff_source,
         exp2_emu_backend=exp2_emu_backend, exp2_emu_freq=exp2_emu_freq)
+    seqlen = q.shape[1]
+    padded = _padded_length(seqlen, bool(causal))
+    if padded != seqlen:
+        # zero rows for q, k, v, out and dout; an infinite lse makes the
+        # padded queries' probabilities exactly zero in the softmax modes
+        q, k, v, out, dout = (_pad_rows(t, padded) for t in (q, k, v, out, dout))
+        lse = _pad_rows(lse.transpose(1, 2), padded, math.inf).transpose(1, 2).contiguous()
     dq, dk, dv = _ops().flash_attn_bwd_bf16(q, k, v, out, dout, lse, mode, grad, route, bool(causal),
                                            scale, cap, bias)
+    if padded != seqlen:
+        dq, dk, dv = (t[:, :seqlen].contiguous() for t in (dq, dk, dv))
     return dq, dk, dv
 
 

@@ -139,3 +139,45 @@ def test_unbuilt_programs_fail_loudly(cuda):
         module(q.to(cuda), k.to(cuda), v.to(cuda))
     with pytest.raises(TypeError, match="bfloat16"):
         build_fa4_module(FA4Config(), head_dim=128)(q.half().to(cuda), k.half().to(cuda), v.half().to(cuda))
+
+
+@pytest.mark.parametrize("group,name,mode,grad,route_bwd,qmul", [
+    ("b5", "native", "softmax_native", 0, 0, 1.0),
+    ("b5", "d2_safe", "softmax_d2", 0, 32, 1.0),
+    ("b2", "polynomial", "softcap_d4", 1, 0, 6.0),
+])
+def test_causal_lengths_off_the_block_grid(oracle, cuda, group, name, mode, grad, route_bwd, qmul):
+    """S = 200: the runtime pads causal attention at the end to whole
+    128-row blocks and cuts the outputs back; results match the references
+    evaluated at S = 200."""
+    configs = {"b2": b2_component_configs, "b5": b5_component_configs}[group]()
+    module = build_fa4_module(configs[name], head_dim=128)
+    q, k, v, do = _qkv(1, 4, 2, 200, 50 + len(name), qmul)
+    out, dq, dk, dv = _run(module, cuda, q, k, v, do)
+    assert out.shape == (1, 4, 200, 128) and dk.shape == (1, 2, 200, 128)
+    scale = 1 / math.sqrt(128)
+    route_fwd = configs[name].exp2_emu_freq or 4
+    qa, ka, va, doa = (_fa4_layout(t) for t in (q, k, v, do))
+    ref_out, ref_lse = reference_fwd(oracle, qa, ka, va, mode, True, scale, 30.0, route_fwd)
+    ok, info = _close(out.cpu().float().transpose(1, 2), ref_out, 1.5e-2)
+    assert ok, ("out", info)
+    from sfu_repro import fa4_runtime as rt
+
+    resolved = module.config
+    o4, lse = rt.flash_attn_fwd(qa.to(cuda), ka.to(cuda), va.to(cuda), softmax_scale=None, causal=True,
+                                softcap=resolved.softcap, score_mod=resolved.score_mod,
+                                exp2_emu_backend=resolved.exp2_emu_backend, exp2_emu_freq=resolved.exp2_emu_freq)
+    assert lse.shape == (1, 4, 200) and (lse.cpu() - ref_lse).abs().max().item() < 2e-2
+    rq, rk, rv = reference_bwd(oracle, qa, ka, va, o4, doa, lse, mode, grad, True, scale, 30.0, route_bwd, 0.0)
+    for label, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert torch.isfinite(got).all(), label
+        ok, info = _close(got, ref.transpose(1, 2), 2.5e-2)
+        assert ok, (label, info)
+
+
+def test_non_causal_lengths_off_the_block_grid_raise(cuda):
+    from sfu_repro import fa4_runtime as rt
+
+    q = torch.zeros(1, 200, 2, 128, dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(ValueError, match="non-causal attention needs seqlen a multiple of 128"):
+        rt.flash_attn_fwd(q, q, q, causal=False)
