@@ -663,7 +663,7 @@ void check_attn_operand(const at::Tensor& t, const char* name) {
 
 std::vector<at::Tensor> flash_attn_fwd_bf16(at::Tensor q, at::Tensor k, at::Tensor v, int64_t mode,
                                             int64_t exp2_route, bool causal, double softmax_scale,
-                                            double softcap, double sigmoid_bias) {
+                                            double softcap, double sigmoid_bias, int64_t valid_keys) {
     check_attn_operand(q, "q");
     check_attn_operand(k, "k");
     check_attn_operand(v, "v");
@@ -688,10 +688,13 @@ std::vector<at::Tensor> flash_attn_fwd_bf16(at::Tensor q, at::Tensor k, at::Tens
                                  k.stride(1), v.stride(0), v.stride(2), v.stride(1), out.stride(0),
                                  out.stride(2), out.stride(1)};
     void* s = current_stream(q);
-    check_launch(launch_flash_attention_fwd_strided_bf16(
+    TORCH_CHECK(valid_keys < 0 || (valid_keys >= 1 && valid_keys <= sq),
+                "valid_keys must be in [1, seqlen] (or negative for all), got ", valid_keys);
+    check_launch(launch_flash_attention_fwd_strided_keys_bf16(
                      out.data_ptr(), lse.data_ptr<float>(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                     b, hq, hkv, sq, d, strides, (int)mode, (int)exp2_route, causal ? 1 : 0,
-                     (float)softmax_scale, (float)softcap, (float)sigmoid_bias, s),
+                     b, hq, hkv, sq, valid_keys < 0 ? sq : valid_keys, d, strides, (int)mode,
+                     (int)exp2_route, causal ? 1 : 0, (float)softmax_scale, (float)softcap,
+                     (float)sigmoid_bias, s),
                  s);
     return {out, lse};
 }
@@ -1305,17 +1308,21 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           },
           "Fused native BF16 Q/K rotary embedding and transpose");
 
-    // RoPE reference evaluator (sfu_repro.rope.polynomial_sincos on the device)
+    // fused attention
     m.def("flash_attn_fwd_bf16", &flash_attn_fwd_bf16, py::arg("q"), py::arg("k"), py::arg("v"),
           py::arg("mode"), py::arg("exp2_route") = 4, py::arg("causal") = true,
           py::arg("softmax_scale"), py::arg("softcap") = 0.0, py::arg("sigmoid_bias") = 0.0,
+          py::arg("valid_keys") = -1,
           "Fused attention forward with the score programs in the tile loop; "
-          "q [B,S,Hq,128], k/v [B,S,Hkv,128] BF16 -> [out [B,S,Hq,128], lse [B,Hq,S] FP32]");
+          "q [B,S,Hq,D], k/v [B,S,Hkv,D] BF16 (D 64 or 128) -> [out [B,S,Hq,D], lse [B,Hq,S] FP32]; "
+          "valid_keys >= 1 masks keys from that index on (operands padded at the end)");
     m.def("flash_attn_bwd_bf16", &flash_attn_bwd_bf16, py::arg("q"), py::arg("k"), py::arg("v"),
           py::arg("out"), py::arg("dout"), py::arg("lse"), py::arg("mode"), py::arg("grad") = 0,
           py::arg("exp2_route") = 0, py::arg("causal") = true, py::arg("softmax_scale"),
           py::arg("softcap") = 0.0, py::arg("sigmoid_bias") = 0.0,
-          "Fused attention backward -> [dq [B,S,Hq,128], dk, dv [B,S,Hkv,128]] BF16");
+          "Fused attention backward -> [dq [B,S,Hq,D], dk, dv [B,S,Hkv,D]] BF16");
+
+    // RoPE reference evaluator (sfu_repro.rope.polynomial_sincos on the device)
     m.def("polynomial_sincos_f32", &polynomial_sincos_f32, py::arg("angles"),
           py::arg("sin_coefficients"), py::arg("cos_coefficients"), py::arg("accurate") = true,
           "Quarter-turn reduction (FP64 or FP32 Cody-Waite) and paired parity polynomials "

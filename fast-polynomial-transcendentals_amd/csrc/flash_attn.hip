@@ -51,6 +51,7 @@ struct AttnParams {
     float* lse;  // [B, Hq, S] natural-log partition function, or null
     AttnStrides qs, ks, vs, os;
     int64_t hq, hkv, seq;
+    int64_t kv_len;  // keys 0 .. kv_len - 1 are real, the rest padding (masked)
     float scale;     // s = q.k * scale
     float cap;       // softcap
     float sig_bias;  // sigmoid attention: p = sigmoid(s + sig_bias)
@@ -135,8 +136,9 @@ constexpr bool fwd_program_heavy() {
 }
 
 // Accumulator register r of 32-key tile kt holds key k0 + kt*32 + 8*(r/4) +
-// 4h + r%4; diag = k0 + 4h - query, so the key is causally masked when
-// diag + that offset > 0.
+// 4h + r%4; diag = k0 + 4h - klast, with klast the last key the query may
+// see (itself under the causal mask, at most the last real key), so the key
+// is masked when diag + that offset > 0.
 template <bool MASKED>
 __device__ __forceinline__ bool key_masked(int diag, int kt, int r) {
     return MASKED && diag + kt * 32 + 8 * (r >> 2) + (r & 3) > 0;
@@ -351,7 +353,15 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     // + 4h, dims 16 ((lane / 16) % 2) + 4 (lane % 4) of a 32-dim slice
     const int vlane = (((lane & 15) >> 2) + 4 * h) * kVRowStr<HD>() + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    const int64_t nkb = p.causal ? (qb + 1) * (kBlockQ / kAttnBlockK) : p.seq / kAttnBlockK;
+    // the last visible key of this lane's query and the smallest and largest
+    // of those over the wave's 32 queries (wave-uniform)
+    const int64_t klim = p.kv_len - 1;
+    const int64_t klast = p.causal && qrow < klim ? qrow : klim;
+    const int64_t wlo = p.causal && q0 < klim ? q0 : klim;
+    const int64_t whi = p.causal && q0 + 31 < klim ? q0 + 31 : klim;
+    const int64_t ktiles = (p.kv_len + kAttnBlockK - 1) / kAttnBlockK;  // tiles holding real keys
+    const int64_t ncausal = p.causal ? (qb + 1) * (kBlockQ / kAttnBlockK) : ktiles;
+    const int64_t nkb = ncausal < ktiles ? ncausal : ktiles;
     load(0);
     store(0);
     __syncthreads();
@@ -360,9 +370,9 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
         const int64_t k0 = kb * kAttnBlockK;
         const bool more = kb + 1 < nkb;
         if (more) load(k0 + kAttnBlockK);  // in flight during this tile's math
-        if (!p.causal || k0 <= q0 + 31) {  // wave-uniform: some key of the tile is visible
-            const int diag = (int)(k0 - qrow) + 4 * h;
-            if (p.causal && k0 + kAttnBlockK - 1 > q0)
+        if (k0 <= whi) {  // wave-uniform: some key of the tile is visible
+            const int diag = (int)(k0 - klast) + 4 * h;
+            if (k0 + kAttnBlockK - 1 > wlo)
                 attend_tile<MODE, ROUTE, true, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap);
             else
                 attend_tile<MODE, ROUTE, false, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap);
@@ -444,15 +454,16 @@ bool stride_ok(const AttnStrides& t) { return t.b >= 0 && t.h >= 0 && t.s >= 0 &
 
 }  // namespace
 
-extern "C" int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q,
-                                                       const void* k, const void* v, int64_t batch,
-                                                       int64_t q_heads, int64_t kv_heads, int64_t seq,
-                                                       int64_t head_dim, const int64_t* strides,
-                                                       int mode, int exp2_route, int causal,
-                                                       float scale, float cap, float sigmoid_bias,
-                                                       void* stream) {
+extern "C" int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* lse, const void* q,
+                                                            const void* k, const void* v, int64_t batch,
+                                                            int64_t q_heads, int64_t kv_heads, int64_t seq,
+                                                            int64_t valid_keys, int64_t head_dim,
+                                                            const int64_t* strides, int mode, int exp2_route,
+                                                            int causal, float scale, float cap,
+                                                            float sigmoid_bias, void* stream) {
     if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || (head_dim != 64 && head_dim != 128) || !strides)
         return hipErrorInvalidValue;
+    if (seq > 0 && (valid_keys < 1 || valid_keys > seq)) return hipErrorInvalidValue;
     if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
         return hipErrorInvalidValue;
     if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f && cap <= __FLT_MAX__))
@@ -473,7 +484,7 @@ extern "C" int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, co
     if (attn_is_sigmoid(mode)) lse = nullptr;  // sigmoid attention has no partition function
     if (batch > 65535 || seq / kAttnBlockQ > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
     AttnParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out, lse,
-                   st[0], st[1], st[2], st[3], q_heads, kv_heads, seq, scale,
+                   st[0], st[1], st[2], st[3], q_heads, kv_heads, seq, valid_keys, scale,
                    cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0};
     const dim3 grid((unsigned)q_heads, (unsigned)(seq / kAttnBlockQ), (unsigned)batch);
     hipStream_t hst = hs(stream);
@@ -493,6 +504,18 @@ extern "C" int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, co
         case kAttnSigmoidD6: launch_fwd<kAttnSigmoidD6, 0>(prm, grid, hst, hd); break;
     }
     return hipGetLastError();
+}
+
+extern "C" int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q,
+                                                       const void* k, const void* v, int64_t batch,
+                                                       int64_t q_heads, int64_t kv_heads, int64_t seq,
+                                                       int64_t head_dim, const int64_t* strides,
+                                                       int mode, int exp2_route, int causal,
+                                                       float scale, float cap, float sigmoid_bias,
+                                                       void* stream) {
+    return launch_flash_attention_fwd_strided_keys_bf16(out, lse, q, k, v, batch, q_heads, kv_heads, seq, seq,
+                                                        head_dim, strides, mode, exp2_route, causal, scale,
+                                                        cap, sigmoid_bias, stream);
 }
 
 extern "C" int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k,

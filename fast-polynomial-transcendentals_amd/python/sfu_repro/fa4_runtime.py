@@ -28,11 +28,12 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
   or the BF16 sigmoid D3..D6 programs on ``s + bias`` (``bias`` defaults to
   ``-ln S``).
 
-Sequence lengths: the kernels work on whole 128-row query blocks.  Causal
-attention of any length is padded at the end to the next multiple of 128
-(zero rows: a padded key comes after every real query, so the mask hides it;
-a padded query's zero output gradient gives it no share of dK / dV) and the
-outputs are cut back; non-causal attention needs a multiple of 128.
+Sequence lengths: the kernels work on whole 128-row query blocks.  Attention
+of any length is padded at the end to the next multiple of 128 with zero
+rows and the outputs are cut back: the forward masks the padded keys
+(``valid_keys``); in the backward a zero K row gives a padded key no share of
+dQ, and a padded query's zero output gradient and infinite lse give it no
+share of dK / dV.
 
 Combinations whose programs are not part of the reference tree (the FP16 /
 BF16 / PWL1 exp2 variants, Sollya attention fits, mixed SFU/polynomial
@@ -308,14 +309,10 @@ def _check_operands(q, k, v):
 _BLOCK = 128  # query / key rows per kernel block
 
 
-def _padded_length(seqlen: int, causal: bool) -> int:
-    """The length the kernels run at: seqlen itself, or for causal attention
-    the next multiple of 128."""
-    if seqlen % _BLOCK == 0:
-        return seqlen
-    if not causal:
-        raise ValueError(f"non-causal attention needs seqlen a multiple of {_BLOCK}, got {seqlen} "
-                         "(causal attention of any length is padded)")
+def _padded_length(seqlen: int) -> int:
+    """The length the kernels run at: the next multiple of 128."""
+    if seqlen < 1:
+        raise ValueError(f"seqlen must be positive, got {seqlen}")
     return (seqlen + _BLOCK - 1) // _BLOCK * _BLOCK
 
 
@@ -343,10 +340,10 @@ def flash_attn_fwd(q, k, v, softmax_scale=None, causal=False, softcap=0.0, score
         sigmoid_coeff_source=sigmoid_coeff_source, exp2_emu_backend=exp2_emu_backend,
         exp2_emu_freq=exp2_emu_freq)
     seqlen = q.shape[1]
-    padded = _padded_length(seqlen, bool(causal))
+    padded = _padded_length(seqlen)
     if padded != seqlen:
         q, k, v = (_pad_rows(t, padded) for t in (q, k, v))
-    out, lse = _ops().flash_attn_fwd_bf16(q, k, v, mode, route, bool(causal), scale, cap, bias)
+    out, lse = _ops().flash_attn_fwd_bf16(q, k, v, mode, route, bool(causal), scale, cap, bias, seqlen)
     if padded != seqlen:
         out, lse = out[:, :seqlen].contiguous(), lse[:, :, :seqlen].contiguous()
     return out, lse
@@ -370,7 +367,7 @@ def flash_attn_bwd(q, k, v, out, dout, lse, softmax_scale=None, causal=False, so
         sigmoid_gradient_degree=sigmoid_gradient_degree, sigmoid_coeff_source=sigmoid_coeff_source,
         exp2_emu_backend=exp2_emu_backend, exp2_emu_freq=exp2_emu_freq)
     seqlen = q.shape[1]
-    padded = _padded_length(seqlen, bool(causal))
+    padded = _padded_length(seqlen)
     if padded != seqlen:
         # zero rows for q, k, v, out and dout; an infinite lse makes the
         # padded queries' probabilities exactly zero in the softmax modes

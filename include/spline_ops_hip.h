@@ -474,6 +474,20 @@ int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q
                                             const int64_t* strides, int mode, int exp2_route,
                                             int causal, float scale, float cap, float sigmoid_bias,
                                             void* stream);
+/* The same forward over a sequence padded to a multiple of 128: keys
+ * valid_keys .. seq - 1 are padding and masked (1 <= valid_keys <= seq), so
+ * attention of any length runs on operands padded at the end (the padded
+ * queries' rows are computed and left to the caller to drop).  Zero-padded
+ * operands need no change to the backward: a zero K row gives the padded
+ * keys no share of dQ, and padded queries with zero dout and an infinite lse
+ * add nothing to dK / dV.  launch_flash_attention_fwd_strided_bf16 is this
+ * with valid_keys = seq. */
+int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* lse, const void* q, const void* k,
+                                                 const void* v, int64_t batch, int64_t q_heads,
+                                                 int64_t kv_heads, int64_t seq, int64_t valid_keys,
+                                                 int64_t head_dim, const int64_t* strides, int mode,
+                                                 int exp2_route, int causal, float scale, float cap,
+                                                 float sigmoid_bias, void* stream);
 /* Backward of the same attention (the runtime behind FA4's flash_attn_bwd,
  * src/sfu_repro/fa4.py:430-461): dq [B, S, Hq, D], dk and dv [B, S, Hkv, D]
  * BF16 from q, k, v, out, dout (BF16) and the forward's lse (softmax modes).

@@ -175,9 +175,38 @@ def test_causal_lengths_off_the_block_grid(oracle, cuda, group, name, mode, grad
         assert ok, (label, info)
 
 
-def test_non_causal_lengths_off_the_block_grid_raise(cuda):
+@pytest.mark.parametrize("mode,mode_name", [(0, "softmax_native"), (4, "softcap_d4"), (5, "sigmoid_native")])
+def test_non_causal_lengths_off_the_block_grid(oracle, cuda, mode, mode_name):
+    """Non-causal attention at S = 200 through the runtime (padded to 256, the
+    padded keys masked in the forward) against the references at S = 200."""
     from sfu_repro import fa4_runtime as rt
 
-    q = torch.zeros(1, 200, 2, 128, dtype=torch.bfloat16, device=cuda)
-    with pytest.raises(ValueError, match="non-causal attention needs seqlen a multiple of 128"):
-        rt.flash_attn_fwd(q, q, q, causal=False)
+    q, k, v, do = (_fa4_layout(t) for t in _qkv(1, 4, 2, 200, 90 + mode, 6.0 if mode == 4 else 1.0))
+    scale = 1 / math.sqrt(128)
+    kwargs = {}
+    if mode == 4:
+        kwargs["score_mod"] = rt.create_softcap_scoremod_backend(30.0, degree=4, backend="device")
+        kwargs["softcap"] = 30.0
+    if mode == 5:
+        kwargs.update(sigmoid_attention=True, sigmoid_sfu_freq=16, sigmoid_sfu_res=16)
+    qd, kd, vd, dod = (t.to(cuda) for t in (q, k, v, do))
+    out, lse = rt.flash_attn_fwd(qd, kd, vd, softmax_scale=scale, causal=False, **kwargs)
+    assert out.shape == (1, 200, 4, 128)
+    bias = -math.log(200) if mode == 5 else 0.0
+    ref_out, ref_lse = reference_fwd(oracle, q, k, v, mode_name, False, scale, 30.0, 4, bias)
+    ok, info = _close(out.cpu().float(), ref_out, 1.5e-2)
+    assert ok, ("out", info)
+    if ref_lse is not None:
+        assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2
+    grad = 1 if mode == 4 else 0
+    bwd_kwargs = dict(kwargs)
+    if mode == 4:
+        bwd_kwargs["score_mod_bwd"] = None
+    dq, dk, dv = rt.flash_attn_bwd(qd, kd, vd, out, dod, lse, softmax_scale=scale, causal=False, **bwd_kwargs)
+    rq, rk, rv = reference_bwd(oracle, q, k, v, out.cpu(), do, lse.cpu(), mode_name, grad, False, scale, 30.0, 0,
+                               bias)
+    for label, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        got = got.cpu().float()
+        assert torch.isfinite(got).all(), label
+        ok, info = _close(got, ref, 2.5e-2)
+        assert ok, (label, info)

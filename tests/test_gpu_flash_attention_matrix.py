@@ -148,3 +148,43 @@ def test_shortest_sequence(capi, oracle, cuda, causal):
     for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
         ok, info = _close(got, ref)
         assert ok, (name, info)
+
+
+@pytest.mark.parametrize("mode,causal", [("softmax_native", False), ("softmax_d2", False), ("softcap_d4", False),
+                                         ("sigmoid_native", False), ("softmax_native", True)])
+def test_valid_keys_mask_padding(capi, oracle, cuda, mode, causal):
+    """launch_flash_attention_fwd_strided_keys_bf16 with valid_keys = 200 of
+    256: the keys from 200 on are masked whatever they hold (random rows
+    here), so the first 200 rows equal the reference at S = 200."""
+    import ctypes
+
+    from attention_reference import default_bias
+    from test_gpu_flash_attention_bwd import _strides
+
+    q, k, v, _ = _inputs(1, 4, 2, 256, 1400 + M[mode] + int(causal), qmul=6.0 if mode == "softcap_d4" else 1.0)
+    scale = 128 ** -0.5
+    bias = default_bias(mode, 200)
+    qd, kd, vd = q.to(cuda), k.to(cuda), v.to(cuda)
+    out = torch.empty_like(qd)
+    lse = torch.zeros(1, 4, 256, dtype=torch.float32, device=cuda)
+    rc = capi.launch_flash_attention_fwd_strided_keys_bf16(
+        capi.ptr(out), capi.ptr(lse), capi.ptr(qd), capi.ptr(kd), capi.ptr(vd), ctypes.c_int64(1),
+        ctypes.c_int64(4), ctypes.c_int64(2), ctypes.c_int64(256), ctypes.c_int64(200), ctypes.c_int64(128),
+        _strides(qd, kd, vd, out), ctypes.c_int(M[mode]), ctypes.c_int(4), ctypes.c_int(int(causal)),
+        ctypes.c_float(scale), ctypes.c_float(30.0), ctypes.c_float(bias), capi.stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    ref_out, ref_lse = reference_fwd(oracle, q[:, :200], k[:, :200], v[:, :200], mode, causal, scale, 30.0, 4, bias)
+    got = out.cpu().float()[:, :200]
+    assert torch.isfinite(got).all()
+    ok, info = _close(got, ref_out, rel=1.5e-2)
+    assert ok, (mode, causal, info)
+    if ref_lse is not None:
+        assert (lse.cpu()[..., :200] - ref_lse).abs().max().item() < 2e-2
+    for bad in (0, 257):
+        rc = capi.launch_flash_attention_fwd_strided_keys_bf16(
+            capi.ptr(out), capi.ptr(lse), capi.ptr(qd), capi.ptr(kd), capi.ptr(vd), ctypes.c_int64(1),
+            ctypes.c_int64(4), ctypes.c_int64(2), ctypes.c_int64(256), ctypes.c_int64(bad), ctypes.c_int64(128),
+            _strides(qd, kd, vd, out), ctypes.c_int(M[mode]), ctypes.c_int(4), ctypes.c_int(int(causal)),
+            ctypes.c_float(scale), ctypes.c_float(30.0), ctypes.c_float(bias), capi.stream())
+        assert rc != 0, bad
