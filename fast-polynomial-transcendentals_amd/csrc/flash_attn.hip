@@ -364,6 +364,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     const int64_t nkb = ncausal < ktiles ? ncausal : ktiles;
     load(0);
     store(0);
+    // every load issued so far (the Q fragments included) completes before
+    // the loop: otherwise the counter waits the compiler places for the Q
+    // fragments inside the loop also wait for the next tile's prefetch
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int64_t kb = 0; kb < nkb; ++kb) {
         const int buf = (int)(kb & 1);
