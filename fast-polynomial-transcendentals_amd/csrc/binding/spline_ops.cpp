@@ -673,7 +673,6 @@ std::vector<at::Tensor> flash_attn_fwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     TORCH_CHECK(q.size(3) == 64 || q.size(3) == 128, "head_dim must be 64 or 128, got ", q.size(3));
     TORCH_CHECK(q.size(2) % k.size(2) == 0, "q heads (", q.size(2),
                 ") must be a multiple of kv heads (", k.size(2), ")");
-    TORCH_CHECK(q.size(1) % 128 == 0, "seqlen must be a multiple of 128, got ", q.size(1));
     c10::OptionalDeviceGuard guard(q.device());
     const int64_t b = q.size(0), sq = q.size(1), hq = q.size(2), hkv = k.size(2);
     const int64_t d = q.size(3);
@@ -1314,7 +1313,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("softmax_scale"), py::arg("softcap") = 0.0, py::arg("sigmoid_bias") = 0.0,
           py::arg("valid_keys") = -1,
           "Fused attention forward with the score programs in the tile loop; "
-          "q [B,S,Hq,D], k/v [B,S,Hkv,D] BF16 (D 64 or 128) -> [out [B,S,Hq,D], lse [B,Hq,S] FP32]; "
+          "q [B,S,Hq,D], k/v [B,S,Hkv,D] BF16 (D 64 or 128, any S) -> [out [B,S,Hq,D], lse [B,Hq,S] FP32]; "
           "valid_keys >= 1 masks keys from that index on (operands padded at the end)");
     m.def("flash_attn_bwd_bf16", &flash_attn_bwd_bf16, py::arg("q"), py::arg("k"), py::arg("v"),
           py::arg("out"), py::arg("dout"), py::arg("lse"), py::arg("mode"), py::arg("grad") = 0,

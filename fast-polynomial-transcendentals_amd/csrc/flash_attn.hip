@@ -290,11 +290,14 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
     if constexpr (!attn_is_sigmoid(MODE)) l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 }
 
-// Grid (q_heads, S / (32 W), batch), W waves of 32 queries per block:
+// Grid (q_heads, ceil(S / (32 W)), batch), W waves of 32 queries per block:
 // blockIdx.y runs over query blocks, heaviest first under the causal mask,
 // and the head index varies fastest, so the first wave of resident blocks
 // takes the longest query blocks of every head.
-template <int MODE, int ROUTE, int HD, int W>
+// RAGGED: S is not a multiple of 128, so the last query block and the last
+// key tile hold rows past the sequence (a separate instantiation keeps those
+// guards out of the aligned kernels).
+template <int MODE, int ROUTE, int HD, int W, bool RAGGED>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) flash_fwd_kernel(AttnParams p) {
     constexpr int kBlockQ = 32 * W;  // queries per block
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
@@ -307,7 +310,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, c32 = lane & 31;
-    const int64_t nqb = p.seq / kBlockQ;
+    const int64_t nqb = (p.seq + kBlockQ - 1) / kBlockQ;  // the last block may be partial
     const int64_t head = blockIdx.x, b = blockIdx.z;
     const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
     const int64_t kvh = head / (p.hq / p.hkv);
@@ -318,10 +321,16 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     const int64_t q0 = qb * kBlockQ + wave * 32;  // first query of this wave
     const int64_t qrow = q0 + c32;                     // this lane's query
 
+    // queries past the sequence (the last block of a length that is not a
+    // multiple of the block) load the last row and are zeroed before the
+    // tile loop; their outputs are not stored.  The loads stay unconditional:
+    // a branch around each would wait for every load before the next.
+    const bool qin = !RAGGED || qrow < p.seq;
+    const int64_t qsrc = qin ? qrow : p.seq - 1;
     bf16x8_t qf[HD / 16];
 #pragma unroll
     for (int c = 0; c < HD / 16; ++c)
-        qf[c] = *reinterpret_cast<const bf16x8_t*>(qp + qrow * p.qs.s + c * 16 + h * 8);
+        qf[c] = *reinterpret_cast<const bf16x8_t*>(qp + qsrc * p.qs.s + c * 16 + h * 8);
 
     f32x16_t oacc[HD / 32];
 #pragma unroll
@@ -336,13 +345,29 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     const int krow = tid / kChunks, kcol = (tid % kChunks) * 8;
     u32x4_t kr[kPasses], vr[kPasses];
     auto load = [&](int64_t k0) {
+        if (!RAGGED || k0 + kAttnBlockK <= p.seq) {  // block-uniform: a whole tile of rows
 #pragma unroll
-        for (int j = 0; j < kPasses; ++j) {
-            kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (k0 + krow + kRowsPass * j) * kss + kcol);
-            vr[j] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + krow + kRowsPass * j) * vss + kcol);
+            for (int j = 0; j < kPasses; ++j) {
+                kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (k0 + krow + kRowsPass * j) * kss + kcol);
+                vr[j] = *reinterpret_cast<const u32x4_t*>(vp + (k0 + krow + kRowsPass * j) * vss + kcol);
+            }
+        } else {  // the sequence ends inside the tile: rows past it read the
+                  // last row (unconditional loads) and are zeroed by the store
+#pragma unroll
+            for (int j = 0; j < kPasses; ++j) {
+                const int64_t row = k0 + krow + kRowsPass * j;
+                const int64_t src = row < p.seq ? row : p.seq - 1;
+                kr[j] = *reinterpret_cast<const u32x4_t*>(kp + src * kss + kcol);
+                vr[j] = *reinterpret_cast<const u32x4_t*>(vp + src * vss + kcol);
+            }
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, int64_t k0) {
+        if (RAGGED && k0 + kAttnBlockK > p.seq) {  // block-uniform: the tile holds rows past the sequence
+#pragma unroll
+            for (int j = 0; j < kPasses; ++j)
+                if (k0 + krow + kRowsPass * j >= p.seq) kr[j] = vr[j] = (u32x4_t){0u, 0u, 0u, 0u};
+        }
 #pragma unroll
         for (int j = 0; j < kPasses; ++j) {
             *reinterpret_cast<u32x4_t*>(&ks[buf][(krow + kRowsPass * j) * kKStr + kcol]) = kr[j];
@@ -363,11 +388,15 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     const int64_t ncausal = p.causal ? (qb + 1) * (kBlockQ / kAttnBlockK) : ktiles;
     const int64_t nkb = ncausal < ktiles ? ncausal : ktiles;
     load(0);
-    store(0);
+    store(0, 0);
     // every load issued so far (the Q fragments included) completes before
     // the loop: otherwise the counter waits the compiler places for the Q
     // fragments inside the loop also wait for the next tile's prefetch
     __builtin_amdgcn_s_waitcnt(0);
+    if (!qin) {
+#pragma unroll
+        for (int c = 0; c < HD / 16; ++c) qf[c] = __builtin_bit_cast(bf16x8_t, (u32x4_t){0u, 0u, 0u, 0u});
+    }
     __syncthreads();
     for (int64_t kb = 0; kb < nkb; ++kb) {
         const int buf = (int)(kb & 1);
@@ -381,7 +410,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
             else
                 attend_tile<MODE, ROUTE, false, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap);
         }
-        if (more) store(buf ^ 1);
+        if (more) store(buf ^ 1, k0 + kAttnBlockK);
         __syncthreads();
     }
 
@@ -392,9 +421,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
         inv = 1.0f / l;
         // log sum exp(s') with s' the (capped) scaled score: m and log2(l) are
         // in log2 units
-        if (p.lse != nullptr && h == 0)
+        if (p.lse != nullptr && h == 0 && qin)
             p.lse[(b * p.hq + head) * p.seq + qrow] = (m + __builtin_log2f(l)) * kLn2;
     }
+    if (!qin) return;
     uint16_t* orow = p.o + b * p.os.b + head * p.os.h + qrow * p.os.s;
 #pragma unroll
     for (int dt = 0; dt < HD / 32; ++dt)
@@ -427,15 +457,22 @@ bool route_supported(int route) {
 // which keep two independent 4-wave blocks per CU; head_dim 64 fits three
 // 4-wave blocks per CU and keeps them (measured on MI355X: 1.03-1.11x for the
 // softmax and hardware modes at D 128, 0.81-0.96x for 8 waves at D 64).
+template <int MODE, int ROUTE, int HD, int W>
+void launch_fwd_shape(const AttnParams& prm, dim3 grid, hipStream_t st) {
+    if (prm.seq % kAttnBlockQ == 0)
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, HD, W, false>), grid, dim3(64 * W), 0, st, prm);
+    else
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, HD, W, true>), grid, dim3(64 * W), 0, st, prm);
+}
+
 template <int MODE, int ROUTE>
 void launch_fwd(const AttnParams& prm, dim3 grid, hipStream_t st, int hd) {
-    if (hd == 128 && !fwd_program_heavy<MODE>() && prm.seq % 256 == 0) {
-        const dim3 g(grid.x, (unsigned)(prm.seq / 256), grid.z);
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 128, 8>), g, dim3(512), 0, st, prm);
+    if (hd == 128 && !fwd_program_heavy<MODE>() && grid.y % 2 == 0) {
+        launch_fwd_shape<MODE, ROUTE, 128, 8>(prm, dim3(grid.x, grid.y / 2, grid.z), st);
     } else if (hd == 64) {
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 64, 4>), grid, dim3(256), 0, st, prm);
+        launch_fwd_shape<MODE, ROUTE, 64, 4>(prm, grid, st);
     } else {
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 128, 4>), grid, dim3(256), 0, st, prm);
+        launch_fwd_shape<MODE, ROUTE, 128, 4>(prm, grid, st);
     }
 }
 
@@ -468,8 +505,7 @@ extern "C" int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* ls
     if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || (head_dim != 64 && head_dim != 128) || !strides)
         return hipErrorInvalidValue;
     if (seq > 0 && (valid_keys < 1 || valid_keys > seq)) return hipErrorInvalidValue;
-    if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
-        return hipErrorInvalidValue;
+    if (q_heads % kv_heads != 0 || mode < 0 || mode >= kAttnModes) return hipErrorInvalidValue;
     if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f && cap <= __FLT_MAX__))
         return hipErrorInvalidValue;
     if (attn_has_exp2_program(mode) && !route_supported(exp2_route)) return hipErrorInvalidValue;
@@ -486,11 +522,12 @@ extern "C" int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* ls
         return hipErrorInvalidValue;
     if (lse && (reinterpret_cast<uintptr_t>(lse) & 3)) return hipErrorInvalidValue;
     if (attn_is_sigmoid(mode)) lse = nullptr;  // sigmoid attention has no partition function
-    if (batch > 65535 || seq / kAttnBlockQ > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
+    const int64_t qblocks = (seq + kAttnBlockQ - 1) / kAttnBlockQ;  // the last one may be partial
+    if (batch > 65535 || qblocks > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
     AttnParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out, lse,
                    st[0], st[1], st[2], st[3], q_heads, kv_heads, seq, valid_keys, scale,
                    cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0};
-    const dim3 grid((unsigned)q_heads, (unsigned)(seq / kAttnBlockQ), (unsigned)batch);
+    const dim3 grid((unsigned)q_heads, (unsigned)qblocks, (unsigned)batch);
     hipStream_t hst = hs(stream);
     switch (mode) {
         case kAttnSoftmaxNative: launch_fwd<kAttnSoftmaxNative, 0>(prm, grid, hst, hd); break;

@@ -28,12 +28,12 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
   or the BF16 sigmoid D3..D6 programs on ``s + bias`` (``bias`` defaults to
   ``-ln S``).
 
-Sequence lengths: the kernels work on whole 128-row query blocks.  Attention
-of any length is padded at the end to the next multiple of 128 with zero
-rows and the outputs are cut back: the forward masks the padded keys
-(``valid_keys``); in the backward a zero K row gives a padded key no share of
-dQ, and a padded query's zero output gradient and infinite lse give it no
-share of dK / dV.
+Sequence lengths: the forward takes any length (the kernel reads no row
+past the sequence and zero-fills the last partial block).  The backward works
+on whole 128-row blocks: attention of any length is padded at the end to the
+next multiple of 128 with zero rows and the gradients are cut back; a zero K
+row gives a padded key no share of dQ, and a padded query's zero output
+gradient and infinite lse give it no share of dK / dV.
 
 Combinations whose programs are not part of the reference tree (the FP16 /
 BF16 / PWL1 exp2 variants, Sollya attention fits, mixed SFU/polynomial
@@ -339,14 +339,9 @@ def flash_attn_fwd(q, k, v, softmax_scale=None, causal=False, softcap=0.0, score
         sigmoid_poly_backend=sigmoid_poly_backend, sigmoid_degree=sigmoid_degree,
         sigmoid_coeff_source=sigmoid_coeff_source, exp2_emu_backend=exp2_emu_backend,
         exp2_emu_freq=exp2_emu_freq)
-    seqlen = q.shape[1]
-    padded = _padded_length(seqlen)
-    if padded != seqlen:
-        q, k, v = (_pad_rows(t, padded) for t in (q, k, v))
-    out, lse = _ops().flash_attn_fwd_bf16(q, k, v, mode, route, bool(causal), scale, cap, bias, seqlen)
-    if padded != seqlen:
-        out, lse = out[:, :seqlen].contiguous(), lse[:, :, :seqlen].contiguous()
-    return out, lse
+    if q.shape[1] < 1:
+        raise ValueError(f"seqlen must be positive, got {q.shape[1]}")
+    return tuple(_ops().flash_attn_fwd_bf16(q, k, v, mode, route, bool(causal), scale, cap, bias))
 
 
 def flash_attn_bwd(q, k, v, out, dout, lse, softmax_scale=None, causal=False, softcap=0.0,

@@ -437,7 +437,7 @@ int launch_evaluate_reduced_sincos(void* sin_out, void* cos_out, const void* red
  * that is not part of the reference tree (src/sfu_repro/fa4.py:454-752 selects
  * them; extras/paper/manuscript/main.tex:483-509 describes the fusion).
  * q [B, Hq, S, D], k and v [B, Hkv, S, D] -> out [B, Hq, S, D], BF16;
- * Hq a multiple of Hkv (grouped-query), S a multiple of 128, head_dim D 64 or 128,
+ * Hq a multiple of Hkv (grouped-query), any S >= 0, head_dim D 64 or 128,
  * every pointer 16-byte aligned; s = q.k * scale.  mode:
  *   0 softmax, hardware exp2 (v_exp_f32)      1 softmax, B5 D2 "safe" exp2
  *   2 softmax, FA4 D3 exp2                     3 softcap cap*tanh(s/cap), FP32
@@ -474,14 +474,13 @@ int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q
                                             const int64_t* strides, int mode, int exp2_route,
                                             int causal, float scale, float cap, float sigmoid_bias,
                                             void* stream);
-/* The same forward over a sequence padded to a multiple of 128: keys
- * valid_keys .. seq - 1 are padding and masked (1 <= valid_keys <= seq), so
- * attention of any length runs on operands padded at the end (the padded
- * queries' rows are computed and left to the caller to drop).  Zero-padded
- * operands need no change to the backward: a zero K row gives the padded
- * keys no share of dQ, and padded queries with zero dout and an infinite lse
- * add nothing to dK / dV.  launch_flash_attention_fwd_strided_bf16 is this
- * with valid_keys = seq. */
+/* The same forward with keys valid_keys .. seq - 1 masked as padding
+ * (1 <= valid_keys <= seq): for operands padded at the end to a length the
+ * backward takes (a multiple of 128), the padded queries' rows are computed
+ * and left to the caller to drop.  Zero-padded operands need no change to the
+ * backward: a zero K row gives the padded keys no share of dQ, and padded
+ * queries with zero dout and an infinite lse add nothing to dK / dV.
+ * launch_flash_attention_fwd_strided_bf16 is this with valid_keys = seq. */
 int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* lse, const void* q, const void* k,
                                                  const void* v, int64_t batch, int64_t q_heads,
                                                  int64_t kv_heads, int64_t seq, int64_t valid_keys,

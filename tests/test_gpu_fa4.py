@@ -147,9 +147,9 @@ def test_unbuilt_programs_fail_loudly(cuda):
     ("b2", "polynomial", "softcap_d4", 1, 0, 6.0),
 ])
 def test_causal_lengths_off_the_block_grid(oracle, cuda, group, name, mode, grad, route_bwd, qmul):
-    """S = 200: the runtime pads causal attention at the end to whole
-    128-row blocks and cuts the outputs back; results match the references
-    evaluated at S = 200."""
+    """S = 200: the forward runs at S = 200 (its last query block partial),
+    the backward pads at the end to whole 128-row blocks and cuts the
+    gradients back; results match the references evaluated at S = 200."""
     configs = {"b2": b2_component_configs, "b5": b5_component_configs}[group]()
     module = build_fa4_module(configs[name], head_dim=128)
     q, k, v, do = _qkv(1, 4, 2, 200, 50 + len(name), qmul)
@@ -177,8 +177,8 @@ def test_causal_lengths_off_the_block_grid(oracle, cuda, group, name, mode, grad
 
 @pytest.mark.parametrize("mode,mode_name", [(0, "softmax_native"), (4, "softcap_d4"), (5, "sigmoid_native")])
 def test_non_causal_lengths_off_the_block_grid(oracle, cuda, mode, mode_name):
-    """Non-causal attention at S = 200 through the runtime (padded to 256, the
-    padded keys masked in the forward) against the references at S = 200."""
+    """Non-causal attention at S = 200 through the runtime (the kernel reads no
+    row past S) against the references at S = 200."""
     from sfu_repro import fa4_runtime as rt
 
     q, k, v, do = (_fa4_layout(t) for t in _qkv(1, 4, 2, 200, 90 + mode, 6.0 if mode == 4 else 1.0))

@@ -130,7 +130,7 @@ def test_rejected_arguments(capi, cuda):
                   ctypes.c_int64(hq), ctypes.c_int64(hkv), ctypes.c_int64(seq), ctypes.c_int64(d),
                   ctypes.c_int(mode), ctypes.c_int(1), ctypes.c_float(0.1), ctypes.c_float(cap),
                   capi.stream())
-    assert call(100, 128, 0) != 0        # S not a multiple of 128
+    assert call(-1, 128, 0) != 0         # negative S
     assert call(128, 96, 0) != 0         # head_dim other than 64 / 128
     assert call(128, 128, 6) != 0        # B3 program outside its fitted length
     assert call(128, 128, 9) != 0        # unknown mode

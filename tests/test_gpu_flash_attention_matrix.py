@@ -188,3 +188,38 @@ def test_valid_keys_mask_padding(capi, oracle, cuda, mode, causal):
             _strides(qd, kd, vd, out), ctypes.c_int(M[mode]), ctypes.c_int(4), ctypes.c_int(int(causal)),
             ctypes.c_float(scale), ctypes.c_float(30.0), ctypes.c_float(bias), capi.stream())
         assert rc != 0, bad
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("s", [1, 77, 200, 333])
+def test_any_length_equals_padded(capi, cuda, s, d):
+    """A sequence of any length runs without padding: the kernel reads no row
+    past S, and its outputs equal, bit for bit, those of the same operands
+    zero-padded to a multiple of 128 with the padded keys masked
+    (launch_flash_attention_fwd_strided_keys_bf16, valid_keys = S)."""
+    import ctypes
+
+    from test_gpu_flash_attention_bwd import _strides
+
+    padded = (s + 127) // 128 * 128
+    q, k, v, _ = _inputs(2, 4, 2, s, 1500 + s + d, qmul=2.0, d=d)
+    pad = lambda t: torch.cat((t, t.new_zeros(t.shape[0], padded - s, *t.shape[2:])), 1)
+    qp, kp, vp = pad(q).to(cuda), pad(k).to(cuda), pad(v).to(cuda)
+    scale = d ** -0.5
+    for mode, route in (("softmax_native", 4), ("softmax_d2", 12), ("softcap_d4", 4), ("sigmoid_native", 4),
+                        ("softmax_pwl2", 4), ("sigmoid_d3", 4)):
+        bias = -math.log(padded)
+        for causal in (True, False):
+            out, lse = fwd(capi, cuda, q, k, v, mode, causal, scale, route=route, bias=bias)
+            pout = torch.empty_like(qp)
+            plse = torch.zeros(2, 4, padded, dtype=torch.float32, device=cuda)
+            rc = capi.launch_flash_attention_fwd_strided_keys_bf16(
+                capi.ptr(pout), capi.ptr(plse), capi.ptr(qp), capi.ptr(kp), capi.ptr(vp), ctypes.c_int64(2),
+                ctypes.c_int64(4), ctypes.c_int64(2), ctypes.c_int64(padded), ctypes.c_int64(s),
+                ctypes.c_int64(d), _strides(qp, kp, vp, pout), ctypes.c_int(M[mode]), ctypes.c_int(route),
+                ctypes.c_int(int(causal)), ctypes.c_float(scale), ctypes.c_float(30.0), ctypes.c_float(bias),
+                capi.stream())
+            assert rc == 0
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int16), pout[:, :s].view(torch.int16)), (mode, causal)
+            assert torch.equal(lse, plse[:, :, :s].contiguous()), (mode, causal)
