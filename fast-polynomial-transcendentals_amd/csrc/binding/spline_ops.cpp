@@ -713,7 +713,6 @@ std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tens
                 "q, k and v must agree in batch, seqlen and head_dim");
     TORCH_CHECK(q.size(3) == 64 || q.size(3) == 128, "head_dim must be 64 or 128, got ", q.size(3));
     TORCH_CHECK(q.size(2) % k.size(2) == 0, "q heads must be a multiple of kv heads");
-    TORCH_CHECK(q.size(1) % 128 == 0, "seqlen must be a multiple of 128, got ", q.size(1));
     const int64_t b = q.size(0), sq = q.size(1), hq = q.size(2), hkv = k.size(2);
     TORCH_CHECK(lse.is_cuda() && lse.scalar_type() == at::kFloat && lse.is_contiguous() &&
                     lse.dim() == 3 && lse.size(0) == b && lse.size(1) == hq && lse.size(2) == sq,

@@ -14,7 +14,7 @@
 //
 // Layout: Q, O [B, Hq, S, D] and K, V [B, Hkv, S, D] at any element strides
 // with a contiguous head dimension (D 64 or 128), BF16, grouped-query heads
-// (Hq a multiple of Hkv), S a multiple of 128, optional causal mask.
+// (Hq a multiple of Hkv), any S (the last block may be partial), optional causal mask.
 // s = q.k * scale.
 //
 // Design (all-transposed MFMA formulation, v_mfma_f32_32x32x16_bf16):

@@ -290,7 +290,11 @@ __device__ __forceinline__ bf16x8_t frag_tr32(const uint16_t* src, int dt, int c
 //    is held to 128 VGPRs, so two blocks (four waves per SIMD) share a CU
 //    (measured on MI355X: 1.14-1.22x on the softmax and softcap modes, a
 //    few spilled registers included).
-template <int MODE, int GRAD, int ROUTE, int HD, int W>
+//  * RAGGED (S not a multiple of 128): rows past the sequence are loaded as
+//    the last row (unconditional loads) and zeroed in LDS, their lse is +inf
+//    and their D 0, and keys past it store nothing, which is the arithmetic
+//    of operands zero-padded at the end.
+template <int MODE, int GRAD, int ROUTE, int HD, int W, bool RAGGED>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2)))
 flash_bwd_dkdv_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
@@ -322,8 +326,9 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
 
     bf16x8_t kf[HD / 32], vf[HD / 32];
     {
-        const uint16_t* kr = p.k + b * p.ks.b + kvh * p.ks.h + key * p.ks.s;
-        const uint16_t* vr = p.v + b * p.vs.b + kvh * p.vs.h + key * p.vs.s;
+        const int64_t ksrc = RAGGED && key >= p.seq ? p.seq - 1 : key;  // dK / dV of such keys are not stored
+        const uint16_t* kr = p.k + b * p.ks.b + kvh * p.ks.h + ksrc * p.ks.s;
+        const uint16_t* vr = p.v + b * p.vs.b + kvh * p.vs.h + ksrc * p.vs.s;
 #pragma unroll
         for (int c = 0; c < HD / 32; ++c) {
             kf[c] = *reinterpret_cast<const bf16x8_t*>(kr + c * 32 + g * 8);
@@ -337,7 +342,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     // query tiles of this head, from the block's first key on under the
     // causal mask
     const int64_t qt0 = p.causal ? kb * kKeys / kQT : 0;
-    const int64_t nit = p.seq / kQT - qt0;
+    const int64_t nit = (p.seq + kQT - 1) / kQT - qt0;
 
     // staging: item i = (tensor, row pair pr, chunk dc) of a tile, tensor 0 =
     // Q, 1 = dO; thread tid moves items tid + kThreads j (rows 2 pr, 2 pr + 1,
@@ -347,7 +352,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     constexpr int kPasses = (kItems + kThreads - 1) / kThreads;
     const uint16_t* sbase[kPasses];  // this thread's first source row of each pass
     int64_t sstride[kPasses];
-    int shalf[kPasses], soff[kPasses];  // tensor and LDS offset of each pass
+    int shalf[kPasses], soff[kPasses], srow[kPasses];  // tensor, LDS offset and tile row of each pass
 #pragma unroll
     for (int j = 0; j < kPasses; ++j) {
         const int i = tid + kThreads * j;
@@ -358,28 +363,51 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
                    (2 * pr) * sstride[j] + dc * 8;
         shalf[j] = half;
         soff[j] = 2 * pr * kRS + dc * 8;
+        srow[j] = 2 * pr;
     }
     auto active = [&](int j) { return kItems % kThreads == 0 || tid + kThreads * j < kItems; };
     u32x4_t ra[kPasses], rb2[kPasses];
     float row_r = 0.0f;
     auto load = [&](int64_t it) {
         const int64_t q0 = (qt0 + it) * kQT;
+        if (!RAGGED || q0 + kQT <= p.seq) {  // block-uniform: a whole tile of rows
 #pragma unroll
-        for (int j = 0; j < kPasses; ++j) {
-            if (active(j)) {
-                const uint16_t* r = sbase[j] + q0 * sstride[j];
-                ra[j] = *reinterpret_cast<const u32x4_t*>(r);
-                rb2[j] = *reinterpret_cast<const u32x4_t*>(r + sstride[j]);
+            for (int j = 0; j < kPasses; ++j) {
+                if (active(j)) {
+                    const uint16_t* r = sbase[j] + q0 * sstride[j];
+                    ra[j] = *reinterpret_cast<const u32x4_t*>(r);
+                    rb2[j] = *reinterpret_cast<const u32x4_t*>(r + sstride[j]);
+                }
+            }
+        } else {  // rows past the sequence read the last row; the store zeroes them
+#pragma unroll
+            for (int j = 0; j < kPasses; ++j) {
+                if (active(j)) {
+                    const uint16_t* base = sbase[j] - srow[j] * sstride[j];
+                    const int64_t r0 = q0 + srow[j], r1 = r0 + 1;
+                    ra[j] = *reinterpret_cast<const u32x4_t*>(base + (r0 < p.seq ? r0 : p.seq - 1) * sstride[j]);
+                    rb2[j] = *reinterpret_cast<const u32x4_t*>(base + (r1 < p.seq ? r1 : p.seq - 1) * sstride[j]);
+                }
             }
         }
         if constexpr (!kSigmoid) {
             if (tid % (kThreads / 2) < kQT) {
-                const int64_t i = (b * p.hq + head) * p.seq + q0 + tid % (kThreads / 2);
+                const int64_t row = q0 + tid % (kThreads / 2);
+                const int64_t i = (b * p.hq + head) * p.seq + (RAGGED && row >= p.seq ? p.seq - 1 : row);
                 row_r = tid >= kThreads / 2 ? p.delta[i] : p.lse[i] * kLog2e;
+                // a query past the sequence: no probability (lse +inf), D 0
+                if (RAGGED && row >= p.seq) row_r = tid >= kThreads / 2 ? 0.0f : __builtin_inff();
             }
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, int64_t q0) {
+        if (RAGGED && q0 + kQT > p.seq) {  // block-uniform: zero the rows past the sequence
+#pragma unroll
+            for (int j = 0; j < kPasses; ++j) {
+                if (q0 + srow[j] >= p.seq) ra[j] = (u32x4_t){0u, 0u, 0u, 0u};
+                if (q0 + srow[j] + 1 >= p.seq) rb2[j] = (u32x4_t){0u, 0u, 0u, 0u};
+            }
+        }
         BwdQTile<HD, kQT>& t = tiles[buf];
 #pragma unroll
         for (int j = 0; j < kPasses; ++j) {
@@ -395,7 +423,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     };
 
     load(0);
-    store(0);
+    store(0, qt0 * kQT);
     __syncthreads();
     for (int64_t it = 0; it < nit; ++it) {
         const int buf = (int)(it & 1);
@@ -465,10 +493,11 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
             }
         }
         }
-        if (more) store(buf ^ 1);
+        if (more) store(buf ^ 1, (qt0 + it + 1) * kQT);
         __syncthreads();
     }
 
+    if (RAGGED && key >= p.seq) return;
     // dK^T / dV^T: register r of dt holds d = 16 dt + 4g + r of key kl
     if (p.dkv_ws != nullptr) {
         const int64_t plane = p.hq * p.seq * HD * (int64_t)gridDim.z;
@@ -535,7 +564,9 @@ struct BwdKTile {
     uint16_t v[kBwdTile * k_row_stride<HD>()];
 };
 
-template <int MODE, int GRAD, int ROUTE, int HD, int W>
+// RAGGED: as in the dK/dV kernel (queries past the sequence read the last
+// row and store nothing; key rows past it are zeroed in LDS).
+template <int MODE, int GRAD, int ROUTE, int HD, int W, bool RAGGED>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) flash_bwd_dq_kernel(AttnBwdParams p) {
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kRS = k_row_stride<HD>(), kChunks = HD / 8;
@@ -545,18 +576,20 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, c32 = lane & 31;
-    const int64_t nqb = p.seq / kBlockQ;
+    const int64_t nqb = (p.seq + kBlockQ - 1) / kBlockQ;
     const int64_t head = blockIdx.x, b = blockIdx.z;
     const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
     const int64_t kvh = head / (p.hq / p.hkv);
     const int64_t q0 = qb * kBlockQ + wave * 32;
     const int64_t qrow = q0 + c32;
+    const bool qin = !RAGGED || qrow < p.seq;
+    const int64_t qsrc = qin ? qrow : p.seq - 1;  // dQ of such queries is not stored
     const float inv_cap = 1.0f / p.cap;
 
     bf16x8_t qf[HD / 16], df[HD / 16];
     {
-        const uint16_t* qr = p.q + b * p.qs.b + head * p.qs.h + qrow * p.qs.s;
-        const uint16_t* dr = p.dout + b * p.dos.b + head * p.dos.h + qrow * p.dos.s;
+        const uint16_t* qr = p.q + b * p.qs.b + head * p.qs.h + qsrc * p.qs.s;
+        const uint16_t* dr = p.dout + b * p.dos.b + head * p.dos.h + qsrc * p.dos.s;
 #pragma unroll
         for (int c = 0; c < HD / 16; ++c) {
             qf[c] = *reinterpret_cast<const bf16x8_t*>(qr + c * 16 + h * 8);
@@ -565,7 +598,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     }
     float lse2 = 0.0f, dl = 0.0f;
     if constexpr (!kSigmoid) {
-        const int64_t i = (b * p.hq + head) * p.seq + qrow;
+        const int64_t i = (b * p.hq + head) * p.seq + qsrc;
         lse2 = p.lse[i] * kLog2e;
         dl = p.delta[i];
     }
@@ -579,7 +612,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     constexpr int kPasses = (kItems + kThreads - 1) / kThreads;
     const uint16_t* sbase[kPasses];  // this thread's first source row of each pass
     int64_t sstride[kPasses];
-    int shalf[kPasses], soff[kPasses];  // tensor and LDS offset of each pass
+    int shalf[kPasses], soff[kPasses], srow[kPasses];  // tensor, LDS offset and tile row of each pass
 #pragma unroll
     for (int j = 0; j < kPasses; ++j) {
         const int i = tid + kThreads * j;
@@ -590,20 +623,40 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
                    (2 * pr) * sstride[j] + dc * 8;
         shalf[j] = half;
         soff[j] = 2 * pr * kRS + dc * 8;
+        srow[j] = 2 * pr;
     }
     auto active = [&](int j) { return kItems % kThreads == 0 || tid + kThreads * j < kItems; };
     u32x4_t ra[kPasses], rb2[kPasses];
     auto load = [&](int64_t k0) {
+        if (!RAGGED || k0 + kBwdTile <= p.seq) {  // block-uniform: a whole tile of rows
 #pragma unroll
-        for (int j = 0; j < kPasses; ++j) {
-            if (active(j)) {
-                const uint16_t* r = sbase[j] + k0 * sstride[j];
-                ra[j] = *reinterpret_cast<const u32x4_t*>(r);
-                rb2[j] = *reinterpret_cast<const u32x4_t*>(r + sstride[j]);
+            for (int j = 0; j < kPasses; ++j) {
+                if (active(j)) {
+                    const uint16_t* r = sbase[j] + k0 * sstride[j];
+                    ra[j] = *reinterpret_cast<const u32x4_t*>(r);
+                    rb2[j] = *reinterpret_cast<const u32x4_t*>(r + sstride[j]);
+                }
+            }
+        } else {  // rows past the sequence read the last row; the store zeroes them
+#pragma unroll
+            for (int j = 0; j < kPasses; ++j) {
+                if (active(j)) {
+                    const uint16_t* base = sbase[j] - srow[j] * sstride[j];
+                    const int64_t r0 = k0 + srow[j], r1 = r0 + 1;
+                    ra[j] = *reinterpret_cast<const u32x4_t*>(base + (r0 < p.seq ? r0 : p.seq - 1) * sstride[j]);
+                    rb2[j] = *reinterpret_cast<const u32x4_t*>(base + (r1 < p.seq ? r1 : p.seq - 1) * sstride[j]);
+                }
             }
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, int64_t k0) {
+        if (RAGGED && k0 + kBwdTile > p.seq) {  // block-uniform: zero the rows past the sequence
+#pragma unroll
+            for (int j = 0; j < kPasses; ++j) {
+                if (k0 + srow[j] >= p.seq) ra[j] = (u32x4_t){0u, 0u, 0u, 0u};
+                if (k0 + srow[j] + 1 >= p.seq) rb2[j] = (u32x4_t){0u, 0u, 0u, 0u};
+            }
+        }
         BwdKTile<HD>& t = tiles[buf];
 #pragma unroll
         for (int j = 0; j < kPasses; ++j) {
@@ -615,9 +668,11 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
         }
     };
 
-    const int64_t nkt = p.causal ? (qb + 1) * (kBlockQ / kBwdTile) : p.seq / kBwdTile;
+    const int64_t ktiles = (p.seq + kBwdTile - 1) / kBwdTile;
+    const int64_t ncausal = p.causal ? (qb + 1) * (kBlockQ / kBwdTile) : ktiles;
+    const int64_t nkt = ncausal < ktiles ? ncausal : ktiles;
     load(0);
-    store(0);
+    store(0, 0);
     __syncthreads();
     for (int64_t kt = 0; kt < nkt; ++kt) {
         const int buf = (int)(kt & 1);
@@ -670,10 +725,11 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
                     dqacc[dt] = mfma32(frag_tr32<HD>(t.k + tr_off, dt, cc), sf, dqacc[dt]);
             }
         }
-        if (more) store(buf ^ 1);
+        if (more) store(buf ^ 1, k0 + kBwdTile);
         __syncthreads();
     }
 
+    if (!qin) return;
     uint16_t* dqr = p.dq + b * p.dqs.b + head * p.dqs.h + qrow * p.dqs.s;
 #pragma unroll
     for (int dt = 0; dt < HD / 32; ++dt)
@@ -692,15 +748,16 @@ using namespace pt;
 
 namespace {
 
-template <int MODE, int GRAD, int ROUTE, int HD>
-void launch_bwd_hd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
-    const dim3 grid((unsigned)prm.hq, (unsigned)(prm.seq / 128), (unsigned)batch);
+template <int MODE, int GRAD, int ROUTE, int HD, bool RAGGED>
+void launch_bwd_shape(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
+    const dim3 grid((unsigned)prm.hq, (unsigned)((prm.seq + 127) / 128), (unsigned)batch);
     // waves (16 keys each) per dK/dV block: the sigmoid modes run faster as
     // independent 4-wave blocks, the softmax modes as 8-wave blocks that stage
     // each query tile once per 128 keys (measured on MI355X)
     constexpr int kW = attn_is_sigmoid(MODE) ? 4 : 8;
-    const dim3 kgrid((unsigned)prm.hq, (unsigned)(prm.seq / (16 * kW)), (unsigned)batch);
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE, HD, kW>), kgrid, dim3(64 * kW), 0, st, prm);
+    const dim3 kgrid((unsigned)prm.hq, (unsigned)((prm.seq + 16 * kW - 1) / (16 * kW)), (unsigned)batch);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE, HD, kW, RAGGED>), kgrid, dim3(64 * kW), 0, st,
+                       prm);
     if (prm.dkv_ws != nullptr) {
         const int64_t n = batch * prm.hkv * prm.seq * (HD / 8);
         hipLaunchKernelGGL((attn_dkv_reduce_kernel<HD>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
@@ -713,12 +770,23 @@ void launch_bwd_hd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
     // the dQ kernel of those modes, -1-3 % for softcap and the sigmoid
     // polynomials)
     constexpr int kQW = HD == 128 && (attn_is_plain_softmax(MODE) || MODE == kAttnSigmoidNative) ? 8 : 4;
-    if (prm.seq % (32 * kQW) == 0) {
-        const dim3 qgrid((unsigned)prm.hq, (unsigned)(prm.seq / (32 * kQW)), (unsigned)batch);
-        hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, kQW>), qgrid, dim3(64 * kQW), 0, st, prm);
-    } else {
-        hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, 4>), grid, dim3(256), 0, st, prm);
+    if constexpr (!RAGGED) {
+        if (prm.seq % (32 * kQW) == 0) {
+            const dim3 qgrid((unsigned)prm.hq, (unsigned)(prm.seq / (32 * kQW)), (unsigned)batch);
+            hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, kQW, false>), qgrid, dim3(64 * kQW), 0,
+                               st, prm);
+            return;
+        }
     }
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, 4, RAGGED>), grid, dim3(256), 0, st, prm);
+}
+
+// S not a multiple of 128 takes the RAGGED kernels, whose last blocks hold
+// rows past the sequence; the aligned kernels carry no such guards.
+template <int MODE, int GRAD, int ROUTE, int HD>
+void launch_bwd_hd(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
+    if (prm.seq % kAttnBlockQ == 0) launch_bwd_shape<MODE, GRAD, ROUTE, HD, false>(prm, batch, st);
+    else launch_bwd_shape<MODE, GRAD, ROUTE, HD, true>(prm, batch, st);
 }
 
 template <int MODE, int GRAD, int ROUTE>
@@ -757,8 +825,7 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
     if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || (head_dim != 64 && head_dim != 128) || !strides)
         return hipErrorInvalidValue;
     const int hd = (int)head_dim;
-    if (q_heads % kv_heads != 0 || seq % kAttnBlockQ != 0 || mode < 0 || mode >= kAttnModes)
-        return hipErrorInvalidValue;
+    if (q_heads % kv_heads != 0 || mode < 0 || mode >= kAttnModes) return hipErrorInvalidValue;
     if ((mode == kAttnSoftcapNative || mode == kAttnSoftcapD4) && !(cap > 0.0f && cap <= __FLT_MAX__))
         return hipErrorInvalidValue;
     if ((mode == kAttnSigmoidB3 || mode == kAttnSigmoidB3D2) && seq != 4096) return hipErrorInvalidValue;
@@ -785,7 +852,7 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
     if (!sig && (!out || !aligned16(out) || !lse || !delta || (reinterpret_cast<uintptr_t>(lse) & 3) ||
                  (reinterpret_cast<uintptr_t>(delta) & 3)))
         return hipErrorInvalidValue;
-    if (batch > 65535 || seq / 128 > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
+    if (batch > 65535 || (seq + 127) / 128 > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
     const bool grouped = q_heads != kv_heads;
     if (grouped && (!dkv_workspace || (reinterpret_cast<uintptr_t>(dkv_workspace) & 15)))
         return hipErrorInvalidValue;

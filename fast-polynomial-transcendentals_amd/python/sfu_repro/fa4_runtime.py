@@ -28,12 +28,10 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
   or the BF16 sigmoid D3..D6 programs on ``s + bias`` (``bias`` defaults to
   ``-ln S``).
 
-Sequence lengths: the forward takes any length (the kernel reads no row
-past the sequence and zero-fills the last partial block).  The backward works
-on whole 128-row blocks: attention of any length is padded at the end to the
-next multiple of 128 with zero rows and the gradients are cut back; a zero K
-row gives a padded key no share of dQ, and a padded query's zero output
-gradient and infinite lse give it no share of dK / dV.
+Sequence lengths: any.  The kernels read no row past the sequence; the rows
+of the last, partial block are zeroed on chip (queries past the sequence get
+an infinite lse and a zero D in the backward), which is the arithmetic of
+operands zero-padded at the end, and nothing past the sequence is stored.
 
 Combinations whose programs are not part of the reference tree (the FP16 /
 BF16 / PWL1 exp2 variants, Sollya attention fits, mixed SFU/polynomial
@@ -306,24 +304,6 @@ def _check_operands(q, k, v):
             raise ValueError(f"{name} must be [batch, seqlen, heads, head_dim]")
 
 
-_BLOCK = 128  # query / key rows per kernel block
-
-
-def _padded_length(seqlen: int) -> int:
-    """The length the kernels run at: the next multiple of 128."""
-    if seqlen < 1:
-        raise ValueError(f"seqlen must be positive, got {seqlen}")
-    return (seqlen + _BLOCK - 1) // _BLOCK * _BLOCK
-
-
-def _pad_rows(t, length: int, value: float = 0.0):
-    """t [B, S, ...] padded along S to `length` (a new tensor)."""
-    pad = length - t.shape[1]
-    if pad == 0:
-        return t
-    return torch.cat((t, t.new_full((t.shape[0], pad, *t.shape[2:]), value)), dim=1)
-
-
 def flash_attn_fwd(q, k, v, softmax_scale=None, causal=False, softcap=0.0, score_mod=None,
                    sigmoid_attention=False, sigmoid_sfu_freq=16, sigmoid_sfu_res=0, sigmoid_bias=None,
                    sigmoid_poly_backend="cute", sigmoid_degree=3, sigmoid_coeff_source="current",
@@ -361,18 +341,10 @@ def flash_attn_bwd(q, k, v, out, dout, lse, softmax_scale=None, causal=False, so
         sigmoid_poly_backend=sigmoid_poly_backend, sigmoid_degree=sigmoid_degree,
         sigmoid_gradient_degree=sigmoid_gradient_degree, sigmoid_coeff_source=sigmoid_coeff_source,
         exp2_emu_backend=exp2_emu_backend, exp2_emu_freq=exp2_emu_freq)
-    seqlen = q.shape[1]
-    padded = _padded_length(seqlen)
-    if padded != seqlen:
-        # zero rows for q, k, v, out and dout; an infinite lse makes the
-        # padded queries' probabilities exactly zero in the softmax modes
-        q, k, v, out, dout = (_pad_rows(t, padded) for t in (q, k, v, out, dout))
-        lse = _pad_rows(lse.transpose(1, 2), padded, math.inf).transpose(1, 2).contiguous()
-    dq, dk, dv = _ops().flash_attn_bwd_bf16(q, k, v, out, dout, lse, mode, grad, route, bool(causal),
-                                           scale, cap, bias)
-    if padded != seqlen:
-        dq, dk, dv = (t[:, :seqlen].contiguous() for t in (dq, dk, dv))
-    return dq, dk, dv
+    if q.shape[1] < 1:
+        raise ValueError(f"seqlen must be positive, got {q.shape[1]}")
+    return tuple(_ops().flash_attn_bwd_bf16(q, k, v, out, dout, lse, mode, grad, route, bool(causal),
+                                            scale, cap, bias))
 
 
 def runtime() -> dict:

@@ -475,12 +475,13 @@ int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q
                                             int causal, float scale, float cap, float sigmoid_bias,
                                             void* stream);
 /* The same forward with keys valid_keys .. seq - 1 masked as padding
- * (1 <= valid_keys <= seq): for operands padded at the end to a length the
- * backward takes (a multiple of 128), the padded queries' rows are computed
- * and left to the caller to drop.  Zero-padded operands need no change to the
- * backward: a zero K row gives the padded keys no share of dQ, and padded
- * queries with zero dout and an infinite lse add nothing to dK / dV.
- * launch_flash_attention_fwd_strided_bf16 is this with valid_keys = seq. */
+ * (1 <= valid_keys <= seq), for callers that keep operands padded at the end
+ * (the padded queries' rows are computed and left to the caller to drop).
+ * Zero-padded operands need no change to the backward: a zero K row gives the
+ * padded keys no share of dQ, and padded queries with zero dout and an
+ * infinite lse add nothing to dK / dV.  Any seq works without padding: the
+ * kernels read no row past seq.  launch_flash_attention_fwd_strided_bf16 is
+ * this with valid_keys = seq. */
 int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* lse, const void* q, const void* k,
                                                  const void* v, int64_t batch, int64_t q_heads,
                                                  int64_t kv_heads, int64_t seq, int64_t valid_keys,

@@ -223,3 +223,30 @@ def test_any_length_equals_padded(capi, cuda, s, d):
             torch.cuda.synchronize()
             assert torch.equal(out.view(torch.int16), pout[:, :s].view(torch.int16)), (mode, causal)
             assert torch.equal(lse, plse[:, :, :s].contiguous()), (mode, causal)
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 2), (2, 2)])
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("s", [1, 77, 200, 333])
+def test_backward_any_length_equals_padded(capi, cuda, s, d, hq, hkv):
+    """The backward at any S reads no row past the sequence; dq, dk, dv equal,
+    bit for bit, those of the operands zero-padded to a multiple of 128 with
+    the lse padded with +inf (grouped heads through the partials workspace,
+    plain heads directly)."""
+    from test_gpu_flash_attention_bwd import bwd
+
+    padded = (s + 127) // 128 * 128
+    q, k, v, do = _inputs(2, hq, hkv, s, 1700 + s + d + hq, qmul=2.0, d=d)
+    pad = lambda t, val=0.0: torch.cat((t, t.new_full((t.shape[0], padded - t.shape[1], *t.shape[2:]), val)), 1)
+    scale = d ** -0.5
+    bias = -math.log(padded)
+    for mode, grad, route in (("softmax_native", 0, 0), ("softmax_d2", 0, 32), ("softcap_d4", 1, 0),
+                              ("sigmoid_native", 0, 0), ("sigmoid_d3", 0, 0), ("softmax_pwl2", 0, 4)):
+        for causal in (True, False):
+            out, lse = fwd(capi, cuda, q, k, v, mode, causal, scale, route=route or 4, bias=bias)
+            got = bwd(capi, cuda, q, k, v, out, do, lse, mode, grad, causal, scale, route=route, bias=bias)[:3]
+            lse_p = pad(lse.transpose(1, 2), math.inf).transpose(1, 2).contiguous()
+            want = bwd(capi, cuda, pad(q), pad(k), pad(v), pad(out), pad(do), lse_p, mode, grad, causal, scale,
+                       route=route, bias=bias)[:3]
+            for name, a, b in zip(("dq", "dk", "dv"), got, want):
+                assert torch.equal(a.view(torch.int32), b[:, :s].contiguous().view(torch.int32)), (mode, causal, name)

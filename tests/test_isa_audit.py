@@ -195,9 +195,14 @@ def test_no_register_spills_outside_the_measured_exception(metadata):
     """No kernel spills VGPRs to scratch memory, except the head_dim-64
     dK/dV kernels of the softmax modes, which are held to 128 VGPRs for four
     waves per SIMD and spill at most a few registers (measured faster than
-    the unspilled two-wave form)."""
+    the unspilled two-wave form); their instantiations for sequences that are
+    not a multiple of 128 (and the softcap D4 one) carry the row guards and
+    spill up to 4 registers / 20 bytes."""
     assert len(metadata) > 900
-    allowed = re.compile(r"pt::flash_bwd_dkdv_kernel<(0|1|2|12), 0, \d+, 64, 8>$")
+    aligned = re.compile(r"pt::flash_bwd_dkdv_kernel<(0|1|2|12), 0, \d+, 64, 8, false>$")
+    ragged = re.compile(r"pt::flash_bwd_dkdv_kernel<(0|1|2|12), 0, \d+, 64, 8, true>$|"
+                        r"pt::flash_bwd_dkdv_kernel<4, \d, 0, 64, 8, true>$")
     bad = [(n, spill, scratch) for n, spill, scratch in metadata
-           if (spill or scratch) and not (allowed.search(n) and spill <= 4 and scratch <= 16)]
+           if (spill or scratch) and not (aligned.search(n) and spill <= 4 and scratch <= 16)
+           and not (ragged.search(n) and spill <= 4 and scratch <= 20)]
     assert not bad, bad
