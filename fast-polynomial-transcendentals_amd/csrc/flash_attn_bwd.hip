@@ -770,15 +770,13 @@ void launch_bwd_shape(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
     // the dQ kernel of those modes, -1-3 % for softcap and the sigmoid
     // polynomials)
     constexpr int kQW = HD == 128 && (attn_is_plain_softmax(MODE) || MODE == kAttnSigmoidNative) ? 8 : 4;
-    if constexpr (!RAGGED) {
-        if (prm.seq % (32 * kQW) == 0) {
-            const dim3 qgrid((unsigned)prm.hq, (unsigned)(prm.seq / (32 * kQW)), (unsigned)batch);
-            hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, kQW, false>), qgrid, dim3(64 * kQW), 0,
-                               st, prm);
-            return;
-        }
+    if (grid.y % (kQW / 4) == 0) {  // whole kQW-wave blocks over the 128-row blocks
+        const dim3 qgrid(grid.x, grid.y / (kQW / 4), grid.z);
+        hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, kQW, RAGGED>), qgrid, dim3(64 * kQW), 0, st,
+                           prm);
+    } else {
+        hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, 4, RAGGED>), grid, dim3(256), 0, st, prm);
     }
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<MODE, GRAD, ROUTE, HD, 4, RAGGED>), grid, dim3(256), 0, st, prm);
 }
 
 // S not a multiple of 128 takes the RAGGED kernels, whose last blocks hold
