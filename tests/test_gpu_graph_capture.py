@@ -16,6 +16,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 S_ATTN = 256  # attention sequence length (a multiple of 128)
+S_RAGGED = 200  # and one that is not
 
 
 def _shifted(logits: torch.Tensor) -> torch.Tensor:
@@ -44,6 +45,11 @@ def _inputs(seed: int) -> dict:
         "k": torch.randn(1, S_ATTN, 2, 128, generator=g).to(torch.bfloat16),
         "v": torch.randn(1, S_ATTN, 2, 128, generator=g).to(torch.bfloat16),
         "dout": torch.randn(1, S_ATTN, 4, 128, generator=g).to(torch.bfloat16),
+        # a length that is not a multiple of 128 (the ragged kernels)
+        "q2": torch.randn(1, S_RAGGED, 4, 128, generator=g).to(torch.bfloat16),
+        "k2": torch.randn(1, S_RAGGED, 2, 128, generator=g).to(torch.bfloat16),
+        "v2": torch.randn(1, S_RAGGED, 2, 128, generator=g).to(torch.bfloat16),
+        "dout2": torch.randn(1, S_RAGGED, 4, 128, generator=g).to(torch.bfloat16),
         "gx": torch.randn(n, generator=g).to(torch.bfloat16),
         "gpacked": torch.randn(24, 520, generator=g).to(torch.bfloat16),
     }
@@ -64,6 +70,7 @@ def _run(spline_ops, t: dict) -> list:
     # softmax with the routed D2 exp2 (B5 forward schedule) and the B2 softcap
     outs += list(spline_ops.flash_attn_fwd_bf16(t["q"], t["k"], t["v"], 1, 12, True, 128 ** -0.5))
     outs += list(spline_ops.flash_attn_fwd_bf16(t["q"], t["k"], t["v"], 4, 4, False, 128 ** -0.5, 30.0))
+    outs += list(spline_ops.flash_attn_fwd_bf16(t["q2"], t["k2"], t["v2"], 1, 12, True, 128 ** -0.5))
     return outs
 
 
@@ -79,6 +86,9 @@ def _run_backward(spline_ops, t: dict) -> list:
     scale = 128 ** -0.5
     out, lse = spline_ops.flash_attn_fwd_bf16(t["q"], t["k"], t["v"], 0, 4, True, scale)
     outs += list(spline_ops.flash_attn_bwd_bf16(t["q"], t["k"], t["v"], out, t["dout"], lse, 0, 0, 0, True,
+                                                scale, 0.0, 0.0))
+    out2, lse2 = spline_ops.flash_attn_fwd_bf16(t["q2"], t["k2"], t["v2"], 0, 4, False, scale)
+    outs += list(spline_ops.flash_attn_bwd_bf16(t["q2"], t["k2"], t["v2"], out2, t["dout2"], lse2, 0, 0, 0, False,
                                                 scale, 0.0, 0.0))
     return outs
 
