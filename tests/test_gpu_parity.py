@@ -7,6 +7,8 @@ include the exhaustive input sweep for the program argument.  All calls go
 through the C ABI (include/spline_ops_hip.h) via ctypes.
 """
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -158,6 +160,27 @@ def test_b3_exhaustive(capi, oracle, cuda):
     assert_bits_equal(_host(y), want_y, "bf16", "B3 y")
     assert_bits_equal(_host(dy), want_dy, "bf16", "B3 dy")
     assert_bits_equal(_host(y_only), want_y, "bf16", "B3 forward-only y")
+
+
+def test_b3_against_reference_emulation_fixture(capi, oracle, cuda):
+    """HIP B3 == the reference's own evaluate_deployed table
+    (scripts/audit_b3_deployed_fit.py:341-366, tests/golden/b3_audit_table.npz),
+    with no oracle in between; C1's 2^20 seed-0 scores looked up in the same table."""
+    t = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "b3_audit_table.npz"))
+    fy, fdy = t["y"], t["dy"]
+    nan_f = ((fdy & 0x7F80) == 0x7F80) & ((fdy & 0x7F) != 0)
+    g = torch.Generator().manual_seed(0)
+    c1 = (torch.rand(2 ** 20, generator=g) * 32 - 16).to(torch.bfloat16)
+    for x in (oracle.all_bits(), c1.view(torch.int16).numpy().view(np.uint16)):
+        xd = _dev(x, "bf16", cuda)
+        y, dy = torch.empty_like(xd), torch.empty_like(xd)
+        capi.call("launch_flash_sigmoid_direct_d3_d4_bf16", y, dy, xd, x.size)
+        torch.cuda.synchronize()
+        gy, gdy = _host(y), _host(dy)
+        assert np.array_equal(gy, fy[x]), np.flatnonzero(gy != fy[x])[:8]
+        nan = nan_f[x]
+        assert np.array_equal(((gdy & 0x7F80) == 0x7F80) & ((gdy & 0x7F) != 0), nan)
+        assert np.array_equal(gdy[~nan], fdy[x][~nan])
 
 
 def test_b3_config1_uniform_scores(capi, oracle, cuda):
