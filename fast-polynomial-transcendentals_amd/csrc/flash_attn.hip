@@ -295,8 +295,8 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
 // and the head index varies fastest, so the first wave of resident blocks
 // takes the longest query blocks of every head.
 // RAGGED: S is not a multiple of 128, so the last query block and the last
-// key tile hold rows past the sequence (a separate instantiation keeps those
-// guards out of the aligned kernels).
+// key tile hold rows past the sequence, or keys from kv_len on are padding
+// (a separate instantiation keeps those guards out of the aligned kernels).
 template <int MODE, int ROUTE, int HD, int W, bool RAGGED>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) flash_fwd_kernel(AttnParams p) {
     constexpr int kBlockQ = 32 * W;  // queries per block
@@ -362,11 +362,14 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
             }
         }
     };
+    // rows from kv_len on (padding keys, and rows past the sequence) are
+    // zeroed before they reach LDS, so whatever the padding holds (NaN, Inf)
+    // the masked P (0) times V stays 0
     auto store = [&](int buf, int64_t k0) {
-        if (RAGGED && k0 + kAttnBlockK > p.seq) {  // block-uniform: the tile holds rows past the sequence
+        if (RAGGED && k0 + kAttnBlockK > p.kv_len) {  // block-uniform: the tile holds rows from kv_len on
 #pragma unroll
             for (int j = 0; j < kPasses; ++j)
-                if (k0 + krow + kRowsPass * j >= p.seq) kr[j] = vr[j] = (u32x4_t){0u, 0u, 0u, 0u};
+                if (k0 + krow + kRowsPass * j >= p.kv_len) kr[j] = vr[j] = (u32x4_t){0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (int j = 0; j < kPasses; ++j) {
@@ -459,7 +462,7 @@ bool route_supported(int route) {
 // softmax and hardware modes at D 128, 0.81-0.96x for 8 waves at D 64).
 template <int MODE, int ROUTE, int HD, int W>
 void launch_fwd_shape(const AttnParams& prm, dim3 grid, hipStream_t st) {
-    if (prm.seq % kAttnBlockQ == 0)
+    if (prm.seq % kAttnBlockQ == 0 && prm.kv_len == prm.seq)
         hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, HD, W, false>), grid, dim3(64 * W), 0, st, prm);
     else
         hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, HD, W, true>), grid, dim3(64 * W), 0, st, prm);

@@ -477,11 +477,15 @@ int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q
 /* The same forward with keys valid_keys .. seq - 1 masked as padding
  * (1 <= valid_keys <= seq), for callers that keep operands padded at the end
  * (the padded queries' rows are computed and left to the caller to drop).
- * Zero-padded operands need no change to the backward: a zero K row gives the
- * padded keys no share of dQ, and padded queries with zero dout and an
- * infinite lse add nothing to dK / dV.  Any seq works without padding: the
- * kernels read no row past seq.  launch_flash_attention_fwd_strided_bf16 is
- * this with valid_keys = seq. */
+ * The padded K and V rows are zeroed on chip before use, so they may hold
+ * anything (NaN and Inf included).  The padded queries attend to the valid
+ * keys: their out rows and lse are finite for finite Q rows.
+ * The backward takes no valid_keys.  It serves padded operands when the
+ * padded K rows are zero, the padded V, Q and out rows finite and the padded
+ * dout rows zero: a zero K row gives the padded keys no share of dQ, and a
+ * zero dout row makes a padded query's dP and D zero, so it adds nothing to
+ * dK / dV.  Any seq works without padding: the kernels read no row past seq.
+ * launch_flash_attention_fwd_strided_bf16 is this with valid_keys = seq. */
 int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* lse, const void* q, const void* k,
                                                  const void* v, int64_t batch, int64_t q_heads,
                                                  int64_t kv_heads, int64_t seq, int64_t valid_keys,
@@ -525,7 +529,9 @@ int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float*
  * the limit is B * Hq * S <= 16,777,216 query rows without grouped heads,
  * and <= 65,280 (D = 128) or <= 130,055 (D = 64) with them.  Calls no
  * allocator.  Calls that overlap on one GPU share the array and race: order
- * them on one stream. */
+ * them on one stream.  The first call on each device looks up the array's
+ * device address (hipGetSymbolAddress, once per device): make that first
+ * call eagerly, outside HIP graph capture; later calls may be captured. */
 #define SPLINE_HIP_BWD_SCRATCH_BYTES (64ll << 20)
 int launch_flash_attention_bwd_strided_bf16_noalloc(void* dq, void* dk, void* dv, const void* q,
                                                     const void* k, const void* v, const void* out,

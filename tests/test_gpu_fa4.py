@@ -147,9 +147,9 @@ def test_unbuilt_programs_fail_loudly(cuda):
     ("b2", "polynomial", "softcap_d4", 1, 0, 6.0),
 ])
 def test_causal_lengths_off_the_block_grid(oracle, cuda, group, name, mode, grad, route_bwd, qmul):
-    """S = 200: the forward runs at S = 200 (its last query block partial),
-    the backward pads at the end to whole 128-row blocks and cuts the
-    gradients back; results match the references evaluated at S = 200."""
+    """S = 200: forward and backward run at S = 200 with no padding (their
+    last query and key blocks partial; rows past S are neither read nor
+    stored); results match the references evaluated at S = 200."""
     configs = {"b2": b2_component_configs, "b5": b5_component_configs}[group]()
     module = build_fa4_module(configs[name], head_dim=128)
     q, k, v, do = _qkv(1, 4, 2, 200, 50 + len(name), qmul)

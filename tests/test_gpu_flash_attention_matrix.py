@@ -190,6 +190,46 @@ def test_valid_keys_mask_padding(capi, oracle, cuda, mode, causal):
         assert rc != 0, bad
 
 
+@pytest.mark.parametrize("seq,valid", [(256, 200), (256, 129), (333, 70)])
+@pytest.mark.parametrize("mode", ["softmax_native", "softcap_d4", "sigmoid_native"])
+def test_valid_keys_padding_nan_inf(capi, cuda, mode, seq, valid):
+    """Padded K / V rows holding NaN and +-Inf change nothing: the outputs of
+    every query row and the lse equal, bit for bit, those with zero padding
+    (keys past valid_keys are zeroed on chip before P.V)."""
+    import ctypes
+
+    from test_gpu_flash_attention_bwd import _strides
+
+    print(f"valid_keys nan/inf {mode} seq {seq} valid {valid}", flush=True)
+    q, k, v, _ = _inputs(1, 4, 2, seq, 1600 + seq + valid + M[mode], qmul=2.0)
+    zk, zv = k.clone(), v.clone()
+    zk[:, valid:] = 0
+    zv[:, valid:] = 0
+    bk, bv = k.clone(), v.clone()
+    bk[:, valid::3], bk[:, valid + 1::3], bk[:, valid + 2::3] = float("nan"), float("inf"), -float("inf")
+    bv[:, valid::3], bv[:, valid + 1::3], bv[:, valid + 2::3] = float("inf"), float("nan"), -float("inf")
+    scale = 128 ** -0.5
+    results = []
+    for kk, vv in ((zk, zv), (bk, bv)):
+        qd, kd, vd = q.to(cuda), kk.to(cuda), vv.to(cuda)
+        out = torch.empty_like(qd)
+        lse = torch.zeros(1, 4, seq, dtype=torch.float32, device=cuda)
+        for causal in (0, 1):
+            rc = capi.launch_flash_attention_fwd_strided_keys_bf16(
+                capi.ptr(out), capi.ptr(lse), capi.ptr(qd), capi.ptr(kd), capi.ptr(vd), ctypes.c_int64(1),
+                ctypes.c_int64(4), ctypes.c_int64(2), ctypes.c_int64(seq), ctypes.c_int64(valid),
+                ctypes.c_int64(128), _strides(qd, kd, vd, out), ctypes.c_int(M[mode]), ctypes.c_int(4),
+                ctypes.c_int(causal), ctypes.c_float(scale), ctypes.c_float(30.0), ctypes.c_float(-5.0),
+                capi.stream())
+            assert rc == 0
+            torch.cuda.synchronize()
+            results.append((out.cpu().clone(), lse.cpu().clone()))
+    for (zo, zl), (bo, bl) in zip(results[:2], results[2:]):
+        assert torch.isfinite(bo.float()).all()
+        assert torch.equal(zo.view(torch.int16), bo.view(torch.int16))
+        assert torch.equal(zl, bl)
+
+
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("s", [1, 77, 200, 333])
 def test_any_length_equals_padded(capi, cuda, s, d):

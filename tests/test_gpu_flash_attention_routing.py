@@ -15,7 +15,8 @@ closer to the first:
   the BF16 rounding of dQ, dK, dV in an L2 norm over all elements.
 
 Also covers the S = 384 backward cases that reach the 4-wave dQ blocks at
-head_dim 128 (the 8-wave blocks need S a multiple of 256)."""
+head_dim 128 (the 8-wave blocks need an even number of 128-row query blocks,
+ceil(S / 128) even; S = 384 has three)."""
 
 import math
 
