@@ -150,12 +150,16 @@ exp2_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, int64_t 
         const uint32_t w[8] = {a.w[0], a.w[1], a.w[2], a.w[3], c.w[0], c.w[1], c.w[2], c.w[3]};
         Vec4 o;
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            o.w[k] = pack_bf(exp2_lane<KIND>(as_f32(w[2 * k])), exp2_lane<KIND>(as_f32(w[2 * k + 1])));
+        for (int k = 0; k < 4; ++k) {
+            float r0, r1;
+            exp2_pair<KIND>(as_f32(w[2 * k]), as_f32(w[2 * k + 1]), r0, r1);
+            o.w[k] = pack_bf(r0, r1);
+        }
         st16<SNT>(y, i, o);
     }
     for (int64_t e = (n8 << 3) + (int64_t)blockIdx.x * kBlock + threadIdx.x; e < n; e += stride) {
-        const float r = exp2_lane<KIND>(x[e]);
+        float r, unused;
+        exp2_pair<KIND>(x[e], x[e], r, unused);
         y[e] = (uint16_t)(pack_bf(r, r) & 0xffffu);
     }
 }
@@ -170,11 +174,19 @@ exp2_f32_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n, i
         const Vec4 a = ld16<LNT>(x, i);
         Vec4 o;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) o.w[k] = as_u32(exp2_lane<KIND>(as_f32(a.w[k])));
+        for (int k = 0; k < 4; k += 2) {
+            float r0, r1;
+            exp2_pair<KIND>(as_f32(a.w[k]), as_f32(a.w[k + 1]), r0, r1);
+            o.w[k] = as_u32(r0);
+            o.w[k + 1] = as_u32(r1);
+        }
         st16<SNT>(y, i, o);
     }
-    for (int64_t e = (n4 << 2) + (int64_t)blockIdx.x * kBlock + threadIdx.x; e < n; e += stride)
-        y[e] = exp2_lane<KIND>(x[e]);
+    for (int64_t e = (n4 << 2) + (int64_t)blockIdx.x * kBlock + threadIdx.x; e < n; e += stride) {
+        float r, unused;
+        exp2_pair<KIND>(x[e], x[e], r, unused);
+        y[e] = r;
+    }
 }
 
 template <int KIND, bool BF_OUT>
@@ -297,6 +309,18 @@ extern "C" int launch_exp2_d3_f32(void* y, const void* x, int64_t size, void* st
 }
 extern "C" int launch_exp2_native_f32(void* y, const void* x, int64_t size, void* stream) {
     return launch_exp2<kExp2Native, false>(y, x, size, stream);
+}
+extern "C" int launch_exp2_pwl2_safe_f32_bf16(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2Pwl2Safe, true>(y, x, size, stream);
+}
+extern "C" int launch_exp2_pwl2_safe_f32(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2Pwl2Safe, false>(y, x, size, stream);
+}
+extern "C" int launch_exp2_pwl2_safe_f16_f32_bf16(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2Pwl2SafeF16, true>(y, x, size, stream);
+}
+extern "C" int launch_exp2_pwl2_safe_f16_f32(void* y, const void* x, int64_t size, void* stream) {
+    return launch_exp2<kExp2Pwl2SafeF16, false>(y, x, size, stream);
 }
 
 // ---- B3-D2 ----------------------------------------------------------------------

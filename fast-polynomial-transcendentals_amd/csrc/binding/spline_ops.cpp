@@ -1127,6 +1127,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "exp2 FA4 D3 fraction, FP32 out");
     m.def("exp2_native_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_native_f32, at::kFloat); },
           "exp2 with v_exp_f32, FP32 out");
+    m.def("exp2_pwl2_safe_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_safe_f32_bf16, at::kBFloat16); },
+          "B5 exp2: FP32 range reduction + PWL2 safe hinge (FP32), BF16 out");
+    m.def("exp2_pwl2_safe_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_safe_f32, at::kFloat); },
+          "B5 exp2 PWL2 safe hinge (FP32), FP32 out");
+    m.def("exp2_pwl2_safe_f16_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_safe_f16_f32_bf16, at::kBFloat16); },
+          "B5 exp2: FP32 range reduction + PWL2 safe hinge on the FP16 fraction (packed FP16), BF16 out");
+    m.def("exp2_pwl2_safe_f16_f32",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_safe_f16_f32, at::kFloat); },
+          "B5 exp2 PWL2 safe hinge on the FP16 fraction (packed FP16), FP32 out");
 
 #define PT_DEF_SINCOS(name, T, doc) \
     m.def(#name, [](at::Tensor a) { return sincos_table(a, launch_##name, T); }, doc)

@@ -93,12 +93,22 @@ __device__ __forceinline__ void softmax_exponents(const f32x16_t& acc, float sca
 // bits0..1), which the backward evaluates to route the same keys.
 template <int MODE, int ROUTE>
 __device__ __forceinline__ float softmax_exp2(float x, int i) {
-    if (ROUTE >= 4 && i % ROUTE < 4) {
-        if constexpr (MODE == kAttnSoftmaxExp2D2) return exp2_lane<kExp2D2>(x);
-        else if constexpr (MODE == kAttnSoftmaxExp2D3) return exp2_lane<kExp2D3>(x);
-        else if constexpr (MODE == kAttnSoftmaxExp2Pwl2) return exp2_lane<kExp2Pwl2>(x);
-    }
+    if constexpr (attn_has_exp2_program(MODE))
+        if (ROUTE >= 4 && i % ROUTE < 4) return exp2_lane<attn_exp2_kind<MODE>()>(x);
     return __builtin_amdgcn_exp2f(x);
+}
+
+// Two exponents, slots i (even) and i + 1: the routing groups of four start
+// at multiples of ROUTE (even), so one decision routes both, and the packed
+// FP16 program evaluates them with one instruction per step.
+template <int MODE, int ROUTE>
+__device__ __forceinline__ void softmax_exp2_pair(float x0, float x1, int i, float& y0, float& y1) {
+    if (ROUTE >= 4 && i % ROUTE < 4) {
+        exp2_pair<attn_exp2_kind<MODE>()>(x0, x1, y0, y1);
+    } else {
+        y0 = __builtin_amdgcn_exp2f(x0);
+        y1 = __builtin_amdgcn_exp2f(x1);
+    }
 }
 
 // Sigmoid-attention probabilities of two scores, before their rounding to
@@ -231,6 +241,18 @@ __device__ __forceinline__ bf16x8_t tile_probs8(const AttnParams& p, const f32x1
             sigmoid_prob2<MODE>(sacc[kt][r] * p.scale, sacc[kt][r + 1] * p.scale, p.sig_bias, pr[e], pr[e + 1]);
             pr[e] = key_masked<MASKED>(diag, kt, r) ? 0.0f : pr[e];
             pr[e + 1] = key_masked<MASKED>(diag, kt, r + 1) ? 0.0f : pr[e + 1];
+        }
+    } else if constexpr (MODE == kAttnSoftmaxExp2Pwl2SafeF16) {
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const int r = 8 * cc + e;
+            float ev0, ev1;
+            softmax_exp2_pair<MODE, ROUTE>(__builtin_fmaf(x[kt][r], sl, -m), __builtin_fmaf(x[kt][r + 1], sl, -m),
+                                           kt * 16 + r, ev0, ev1);
+            pr[e] = key_masked<MASKED>(diag, kt, r) ? 0.0f : ev0;
+            pr[e + 1] = key_masked<MASKED>(diag, kt, r + 1) ? 0.0f : ev1;
+            ls[e & 3] += pr[e];
+            ls[(e + 1) & 3] += pr[e + 1];
         }
     } else {
 #pragma unroll
@@ -537,6 +559,12 @@ extern "C" int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* ls
         case kAttnSoftmaxExp2D2: launch_routed<kAttnSoftmaxExp2D2>(prm, grid, hst, exp2_route, hd); break;
         case kAttnSoftmaxExp2D3: launch_routed<kAttnSoftmaxExp2D3>(prm, grid, hst, exp2_route, hd); break;
         case kAttnSoftmaxExp2Pwl2: launch_routed<kAttnSoftmaxExp2Pwl2>(prm, grid, hst, exp2_route, hd); break;
+        case kAttnSoftmaxExp2Pwl2Safe:
+            launch_routed<kAttnSoftmaxExp2Pwl2Safe>(prm, grid, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2Pwl2SafeF16:
+            launch_routed<kAttnSoftmaxExp2Pwl2SafeF16>(prm, grid, hst, exp2_route, hd);
+            break;
         case kAttnSoftcapNative: launch_fwd<kAttnSoftcapNative, 0>(prm, grid, hst, hd); break;
         case kAttnSoftcapD4: launch_fwd<kAttnSoftcapD4, 0>(prm, grid, hst, hd); break;
         case kAttnSigmoidNative: launch_fwd<kAttnSigmoidNative, 0>(prm, grid, hst, hd); break;

@@ -27,15 +27,28 @@ enum AttnMode : int {
     kAttnSigmoidD3 = 8,  // 8..11: BF16 sigmoid D3..D6 on bf16(s + bias)
     kAttnSigmoidD6 = 11,
     kAttnSoftmaxExp2Pwl2 = 12,
-    kAttnModes = 13,
+    kAttnSoftmaxExp2Pwl2Safe = 13,     // B5 PWL2 "safe" hinge, FP32
+    kAttnSoftmaxExp2Pwl2SafeF16 = 14,  // B5 PWL2 "safe" hinge, packed FP16 fraction
+    kAttnModes = 15,
 };
 
 constexpr bool attn_is_sigmoid(int mode) { return mode >= kAttnSigmoidNative && mode <= kAttnSigmoidD6; }
 constexpr bool attn_is_plain_softmax(int mode) {
-    return mode <= kAttnSoftmaxExp2D3 || mode == kAttnSoftmaxExp2Pwl2;
+    return mode <= kAttnSoftmaxExp2D3 || mode >= kAttnSoftmaxExp2Pwl2;
 }
 constexpr bool attn_has_exp2_program(int mode) {
-    return mode == kAttnSoftmaxExp2D2 || mode == kAttnSoftmaxExp2D3 || mode == kAttnSoftmaxExp2Pwl2;
+    return mode == kAttnSoftmaxExp2D2 || mode == kAttnSoftmaxExp2D3 || mode >= kAttnSoftmaxExp2Pwl2;
+}
+
+// The exp2 program of a softmax mode.
+template <int MODE>
+constexpr int attn_exp2_kind() {
+    return MODE == kAttnSoftmaxExp2D2            ? kExp2D2
+           : MODE == kAttnSoftmaxExp2D3          ? kExp2D3
+           : MODE == kAttnSoftmaxExp2Pwl2        ? kExp2Pwl2
+           : MODE == kAttnSoftmaxExp2Pwl2Safe    ? kExp2Pwl2Safe
+           : MODE == kAttnSoftmaxExp2Pwl2SafeF16 ? kExp2Pwl2SafeF16
+                                                 : kExp2Native;
 }
 
 constexpr int kHeadDim = 128;

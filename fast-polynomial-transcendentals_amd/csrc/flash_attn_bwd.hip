@@ -71,10 +71,6 @@ __device__ __forceinline__ int route_slot(int64_t key) {
     return 16 * (int)((key >> 5) & 1) + 4 * (int)((key >> 3) & 3) + (int)(key & 3);
 }
 
-template <int MODE>
-constexpr int exp2_kind() {
-    return MODE == kAttnSoftmaxExp2D2 ? kExp2D2 : MODE == kAttnSoftmaxExp2D3 ? kExp2D3 : kExp2Pwl2;
-}
 
 // Probability and gradient w.r.t. the raw dot product (q.k) of two scores
 // (two queries of one key, or two keys whose routing slots share a group of
@@ -92,12 +88,13 @@ __device__ __forceinline__ void score_grad2(const AttnBwdParams& p, float inv_ca
         const float sl = p.scale * kLog2e;
         const float x0 = __builtin_fmaf(a0, sl, -lse0), x1 = __builtin_fmaf(a1, sl, -lse1);
         if constexpr (attn_has_exp2_program(MODE) && ROUTE == 4) {
-            p0 = exp2_lane<exp2_kind<MODE>()>(x0);
-            p1 = exp2_lane<exp2_kind<MODE>()>(x1);
+            exp2_pair<attn_exp2_kind<MODE>()>(x0, x1, p0, p1);
         } else if constexpr (attn_has_exp2_program(MODE) && ROUTE > 4) {
             if (any_poly) {
-                p0 = poly ? exp2_lane<exp2_kind<MODE>()>(x0) : __builtin_amdgcn_exp2f(x0);
-                p1 = poly ? exp2_lane<exp2_kind<MODE>()>(x1) : __builtin_amdgcn_exp2f(x1);
+                float q0, q1;
+                exp2_pair<attn_exp2_kind<MODE>()>(x0, x1, q0, q1);
+                p0 = poly ? q0 : __builtin_amdgcn_exp2f(x0);
+                p1 = poly ? q1 : __builtin_amdgcn_exp2f(x1);
             } else {
                 p0 = __builtin_amdgcn_exp2f(x0);
                 p1 = __builtin_amdgcn_exp2f(x1);
@@ -877,6 +874,12 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
         case kAttnSoftmaxExp2D2: launch_bwd_routed<kAttnSoftmaxExp2D2>(prm, batch, hst, exp2_route, hd); break;
         case kAttnSoftmaxExp2D3: launch_bwd_routed<kAttnSoftmaxExp2D3>(prm, batch, hst, exp2_route, hd); break;
         case kAttnSoftmaxExp2Pwl2: launch_bwd_routed<kAttnSoftmaxExp2Pwl2>(prm, batch, hst, exp2_route, hd); break;
+        case kAttnSoftmaxExp2Pwl2Safe:
+            launch_bwd_routed<kAttnSoftmaxExp2Pwl2Safe>(prm, batch, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2Pwl2SafeF16:
+            launch_bwd_routed<kAttnSoftmaxExp2Pwl2SafeF16>(prm, batch, hst, exp2_route, hd);
+            break;
         case kAttnSoftcapNative: launch_bwd<kAttnSoftcapNative, kGradNatural, 0>(prm, batch, hst, hd); break;
         case kAttnSoftcapD4:
             if (grad == kGradAnalytical) launch_bwd<kAttnSoftcapD4, kGradAnalytical, 0>(prm, batch, hst, hd);

@@ -145,8 +145,22 @@ struct SoftcapConsts {
 // the continuous two-piece FP32 fraction of the full-range benchmark
 // (autonumerics_zero/cuda_benchmarks/benchmark_exp2_pwl2.cu:126-170):
 // p = 0.98946118 + 0.82085252 f + 0.34246066 max(f - 0.5, 0).
+// PWL2 "safe" is the endpoint-constrained hinge p = 1 + a f + c max(f - 1/2, 0)
+// with c = 2 (1 - a) (appendix_exp2.tex:22-27): p(0) = 1 and p(1) = 2, so
+// p >= 1 and the -127 clamp cannot wrap the exponent field.  FP32
+// (pwl2_safe): the sampled-minimax a = 0.7980513010317143, c =
+// 0.4038973979365714 (evidence/report-data/b5_exp2_softmax_constrained_fits.json,
+// two_piece_linear.sampled_minimax) rounded to FP32.  Packed FP16
+// (pwl2_safe_f16): a = 0.7978515625, c = 0.40380859375, the FP16 coefficients
+// of appendix_exp2.tex:72-76, on f rounded to FP16 (RNE); both endpoints stay
+// exact after FP16 rounding.  The FP16 core evaluates two lanes per
+// instruction: f16 = rne16(f); h = max(f16 - 1/2, 0) (v_pk_add_f16,
+// v_pk_max_f16); b = fma(f16, a, 1); p = fma(h, c, b) (v_pk_fma_f16, one
+// rounding each); p is widened to FP32 exactly for the exponent add.  FA4's
+// own 16-bit instruction sequence is not in the reference tree; this order is
+// the FP32 hinge's (fma(f, a, 1), then fma(hinge, c, .)).
 // Defined for x < 128 (softmax exponents are <= 0); -inf and NaN give +0
-// (D2, D3) or the value at the clamp (PWL2).
+// (D2, D3, the PWL2 safe programs) or the value at the clamp (PWL2).
 //
 // The PWL2 fraction starts below one (p(0) = 0.98946), so at n = -127 the
 // exponent field of (n << 23) + bits(p) wraps below zero and the bits are a
@@ -158,7 +172,21 @@ struct SoftcapConsts {
 // The programs agree with the reference's bit for bit on x >= -126.
 // ---------------------------------------------------------------------------
 
-enum Exp2Kind : int { kExp2D2 = 0, kExp2D3 = 1, kExp2Native = 2, kExp2Pwl2 = 3 };
+enum Exp2Kind : int {
+    kExp2D2 = 0,
+    kExp2D3 = 1,
+    kExp2Native = 2,
+    kExp2Pwl2 = 3,
+    kExp2Pwl2Safe = 4,
+    kExp2Pwl2SafeF16 = 5
+};
+
+struct Pwl2SafeConsts {
+    static constexpr float a = 0.7980513010317143f;
+    static constexpr float c = 0.4038973979365714f;
+    static constexpr float a16 = 0.7978515625f;   // 0x3A62
+    static constexpr float c16 = 0.40380859375f;  // 0x3676
+};
 
 template <int KIND>
 __device__ __forceinline__ float exp2_lane(float x) {
@@ -175,6 +203,9 @@ __device__ __forceinline__ float exp2_lane(float x) {
         } else if constexpr (KIND == kExp2Pwl2) {
             p = __builtin_fmaf(f, 0.820852518081665f, 0.9894611835479736f);
             p = __builtin_fmaf(__builtin_fmaxf(f - 0.5f, 0.0f), 0.34246066212654114f, p);
+        } else if constexpr (KIND == kExp2Pwl2Safe) {
+            p = __builtin_fmaf(f, Pwl2SafeConsts::a, 1.0f);
+            p = __builtin_fmaf(__builtin_fmaxf(f - 0.5f, 0.0f), Pwl2SafeConsts::c, p);
         } else {
             p = __builtin_fmaf(f, 0.077119089663028717041015625f, 0.227564394474029541015625f);
             p = __builtin_fmaf(p, f, 0.695146143436431884765625f);
@@ -182,6 +213,30 @@ __device__ __forceinline__ float exp2_lane(float x) {
         }
         const int n = (int)fl;  // v_cvt_i32_f32 (saturating)
         return as_f32(((uint32_t)n << 23) + as_u32(p));
+    }
+}
+
+// Two lanes of one program.  The packed FP16 PWL2 evaluates both fractions
+// with one instruction per step; every other program is exp2_lane per lane.
+template <int KIND>
+__device__ __forceinline__ void exp2_pair(float x0, float x1, float& y0, float& y1) {
+    if constexpr (KIND == kExp2Pwl2SafeF16) {
+        x0 = __builtin_fmaxf(x0, -127.0f);
+        x1 = __builtin_fmaxf(x1, -127.0f);
+        const float fl0 = __builtin_floorf(x0), fl1 = __builtin_floorf(x1);
+        const h2_t f = {(_Float16)(x0 - fl0), (_Float16)(x1 - fl1)};  // v_cvt_pk_f16_f32 (RNE)
+        const h2_t half = {(_Float16)0.5f, (_Float16)0.5f};
+        const h2_t zero = {(_Float16)0.0f, (_Float16)0.0f};
+        const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+        const h2_t a = {(_Float16)Pwl2SafeConsts::a16, (_Float16)Pwl2SafeConsts::a16};
+        const h2_t c = {(_Float16)Pwl2SafeConsts::c16, (_Float16)Pwl2SafeConsts::c16};
+        const h2_t hinge = __builtin_elementwise_max(f - half, zero);
+        const h2_t p = __builtin_elementwise_fma(hinge, c, __builtin_elementwise_fma(f, a, one));
+        y0 = as_f32(((uint32_t)(int)fl0 << 23) + as_u32((float)p.x));
+        y1 = as_f32(((uint32_t)(int)fl1 << 23) + as_u32((float)p.y));
+    } else {
+        y0 = exp2_lane<KIND>(x0);
+        y1 = exp2_lane<KIND>(x1);
     }
 }
 

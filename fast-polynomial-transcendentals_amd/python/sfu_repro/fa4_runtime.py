@@ -16,7 +16,9 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
   MI355X the automatic route keeps the hardware unit, which issues faster
   than any polynomial fraction); otherwise four of every ``exp2_emu_freq``
   exponents take the ``exp2_emu_backend`` program (``d3``: FA4 D3,
-  ``d2_safe``: the B5 D2 fraction, ``pwl2``: the two-piece hinge), key j
+  ``d2_safe``: the B5 D2 fraction, ``pwl2``: the two-piece hinge,
+  ``pwl2_safe``: the endpoint-constrained hinge in FP32, ``pwl2_safe_f16``:
+  the same hinge on the fraction rounded to FP16, packed FP16), key j
   when slot(j) % freq < 4 with slot(j) = 16 bit5(j) + 4 bits3..4(j) +
   bits0..1(j), in the forward and the backward alike;
 * softcap: ``softcap > 0`` with no score_mod -> FP32 hardware tanh; a
@@ -33,8 +35,8 @@ of the last, partial block are zeroed on chip (queries past the sequence get
 an infinite lse and a zero D in the backward), which is the arithmetic of
 operands zero-padded at the end, and nothing past the sequence is stored.
 
-Combinations whose programs are not part of the reference tree (the FP16 /
-BF16 / PWL1 exp2 variants, Sollya attention fits, mixed SFU/polynomial
+Combinations whose programs are not part of the reference tree (the other
+FP16 / BF16 exp2 variants and PWL1, Sollya attention fits, mixed SFU/polynomial
 sigmoid lanes, and the ``cute`` backends -- FA4's CuTe FP32 score programs,
 whose coefficients live in FA4) raise ``NotImplementedError`` naming what is
 missing.
@@ -61,6 +63,8 @@ MODE_SIGMOID_B3 = 6
 MODE_SIGMOID_B3_D2 = 7
 MODE_SIGMOID_D3 = 8  # 8..11: D3..D6
 MODE_SOFTMAX_PWL2 = 12
+MODE_SOFTMAX_PWL2_SAFE = 13
+MODE_SOFTMAX_PWL2_SAFE_F16 = 14
 
 # derivative programs (AttnGrad in flash_attn_bwd.hip)
 GRAD_NATURAL = 0
@@ -70,7 +74,8 @@ GRAD_EXACT_1MT2 = 3
 GRAD_ALGEBRAIC = 4
 GRAD_DIRECT = 5
 
-BUILT_EXP2_BACKENDS = {"d3": MODE_SOFTMAX_D3, "d2_safe": MODE_SOFTMAX_D2, "pwl2": MODE_SOFTMAX_PWL2}
+BUILT_EXP2_BACKENDS = {"d3": MODE_SOFTMAX_D3, "d2_safe": MODE_SOFTMAX_D2, "pwl2": MODE_SOFTMAX_PWL2,
+                       "pwl2_safe": MODE_SOFTMAX_PWL2_SAFE, "pwl2_safe_f16": MODE_SOFTMAX_PWL2_SAFE_F16}
 SUPPORTED_ROUTES = (0, 4, 6, 8, 10, 12, 16, 20, 24, 32)
 _SOFTCAP_BWD = {"analytical": GRAD_ANALYTICAL, "ste": GRAD_STE, "exact_1mt2": GRAD_EXACT_1MT2}
 

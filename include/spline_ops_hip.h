@@ -299,6 +299,23 @@ int launch_exp2_native_f32_bf16(void* y, const void* x, int64_t size, void* stre
 int launch_exp2_d2_f32(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_d3_f32(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_native_f32(void* y, const void* x, int64_t size, void* stream);
+/* B5 PWL2 "safe" hinge p(f) = 1 + a f + c max(f - 1/2, 0), c = 2 (1 - a),
+ * p(0) = 1, p(1) = 2 (extras/paper/manuscript/appendix_exp2.tex:22-27), on
+ * the same FP32 range reduction, -127 clamp and exponent add; the exp2
+ * backends `pwl2_safe` and `pwl2_safe_f16` of src/sfu_repro/fa4.py:33-46
+ * (`pwl2_safe_f16` is the public B5 candidate, fa4.py:739-743,
+ * configs/torchtitan/b5_pwl2_safe_f16.toml).  pwl2_safe: FP32 arithmetic,
+ * a = 0.7980513010, c = 0.4038973979 (sampled minimax, evidence/report-data/
+ * b5_exp2_softmax_constrained_fits.json).  pwl2_safe_f16: the fraction
+ * rounded to FP16 (RNE) and the hinge in packed FP16 (v_pk_add_f16,
+ * v_pk_max_f16, two v_pk_fma_f16: b = fma(f, a, 1), p = fma(h, c, b)) with
+ * a = 0.7978515625, c = 0.40380859375 (appendix_exp2.tex:72-76).  FA4's
+ * 16-bit instruction order is not in the reference tree; this one is the FP32
+ * hinge's. */
+int launch_exp2_pwl2_safe_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl2_safe_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl2_safe_f16_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl2_safe_f16_f32(void* y, const void* x, int64_t size, void* stream);
 
 /* ---- paired sin/cos tables: FP32 angles [size] -> out [2, size] ----------
  * Plane 0 holds cos, plane 1 sin.  Replaces launch_sincos_*_{bf16,fp16,f32}
@@ -460,9 +477,12 @@ int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k, con
  * sigmoid modes leave it untouched.  Extra modes:
  *   7 sigmoid attention with the B3-D2 exp2 program (fitted for S = 4096)
  *   8..11 sigmoid attention with the BF16 sigmoid D3..D6 program on
- *     bf16(s + sigmoid_bias)          12 softmax, PWL2 hinge exp2.
+ *     bf16(s + sigmoid_bias)          12 softmax, PWL2 hinge exp2
+ *   13 softmax, PWL2 "safe" hinge exp2 (FP32; FA4 backend pwl2_safe)
+ *   14 softmax, PWL2 "safe" hinge exp2 with the packed FP16 fraction (FA4
+ *     backend pwl2_safe_f16; the programs of launch_exp2_pwl2_safe*).
  * sigmoid_bias: the bias of the hardware and D3..D6 sigmoid modes.
- * exp2_route (modes 1, 2, 12): key j of a query row takes the polynomial when
+ * exp2_route (modes 1, 2, 12, 13, 14): key j of a query row takes the polynomial when
  * slot(j) % exp2_route < 4, else v_exp_f32, with slot(j) = 16 bit5(j) +
  * 4 bits3..4(j) + bits0..1(j) (the slot of j's exponent in the kernel's
  * registers), so four of every exp2_route exponents are routed; one of 4
@@ -507,7 +527,7 @@ int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* lse, const vo
  *              straight-through (ste) / 1 - T(u)^2 (exact_1mt2)
  *   4 / 5      mode 6 only: y (1 - y) (algebraic) / the B3 factored D4
  *              derivative (direct).
- * exp2_route (modes 1, 2, 12): 0 hardware exp2, 4 the polynomial everywhere,
+ * exp2_route (modes 1, 2, 12, 13, 14): 0 hardware exp2, 4 the polynomial everywhere,
  * 6..32 the polynomial for the keys the forward routes with that value
  * (FA4's exp2_emu_freq_bwd). */
 int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float* delta,

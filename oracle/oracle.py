@@ -255,7 +255,7 @@ def softcap_bwd_bf16(go: np.ndarray, s: np.ndarray, cap: float) -> np.ndarray:
     return g
 
 
-EXP2_D2, EXP2_D3, EXP2_PWL2 = 0, 1, 2
+EXP2_D2, EXP2_D3, EXP2_PWL2, EXP2_PWL2_SAFE, EXP2_PWL2_SAFE_F16 = 0, 1, 2, 3, 4
 
 
 def exp2(kind: int, x: np.ndarray, out_bf16: bool = True) -> np.ndarray:

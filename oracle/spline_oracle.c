@@ -722,12 +722,28 @@ static int32_t sat_i32(float v) {
     return (int32_t)v;
 }
 
+/* maxNum: a NaN operand yields the other operand (v_pk_max_f16). */
+static double h_max(double a, double b) {
+    if (isnan(a)) return b;
+    if (isnan(b)) return a;
+    return a > b ? a : b;
+}
+
 static float exp2_prog(int kind, float x) {
     x = fmaxf(x, -127.0f);
     float fl = floorf(x);
     float fr = x - fl;
     float p;
-    if (kind == 0) { /* D2 safe: appendix_exp2.tex:29-32 */
+    if (kind == 3) { /* PWL2 safe, FP32: appendix_exp2.tex:22-27, sampled-minimax a, c = 2(1 - a) */
+        p = fmaf(fr, 0.7980513010317143f, 1.0f);
+        p = fmaf(fmaxf(fr - 0.5f, 0.0f), 0.4038973979365714f, p);
+    } else if (kind == 4) { /* PWL2 safe, packed FP16: appendix_exp2.tex:72-76 */
+        const fmt_t* h = &FMT_F16;
+        double f16 = round_fmt((double)fr, h);
+        double hinge = h_max(h_add(f16, -0.5, h), 0.0);
+        double base = h_fma(f16, 0.7978515625, 1.0, h);
+        p = (float)h_fma(hinge, 0.40380859375, base, h);
+    } else if (kind == 0) { /* D2 safe: appendix_exp2.tex:29-32 */
         p = fmaf(fr, 0.33976602809999057f, 0.6602339719000094f);
         p = fmaf(p, fr, 1.0f);
     } else if (kind == 2) { /* two-piece hinge, benchmark_exp2_pwl2.cu:126-170 */
@@ -746,10 +762,11 @@ static float exp2_prog(int kind, float x) {
     return r;
 }
 
-/* kind: 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge.  out_bf16: BF16 bits into
- * y16, else FP32 into y32. */
+/* kind: 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge, 3 = PWL2 safe (FP32),
+ * 4 = PWL2 safe (packed FP16).  out_bf16: BF16 bits into y16, else FP32 into
+ * y32. */
 int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n) {
-    if (n < 0 || kind < 0 || kind > 2) return -1;
+    if (n < 0 || kind < 0 || kind > 4) return -1;
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
         float r = exp2_prog(kind, x[i]);

@@ -94,11 +94,16 @@ int orc_b3_exp2_d2_bf16(const uint16_t* x, uint16_t* y, uint16_t* dy, int64_t n,
 int orc_softcap_fwd_bf16(const uint16_t* s, uint16_t* y, int64_t n, float cap);
 int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int64_t n, float cap);
 
-/* ---- B5 exp2: kind 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge -----------------
+/* ---- B5 exp2: kind 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge, 3 = PWL2 safe
+ * (FP32), 4 = PWL2 safe (packed FP16) ---------------------------------------
  * The FP32 programs are pinned (p(0) = 1, p(1) = 2, the published fit and
  * error metrics); the deployed 16-bit output rounding is parity unpinned
  * (it lives in the absent FlashAttention-4): here one RNE of the FP32
- * result. */
+ * result.  Kind 4's FP16 core (f rounded to FP16, h = max(f - 1/2, 0),
+ * p = fma(h, c, fma(f, a, 1)), one FP16 rounding per step) is pinned by its
+ * published coefficients, its endpoints after FP16 rounding and its
+ * published maximum relative error (appendix_exp2.tex:72-76); FA4's own
+ * instruction order is not in the reference tree. */
 int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n);
 
 /* ---- paired sin/cos: prog 0 BF16 D3/D4, 1 BF16 D5/D6, 2 FP16 D3/D4,

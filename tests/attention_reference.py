@@ -12,8 +12,10 @@ import torch
 
 M = {"softmax_native": 0, "softmax_d2": 1, "softmax_d3": 2, "softcap_native": 3, "softcap_d4": 4,
      "sigmoid_native": 5, "sigmoid_b3": 6, "sigmoid_b3_d2": 7, "sigmoid_d3": 8, "sigmoid_d4": 9,
-     "sigmoid_d5": 10, "sigmoid_d6": 11, "softmax_pwl2": 12}
-EXP2_KIND = {"softmax_d2": 0, "softmax_d3": 1, "softmax_pwl2": 2}
+     "sigmoid_d5": 10, "sigmoid_d6": 11, "softmax_pwl2": 12, "softmax_pwl2_safe": 13,
+     "softmax_pwl2_safe_f16": 14}
+EXP2_KIND = {"softmax_d2": 0, "softmax_d3": 1, "softmax_pwl2": 2, "softmax_pwl2_safe": 3,
+             "softmax_pwl2_safe_f16": 4}
 LOG2E = 1.4426950408889634
 
 
@@ -42,7 +44,7 @@ def probs_and_grad(oracle, a, mode, grad, scale, cap, bias, lse2, route):
     """P and the derivative factor g of raw dot products a [B, H, Sq, Sk]
     (float32), as the kernel evaluates them."""
     shape = a.shape
-    if mode in ("softmax_native", "softmax_d2", "softmax_d3", "softmax_pwl2"):
+    if mode == "softmax_native" or mode in EXP2_KIND:
         x = a * np.float32(scale * LOG2E) - lse2[..., None]
         p = torch.exp2(x.double()).float()
         if mode in EXP2_KIND and route:

@@ -163,8 +163,11 @@ def test_forward_program_selection():
     assert sel(seqlen=256, exp2_emu_backend="d2_safe", exp2_emu_freq=12)[:2] == (rt.MODE_SOFTMAX_D2, 12)
     assert sel(seqlen=256, exp2_emu_backend="d3", exp2_emu_freq=4)[:2] == (rt.MODE_SOFTMAX_D3, 4)
     assert sel(seqlen=256, exp2_emu_backend="pwl2", exp2_emu_freq=8)[:2] == (rt.MODE_SOFTMAX_PWL2, 8)
-    with pytest.raises(NotImplementedError, match="pwl2_safe_f16"):
-        sel(seqlen=256, exp2_emu_backend="pwl2_safe_f16", exp2_emu_freq=12)
+    assert sel(seqlen=256, exp2_emu_backend="pwl2_safe", exp2_emu_freq=12)[:2] == (rt.MODE_SOFTMAX_PWL2_SAFE, 12)
+    assert sel(seqlen=256, exp2_emu_backend="pwl2_safe_f16", exp2_emu_freq=12)[:2] == \
+        (rt.MODE_SOFTMAX_PWL2_SAFE_F16, 12)
+    with pytest.raises(NotImplementedError, match="pwl1_safe_f16"):
+        sel(seqlen=256, exp2_emu_backend="pwl1_safe_f16", exp2_emu_freq=12)
     with pytest.raises(NotImplementedError, match="routing frequency 14"):
         sel(seqlen=256, exp2_emu_backend="d3", exp2_emu_freq=14)
     assert sel(seqlen=256, softcap=30.0) == (rt.MODE_SOFTCAP_NATIVE, 4, 30.0, 0.0)
@@ -196,6 +199,8 @@ def test_backward_program_selection():
     sel = rt.select_backward
     assert sel(seqlen=256) == (rt.MODE_SOFTMAX_NATIVE, rt.GRAD_NATURAL, 0, 1.0, 0.0)
     assert sel(seqlen=256, exp2_emu_backend="d2_safe", exp2_emu_freq=32)[:3] == (rt.MODE_SOFTMAX_D2, 0, 32)
+    assert sel(seqlen=256, exp2_emu_backend="pwl2_safe_f16", exp2_emu_freq=32)[:3] == \
+        (rt.MODE_SOFTMAX_PWL2_SAFE_F16, 0, 32)
     for mode_name, grad in (("analytical", rt.GRAD_ANALYTICAL), ("ste", rt.GRAD_STE),
                             ("exact_1mt2", rt.GRAD_EXACT_1MT2)):
         fwd = rt.create_softcap_scoremod_backend(30.0)

@@ -131,7 +131,7 @@ def test_c4_routed_swiglu_full(capi, oracle, cuda):
     assert_bits_equal(np.ascontiguousarray(gp[:, h:]).reshape(-1), want_gu, "bf16", "C4 bwd grad_up packed")
 
 
-@pytest.mark.parametrize("kind,name", [(0, "d2"), (1, "d3")])
+@pytest.mark.parametrize("kind,name", [(0, "d2"), (1, "d3"), (4, "pwl2_safe_f16")])
 def test_c5_exp2_full(capi, oracle, cuda, kind, name):
     """C5 B5: exp2 of FP32 logits [4, 32, 4096, 128]
     N(0, 4^2) minus the row max, BF16 out."""

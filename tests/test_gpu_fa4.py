@@ -57,6 +57,7 @@ CASES = [
     ("b2", "polynomial", "softcap_d4", 1, 0, 6.0),
     ("b5", "native", "softmax_native", 0, 0, 1.0),
     ("b5", "d2_safe", "softmax_d2", 0, 32, 1.0),
+    ("b5", "pwl2_safe_f16", "softmax_pwl2_safe_f16", 0, 32, 1.0),
 ]
 
 
@@ -133,9 +134,10 @@ def test_qk_norm_and_module_patching(cuda):
 
 
 def test_unbuilt_programs_fail_loudly(cuda):
-    module = build_fa4_module(b5_component_configs()["pwl2_safe_f16"], head_dim=128)
+    cfg = FA4Config(mode="softmax", exp2_emu_backend="pwl1_safe_f16", exp2_emu_freq=12, exp2_emu_freq_bwd=32)
+    module = build_fa4_module(cfg, head_dim=128)
     q, k, v, _ = _qkv(1, 1, 1, 128, 80)
-    with pytest.raises(NotImplementedError, match="pwl2_safe_f16"):
+    with pytest.raises(NotImplementedError, match="pwl1_safe_f16"):
         module(q.to(cuda), k.to(cuda), v.to(cuda))
     with pytest.raises(TypeError, match="bfloat16"):
         build_fa4_module(FA4Config(), head_dim=128)(q.half().to(cuda), k.half().to(cuda), v.half().to(cuda))
@@ -144,6 +146,7 @@ def test_unbuilt_programs_fail_loudly(cuda):
 @pytest.mark.parametrize("group,name,mode,grad,route_bwd,qmul", [
     ("b5", "native", "softmax_native", 0, 0, 1.0),
     ("b5", "d2_safe", "softmax_d2", 0, 32, 1.0),
+    ("b5", "pwl2_safe_f16", "softmax_pwl2_safe_f16", 0, 32, 1.0),
     ("b2", "polynomial", "softcap_d4", 1, 0, 6.0),
 ])
 def test_causal_lengths_off_the_block_grid(oracle, cuda, group, name, mode, grad, route_bwd, qmul):

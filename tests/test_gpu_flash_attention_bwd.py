@@ -87,6 +87,7 @@ def _close(got, ref, rel=2.5e-2):
 CASES = [
     ("softmax_native", 0, 0), ("softmax_d2", 0, 4), ("softmax_d2", 0, 32), ("softmax_d3", 0, 4),
     ("softmax_d3", 0, 12), ("softmax_pwl2", 0, 4), ("softmax_d2", 0, 6), ("softmax_pwl2", 0, 10),
+    ("softmax_pwl2_safe", 0, 4), ("softmax_pwl2_safe_f16", 0, 4), ("softmax_pwl2_safe_f16", 0, 32),
     ("softcap_native", 0, 0), ("softcap_d4", 1, 0),
     ("softcap_d4", 2, 0), ("softcap_d4", 3, 0), ("sigmoid_native", 0, 0), ("sigmoid_d3", 0, 0),
     ("sigmoid_d6", 0, 0),
@@ -254,7 +255,8 @@ def test_grouped_heads_need_the_partials_workspace(capi, cuda):
 
 
 @pytest.mark.parametrize("mode,route", [("softmax_pwl2", 4), ("softmax_pwl2", 10), ("softmax_d2", 4),
-                                        ("softmax_d3", 4)])
+                                        ("softmax_d3", 4), ("softmax_pwl2_safe", 4), ("softmax_pwl2_safe_f16", 4),
+                                        ("softmax_pwl2_safe_f16", 12)])
 def test_wide_score_range(capi, oracle, cuda, mode, route):
     """Scores spread over hundreds of log2 units, so many softmax exponents
     (against the row maximum forward, against lse backward) fall below
@@ -274,7 +276,7 @@ def test_wide_score_range(capi, oracle, cuda, mode, route):
     # 8 below the true one), the reference against the true maximum, so a
     # routed exponent's program error (PWL2 up to 1.05 % relative) can differ
     # by up to twice that between the two sums
-    bound = 2.5e-2 if mode == "softmax_pwl2" else 1e-2
+    bound = 2.5e-2 if mode.startswith("softmax_pwl2") else 1e-2
     assert (lse.cpu() - rl).abs().max().item() < bound
     dq, dk, dv, _ = bwd(capi, cuda, q, k, v, out, do, lse, mode, 0, True, scale, route=route)
     rq, rk, rv = reference_bwd(oracle, q, k, v, out, do, lse, mode, 0, True, scale, 30.0, route, 0.0)

@@ -237,6 +237,54 @@ def test_exp2_full_range_errors_match_published_metrics(oracle, kind, golden):
         assert abs(g - want) <= 2e-8 * max(1.0, want / 1e-4) + 1e-6 * want, (got, golden)
 
 
+def test_exp2_pwl2_safe_coefficients_endpoints_and_published_errors(oracle):
+    """B5 PWL2 "safe" hinge p(f) = 1 + a f + c max(f - 1/2, 0)
+    (extras/paper/manuscript/appendix_exp2.tex:22-27).
+
+    * The packed FP16 coefficients a = 0.7978515625, c = 0.40380859375
+      (appendix_exp2.tex:72-76) are the FP16 roundings of the FP32 sampled-
+      minimax fit (evidence/report-data/b5_exp2_softmax_constrained_fits.json,
+      two_piece_linear.sampled_minimax: a = 0.7980513010, c = 0.4038973979).
+    * Endpoints: p(0) = 1, so integers give exact powers of two; p(1) = 2
+      after FP16 rounding, so just below an integer n the FP16 program gives
+      exactly 2^n (the fraction rounds to 1.0 in FP16).
+    * Published maximum relative errors: the FP16 program 1.132e-2 ("after
+      rounding", appendix_exp2.tex:72-76: the fraction rounded to FP16 on the
+      fit's 1,000,001-point grid, against exact 2^f), the FP32 program the
+      sampled-minimax 1.0739475e-2 of the evidence file.  A dropped hinge, a
+      wrong coefficient or FP32 arithmetic in place of FP16 (1.081e-2) moves
+      them out of the stated digits.
+    """
+    f16 = lambda v: float(np.float16(v))
+    assert f16(0.7980513010317143) == 0.7978515625 and f16(0.4038973979365714) == 0.40380859375
+    n = np.arange(-126, 9, dtype=np.float32)
+    for kind in (oracle.EXP2_PWL2_SAFE, oracle.EXP2_PWL2_SAFE_F16):
+        assert np.array_equal(oracle.exp2(kind, n, False), np.exp2(n.astype(np.float64)).astype(np.float32))
+    below = np.nextafter(n[1:], np.float32(-np.inf)).astype(np.float32)
+    assert np.array_equal(oracle.exp2(oracle.EXP2_PWL2_SAFE_F16, below, False),
+                          np.exp2(n[1:].astype(np.float64)).astype(np.float32))
+    g = np.linspace(0.0, 1.0, 1_000_001)
+    x = g.astype(np.float32)
+    rel16 = np.abs(oracle.exp2(oracle.EXP2_PWL2_SAFE_F16, x, False) / np.exp2(g) - 1).max()
+    assert 1.1315e-2 <= rel16 < 1.1325e-2, rel16
+    rel32 = np.abs(oracle.exp2(oracle.EXP2_PWL2_SAFE, x, False) / np.exp2(x.astype(np.float64)) - 1).max()
+    assert abs(rel32 - 1.0739475e-2) < 2e-7, rel32
+    # the fraction is rounded to FP16 to nearest, ties to even: f = 1/2 +
+    # 1.5 ulp16 is a tie and rounds up to 1/2 + 2 ulp16 (RTZ would give + 1)
+    ulp = 2.0 ** -11
+    tie = oracle.exp2(oracle.EXP2_PWL2_SAFE_F16, np.array([0.5 + 1.5 * ulp, 0.5 + 2 * ulp], np.float32), False)
+    assert tie[0] == tie[1]
+    # p >= 1 keeps the exponent field from wrapping at the -127 clamp: masked
+    # (-inf), NaN and clamped exponents give +0, and [-127, -126] stays in
+    # [0, 2^-126]
+    low = np.array([-np.inf, -127.0, -1000.0, np.nan], dtype=np.float32)
+    edge = np.linspace(-127.0, -126.0, 4097, dtype=np.float32)
+    for kind in (oracle.EXP2_PWL2_SAFE, oracle.EXP2_PWL2_SAFE_F16):
+        assert oracle.exp2(kind, low, False).view(np.uint32).tolist() == [0, 0, 0, 0]
+        e = oracle.exp2(kind, edge, False)
+        assert np.isfinite(e).all() and (e >= 0).all() and (e <= 2.0 ** -126).all()
+
+
 # ---- sin/cos and RoPE -------------------------------------------------------------
 
 @pytest.mark.parametrize("prog,bound", [(0, 1.3e-2), (1, 9e-3), (2, 1e-2), (3, 1.5e-3), (4, 1.2e-3), (5, 1.2e-3)])
