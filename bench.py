@@ -65,10 +65,10 @@ def parse():
                    help="also write every row to this file, in the version-1 result envelope "
                         "(sfu_repro.artifact)")
     p.add_argument("--pmc-pass", action="store_true",
-                   help="counter pass: 4 launches each of the C1 B3 kernels (direct, hardware "
-                        "control, B3-D2), the C3 softcap (polynomial, hardware, copy) and the 2^28 "
-                        "sweep kernels, then 3 plain 256 MiB copies (torch copy_) as the "
-                        "byte-count calibration")
+                   help="counter pass: 4 launches each of every configuration's polynomial and "
+                        "hardware kernels (C1 B3, C2 SiLU, C3 softcap fwd/bwd and copy, C4 SwiGLU "
+                        "and its 2^28 equivalent, C5 exp2 and RoPE) and of the 2^28 sweep kernels, "
+                        "then 3 plain 256 MiB copies (torch copy_) as the byte-count calibration")
     p.add_argument("--pmc-probes", action="store_true",
                    help="counter pass over the sin/cos repeated-evaluation probes: each "
                         "polynomial and native probe of the bench launched 4 times")
@@ -346,7 +346,7 @@ def sweep(lib, reps: int, emit):
                     row[f"{label}_gbs"] = round(4 * n / ms / 1e6, 1)
                 row["poly_gelem_s"] = round(n / poly_ms / 1e6, 2)
                 row["native_gelem_s"] = round(n / nat_ms / 1e6, 2)
-                row["poly_frac_hbm_peak"] = round(row["poly_gbs"] / HBM_PEAK_GBS, 4)
+                row["poly_frac_8tbs"] = round(row["poly_gbs"] / HBM_PEAK_GBS, 4)
                 row["poly_frac_copy"] = round(copy_ms / poly_ms, 4)
                 row["speedup"] = round(nat_ms / poly_ms, 3)
                 if n_log2 in (20, 28):
@@ -377,7 +377,8 @@ def attention_rows(lib, reps: int, eager_launches: int = 0):
 def attention_rows_at(lib, reps: int, shape, eager_launches: int = 0):
     """The attention programs inside the fused forward and backward at the
     reference's component shape (causal GQA, B=1, S=4096, Hq=32, Hkv=8,
-    D=128; and D=64, its Llama 1B training model's head size): B5 softmax with the D2 / D3 exp2 (every exponent, and the B5
+    D=128; and D=64, its Llama 1B training model's head size): B5 softmax
+    with the D2 / D3 / packed-FP16 PWL2-safe exp2 (every exponent, and the B5
     schedule: four of every 12 forward, 32 backward) against hardware exp2,
     B2 softcap 30 with the D4 tanh (analytical backward) against hardware
     tanh, B3 sigmoid attention with the direct D3 / D4 programs against
@@ -434,11 +435,13 @@ def attention_rows_at(lib, reps: int, shape, eager_launches: int = 0):
 
     groups = [("fwd", "B5 softmax exp2", flops,
                [("poly_d2", fa(1, q)), ("poly_d3", fa(2, q)), ("poly_d2_route12", fa(1, q, 12)),
+                ("poly_pwl2_safe_f16_route12", fa(14, q, 12)), ("poly_pwl2_safe_f16", fa(14, q)),
                 ("native", fa(0, q))]),
               ("fwd", "B2 softcap 30", flops, [("poly_d4", fa(4, qs)), ("native", fa(3, qs))]),
               ("fwd", "B3 sigmoid attention", flops, [("poly_b3", fa(6, q)), ("native", fa(5, q))]),
               ("bwd", "B5 softmax exp2", 2.5 * flops,
-               [("poly_d2_route32", fa_bwd(1, 0, q, 12, 32)), ("native", fa_bwd(0, 0, q))]),
+               [("poly_d2_route32", fa_bwd(1, 0, q, 12, 32)),
+                ("poly_pwl2_safe_f16_route32", fa_bwd(14, 0, q, 12, 32)), ("native", fa_bwd(0, 0, q))]),
               ("bwd", "B2 softcap 30", 2.5 * flops,
                [("poly_d4_analytical", fa_bwd(4, 1, qs)), ("native", fa_bwd(3, 0, qs))]),
               ("bwd", "B3 sigmoid attention", 2.5 * flops,
@@ -660,27 +663,65 @@ def _launcher(lib, name, *args):
     return launch
 
 
-def _row(function, config, dtype, elements, alg_bytes, launches, reps):
-    """Time each (label, launch) and report us, Gelem/s, GB/s, HBM fraction."""
+MALL_BYTES = 256 << 20
+
+
+def cold_sets(in_bytes: int) -> int:
+    """Buffer sets a cold (HBM) row rotates through: together their inputs
+    exceed three times the 256 MiB MALL, so a set has been evicted by the
+    time its turn comes again and every launch streams from HBM."""
+    return max(2, -(-3 * MALL_BYTES // in_bytes))
+
+
+def _rotating(launches):
+    """One launch closure that cycles through `launches` (one per buffer
+    set); captured into a graph, the replay keeps the rotation."""
+    state = {"i": 0}
+
+    def launch():
+        fn = launches[state["i"] % len(launches)]
+        state["i"] += 1
+        fn()
+
+    launch.tensors = tuple(t for fn in launches for t in fn.tensors)
+    launch.sets = len(launches)
+    return launch
+
+
+def _reps_for(reps: int, sets: int) -> int:
+    """`reps` rounded up to whole rotations, so every replay starts at set 0
+    after the last set of the previous one."""
+    return -(-reps // sets) * sets
+
+
+def _row(function, config, dtype, elements, alg_bytes, launches, reps, regime="hbm"):
+    """Time each (label, launch) and report us, Gelem/s, GB/s, fraction of
+    8 TB/s.  regime: where the operands live across back-to-back launches --
+    "l2", "mall" (they fit the 256 MiB MALL and stay there) or "hbm" (larger
+    than the MALL, or rotated through enough buffer sets to be evicted); the
+    fraction of 8 TB/s is an HBM roofline figure only for "hbm" rows."""
     row = {"function": function, "config": config, "dtype": dtype, "elements": elements,
-           "bytes_per_launch": alg_bytes}
+           "bytes_per_launch": alg_bytes, "regime": regime}
     times = time_graphs_alternating([fn for _, fn in launches], reps)
     for (label, _), ms in zip(launches, times):
         row[f"{label}_us"] = round(ms * 1e3, 3)
         row[f"{label}_gelem_s"] = round(elements / ms / 1e6, 2)
         row[f"{label}_gbs"] = round(alg_bytes / ms / 1e6, 1)
     if "poly_gbs" in row:
-        row["poly_frac_hbm_peak"] = round(row["poly_gbs"] / HBM_PEAK_GBS, 4)
+        row["poly_frac_8tbs"] = round(row["poly_gbs"] / HBM_PEAK_GBS, 4)
     if "native_us" in row and "poly_us" in row:
         row["speedup"] = round(row["native_us"] / row["poly_us"], 3)
+    if "copy_us" in row and "poly_us" in row:
+        row["poly_frac_copy"] = round(row["copy_us"] / row["poly_us"], 3)
     return row
 
 
 def _summary(row):
     """The compact per-configuration entry of the headline line:
-    [polynomial us, native us (None without a native kernel), fraction of 8 TB/s]."""
+    [polynomial us, native us (None without a native kernel), fraction of
+    8 TB/s, regime]."""
     return [round(row["poly_us"], 2), round(row["native_us"], 2) if "native_us" in row else None,
-            round(row["poly_frac_hbm_peak"], 3)]
+            round(row["poly_frac_8tbs"], 3), row["regime"]]
 
 
 def _with_numerics(row, label, out, ref, where=None):
@@ -748,7 +789,7 @@ def config_rows(lib, reps: int, emit, headline=None):
     nat = _launcher(lib, "launch_flash_sigmoid_native_bf16", y, dy, s, n)
     d2 = _launcher(lib, "launch_flash_sigmoid_exp2_d2_bf16", y, dy, s, n)
     row = _row("b3_sigmoid", "C1 B3 2^20 U[-16,16] seed 0 (y, dy)", "bf16", n, 6 * n,
-               [("poly", poly), ("native", nat), ("poly_exp2_d2", d2)], reps)
+               [("poly", poly), ("native", nat), ("poly_exp2_d2", d2)], reps, "l2")
     ref_y = torch.sigmoid(s.float() - math.log(4096.0))
     ref_dy = ref_y * (1 - ref_y)
     # each program also over its fitted domain: B3's clamp |s| <= 6, the
@@ -765,42 +806,74 @@ def config_rows(lib, reps: int, emit, headline=None):
     summary["C1_b3"] = _summary(row)
     del s, y, dy, ref_y, ref_dy
 
-    # C2 / B1: FP16 [8192, 14336] N(0, 2^2) and the L2-resident [256, 4096].
+    # C2 / B1: FP16 [8192, 14336] N(0, 2^2) and the L2-resident
+    # [256, 4096].  The 235 MB input fits the MALL: the warm row (one buffer
+    # set, back to back) is a MALL figure; the cold row rotates buffer sets.
     gd = torch.Generator(device=dev).manual_seed(0)
-    for shape, tag in (((8192, 14336), "C2_silu"), ((256, 4096), "C2_silu_l2")):
-        x = (torch.randn(shape, device=dev, generator=gd) * 2).half()
-        yy = torch.empty_like(x)
-        n = x.numel()
-        r = big if n > (1 << 24) else reps
-        poly = _launcher(lib, "launch_swish_fwd_d3_kernel", yy, x, n)
-        nat = _launcher(lib, "launch_swish_fwd_native_kernel", yy, x, n)
-        row = _row("swish_fwd_d3", f"C2 B1 {list(shape)} N(0,2^2)", "fp16", n, 4 * n,
-                   [("poly", poly), ("native", nat)], r)
-        ref = torch.nn.functional.silu(x.float())
-        for label, fn in (("poly", poly), ("native", nat)):
-            fn()
-            _with_numerics(row, label, yy, ref)
-        emit(row)
-        summary[tag] = _summary(row)
-        if tag == "C2_silu":
-            go = torch.randn(shape, device=dev, generator=gd).half()
-            poly = _launcher(lib, "launch_swish_bwd_d3_kernel", yy, go, x, n)
-            nat = _launcher(lib, "launch_swish_bwd_native_kernel", yy, go, x, n)
-            row = _row("swish_bwd_d3", f"C2 B1 {list(shape)} grad_in = grad_out * silu'(x)", "fp16",
-                       n, 6 * n, [("poly", poly), ("native", nat)], r)
-            sg = torch.sigmoid(x.float())
-            ref = go.float() * sg * (1 + x.float() * (1 - sg))
-            for label, fn in (("poly", poly), ("native", nat)):
-                fn()
-                _with_numerics(row, label, yy, ref)
-            emit(row)
-            summary["C2_silu_bwd"] = _summary(row)
-            del go, sg
-        del x, yy, ref
-        torch.cuda.empty_cache()
+    shape = (8192, 14336)
+    n = shape[0] * shape[1]
+    sets = cold_sets(2 * n)
+    xs = [(torch.randn(shape, device=dev, generator=gd) * 2).half() for _ in range(sets)]
+    ys = [torch.empty_like(xs[0]) for _ in range(sets)]
+    x, yy = xs[0], ys[0]
+    cfg = f"C2 B1 {list(shape)} N(0,2^2)"
+    ref = torch.nn.functional.silu(x.float())
+    poly = _launcher(lib, "launch_swish_fwd_d3_kernel", yy, x, n)
+    nat = _launcher(lib, "launch_swish_fwd_native_kernel", yy, x, n)
+    row = _row("swish_fwd_d3", cfg, "fp16", n, 4 * n, [("poly", poly), ("native", nat)], big, "mall")
+    for label, fn in (("poly", poly), ("native", nat)):
+        fn()
+        _with_numerics(row, label, yy, ref)
+    emit(row)
+    summary["C2_silu_mall"] = _summary(row)
+    # "copy": the one-pass copy of the same tensors (the 1:1 stream ceiling at this size)
+    cold = [("poly", _rotating([_launcher(lib, "launch_swish_fwd_d3_kernel", o, i, n) for i, o in zip(xs, ys)])),
+            ("native", _rotating([_launcher(lib, "launch_swish_fwd_native_kernel", o, i, n)
+                                  for i, o in zip(xs, ys)])),
+            ("copy", _rotating([make_unary(lib, "spline_hip_copy16", o, i) for i, o in zip(xs, ys)]))]
+    row = _row("swish_fwd_d3", cfg + f" cold: {sets} buffer sets", "fp16", n, 4 * n, cold,
+               _reps_for(big, sets))
+    emit(row)
+    summary["C2_silu"] = _summary(row)
+    gos = [torch.randn(shape, device=dev, generator=gd).half() for _ in range(sets)]
+    go = gos[0]
+    poly = _launcher(lib, "launch_swish_bwd_d3_kernel", yy, go, x, n)
+    nat = _launcher(lib, "launch_swish_bwd_native_kernel", yy, go, x, n)
+    cfgb = f"C2 B1 {list(shape)} grad_in = grad_out * silu'(x)"
+    row = _row("swish_bwd_d3", cfgb, "fp16", n, 6 * n, [("poly", poly), ("native", nat)], big, "mall")
+    sg = torch.sigmoid(x.float())
+    ref = go.float() * sg * (1 + x.float() * (1 - sg))
+    for label, fn in (("poly", poly), ("native", nat)):
+        fn()
+        _with_numerics(row, label, yy, ref)
+    emit(row)
+    # "copy": the two-reads-per-write product x * grad_out (the 2:1 stream ceiling)
+    cold = [(label, _rotating([_launcher(lib, name, o, g_, i, n) for i, o, g_ in zip(xs, ys, gos)]))
+            for label, name in (("poly", "launch_swish_bwd_d3_kernel"), ("native", "launch_swish_bwd_native_kernel"))]
+    cold.append(("copy", _rotating([_launcher(lib, "launch_multiply_kernel", o, g_, i, n)
+                                    for i, o, g_ in zip(xs, ys, gos)])))
+    row = _row("swish_bwd_d3", cfgb + f" cold: {sets} buffer sets", "fp16", n, 6 * n, cold, _reps_for(big, sets))
+    emit(row)
+    summary["C2_silu_bwd"] = _summary(row)
+    del xs, ys, gos, x, yy, go, sg, ref, cold, poly, nat
+    torch.cuda.empty_cache()
+    x = (torch.randn(256, 4096, device=dev, generator=gd) * 2).half()
+    yy = torch.empty_like(x)
+    n = x.numel()
+    poly = _launcher(lib, "launch_swish_fwd_d3_kernel", yy, x, n)
+    nat = _launcher(lib, "launch_swish_fwd_native_kernel", yy, x, n)
+    row = _row("swish_fwd_d3", "C2 B1 [256, 4096] N(0,2^2)", "fp16", n, 4 * n,
+               [("poly", poly), ("native", nat)], reps, "l2")
+    ref = torch.nn.functional.silu(x.float())
+    for label, fn in (("poly", poly), ("native", nat)):
+        fn()
+        _with_numerics(row, label, yy, ref)
+    emit(row)
+    summary["C2_silu_l2"] = _summary(row)
+    del x, yy, ref
 
     # C3 / B2: softcap, graph-replay rows (the headline times the
-    # same forward kernels with plain back-to-back launches).
+    # same forward kernels with plain back-to-back launches).  1 GiB in: HBM.
     sc = c3_scores(dev)
     out = torch.empty_like(sc)
     n = sc.numel()
@@ -817,13 +890,15 @@ def config_rows(lib, reps: int, emit, headline=None):
     torch.cuda.empty_cache()
     go = torch.randn(C3_SHAPE, device=dev, generator=gd).bfloat16()
     bwd = _launcher(lib, "launch_softcap_tanh_d4_bwd_bf16", out, go, sc, n, C3_CAP)
+    bwd_nat = _launcher(lib, "launch_softcap_tanh_native_bwd_bf16", out, go, sc, n, C3_CAP)
     row = _row("softcap_tanh_d4_bwd", "C3 B2 [4,32,2048,2048] cap=30 grad_scores", "bf16", n, 6 * n,
-               [("poly", bwd)], big)
+               [("poly", bwd), ("native", bwd_nat)], big)
     t = torch.tanh(sc.float() / C3_CAP)
     ref = go.float() * (1 - t * t)
     del t
-    bwd()
-    _with_numerics(row, "poly", out, ref)
+    for label, fn in (("poly", bwd), ("native", bwd_nat)):
+        fn()
+        _with_numerics(row, label, out, ref)
     emit(row)
     summary["C3_softcap_bwd"] = _summary(row)
     if headline is not None:
@@ -833,15 +908,20 @@ def config_rows(lib, reps: int, emit, headline=None):
 
     # C4 / B4: routed SwiGLU, 64 experts x 128 tokens (Zipf(1.1)
     # ragged counts), hidden 2048, N(0, 1).  The activation is elementwise
-    # over [sum(counts), H].
+    # over [sum(counts), H]; 101 MB fits the MALL (warm rows), the cold rows
+    # rotate buffer sets, and a 2^28-element SwiGLU is the HBM-sized
+    # equivalent.
     p = np.arange(1, 65, dtype=np.float64) ** -1.1
     counts = np.random.default_rng(0).multinomial(64 * 128, p / p.sum())
     rows_total, h = int(counts.sum()), 2048
-    gate = torch.randn(rows_total, h, device=dev, generator=gd).bfloat16()
-    up = torch.randn(rows_total, h, device=dev, generator=gd).bfloat16()
-    go = torch.randn(rows_total, h, device=dev, generator=gd).bfloat16()
-    o, gg, gu = torch.empty_like(gate), torch.empty_like(gate), torch.empty_like(gate)
-    n = gate.numel()
+    n = rows_total * h
+    sets = cold_sets(4 * n)
+    gates = [torch.randn(rows_total, h, device=dev, generator=gd).bfloat16() for _ in range(sets)]
+    ups = [torch.randn(rows_total, h, device=dev, generator=gd).bfloat16() for _ in range(sets)]
+    gos = [torch.randn(rows_total, h, device=dev, generator=gd).bfloat16() for _ in range(sets)]
+    outs = [torch.empty_like(gates[0]) for _ in range(sets)]
+    gate, up, go, o = gates[0], ups[0], gos[0], outs[0]
+    gg, gu = torch.empty_like(gate), torch.empty_like(gate)
     cfg = f"C4 B4 experts=64 rows={rows_total} (max expert {int(counts.max())}) H=2048"
     sg = torch.sigmoid(gate.float())
     ref_fwd = gate.float() * sg * up.float()
@@ -849,19 +929,37 @@ def config_rows(lib, reps: int, emit, headline=None):
     ref_gg = go.float() * up.float() * sg * (1 + gate.float() * (1 - sg))
     poly = _launcher(lib, "launch_swish_mul_fwd_d3_kernel_bf16", o, gate, up, n)
     nat = _launcher(lib, "launch_swish_mul_fwd_native_kernel_bf16", o, gate, up, n)
-    row = _row("swish_mul_fwd_d3", cfg, "bf16", n, 6 * n, [("poly", poly), ("native", nat)], reps)
+    row = _row("swish_mul_fwd_d3", cfg, "bf16", n, 6 * n, [("poly", poly), ("native", nat)], reps, "mall")
     for label, fn in (("poly", poly), ("native", nat)):
         fn()
         _with_numerics(row, label, o, ref_fwd)
     emit(row)
+    summary["C4_swiglu_fwd_mall"] = _summary(row)
+    # "copy": the product gate * up, the same two-reads-per-write stream
+    cold = [(label, _rotating([_launcher(lib, name, oo, g_, u_, n) for g_, u_, oo in zip(gates, ups, outs)]))
+            for label, name in (("poly", "launch_swish_mul_fwd_d3_kernel_bf16"),
+                                ("native", "launch_swish_mul_fwd_native_kernel_bf16"),
+                                ("copy", "launch_multiply_kernel_bf16"))]
+    row = _row("swish_mul_fwd_d3", cfg + f" cold: {sets} buffer sets", "bf16", n, 6 * n, cold,
+               _reps_for(reps, sets))
+    emit(row)
     summary["C4_swiglu_fwd"] = _summary(row)
     poly = _launcher(lib, "launch_swish_mul_bwd_d3_kernel_bf16", gg, gu, go, gate, up, n)
     nat = _launcher(lib, "launch_swish_mul_bwd_native_kernel_bf16", gg, gu, go, gate, up, n)
-    row = _row("swish_mul_bwd_d3", cfg, "bf16", n, 10 * n, [("poly", poly), ("native", nat)], reps)
+    row = _row("swish_mul_bwd_d3", cfg, "bf16", n, 10 * n, [("poly", poly), ("native", nat)], reps, "mall")
     for label, fn in (("poly", poly), ("native", nat)):
         fn()
         _with_numerics(row, label + "_grad_gate", gg, ref_gg)
         _with_numerics(row, label + "_grad_up", gu, ref_gu)
+    emit(row)
+    # cold backward: grad_gate into the set's own output buffer, grad_up into
+    # the next set's (written, never read)
+    cold = [(label, _rotating([_launcher(lib, name, outs[i], outs[(i + 1) % sets], gos[i], gates[i], ups[i], n)
+                               for i in range(sets)]))
+            for label, name in (("poly", "launch_swish_mul_bwd_d3_kernel_bf16"),
+                                ("native", "launch_swish_mul_bwd_native_kernel_bf16"))]
+    row = _row("swish_mul_bwd_d3", cfg + f" cold: {sets} buffer sets", "bf16", n, 10 * n, cold,
+               _reps_for(reps, sets))
     emit(row)
     summary["C4_swiglu_bwd"] = _summary(row)
     packed = torch.cat((gate, up), -1)
@@ -869,50 +967,83 @@ def config_rows(lib, reps: int, emit, headline=None):
     poly = _launcher(lib, "launch_swish_mul_packed_fwd_d3_kernel_bf16", o, packed, rows_total, h)
     nat = _launcher(lib, "launch_swish_mul_packed_fwd_native_kernel_bf16", o, packed, rows_total, h)
     row = _row("swish_mul_packed_fwd_d3", cfg + " packed [rows,4096]", "bf16", n, 6 * n,
-               [("poly", poly), ("native", nat)], reps)
+               [("poly", poly), ("native", nat)], reps, "mall")
     for label, fn in (("poly", poly), ("native", nat)):
         fn()
         _with_numerics(row, label, o, ref_fwd)
     emit(row)
-    summary["C4_packed_fwd"] = _summary(row)
     poly = _launcher(lib, "launch_swish_mul_packed_bwd_d3_kernel_bf16", gp, go, packed, rows_total, h)
     nat = _launcher(lib, "launch_swish_mul_packed_bwd_native_kernel_bf16", gp, go, packed, rows_total, h)
     row = _row("swish_mul_packed_bwd_d3", cfg + " packed [rows,4096]", "bf16", n, 10 * n,
-               [("poly", poly), ("native", nat)], reps)
+               [("poly", poly), ("native", nat)], reps, "mall")
     for label, fn in (("poly", poly), ("native", nat)):
         fn()
         _with_numerics(row, label + "_grad_gate", gp[:, :h], ref_gg)
         _with_numerics(row, label + "_grad_up", gp[:, h:], ref_gu)
     emit(row)
-    summary["C4_packed_bwd"] = _summary(row)
-    del gate, up, go, o, gg, gu, packed, gp, sg, ref_fwd, ref_gu, ref_gg
+    del gates, ups, gos, outs, gate, up, go, o, gg, gu, packed, gp, sg, ref_fwd, ref_gu, ref_gg, cold, poly, nat
+    torch.cuda.empty_cache()
+    n = 1 << 28
+    gate = torch.randn(n, device=dev, generator=gd).bfloat16()
+    up = torch.randn(n, device=dev, generator=gd).bfloat16()
+    o, o2 = torch.empty_like(gate), torch.empty_like(gate)
+    cfg28 = "C4 B4 HBM equivalent: SwiGLU over 2^28 elements N(0,1)"
+    poly = _launcher(lib, "launch_swish_mul_fwd_d3_kernel_bf16", o, gate, up, n)
+    nat = _launcher(lib, "launch_swish_mul_fwd_native_kernel_bf16", o, gate, up, n)
+    prod = _launcher(lib, "launch_multiply_kernel_bf16", o, gate, up, n)
+    row = _row("swish_mul_fwd_d3", cfg28, "bf16", n, 6 * n, [("poly", poly), ("native", nat), ("copy", prod)], big)
+    emit(row)
+    summary["C4_swiglu_fwd_2^28"] = _summary(row)
+    go = torch.randn(n, device=dev, generator=gd).bfloat16()
+    poly = _launcher(lib, "launch_swish_mul_bwd_d3_kernel_bf16", o, o2, go, gate, up, n)
+    nat = _launcher(lib, "launch_swish_mul_bwd_native_kernel_bf16", o, o2, go, gate, up, n)
+    row = _row("swish_mul_bwd_d3", cfg28, "bf16", n, 10 * n, [("poly", poly), ("native", nat)], big)
+    emit(row)
+    summary["C4_swiglu_bwd_2^28"] = _summary(row)
+    del gate, up, o, o2, go, poly, nat
     torch.cuda.empty_cache()
 
     # C5 / B5: exp2 on FP32 logits [4, 32, 4096, 128] N(0, 4^2)
-    # minus the row max -> BF16.
-    lg = torch.randn(4, 32, 4096, 128, device=dev, generator=gd) * 4
-    lg = lg - lg.amax(-1, keepdim=True)
-    e = torch.empty(lg.shape, dtype=torch.bfloat16, device=dev)
-    n = lg.numel()
-    launches = [("poly", _launcher(lib, "launch_exp2_d2_f32_bf16", e, lg, n)),
-                ("poly_d3", _launcher(lib, "launch_exp2_d3_f32_bf16", e, lg, n)),
-                ("native", _launcher(lib, "launch_exp2_native_f32_bf16", e, lg, n))]
-    row = _row("exp2_d2", "C5 B5 [4,32,4096,128] FP32->BF16", "f32->bf16", n, 6 * n, launches, big)
+    # minus the row max -> BF16.  The 256 MiB input is the MALL's size: the
+    # warm row keeps part of it there, the cold row rotates buffer sets.
+    shape = (4, 32, 4096, 128)
+    n = 4 * 32 * 4096 * 128
+    sets = cold_sets(4 * n)
+    lgs = []
+    for _ in range(sets):
+        lg = torch.randn(shape, device=dev, generator=gd) * 4
+        lgs.append(lg - lg.amax(-1, keepdim=True))
+        del lg
+    es = [torch.empty(shape, dtype=torch.bfloat16, device=dev) for _ in range(sets)]
+    lg, e = lgs[0], es[0]
+    programs = (("poly", "launch_exp2_d2_f32_bf16"), ("poly_d3", "launch_exp2_d3_f32_bf16"),
+                ("poly_pwl2_safe_f16", "launch_exp2_pwl2_safe_f16_f32_bf16"),
+                ("native", "launch_exp2_native_f32_bf16"))
+    launches = [(label, _launcher(lib, name, e, lg, n)) for label, name in programs]
+    cfg = "C5 B5 [4,32,4096,128] FP32->BF16"
+    row = _row("exp2_d2", cfg, "f32->bf16", n, 6 * n, launches, big, "mall")
     ref = torch.exp2(lg)
     for label, fn in launches:
         fn()
         _with_numerics(row, label, e, ref)
     emit(row)
+    summary["C5_exp2_mall"] = _summary(row)
+    cold = [(label, _rotating([_launcher(lib, name, ee, ll, n) for ll, ee in zip(lgs, es)]))
+            for label, name in programs]
+    row = _row("exp2_d2", cfg + f" cold: {sets} buffer sets", "f32->bf16", n, 6 * n, cold, _reps_for(big, sets))
+    emit(row)
     summary["C5_exp2"] = _summary(row)
-    del lg, e, ref
+    del lgs, es, lg, e, ref, launches, cold
     torch.cuda.empty_cache()
 
     # C5 / RoPE: BF16 Q, K [4, 4096, 32, 128], theta 500000, positions 0..4095.
     b, sl, hh, d = 4, 4096, 32, 128
-    q = torch.randn(b, sl, hh, d, device=dev, generator=gd).bfloat16()
-    k = torch.randn(b, sl, hh, d, device=dev, generator=gd).bfloat16()
-    qo = torch.empty(b, hh, sl, d, dtype=torch.bfloat16, device=dev)
-    ko = torch.empty_like(qo)
+    sets = cold_sets(2 * 2 * b * sl * hh * d)
+    qs = [torch.randn(b, sl, hh, d, device=dev, generator=gd).bfloat16() for _ in range(sets)]
+    ks = [torch.randn(b, sl, hh, d, device=dev, generator=gd).bfloat16() for _ in range(sets)]
+    qos = [torch.empty(b, hh, sl, d, dtype=torch.bfloat16, device=dev) for _ in range(sets)]
+    kos = [torch.empty_like(qos[0]) for _ in range(sets)]
+    q, k, qo, ko = qs[0], ks[0], qos[0], kos[0]
     dims = torch.arange(0, d, 2, dtype=torch.float64)
     freq = 500000.0 ** (-dims / d)
     inc = torch.round(freq * (2.0 ** 32) / (2 * math.pi)).to(torch.int64).to(torch.int32).to(dev)
@@ -920,15 +1051,33 @@ def config_rows(lib, reps: int, emit, headline=None):
     n = q.numel() + k.numel()
     poly = _launcher(lib, "launch_rope_apply_fixed_half_turn_d5_d6_bf16", qo, ko, q, k, inc, b, sl, hh, hh, d)
     nat = _launcher(lib, "launch_rope_apply_native_bf16", qo, ko, q, k, fr, b, sl, hh, hh, d)
-    row = _row("rope_apply_d5_d6", "C5 RoPE Q,K [4,4096,32,128] theta=5e5", "bf16", n, 4 * n,
-               [("poly", poly), ("native", nat)], big)
+    cfg = "C5 RoPE Q,K [4,4096,32,128] theta=5e5"
+    row = _row("rope_apply_d5_d6", cfg, "bf16", n, 4 * n, [("poly", poly), ("native", nat)], big, "mall")
     ref_q = rope_reference(q, 500000.0)
     for label, fn in (("poly", poly), ("native", nat)):
         fn()
         _with_numerics(row, label + "_q", qo, ref_q)
     emit(row)
+    summary["C5_rope_mall"] = _summary(row)
+    # "copy": one-pass copies of Q and K (two launches, the 1:1 stream of the same bytes)
+    def _copies(q_, k_, qo_, ko_):
+        cq, ck = make_unary(lib, "spline_hip_copy16", qo_, q_), make_unary(lib, "spline_hip_copy16", ko_, k_)
+
+        def launch():
+            cq()
+            ck()
+        launch.tensors = cq.tensors + ck.tensors
+        return launch
+
+    cold = [("poly", _rotating([_launcher(lib, "launch_rope_apply_fixed_half_turn_d5_d6_bf16", qo_, ko_, q_, k_,
+                                          inc, b, sl, hh, hh, d) for q_, k_, qo_, ko_ in zip(qs, ks, qos, kos)])),
+            ("native", _rotating([_launcher(lib, "launch_rope_apply_native_bf16", qo_, ko_, q_, k_, fr, b, sl, hh,
+                                            hh, d) for q_, k_, qo_, ko_ in zip(qs, ks, qos, kos)])),
+            ("copy", _rotating([_copies(q_, k_, qo_, ko_) for q_, k_, qo_, ko_ in zip(qs, ks, qos, kos)]))]
+    row = _row("rope_apply_d5_d6", cfg + f" cold: {sets} buffer sets", "bf16", n, 4 * n, cold, _reps_for(big, sets))
+    emit(row)
     summary["C5_rope"] = _summary(row)
-    del q, k, qo, ko, ref_q
+    del qs, ks, qos, kos, q, k, qo, ko, ref_q, cold
     torch.cuda.empty_cache()
     return summary
 
@@ -965,11 +1114,17 @@ def stream_ceiling(lib, x, y, steps: int, warmup: int):
 
 
 def pmc_pass(lib):
-    """Counter pass (rocprofv3 --pmc): 3 eager launches of each
-    configuration's polynomial and native kernel (C1 B3, C2 SiLU, C3
-    softcap, C4 SwiGLU, C5 exp2 and RoPE), of the 2^28 sweep kernels and of
-    the one-pass copy, then 3 plain 256 MiB torch copy_ launches as the
-    byte-count calibration.  Prints the launch plan."""
+    """Counter pass (rocprofv3 --pmc): 4 eager launches (the first one warm)
+    of each configuration's polynomial and native kernels -- C1 B3 (direct,
+    hardware control, B3-D2), C2 SiLU fwd / bwd, C3 softcap fwd / bwd and
+    the copy of the same tensor, C4 SwiGLU fwd / bwd (separate and packed,
+    and the 2^28-element equivalent), C5 exp2 (D2, PWL2 safe FP16, hardware)
+    and RoPE -- and of the 2^28 sweep kernels, then 3 plain 256 MiB torch
+    copy_ launches as the byte-count calibration.  Prints the launch plan
+    (tag, elements, grid) so dispatches can be matched to configurations."""
+    import math
+
+    import numpy as np
     import torch
 
     dev = torch.device("cuda:0")
@@ -991,13 +1146,75 @@ def pmc_pass(lib):
                       ("C1 b3 exp2 d2", "launch_flash_sigmoid_exp2_d2_bf16")):
         run(tag, _launcher(lib, name, y, dy, s, s.numel()), s.numel())
     del s, y, dy
+    gd = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.randn(8192, 14336, device=dev, generator=gd) * 2).half()
+    yy, go = torch.empty_like(x), torch.randn(8192, 14336, device=dev, generator=gd).half()
+    n = x.numel()
+    run("C2 silu d3", _launcher(lib, "launch_swish_fwd_d3_kernel", yy, x, n), n)
+    run("C2 silu native", _launcher(lib, "launch_swish_fwd_native_kernel", yy, x, n), n)
+    run("C2 silu bwd d3", _launcher(lib, "launch_swish_bwd_d3_kernel", yy, go, x, n), n)
+    run("C2 silu bwd native", _launcher(lib, "launch_swish_bwd_native_kernel", yy, go, x, n), n)
+    del x, yy, go
+    torch.cuda.empty_cache()
     sc = c3_scores(dev)
     out = torch.empty_like(sc)
     n = sc.numel()
     run("C3 softcap d4", _launcher(lib, "launch_softcap_tanh_d4_bf16", out, sc, n, C3_CAP), n)
     run("C3 softcap native", _launcher(lib, "launch_softcap_tanh_native_bf16", out, sc, n, C3_CAP), n)
     run("C3 copy", make_unary(lib, "spline_hip_copy16", out, sc), n)
-    del sc, out
+    go = torch.randn(C3_SHAPE, device=dev, generator=gd).bfloat16()
+    run("C3 softcap d4 bwd", _launcher(lib, "launch_softcap_tanh_d4_bwd_bf16", out, go, sc, n, C3_CAP), n)
+    run("C3 softcap native bwd", _launcher(lib, "launch_softcap_tanh_native_bwd_bf16", out, go, sc, n, C3_CAP), n)
+    del sc, out, go
+    torch.cuda.empty_cache()
+    p = np.arange(1, 65, dtype=np.float64) ** -1.1
+    counts = np.random.default_rng(0).multinomial(64 * 128, p / p.sum())
+    rows_total, h = int(counts.sum()), 2048
+    for label, n_el in (("C4", rows_total * h), ("C4 2^28", 1 << 28)):
+        gate = torch.randn(n_el, device=dev, generator=gd).bfloat16()
+        up = torch.randn(n_el, device=dev, generator=gd).bfloat16()
+        go = torch.randn(n_el, device=dev, generator=gd).bfloat16()
+        o, o2 = torch.empty_like(gate), torch.empty_like(gate)
+        for prog in ("d3", "native"):
+            run(f"{label} swiglu {prog}", _launcher(lib, f"launch_swish_mul_fwd_{prog}_kernel_bf16", o, gate, up, n_el),
+                n_el)
+            run(f"{label} swiglu bwd {prog}",
+                _launcher(lib, f"launch_swish_mul_bwd_{prog}_kernel_bf16", o, o2, go, gate, up, n_el), n_el)
+        if label == "C4":
+            packed = torch.cat((gate.view(rows_total, h), up.view(rows_total, h)), -1)
+            gp = torch.empty_like(packed)
+            for prog in ("d3", "native"):
+                run(f"C4 packed swiglu {prog}",
+                    _launcher(lib, f"launch_swish_mul_packed_fwd_{prog}_kernel_bf16", o, packed, rows_total, h),
+                    n_el)
+                run(f"C4 packed swiglu bwd {prog}",
+                    _launcher(lib, f"launch_swish_mul_packed_bwd_{prog}_kernel_bf16", gp, go, packed, rows_total, h),
+                    n_el)
+            del packed, gp
+        del gate, up, go, o, o2
+        torch.cuda.empty_cache()
+    lg = torch.randn(4, 32, 4096, 128, device=dev, generator=gd) * 4
+    lg = lg - lg.amax(-1, keepdim=True)
+    e = torch.empty(lg.shape, dtype=torch.bfloat16, device=dev)
+    n = lg.numel()
+    for prog in ("d2", "pwl2_safe_f16", "native"):
+        run(f"C5 exp2 {prog}", _launcher(lib, f"launch_exp2_{prog}_f32_bf16", e, lg, n), n)
+    del lg, e
+    torch.cuda.empty_cache()
+    b, sl, hh, d = 4, 4096, 32, 128
+    q = torch.randn(b, sl, hh, d, device=dev, generator=gd).bfloat16()
+    k = torch.randn(b, sl, hh, d, device=dev, generator=gd).bfloat16()
+    qo = torch.empty(b, hh, sl, d, dtype=torch.bfloat16, device=dev)
+    ko = torch.empty_like(qo)
+    dims = torch.arange(0, d, 2, dtype=torch.float64)
+    freq = 500000.0 ** (-dims / d)
+    inc = torch.round(freq * (2.0 ** 32) / (2 * math.pi)).to(torch.int64).to(torch.int32).to(dev)
+    fr = freq.float().to(dev)
+    n = q.numel() + k.numel()
+    run("C5 rope d5 d6", _launcher(lib, "launch_rope_apply_fixed_half_turn_d5_d6_bf16", qo, ko, q, k, inc, b, sl, hh,
+                                   hh, d), n)
+    run("C5 rope native", _launcher(lib, "launch_rope_apply_native_bf16", qo, ko, q, k, fr, b, sl, hh, hh, d), n)
+    del q, k, qo, ko
     torch.cuda.empty_cache()
     n = 1 << 28
     g = torch.Generator(device=dev).manual_seed(28)
@@ -1196,9 +1413,9 @@ def main():
         cpu["torch_fp32_gelem_s"] = cpu_torch_native(sample, C3_CAP)["value"]
         line["cpu_baseline"] = cpu
     headline_summary = [round(ms_per_step * 1e3, 2), round(native_ms * 1e3, 2),
-                        round(achieved_gbs / HBM_PEAK_GBS, 3)]
+                        round(achieved_gbs / HBM_PEAK_GBS, 3), "hbm"]
     if not args.no_sweep:
-        line["configs_fields"] = ["poly_us", "native_us", "frac_hbm"]
+        line["configs_fields"] = ["poly_us", "native_us", "frac_8tbs", "regime"]
         line["configs"] = config_rows(lib, args.sweep_reps, emit, headline_summary)
         sweep(lib, args.sweep_reps, emit)
         for row in probe_rows(lib, args.sweep_reps):

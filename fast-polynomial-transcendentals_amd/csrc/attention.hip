@@ -125,6 +125,20 @@ struct SoftcapNativeOp {
     }
 };
 
+// Native backward baseline (FA4's softcap_backward_mode 'native',
+// src/sfu_repro/fa4.py:306-311): grad_out * (1 - tanh^2(s / cap)) in FP32
+// with the hardware tanh of SoftcapNativeOp, one RNE rounding to BF16.
+struct SoftcapNativeBwdOp {
+    static constexpr int NIN = 2, NOUT = 1;  // (grad_out, scores) -> grad_scores
+    static constexpr bool kParams = true;
+    __device__ __forceinline__ static void pair(const uint32_t (&a)[2], uint32_t (&b)[1],
+                                                const float (&prm)[2]) {
+        const float d0 = native_lane<kTanh, kBwd>(bf_lo(a[1]) * prm[1]);
+        const float d1 = native_lane<kTanh, kBwd>(bf_hi(a[1]) * prm[1]);
+        b[0] = pack_bf(bf_lo(a[0]) * d0, bf_hi(a[0]) * d1);
+    }
+};
+
 struct SoftcapBwdOp {
     static constexpr int NIN = 2, NOUT = 1;  // (grad_out, scores) -> grad_scores
     static constexpr bool kParams = true;
@@ -288,6 +302,15 @@ extern "C" int launch_softcap_tanh_d4_bwd_bf16(void* grad_scores, const void* gr
         return hipErrorInvalidValue;
     Streams<2, 1> s{{grad_out, scores}, {grad_scores}, {cap, 1.0f / cap}};
     return launch_pairwise<SoftcapBwdOp>(s, size, hs(stream));
+}
+
+extern "C" int launch_softcap_tanh_native_bwd_bf16(void* grad_scores, const void* grad_out,
+                                                   const void* scores, int64_t size, float cap,
+                                                   void* stream) {
+    if (bad_args(size, {grad_scores, grad_out, scores}) || !(cap > 0.0f && cap <= __FLT_MAX__))
+        return hipErrorInvalidValue;
+    Streams<2, 1> s{{grad_out, scores}, {grad_scores}, {cap, 1.0f / cap}};
+    return launch_pairwise<SoftcapNativeBwdOp>(s, size, hs(stream));
 }
 
 // ---- B5 exp2 ------------------------------------------------------------------

@@ -394,7 +394,9 @@ at::Tensor softcap_tanh_native_bf16(at::Tensor scores, double cap) {
     return softcap_fwd(scores, cap, launch_softcap_tanh_native_bf16);
 }
 
-at::Tensor softcap_tanh_bwd_bf16(at::Tensor grad_out, at::Tensor scores, double cap) {
+using SoftcapBwdLauncher = int (*)(void*, const void*, const void*, int64_t, float, void*);
+
+at::Tensor softcap_bwd(at::Tensor grad_out, at::Tensor scores, double cap, SoftcapBwdLauncher fn) {
     CHECK_CUDA(grad_out);
     CHECK_CUDA(scores);
     CHECK_CONTIGUOUS(grad_out);
@@ -407,11 +409,18 @@ at::Tensor softcap_tanh_bwd_bf16(at::Tensor grad_out, at::Tensor scores, double 
     c10::OptionalDeviceGuard guard(scores.device());
     at::Tensor g = at::empty_like(scores);
     void* s = current_stream(scores);
-    check_launch(launch_softcap_tanh_d4_bwd_bf16(g.data_ptr(), grad_out.data_ptr(),
-                                                 scores.data_ptr(), scores.numel(),
-                                                 static_cast<float>(cap), s),
+    check_launch(fn(g.data_ptr(), grad_out.data_ptr(), scores.data_ptr(), scores.numel(),
+                    static_cast<float>(cap), s),
                  s);
     return g;
+}
+
+at::Tensor softcap_tanh_bwd_bf16(at::Tensor grad_out, at::Tensor scores, double cap) {
+    return softcap_bwd(grad_out, scores, cap, launch_softcap_tanh_d4_bwd_bf16);
+}
+
+at::Tensor softcap_tanh_native_bwd_bf16(at::Tensor grad_out, at::Tensor scores, double cap) {
+    return softcap_bwd(grad_out, scores, cap, launch_softcap_tanh_native_bwd_bf16);
 }
 
 using Exp2Launcher = int (*)(void*, const void*, int64_t, void*);
@@ -1115,6 +1124,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("cap") = 30.0, "Native softcap baseline cap*tanh(s/cap) in FP32");
     m.def("softcap_tanh_bwd_bf16", &softcap_tanh_bwd_bf16, py::arg("grad_out"), py::arg("scores"),
           py::arg("cap") = 30.0, "B2 softcap gradient from the differentiated D4 program");
+    m.def("softcap_tanh_native_bwd_bf16", &softcap_tanh_native_bwd_bf16, py::arg("grad_out"),
+          py::arg("scores"), py::arg("cap") = 30.0,
+          "Native softcap gradient baseline grad_out * (1 - tanh^2(s/cap)) in FP32");
     m.def("exp2_d2_f32_to_bf16", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_f32_bf16, at::kBFloat16); },
           "B5 exp2: FP32 range reduction + D2 safe fraction, BF16 out");
     m.def("exp2_d3_f32_to_bf16", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d3_f32_bf16, at::kBFloat16); },

@@ -188,15 +188,17 @@ DeviceShape device_shape();
 //  * outputs of 64 MiB or more are stored non-temporally: they cannot stay
 //    in L2, and bypassing the MALL keeps it for the inputs (+12-15 % HBM
 //    throughput for a 1:1 read/write stream);
-//  * inputs larger than the MALL are also loaded non-temporally (+4 %);
-//    inputs that fit are loaded normally so repeated passes can hit the MALL.
+//  * inputs of the MALL's size or larger are also loaded non-temporally
+//    (+4 % above it; at exactly 256 MiB, streamed from HBM: 978 against
+//    998 ns per 2^20 FP32 exp2 inputs, 623 against 635 for FP16 SiLU);
+//    smaller inputs are loaded normally so repeated passes can hit the MALL.
 constexpr int64_t kNtStoreBytes = 64ll << 20;
 constexpr int64_t kMallBytes = 256ll << 20;
 
 enum NtMode : int { kNtNone = 0, kNtStore = 1, kNtBoth = 2 };
 
 inline int nt_mode(int64_t in_bytes, int64_t out_bytes) {
-    if (in_bytes > kMallBytes) return kNtBoth;
+    if (in_bytes >= kMallBytes) return kNtBoth;
     if (out_bytes >= kNtStoreBytes) return kNtStore;
     return kNtNone;
 }

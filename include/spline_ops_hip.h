@@ -286,6 +286,11 @@ int launch_softcap_tanh_d4_bwd_bf16(void* grad_scores, const void* grad_out, con
 /* Native baseline: cap * tanh(s / cap) in FP32 with v_exp_f32 / v_rcp_f32. */
 int launch_softcap_tanh_native_bf16(void* out, const void* scores, int64_t size, float cap,
                                     void* stream);
+/* Native backward baseline, FA4's softcap_backward_mode 'native'
+ * (src/sfu_repro/fa4.py:306-311): grad_scores = bf16(grad_out *
+ * (1 - tanh^2(s / cap))), tanh in FP32 with v_exp_f32 / v_rcp_f32. */
+int launch_softcap_tanh_native_bwd_bf16(void* grad_scores, const void* grad_out, const void* scores,
+                                        int64_t size, float cap, void* stream);
 
 /* ---- B5: exp2 with FP32 range reduction ---------------------------------
  * FA4's e2e_asm2 reduction (autonumerics_zero/cuda_benchmarks/

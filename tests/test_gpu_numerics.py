@@ -105,6 +105,20 @@ def softcap_case(capi, cuda, native):
     return errors(y, 30.0 * torch.tanh(x.double() / 30.0), x, central=30.0 * CENTRAL)
 
 
+def softcap_bwd_case(capi, cuda, native):
+    """The derivative factor itself (grad_out = 1) against 1 - tanh^2(s/cap)."""
+    import ctypes
+
+    x = _all_inputs("bf16", cuda)
+    go = torch.ones_like(x)
+    g = torch.empty_like(x)
+    name = "launch_softcap_tanh_native_bwd_bf16" if native else "launch_softcap_tanh_d4_bwd_bf16"
+    assert getattr(capi, name)(capi.ptr(g), capi.ptr(go), capi.ptr(x), ctypes.c_int64(x.numel()),
+                               ctypes.c_float(30.0), capi.stream()) == 0
+    torch.cuda.synchronize()
+    return errors(g, 1.0 - torch.tanh(x.double() / 30.0) ** 2, x, central=30.0 * CENTRAL)
+
+
 def b3_case(capi, cuda, which):
     x = _all_inputs("bf16", cuda)
     y, dy = torch.empty_like(x), torch.empty_like(x)
@@ -210,6 +224,11 @@ BOUNDS = {
     "gelu d6 bf16": {'max_abs': 2.7e+36, 'abs_central': 0.046, 'max_ulp': 15372, 'max_rel': 26.0},
     "softcap d4 bf16": {'max_abs': 0.41, 'abs_central': 0.41, 'max_ulp': 21, 'max_rel': 0.094},
     "softcap native bf16": {'max_abs': 0.063, 'abs_central': 0.063, 'max_ulp': 0, 'max_rel': 0.0036},
+    # the D4 derivative polynomial is zero where the forward saturates
+    # (|s| >= 2.609375 cap), where 1 - tanh^2 is small but not zero: hence the
+    # relative and ULP figures in the tail
+    "softcap d4 bwd bf16": {'max_abs': 0.086, 'abs_central': 0.086, 'max_ulp': 15533, 'max_rel': 3.5},
+    "softcap native bwd bf16": {'max_abs': 0.002, 'abs_central': 0.002, 'max_ulp': 1, 'max_rel': 0.004},
     "b3 direct bf16": {'abs_central': 0.033, 'max_ulp': 79, 'max_rel': 0.37, 'dy_abs_central': 0.026, 'dy_max_ulp': 67, 'dy_max_rel': 0.31},
     "b3 exp2_d2 bf16": {'abs_central': 0.057, 'max_ulp': 51, 'max_rel': 0.27, 'dy_abs_central': 0.03, 'dy_max_ulp': 30, 'dy_max_rel': 0.18},
     "b3 native bf16": {'abs_central': 0.002, 'max_ulp': 0, 'max_rel': 0.0038, 'dy_abs_central': 0.00049, 'dy_max_ulp': 1, 'dy_max_rel': 0.0038},
@@ -250,6 +269,11 @@ def test_unary_bounds(capi, cuda, fam, deg, fmt):
 @pytest.mark.parametrize("native", [False, True])
 def test_softcap_bounds(capi, cuda, native):
     _bound_check(f"softcap {'native' if native else 'd4'} bf16", softcap_case(capi, cuda, native))
+
+
+@pytest.mark.parametrize("native", [False, True])
+def test_softcap_backward_bounds(capi, cuda, native):
+    _bound_check(f"softcap {'native' if native else 'd4'} bwd bf16", softcap_bwd_case(capi, cuda, native))
 
 
 @pytest.mark.parametrize("which", ["direct", "exp2_d2", "native"])

@@ -239,9 +239,10 @@ def test_zero_size_and_bad_args(capi, cuda):
             rc = getattr(capi, name)(capi.ptr(s), capi.ptr(s), ctypes.c_int64(64), ctypes.c_float(cap),
                                      capi.stream())
             assert rc != 0, (name, cap)
-        rc = capi.launch_softcap_tanh_d4_bwd_bf16(capi.ptr(s), capi.ptr(s), capi.ptr(s), ctypes.c_int64(64),
-                                                  ctypes.c_float(cap), capi.stream())
-        assert rc != 0, cap
+        for name in ("launch_softcap_tanh_d4_bwd_bf16", "launch_softcap_tanh_native_bwd_bf16"):
+            rc = getattr(capi, name)(capi.ptr(s), capi.ptr(s), capi.ptr(s), ctypes.c_int64(64),
+                                     ctypes.c_float(cap), capi.stream())
+            assert rc != 0, (name, cap)
     # the attention softcap modes check cap before an empty batch returns
     strides = (ctypes.c_int64 * 12)(*([128 * 128, 128 * 128, 128] * 4))
     null = ctypes.c_void_p(0)
@@ -254,11 +255,11 @@ def test_zero_size_and_bad_args(capi, cuda):
             assert (rc == 0) == ok, (mode, cap, rc)
 
 
-@pytest.mark.parametrize("reps", [1024, 2056])
+@pytest.mark.parametrize("reps", [1024, 2047, 2048, 2056])
 @pytest.mark.parametrize("fmt", ["f16", "bf16"])
 def test_large_streaming_paths(capi, oracle, cuda, reps, fmt):
-    """Outputs >= 64 MiB take the non-temporal store path, inputs > 256 MiB
-    also non-temporal loads.  Tiling all 65536 patterns makes the expected
+    """Outputs >= 64 MiB take the non-temporal store path, inputs >= 256 MiB
+    (2048 tiles) also non-temporal loads.  Tiling all 65536 patterns makes the expected
     output the tiled oracle table (a size-independent check)."""
     x = torch.from_numpy(oracle.all_bits().view(np.int16)).to(cuda).repeat(reps)
     x = x.view(DTYPES[fmt])
