@@ -85,3 +85,37 @@ def test_reference_accuracy_checks_on_device(cuda):
     assert quadrant.tolist() == [0, 2, 3, 0, 1, 2]
     with pytest.raises(RuntimeError, match="1 to 8 coefficients"):
         polynomial_sincos(angles[:4], polynomial=SincosPolynomial(tuple([1.0] * 9), (1.0,), "x"))
+
+
+def test_device_evaluator_equals_the_reference_module(cuda):
+    """The device evaluator against the reference module's own CPU outputs
+    (tests/golden/rope_evaluator.json, written from
+    src/sfu_repro/rope/polynomial_sincos.py by
+    tests/golden/make_rope_evaluator_fixture.py): every cos / sin bit over
+    131,122 FP32 and FP64 angles, three coefficient sets, both reductions."""
+    import hashlib
+    import json
+    import os
+
+    from golden.make_rope_evaluator_fixture import angle_set
+
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "rope_evaluator.json")) as f:
+        doc = json.load(f)
+    polys = {"SOLLYA_D3_D4": SOLLYA_D3_D4, "UNIFORM_D5_D4": UNIFORM_D5_D4, "UNIFORM_D7_D6": UNIFORM_D7_D6}
+    angles = angle_set()
+
+    def canon(t):
+        a = t.cpu().numpy()
+        b = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).copy()
+        b[np.isnan(a)] = 0x7FC00000
+        return b
+
+    for case in doc["cases"]:
+        a = torch.from_numpy(angles.astype(case["dtype"])).to(cuda)
+        cos, sin = polynomial_sincos(a, polynomial=polys[case["polynomial"]], accurate_reduction=case["accurate"])
+        cb, sb = canon(cos), canon(sin)
+        what = (case["dtype"], case["polynomial"], case["accurate"])
+        assert cb[::doc["sample_step"]].tolist() == case["cos_sample"], what
+        assert sb[::doc["sample_step"]].tolist() == case["sin_sample"], what
+        assert hashlib.sha256(cb.tobytes()).hexdigest() == case["cos_sha256"], what
+        assert hashlib.sha256(sb.tobytes()).hexdigest() == case["sin_sha256"], what

@@ -98,3 +98,45 @@ def test_evaluator_refuses_host_tensors():
         polynomial_sincos(torch.zeros(4))
     with pytest.raises(TypeError, match="floating-point"):
         polynomial_sincos(torch.zeros(4, dtype=torch.int32))
+
+
+def _fixture():
+    import json
+    import os
+
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "rope_evaluator.json")) as f:
+        return json.load(f)
+
+
+def _canonical(a):
+    b = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).copy()
+    b[np.isnan(a)] = 0x7FC00000
+    return b
+
+
+def test_oracle_equals_the_reference_module_bit_for_bit(oracle):
+    """tests/golden/rope_evaluator.json holds the reference module's own
+    outputs (src/sfu_repro/rope/polynomial_sincos.py run on CPU torch by
+    tests/golden/make_rope_evaluator_fixture.py) for FP32 and FP64 angles, the
+    three coefficient sets and both reductions; the oracle reproduces every
+    cos and sin bit pattern (SHA-256 over 131,122 angles, plus sampled
+    values for a readable diff)."""
+    import hashlib
+
+    from golden.make_rope_evaluator_fixture import angle_set
+
+    doc = _fixture()
+    angles = angle_set()
+    assert angles.size == doc["count"] and len(doc["cases"]) == 12
+    polys = {"SOLLYA_D3_D4": SOLLYA_D3_D4, "UNIFORM_D5_D4": UNIFORM_D5_D4, "UNIFORM_D7_D6": UNIFORM_D7_D6}
+    step = doc["sample_step"]
+    with np.errstate(over="ignore", invalid="ignore"):
+        for case in doc["cases"]:
+            poly = polys[case["polynomial"]]
+            cos, sin = _ref(oracle, angles.astype(case["dtype"]), poly, case["accurate"])
+            cb, sb = _canonical(cos), _canonical(sin)
+            what = (case["dtype"], case["polynomial"], case["accurate"])
+            assert cb[::step].tolist() == case["cos_sample"], what
+            assert sb[::step].tolist() == case["sin_sample"], what
+            assert hashlib.sha256(cb.tobytes()).hexdigest() == case["cos_sha256"], what
+            assert hashlib.sha256(sb.tobytes()).hexdigest() == case["sin_sha256"], what
