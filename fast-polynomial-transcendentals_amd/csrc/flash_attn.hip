@@ -319,8 +319,19 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
 // RAGGED: S is not a multiple of 128, so the last query block and the last
 // key tile hold rows past the sequence, or keys from kv_len on are padding
 // (a separate instantiation keeps those guards out of the aligned kernels).
+// Waves per SIMD the register allocation is held to: 2 (up to 256 VGPRs).
+// The head_dim-64 kernels fit three 4-wave blocks per CU (<= 168 VGPRs)
+// by themselves, except the packed FP16 PWL2 exp2, whose packed pairs keep
+// more values live (170 VGPRs at route 12): it is held to 3 where that costs
+// no spill (routes above 8; at 4 and 8 it would spill 2-17 registers).
+template <int MODE, int ROUTE, int HD>
+constexpr int fwd_waves_per_eu() {
+    return HD == 64 && MODE == kAttnSoftmaxExp2Pwl2SafeF16 && ROUTE > 8 ? 3 : 2;
+}
+
 template <int MODE, int ROUTE, int HD, int W, bool RAGGED>
-__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) flash_fwd_kernel(AttnParams p) {
+__global__ void __launch_bounds__(64 * W)
+    __attribute__((amdgpu_waves_per_eu(fwd_waves_per_eu<MODE, ROUTE, HD>()))) flash_fwd_kernel(AttnParams p) {
     constexpr int kBlockQ = 32 * W;  // queries per block
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kKStr = HD + 8;
