@@ -229,7 +229,8 @@ def test_rejected_backward_arguments(capi, cuda):
     assert call(6, 4) != 0          # B3 outside its fitted length
     assert call(1, 0, route=7) != 0  # unsupported routing
     assert call(4, 1, cap=0.0) != 0
-    assert call(13, 0) != 0
+    assert call(15, 0) != 0         # past the last mode (14)
+    assert call(-1, 0) != 0
     assert call(0, 0) == 0
     torch.cuda.synchronize()
 
