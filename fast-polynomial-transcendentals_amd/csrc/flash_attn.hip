@@ -58,9 +58,11 @@ struct AttnParams {
     int causal;
 };
 
-// Softmax exponents x = s * log2(e) of 16 accumulator registers (one
-// 32-key tile), with the softcap transform where the mode has one.  The D4
-// program runs on BF16 pairs: u = bf16(bf16(s) * (1/cap)),
+// Softmax scores of 16 accumulator registers (one 32-key tile), in the
+// units the caller's exponent FMA scales by sl: the raw dot products for
+// plain softmax (sl = scale * log2 e), the capped score y for the softcap
+// modes (sl = log2 e, so the product by log2 e is the exponent FMA's own).
+// The D4 program runs on BF16 pairs: u = bf16(bf16(s) * (1/cap)),
 // y = bf16(cap * TANH_D4_BF16(u)), the B2 program on the BF16 score.
 template <int MODE>
 __device__ __forceinline__ void softmax_exponents(const f32x16_t& acc, float scale, float cap,
@@ -71,13 +73,13 @@ __device__ __forceinline__ void softmax_exponents(const f32x16_t& acc, float sca
             const uint32_t u = pack_bf(rbf(acc[r] * scale) * inv_cap, rbf(acc[r + 1] * scale) * inv_cap);
             float t0, t1;
             SoftcapConsts::T::eval2(u, t0, t1);
-            x[r] = rbf(t0 * cap) * kLog2e;
-            x[r + 1] = rbf(t1 * cap) * kLog2e;
+            x[r] = rbf(t0 * cap);
+            x[r + 1] = rbf(t1 * cap);
         }
     } else if constexpr (MODE == kAttnSoftcapNative) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-            x[r] = cap * native_lane<kTanh, kFwd>(acc[r] * scale * inv_cap) * kLog2e;
+            x[r] = cap * native_lane<kTanh, kFwd>(acc[r] * scale * inv_cap);
     } else {
         const float sl = scale * kLog2e;
 #pragma unroll
@@ -302,7 +304,7 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
     tile_scores<HD, !fwd_program_heavy<MODE>()>(ks, qf, sacc, h, c32);
     float x[2][16];
     float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float sl = attn_is_plain_softmax(MODE) ? p.scale * kLog2e : 1.0f;
+    const float sl = attn_is_plain_softmax(MODE) ? p.scale * kLog2e : kLog2e;
     tile_softmax_state<MODE, MASKED, HD>(p, sacc, x, oacc, m, l, diag, inv_cap, sl);
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)

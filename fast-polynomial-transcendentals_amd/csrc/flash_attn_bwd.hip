@@ -108,16 +108,16 @@ __device__ __forceinline__ void score_grad2(const AttnBwdParams& p, float inv_ca
     } else if constexpr (MODE == kAttnSoftcapNative) {
         const float t0 = native_lane<kTanh, kFwd>(a0 * p.scale * inv_cap);
         const float t1 = native_lane<kTanh, kFwd>(a1 * p.scale * inv_cap);
-        p0 = __builtin_amdgcn_exp2f(p.cap * t0 * kLog2e - lse0);
-        p1 = __builtin_amdgcn_exp2f(p.cap * t1 * kLog2e - lse1);
+        p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(p.cap * t0, kLog2e, -lse0));
+        p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(p.cap * t1, kLog2e, -lse1));
         ds0 = p0 * (dp0 - dl0) * (1.0f - t0 * t0) * p.scale;
         ds1 = p1 * (dp1 - dl1) * (1.0f - t1 * t1) * p.scale;
     } else if constexpr (MODE == kAttnSoftcapD4) {
         const uint32_t u = pack_bf(rbf(a0 * p.scale) * inv_cap, rbf(a1 * p.scale) * inv_cap);
         float t0, t1;
         SoftcapConsts::T::eval2(u, t0, t1);
-        p0 = __builtin_amdgcn_exp2f(rbf(t0 * p.cap) * kLog2e - lse0);
-        p1 = __builtin_amdgcn_exp2f(rbf(t1 * p.cap) * kLog2e - lse1);
+        p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(rbf(t0 * p.cap), kLog2e, -lse0));
+        p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(rbf(t1 * p.cap), kLog2e, -lse1));
         float g0 = 1.0f, g1 = 1.0f;
         if constexpr (GRAD == kGradAnalytical) {
             const uint32_t t2 = u & 0x7fff7fffu;
