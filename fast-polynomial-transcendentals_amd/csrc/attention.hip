@@ -346,6 +346,23 @@ extern "C" int launch_exp2_pwl2_safe_f16_f32(void* y, const void* x, int64_t siz
     return launch_exp2<kExp2Pwl2SafeF16, false>(y, x, size, stream);
 }
 
+// The remaining FA4 exp2 backends (src/sfu_repro/fa4.py:33-46).
+#define PT_EXP2_ENTRY(NAME, KIND)                                                                   \
+    extern "C" int launch_exp2_##NAME##_f32_bf16(void* y, const void* x, int64_t size, void* stream) { \
+        return launch_exp2<KIND, true>(y, x, size, stream);                                        \
+    }                                                                                              \
+    extern "C" int launch_exp2_##NAME##_f32(void* y, const void* x, int64_t size, void* stream) {      \
+        return launch_exp2<KIND, false>(y, x, size, stream);                                       \
+    }
+PT_EXP2_ENTRY(pwl1_safe, kExp2Pwl1Safe)
+PT_EXP2_ENTRY(pwl1_safe_f16, kExp2Pwl1SafeF16)
+PT_EXP2_ENTRY(pwl2_safe_bf16, kExp2Pwl2SafeBF16)
+PT_EXP2_ENTRY(d2_safe_noclamp, kExp2D2NoClamp)
+PT_EXP2_ENTRY(d2_safe_f16, kExp2D2SafeF16)
+PT_EXP2_ENTRY(d2_safe_bf16, kExp2D2SafeBF16)
+PT_EXP2_ENTRY(pwl2_f16, kExp2Pwl2F16)
+#undef PT_EXP2_ENTRY
+
 // ---- B3-D2 ----------------------------------------------------------------------
 
 extern "C" int launch_flash_sigmoid_exp2_d2_bf16(void* y, void* dy, const void* scores,

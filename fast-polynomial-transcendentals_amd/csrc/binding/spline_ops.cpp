@@ -1150,6 +1150,41 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("exp2_pwl2_safe_f16_f32",
           [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_safe_f16_f32, at::kFloat); },
           "B5 exp2 PWL2 safe hinge on the FP16 fraction (packed FP16), FP32 out");
+    m.def("exp2_pwl1_safe_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl1_safe_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction + D1 safe line 1 + f (FP32), BF16 out");
+    m.def("exp2_pwl1_safe_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl1_safe_f32, at::kFloat); },
+          "exp2: FP32 range reduction + D1 safe line 1 + f (FP32), FP32 out");
+    m.def("exp2_pwl1_safe_f16_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl1_safe_f16_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction + D1 safe line on the FP16 fraction, BF16 out");
+    m.def("exp2_pwl1_safe_f16_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl1_safe_f16_f32, at::kFloat); },
+          "exp2: FP32 range reduction + D1 safe line on the FP16 fraction, FP32 out");
+    m.def("exp2_pwl2_safe_bf16_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_safe_bf16_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction + PWL2 safe hinge in BF16, BF16 out");
+    m.def("exp2_pwl2_safe_bf16_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_safe_bf16_f32, at::kFloat); },
+          "exp2: FP32 range reduction + PWL2 safe hinge in BF16, FP32 out");
+    m.def("exp2_d2_safe_noclamp_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_safe_noclamp_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction + D2 safe fraction, no -127 clamp, BF16 out");
+    m.def("exp2_d2_safe_noclamp_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_safe_noclamp_f32, at::kFloat); },
+          "exp2: FP32 range reduction + D2 safe fraction, no -127 clamp, FP32 out");
+    m.def("exp2_d2_safe_f16_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_safe_f16_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction + D2 safe fraction in packed FP16, BF16 out");
+    m.def("exp2_d2_safe_f16_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_safe_f16_f32, at::kFloat); },
+          "exp2: FP32 range reduction + D2 safe fraction in packed FP16, FP32 out");
+    m.def("exp2_d2_safe_bf16_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_safe_bf16_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction + D2 safe fraction in BF16, BF16 out");
+    m.def("exp2_d2_safe_bf16_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_d2_safe_bf16_f32, at::kFloat); },
+          "exp2: FP32 range reduction + D2 safe fraction in BF16, FP32 out");
+    m.def("exp2_pwl2_f16_f32_to_bf16",
+          [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_f16_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction + the reference's FP16 hinge (FractionalPwl2Hinge), BF16 out");
+    m.def("exp2_pwl2_f16_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_f16_f32, at::kFloat); },
+          "exp2: FP32 range reduction + the reference's FP16 hinge (FractionalPwl2Hinge), FP32 out");
 
 #define PT_DEF_SINCOS(name, T, doc) \
     m.def(#name, [](at::Tensor a) { return sincos_table(a, launch_##name, T); }, doc)

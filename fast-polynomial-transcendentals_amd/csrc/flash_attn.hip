@@ -244,7 +244,7 @@ __device__ __forceinline__ bf16x8_t tile_probs8(const AttnParams& p, const f32x1
             pr[e] = key_masked<MASKED>(diag, kt, r) ? 0.0f : pr[e];
             pr[e + 1] = key_masked<MASKED>(diag, kt, r + 1) ? 0.0f : pr[e + 1];
         }
-    } else if constexpr (MODE == kAttnSoftmaxExp2Pwl2SafeF16) {
+    } else if constexpr (exp2_is_f16(attn_exp2_kind<MODE>())) {
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
             const int r = 8 * cc + e;
@@ -323,12 +323,13 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
 // (a separate instantiation keeps those guards out of the aligned kernels).
 // Waves per SIMD the register allocation is held to: 2 (up to 256 VGPRs).
 // The head_dim-64 kernels fit three 4-wave blocks per CU (<= 168 VGPRs)
-// by themselves, except the packed FP16 PWL2 exp2, whose packed pairs keep
-// more values live (170 VGPRs at route 12): it is held to 3 where that costs
-// no spill (routes above 8; at 4 and 8 it would spill 2-17 registers).
+// by themselves, except the packed FP16 exp2 programs, whose packed pairs
+// keep more values live (170 VGPRs for the PWL2 hinge at route 12): they are
+// held to 3 where that costs no spill (routes above 8; at 4 and 8 the hinge
+// would spill 2-17 registers).
 template <int MODE, int ROUTE, int HD>
 constexpr int fwd_waves_per_eu() {
-    return HD == 64 && MODE == kAttnSoftmaxExp2Pwl2SafeF16 && ROUTE > 8 ? 3 : 2;
+    return HD == 64 && exp2_is_f16(attn_exp2_kind<MODE>()) && ROUTE > 8 ? 3 : 2;
 }
 
 template <int MODE, int ROUTE, int HD, int W, bool RAGGED>
@@ -503,12 +504,22 @@ void launch_fwd_shape(const AttnParams& prm, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, HD, W, true>), grid, dim3(64 * W), 0, st, prm);
 }
 
+// An odd number of 128-query blocks takes 4-wave blocks at head_dim 128,
+// except for the packed FP16 exp2 programs: their 4-wave kernels would spill
+// (both lanes of each packed pair stay live: up to 17 registers at routes 4
+// and 6), so they run the 8-wave ragged kernel, whose last block holds 128
+// queries past the sequence that load the last row and store nothing.
 template <int MODE, int ROUTE>
 void launch_fwd(const AttnParams& prm, dim3 grid, hipStream_t st, int hd) {
-    if (hd == 128 && !fwd_program_heavy<MODE>() && grid.y % 2 == 0) {
-        launch_fwd_shape<MODE, ROUTE, 128, 8>(prm, dim3(grid.x, grid.y / 2, grid.z), st);
-    } else if (hd == 64) {
+    if (hd == 64) {
         launch_fwd_shape<MODE, ROUTE, 64, 4>(prm, grid, st);
+    } else if constexpr (fwd_program_heavy<MODE>()) {
+        launch_fwd_shape<MODE, ROUTE, 128, 4>(prm, grid, st);
+    } else if (grid.y % 2 == 0) {
+        launch_fwd_shape<MODE, ROUTE, 128, 8>(prm, dim3(grid.x, grid.y / 2, grid.z), st);
+    } else if constexpr (exp2_is_f16(attn_exp2_kind<MODE>())) {
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, ROUTE, 128, 8, true>), dim3(grid.x, (grid.y + 1) / 2, grid.z),
+                           dim3(64 * 8), 0, st, prm);
     } else {
         launch_fwd_shape<MODE, ROUTE, 128, 4>(prm, grid, st);
     }
@@ -578,6 +589,23 @@ extern "C" int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* ls
         case kAttnSoftmaxExp2Pwl2SafeF16:
             launch_routed<kAttnSoftmaxExp2Pwl2SafeF16>(prm, grid, hst, exp2_route, hd);
             break;
+        case kAttnSoftmaxExp2Pwl1Safe: launch_routed<kAttnSoftmaxExp2Pwl1Safe>(prm, grid, hst, exp2_route, hd); break;
+        case kAttnSoftmaxExp2Pwl1SafeF16:
+            launch_routed<kAttnSoftmaxExp2Pwl1SafeF16>(prm, grid, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2Pwl2SafeBF16:
+            launch_routed<kAttnSoftmaxExp2Pwl2SafeBF16>(prm, grid, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2D2NoClamp:
+            launch_routed<kAttnSoftmaxExp2D2NoClamp>(prm, grid, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2D2SafeF16:
+            launch_routed<kAttnSoftmaxExp2D2SafeF16>(prm, grid, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2D2SafeBF16:
+            launch_routed<kAttnSoftmaxExp2D2SafeBF16>(prm, grid, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2Pwl2F16: launch_routed<kAttnSoftmaxExp2Pwl2F16>(prm, grid, hst, exp2_route, hd); break;
         case kAttnSoftcapNative: launch_fwd<kAttnSoftcapNative, 0>(prm, grid, hst, hd); break;
         case kAttnSoftcapD4: launch_fwd<kAttnSoftcapD4, 0>(prm, grid, hst, hd); break;
         case kAttnSigmoidNative: launch_fwd<kAttnSigmoidNative, 0>(prm, grid, hst, hd); break;

@@ -29,7 +29,15 @@ enum AttnMode : int {
     kAttnSoftmaxExp2Pwl2 = 12,
     kAttnSoftmaxExp2Pwl2Safe = 13,     // B5 PWL2 "safe" hinge, FP32
     kAttnSoftmaxExp2Pwl2SafeF16 = 14,  // B5 PWL2 "safe" hinge, packed FP16 fraction
-    kAttnModes = 15,
+    // 15..21: the remaining FA4 exp2 backends (exp2_kind order 6..12)
+    kAttnSoftmaxExp2Pwl1Safe = 15,
+    kAttnSoftmaxExp2Pwl1SafeF16 = 16,
+    kAttnSoftmaxExp2Pwl2SafeBF16 = 17,
+    kAttnSoftmaxExp2D2NoClamp = 18,
+    kAttnSoftmaxExp2D2SafeF16 = 19,
+    kAttnSoftmaxExp2D2SafeBF16 = 20,
+    kAttnSoftmaxExp2Pwl2F16 = 21,
+    kAttnModes = 22,
 };
 
 constexpr bool attn_is_sigmoid(int mode) { return mode >= kAttnSigmoidNative && mode <= kAttnSigmoidD6; }
@@ -48,7 +56,9 @@ constexpr int attn_exp2_kind() {
            : MODE == kAttnSoftmaxExp2Pwl2        ? kExp2Pwl2
            : MODE == kAttnSoftmaxExp2Pwl2Safe    ? kExp2Pwl2Safe
            : MODE == kAttnSoftmaxExp2Pwl2SafeF16 ? kExp2Pwl2SafeF16
-                                                 : kExp2Native;
+           : MODE >= kAttnSoftmaxExp2Pwl1Safe && MODE <= kAttnSoftmaxExp2Pwl2F16
+               ? kExp2Pwl1Safe + (MODE - kAttnSoftmaxExp2Pwl1Safe)
+               : kExp2Native;
 }
 
 constexpr int kHeadDim = 128;

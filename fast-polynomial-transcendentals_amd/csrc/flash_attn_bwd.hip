@@ -392,8 +392,13 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
                 const int64_t row = q0 + tid % (kThreads / 2);
                 const int64_t i = (b * p.hq + head) * p.seq + (RAGGED && row >= p.seq ? p.seq - 1 : row);
                 row_r = tid >= kThreads / 2 ? p.delta[i] : p.lse[i] * kLog2e;
-                // a query past the sequence: no probability (lse +inf), D 0
-                if (RAGGED && row >= p.seq) row_r = tid >= kThreads / 2 ? 0.0f : __builtin_inff();
+                // a query past the sequence: no probability (lse +inf), D 0.
+                // The unclamped D2 program has no clamp before its range
+                // reduction, so its exp2(-inf) is NaN: there such a query
+                // takes lse 0 (P = 1 against its zeroed Q and dO rows, so its
+                // dS is 0 and it adds nothing to dK or dV)
+                constexpr float kPadLse = MODE == kAttnSoftmaxExp2D2NoClamp ? 0.0f : __builtin_inff();
+                if (RAGGED && row >= p.seq) row_r = tid >= kThreads / 2 ? 0.0f : kPadLse;
             }
         }
     };
@@ -879,6 +884,27 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
             break;
         case kAttnSoftmaxExp2Pwl2SafeF16:
             launch_bwd_routed<kAttnSoftmaxExp2Pwl2SafeF16>(prm, batch, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2Pwl1Safe:
+            launch_bwd_routed<kAttnSoftmaxExp2Pwl1Safe>(prm, batch, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2Pwl1SafeF16:
+            launch_bwd_routed<kAttnSoftmaxExp2Pwl1SafeF16>(prm, batch, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2Pwl2SafeBF16:
+            launch_bwd_routed<kAttnSoftmaxExp2Pwl2SafeBF16>(prm, batch, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2D2NoClamp:
+            launch_bwd_routed<kAttnSoftmaxExp2D2NoClamp>(prm, batch, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2D2SafeF16:
+            launch_bwd_routed<kAttnSoftmaxExp2D2SafeF16>(prm, batch, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2D2SafeBF16:
+            launch_bwd_routed<kAttnSoftmaxExp2D2SafeBF16>(prm, batch, hst, exp2_route, hd);
+            break;
+        case kAttnSoftmaxExp2Pwl2F16:
+            launch_bwd_routed<kAttnSoftmaxExp2Pwl2F16>(prm, batch, hst, exp2_route, hd);
             break;
         case kAttnSoftcapNative: launch_bwd<kAttnSoftcapNative, kGradNatural, 0>(prm, batch, hst, hd); break;
         case kAttnSoftcapD4:

@@ -173,65 +173,139 @@ struct SoftcapConsts {
 // ---------------------------------------------------------------------------
 
 enum Exp2Kind : int {
-    kExp2D2 = 0,
-    kExp2D3 = 1,
-    kExp2Native = 2,
-    kExp2Pwl2 = 3,
-    kExp2Pwl2Safe = 4,
-    kExp2Pwl2SafeF16 = 5
+    kExp2D2 = 0,             // d2_safe
+    kExp2D3 = 1,             // d3
+    kExp2Native = 2,         // v_exp_f32
+    kExp2Pwl2 = 3,           // pwl2 (FP32 least-squares hinge)
+    kExp2Pwl2Safe = 4,       // pwl2_safe
+    kExp2Pwl2SafeF16 = 5,    // pwl2_safe_f16
+    kExp2Pwl1Safe = 6,       // pwl1_safe
+    kExp2Pwl1SafeF16 = 7,    // pwl1_safe_f16
+    kExp2Pwl2SafeBF16 = 8,   // pwl2_safe_bf16
+    kExp2D2NoClamp = 9,      // d2_safe_noclamp
+    kExp2D2SafeF16 = 10,     // d2_safe_f16
+    kExp2D2SafeBF16 = 11,    // d2_safe_bf16
+    kExp2Pwl2F16 = 12,       // pwl2_f16
+    kExp2Kinds = 13
 };
+
+// Programs whose fraction runs in packed FP16 (two lanes per instruction).
+constexpr bool exp2_is_f16(int kind) {
+    return kind == kExp2Pwl2SafeF16 || kind == kExp2Pwl1SafeF16 || kind == kExp2D2SafeF16 || kind == kExp2Pwl2F16;
+}
+// The lower clamp of the exponent: FA4's -127, or -126 for the hinges whose
+// fraction starts below one (there -127 would wrap the exponent field into
+// NaN bits); d2_safe_noclamp has none.
+constexpr float exp2_clamp(int kind) { return kind == kExp2Pwl2 || kind == kExp2Pwl2F16 ? -126.0f : -127.0f; }
 
 struct Pwl2SafeConsts {
     static constexpr float a = 0.7980513010317143f;
     static constexpr float c = 0.4038973979365714f;
     static constexpr float a16 = 0.7978515625f;   // 0x3A62
     static constexpr float c16 = 0.40380859375f;  // 0x3676
+    static constexpr float abf = 0.796875f;       // 0x3F4C, bf16(a)
+    static constexpr float cbf = 0.404296875f;    // 0x3ECF, bf16(c)
 };
+
+// D2 "safe" fraction with 16-bit coefficients: c1 = 0.6602339719 and
+// c2 = 1 - c1 rounded to FP16 / BF16; both roundings give 0.66015625 and
+// 0.33984375, whose sum is exactly one, so p(1) = 2 survives the rounding.
+struct D2SafeConsts {
+    static constexpr float c1 = 0.6602339719000094f;
+    static constexpr float c2 = 0.33976602809999057f;
+    static constexpr float c1_16 = 0.66015625f;   // FP16 0x3948, BF16 0x3F29
+    static constexpr float c2_16 = 0.33984375f;   // FP16 0x3570, BF16 0x3EAE
+};
+
+// The reference's FP16 hinge (FractionalPwl2Hinge,
+// autonumerics_zero/cuda_benchmarks/benchmark_exp2_pwl2.cu:84-99): offset
+// 0x3BEA, slope 0x3A91, slope change 0x357B at f = 1/2.
+struct Pwl2F16Consts {
+    static constexpr float offset = 0.9892578125f;
+    static constexpr float slope = 0.82080078125f;
+    static constexpr float delta = 0.342529296875f;
+};
+
+// The fraction program on f in [0, 1) for the FP32 and BF16 programs.
+// BF16 steps are an FP32 FMA of BF16 values rounded once to BF16 (RNE);
+// the hinge max(bf16(f) - 1/2, 0) is exact in BF16.
+template <int KIND>
+__device__ __forceinline__ float exp2_frac(float f) {
+    if constexpr (KIND == kExp2D2 || KIND == kExp2D2NoClamp) {
+        return __builtin_fmaf(__builtin_fmaf(f, D2SafeConsts::c2, D2SafeConsts::c1), f, 1.0f);
+    } else if constexpr (KIND == kExp2Pwl2) {
+        const float p = __builtin_fmaf(f, 0.820852518081665f, 0.9894611835479736f);
+        return __builtin_fmaf(__builtin_fmaxf(f - 0.5f, 0.0f), 0.34246066212654114f, p);
+    } else if constexpr (KIND == kExp2Pwl2Safe) {
+        const float p = __builtin_fmaf(f, Pwl2SafeConsts::a, 1.0f);
+        return __builtin_fmaf(__builtin_fmaxf(f - 0.5f, 0.0f), Pwl2SafeConsts::c, p);
+    } else if constexpr (KIND == kExp2Pwl1Safe) {
+        return f + 1.0f;
+    } else if constexpr (KIND == kExp2Pwl2SafeBF16) {
+        const float fb = rbf(f);
+        const float b = rbf(__builtin_fmaf(fb, Pwl2SafeConsts::abf, 1.0f));
+        return rbf(__builtin_fmaf(__builtin_fmaxf(fb - 0.5f, 0.0f), Pwl2SafeConsts::cbf, b));
+    } else if constexpr (KIND == kExp2D2SafeBF16) {
+        const float fb = rbf(f);
+        return rbf(__builtin_fmaf(rbf(__builtin_fmaf(fb, D2SafeConsts::c2_16, D2SafeConsts::c1_16)), fb, 1.0f));
+    } else {
+        static_assert(KIND == kExp2D3, "FP16 programs run in pairs (exp2_pair)");
+        float p = __builtin_fmaf(f, 0.077119089663028717041015625f, 0.227564394474029541015625f);
+        p = __builtin_fmaf(p, f, 0.695146143436431884765625f);
+        return __builtin_fmaf(p, f, 1.0f);
+    }
+}
+
+// The packed FP16 fraction of two lanes (f rounded to FP16 by the caller),
+// one instruction per step, each step one FP16 rounding.
+template <int KIND>
+__device__ __forceinline__ h2_t exp2_frac_f16(h2_t f) {
+    const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+    if constexpr (KIND == kExp2Pwl1SafeF16) {
+        return f + one;
+    } else if constexpr (KIND == kExp2D2SafeF16) {
+        const h2_t c1 = {(_Float16)D2SafeConsts::c1_16, (_Float16)D2SafeConsts::c1_16};
+        const h2_t c2 = {(_Float16)D2SafeConsts::c2_16, (_Float16)D2SafeConsts::c2_16};
+        return __builtin_elementwise_fma(__builtin_elementwise_fma(f, c2, c1), f, one);
+    } else {
+        static_assert(KIND == kExp2Pwl2SafeF16 || KIND == kExp2Pwl2F16, "not an FP16 hinge");
+        constexpr float a = KIND == kExp2Pwl2F16 ? Pwl2F16Consts::slope : Pwl2SafeConsts::a16;
+        constexpr float c = KIND == kExp2Pwl2F16 ? Pwl2F16Consts::delta : Pwl2SafeConsts::c16;
+        constexpr float b = KIND == kExp2Pwl2F16 ? Pwl2F16Consts::offset : 1.0f;
+        const h2_t half = {(_Float16)0.5f, (_Float16)0.5f};
+        const h2_t zero = {(_Float16)0.0f, (_Float16)0.0f};
+        const h2_t av = {(_Float16)a, (_Float16)a}, cv = {(_Float16)c, (_Float16)c}, bv = {(_Float16)b, (_Float16)b};
+        const h2_t hinge = __builtin_elementwise_max(f - half, zero);
+        return __builtin_elementwise_fma(hinge, cv, __builtin_elementwise_fma(f, av, bv));
+    }
+}
 
 template <int KIND>
 __device__ __forceinline__ float exp2_lane(float x) {
+    static_assert(!exp2_is_f16(KIND), "FP16 programs run in pairs (exp2_pair)");
     if constexpr (KIND == kExp2Native) {
         return __builtin_amdgcn_exp2f(x);
     } else {
-        x = __builtin_fmaxf(x, KIND == kExp2Pwl2 ? -126.0f : -127.0f);
+        if constexpr (KIND != kExp2D2NoClamp) x = __builtin_fmaxf(x, exp2_clamp(KIND));
         const float fl = __builtin_floorf(x);
-        const float f = x - fl;
-        float p;
-        if constexpr (KIND == kExp2D2) {
-            p = __builtin_fmaf(f, 0.33976602809999057f, 0.6602339719000094f);
-            p = __builtin_fmaf(p, f, 1.0f);
-        } else if constexpr (KIND == kExp2Pwl2) {
-            p = __builtin_fmaf(f, 0.820852518081665f, 0.9894611835479736f);
-            p = __builtin_fmaf(__builtin_fmaxf(f - 0.5f, 0.0f), 0.34246066212654114f, p);
-        } else if constexpr (KIND == kExp2Pwl2Safe) {
-            p = __builtin_fmaf(f, Pwl2SafeConsts::a, 1.0f);
-            p = __builtin_fmaf(__builtin_fmaxf(f - 0.5f, 0.0f), Pwl2SafeConsts::c, p);
-        } else {
-            p = __builtin_fmaf(f, 0.077119089663028717041015625f, 0.227564394474029541015625f);
-            p = __builtin_fmaf(p, f, 0.695146143436431884765625f);
-            p = __builtin_fmaf(p, f, 1.0f);
-        }
+        const float p = exp2_frac<KIND>(x - fl);
         const int n = (int)fl;  // v_cvt_i32_f32 (saturating)
         return as_f32(((uint32_t)n << 23) + as_u32(p));
     }
 }
 
-// Two lanes of one program.  The packed FP16 PWL2 evaluates both fractions
-// with one instruction per step; every other program is exp2_lane per lane.
+// Two lanes of one program.  The packed FP16 programs evaluate both
+// fractions with one instruction per step (f rounded to FP16 by
+// v_cvt_pk_f16_f32, RNE; p widened to FP32 exactly for the exponent add);
+// every other program is exp2_lane per lane.
 template <int KIND>
 __device__ __forceinline__ void exp2_pair(float x0, float x1, float& y0, float& y1) {
-    if constexpr (KIND == kExp2Pwl2SafeF16) {
-        x0 = __builtin_fmaxf(x0, -127.0f);
-        x1 = __builtin_fmaxf(x1, -127.0f);
+    if constexpr (exp2_is_f16(KIND)) {
+        x0 = __builtin_fmaxf(x0, exp2_clamp(KIND));
+        x1 = __builtin_fmaxf(x1, exp2_clamp(KIND));
         const float fl0 = __builtin_floorf(x0), fl1 = __builtin_floorf(x1);
-        const h2_t f = {(_Float16)(x0 - fl0), (_Float16)(x1 - fl1)};  // v_cvt_pk_f16_f32 (RNE)
-        const h2_t half = {(_Float16)0.5f, (_Float16)0.5f};
-        const h2_t zero = {(_Float16)0.0f, (_Float16)0.0f};
-        const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
-        const h2_t a = {(_Float16)Pwl2SafeConsts::a16, (_Float16)Pwl2SafeConsts::a16};
-        const h2_t c = {(_Float16)Pwl2SafeConsts::c16, (_Float16)Pwl2SafeConsts::c16};
-        const h2_t hinge = __builtin_elementwise_max(f - half, zero);
-        const h2_t p = __builtin_elementwise_fma(hinge, c, __builtin_elementwise_fma(f, a, one));
+        const h2_t f = {(_Float16)(x0 - fl0), (_Float16)(x1 - fl1)};
+        const h2_t p = exp2_frac_f16<KIND>(f);
         y0 = as_f32(((uint32_t)(int)fl0 << 23) + as_u32((float)p.x));
         y1 = as_f32(((uint32_t)(int)fl1 << 23) + as_u32((float)p.y));
     } else {

@@ -40,6 +40,7 @@ SUPPORTED_EXP2_BACKENDS = (
     "pwl1_safe_f16",
     "pwl2_safe",
     "pwl2_safe_f16",
+    "pwl2_safe_bf16",
     "d2_safe",
     "d2_safe_noclamp",
     "d2_safe_f16",

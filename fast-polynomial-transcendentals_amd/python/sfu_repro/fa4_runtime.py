@@ -18,7 +18,10 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
   exponents take the ``exp2_emu_backend`` program (``d3``: FA4 D3,
   ``d2_safe``: the B5 D2 fraction, ``pwl2``: the two-piece hinge,
   ``pwl2_safe``: the endpoint-constrained hinge in FP32, ``pwl2_safe_f16``:
-  the same hinge on the fraction rounded to FP16, packed FP16), key j
+  the same hinge on the fraction rounded to FP16, packed FP16, and the rest
+  of FA4's list: ``pwl1_safe`` (1 + f), ``pwl1_safe_f16``, ``pwl2_safe_bf16``,
+  ``d2_safe_noclamp`` (no -127 clamp), ``d2_safe_f16``, ``d2_safe_bf16`` and
+  ``pwl2_f16`` (the reference's FP16 hinge); see spline_ops_hip.h), key j
   when slot(j) % freq < 4 with slot(j) = 16 bit5(j) + 4 bits3..4(j) +
   bits0..1(j), in the forward and the backward alike;
 * softcap: ``softcap > 0`` with no score_mod -> FP32 hardware tanh; a
@@ -35,8 +38,8 @@ of the last, partial block are zeroed on chip (queries past the sequence get
 an infinite lse and a zero D in the backward), which is the arithmetic of
 operands zero-padded at the end, and nothing past the sequence is stored.
 
-Combinations whose programs are not part of the reference tree (the other
-FP16 / BF16 exp2 variants and PWL1, Sollya attention fits, mixed SFU/polynomial
+Combinations whose programs are not part of the reference tree (Sollya
+attention fits, mixed SFU/polynomial
 sigmoid lanes, and the ``cute`` backends -- FA4's CuTe FP32 score programs,
 whose coefficients live in FA4) raise ``NotImplementedError`` naming what is
 missing.
@@ -65,6 +68,8 @@ MODE_SIGMOID_D3 = 8  # 8..11: D3..D6
 MODE_SOFTMAX_PWL2 = 12
 MODE_SOFTMAX_PWL2_SAFE = 13
 MODE_SOFTMAX_PWL2_SAFE_F16 = 14
+MODE_SOFTMAX_PWL1_SAFE = 15  # 15..21: pwl1_safe, pwl1_safe_f16, pwl2_safe_bf16, d2_safe_noclamp,
+#                              d2_safe_f16, d2_safe_bf16, pwl2_f16
 
 # derivative programs (AttnGrad in flash_attn_bwd.hip)
 GRAD_NATURAL = 0
@@ -75,7 +80,10 @@ GRAD_ALGEBRAIC = 4
 GRAD_DIRECT = 5
 
 BUILT_EXP2_BACKENDS = {"d3": MODE_SOFTMAX_D3, "d2_safe": MODE_SOFTMAX_D2, "pwl2": MODE_SOFTMAX_PWL2,
-                       "pwl2_safe": MODE_SOFTMAX_PWL2_SAFE, "pwl2_safe_f16": MODE_SOFTMAX_PWL2_SAFE_F16}
+                       "pwl2_safe": MODE_SOFTMAX_PWL2_SAFE, "pwl2_safe_f16": MODE_SOFTMAX_PWL2_SAFE_F16,
+                       **{name: MODE_SOFTMAX_PWL1_SAFE + i for i, name in enumerate(
+                           ("pwl1_safe", "pwl1_safe_f16", "pwl2_safe_bf16", "d2_safe_noclamp", "d2_safe_f16",
+                            "d2_safe_bf16", "pwl2_f16"))}}
 SUPPORTED_ROUTES = (0, 4, 6, 8, 10, 12, 16, 20, 24, 32)
 _SOFTCAP_BWD = {"analytical": GRAD_ANALYTICAL, "ste": GRAD_STE, "exact_1mt2": GRAD_EXACT_1MT2}
 

@@ -321,6 +321,41 @@ int launch_exp2_pwl2_safe_f32_bf16(void* y, const void* x, int64_t size, void* s
 int launch_exp2_pwl2_safe_f32(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_pwl2_safe_f16_f32_bf16(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_pwl2_safe_f16_f32(void* y, const void* x, int64_t size, void* stream);
+/* The remaining exp2 backends of FA4 (src/sfu_repro/fa4.py:33-46), on the
+ * same reduction and exponent add.  The forms are the appendix's
+ * (extras/paper/manuscript/appendix_exp2.tex:17-32); their 16-bit programs
+ * are not in the reference tree, so the precisions below are this build's:
+ *   pwl1_safe        p = 1 + f (FP32), the only endpoint-safe line;
+ *   pwl1_safe_f16    p = fp16(fp16(f) + 1);
+ *   pwl2_safe_bf16   the PWL2 safe hinge on bf16(f) with bf16(a) = 0.796875,
+ *                    bf16(c) = 0.404296875, each FMA rounded to BF16;
+ *   d2_safe_noclamp  the D2 safe fraction without the -127 clamp (exponents
+ *                    below -127 wrap the exponent field, as in FA4's variant);
+ *   d2_safe_f16      p = fp16(fma(fp16(fma(f, c2, c1)), f, 1)) on fp16(f),
+ *                    c1 = 0.66015625, c2 = 0.33984375 (the FP16 roundings of
+ *                    the D2 fit, summing to one: p(1) = 2);
+ *   d2_safe_bf16     the same with BF16 f and BF16 rounding per FMA (the same
+ *                    two coefficients are BF16 values);
+ *   pwl2_f16         the reference's FP16 hinge (FractionalPwl2Hinge,
+ *                    autonumerics_zero/cuda_benchmarks/benchmark_exp2_pwl2.cu:84-99:
+ *                    offset 0x3BEA, slope 0x3A91, change 0x357B) on fp16(f),
+ *                    clamped at -126 like pwl2 (its fraction starts below one).
+ * Every program keeps p(0) = 1 and p(1) = 2 after its rounding except
+ * pwl2_f16 (p(0) = 0.98926). */
+int launch_exp2_pwl1_safe_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl1_safe_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl1_safe_f16_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl1_safe_f16_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl2_safe_bf16_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl2_safe_bf16_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d2_safe_noclamp_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d2_safe_noclamp_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d2_safe_f16_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d2_safe_f16_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d2_safe_bf16_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_d2_safe_bf16_f32(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl2_f16_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl2_f16_f32(void* y, const void* x, int64_t size, void* stream);
 
 /* ---- paired sin/cos tables: FP32 angles [size] -> out [2, size] ----------
  * Plane 0 holds cos, plane 1 sin.  Replaces launch_sincos_*_{bf16,fp16,f32}
@@ -486,8 +521,13 @@ int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k, con
  *   13 softmax, PWL2 "safe" hinge exp2 (FP32; FA4 backend pwl2_safe)
  *   14 softmax, PWL2 "safe" hinge exp2 with the packed FP16 fraction (FA4
  *     backend pwl2_safe_f16; the programs of launch_exp2_pwl2_safe*).
+ *   15..21 softmax with FA4's remaining exp2 backends, the programs of the
+ *     launch_exp2_<backend>* entry points: 15 pwl1_safe, 16 pwl1_safe_f16,
+ *     17 pwl2_safe_bf16, 18 d2_safe_noclamp (no clamp: exponents below -127
+ *     wrap, so the backward needs a finite lse), 19 d2_safe_f16,
+ *     20 d2_safe_bf16, 21 pwl2_f16 (clamped at -126, as mode 12).
  * sigmoid_bias: the bias of the hardware and D3..D6 sigmoid modes.
- * exp2_route (modes 1, 2, 12, 13, 14): key j of a query row takes the polynomial when
+ * exp2_route (modes 1, 2 and 12..21): key j of a query row takes the polynomial when
  * slot(j) % exp2_route < 4, else v_exp_f32, with slot(j) = 16 bit5(j) +
  * 4 bits3..4(j) + bits0..1(j) (the slot of j's exponent in the kernel's
  * registers), so four of every exp2_route exponents are routed; one of 4
@@ -532,7 +572,7 @@ int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* lse, const vo
  *              straight-through (ste) / 1 - T(u)^2 (exact_1mt2)
  *   4 / 5      mode 6 only: y (1 - y) (algebraic) / the B3 factored D4
  *              derivative (direct).
- * exp2_route (modes 1, 2, 12, 13, 14): 0 hardware exp2, 4 the polynomial everywhere,
+ * exp2_route (modes 1, 2 and 12..21): 0 hardware exp2, 4 the polynomial everywhere,
  * 6..32 the polynomial for the keys the forward routes with that value
  * (FA4's exp2_emu_freq_bwd). */
 int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float* delta,

@@ -90,6 +90,8 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_softcap_fwd_bf16.argtypes = [u16p, u16p, i64, ctypes.c_float]
     l.orc_softcap_bwd_bf16.argtypes = [u16p, u16p, u16p, i64, ctypes.c_float]
     l.orc_exp2.argtypes = [ci, ci, f32p, u16p, f32p, i64]
+    l.orc_exp2_fraction.argtypes = [ci, f32p, f32p, i64]
+    l.orc_exp2_fraction.restype = ctypes.c_int
     l.orc_sincos.argtypes = [ci, ci, ci, f32p, u16p, u16p, i64]
     l.orc_rope_sincos_table.argtypes = [i32p, u16p, i64, i64]
     l.orc_rope_apply.argtypes = [ci, u16p, u16p, i32p, u16p, u16p, i64, i64, i64, i64, i64]
@@ -256,6 +258,12 @@ def softcap_bwd_bf16(go: np.ndarray, s: np.ndarray, cap: float) -> np.ndarray:
 
 
 EXP2_D2, EXP2_D3, EXP2_PWL2, EXP2_PWL2_SAFE, EXP2_PWL2_SAFE_F16 = 0, 1, 2, 3, 4
+(EXP2_PWL1_SAFE, EXP2_PWL1_SAFE_F16, EXP2_PWL2_SAFE_BF16, EXP2_D2_NOCLAMP, EXP2_D2_SAFE_F16,
+ EXP2_D2_SAFE_BF16, EXP2_PWL2_F16) = range(5, 12)
+# FA4 backend name -> oracle kind
+EXP2_BACKEND_KIND = {"d2_safe": 0, "d3": 1, "pwl2": 2, "pwl2_safe": 3, "pwl2_safe_f16": 4, "pwl1_safe": 5,
+                     "pwl1_safe_f16": 6, "pwl2_safe_bf16": 7, "d2_safe_noclamp": 8, "d2_safe_f16": 9,
+                     "d2_safe_bf16": 10, "pwl2_f16": 11}
 
 
 def exp2(kind: int, x: np.ndarray, out_bf16: bool = True) -> np.ndarray:
@@ -265,6 +273,14 @@ def exp2(kind: int, x: np.ndarray, out_bf16: bool = True) -> np.ndarray:
     _check(lib().orc_exp2(kind, int(out_bf16), _p(x, ctypes.c_float), _p(y16),
                           _p(y32, ctypes.c_float), x.size))
     return y16 if out_bf16 else y32
+
+
+def exp2_fraction(kind: int, f: np.ndarray) -> np.ndarray:
+    """p(f) of an exp2 program's fraction alone (no range reduction)."""
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    p = np.empty(f.shape, dtype=np.float32)
+    _check(lib().orc_exp2_fraction(kind, _p(f, ctypes.c_float), _p(p, ctypes.c_float), f.size))
+    return p
 
 
 # half-turn sin/cos programs (same ids as the device SinCosId enum)

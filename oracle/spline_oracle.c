@@ -729,12 +729,49 @@ static double h_max(double a, double b) {
     return a > b ? a : b;
 }
 
+/* The 16-bit programs of the remaining FA4 exp2 backends (this build's
+ * definitions; FA4's are not in the reference tree): BF16 steps are an FP32
+ * FMA of BF16 values rounded once (h_fma_f32), FP16 steps single-rounding
+ * FP16 operations. */
+static float exp2_frac16(int kind, float fr) {
+    const fmt_t* h = &FMT_F16;
+    const fmt_t* b = &FMT_BF16;
+    if (kind == 6) { /* pwl1_safe_f16: fp16(fp16(f) + 1) */
+        return (float)h_add(round_fmt((double)fr, h), 1.0, h);
+    } else if (kind == 7) { /* pwl2_safe_bf16: hinge on bf16(f), a = 0.796875, c = 0.404296875 */
+        double fb = round_fmt((double)fr, b);
+        double base = h_fma_f32(fb, 0.796875, 1.0, b);
+        double hinge = h_max(h_add(fb, -0.5, b), 0.0);
+        return (float)h_fma_f32(hinge, 0.404296875, base, b);
+    } else if (kind == 9) { /* d2_safe_f16: c1 = 0.66015625, c2 = 0.33984375 */
+        double f16 = round_fmt((double)fr, h);
+        double q = h_fma(f16, 0.33984375, 0.66015625, h);
+        return (float)h_fma(q, f16, 1.0, h);
+    } else if (kind == 10) { /* d2_safe_bf16 */
+        double fb = round_fmt((double)fr, b);
+        double q = h_fma_f32(fb, 0.33984375, 0.66015625, b);
+        return (float)h_fma_f32(q, fb, 1.0, b);
+    } else { /* 11, pwl2_f16: FractionalPwl2Hinge, benchmark_exp2_pwl2.cu:84-99 */
+        double f16 = round_fmt((double)fr, h);
+        double hinge = h_max(h_add(f16, -0.5, h), 0.0);
+        double base = h_fma(f16, 0.82080078125, 0.9892578125, h);  /* 0x3A91, 0x3BEA */
+        return (float)h_fma(hinge, 0.342529296875, base, h);        /* 0x357B */
+    }
+}
+
 static float exp2_prog(int kind, float x) {
-    x = fmaxf(x, -127.0f);
+    if (kind != 8) x = fmaxf(x, kind == 11 ? -126.0f : -127.0f);  /* 8: d2_safe_noclamp */
     float fl = floorf(x);
     float fr = x - fl;
     float p;
-    if (kind == 3) { /* PWL2 safe, FP32: appendix_exp2.tex:22-27, sampled-minimax a, c = 2(1 - a) */
+    if (kind == 5) {  /* pwl1_safe: 1 + f */
+        p = fr + 1.0f;
+    } else if (kind == 6 || kind == 7 || kind >= 9) {
+        p = exp2_frac16(kind, fr);
+    } else if (kind == 8) {  /* d2_safe_noclamp: the D2 safe fraction */
+        p = fmaf(fr, 0.33976602809999057f, 0.6602339719000094f);
+        p = fmaf(p, fr, 1.0f);
+    } else if (kind == 3) { /* PWL2 safe, FP32: appendix_exp2.tex:22-27, sampled-minimax a, c = 2(1 - a) */
         p = fmaf(fr, 0.7980513010317143f, 1.0f);
         p = fmaf(fmaxf(fr - 0.5f, 0.0f), 0.4038973979365714f, p);
     } else if (kind == 4) { /* PWL2 safe, packed FP16: appendix_exp2.tex:72-76 */
@@ -762,11 +799,23 @@ static float exp2_prog(int kind, float x) {
     return r;
 }
 
+/* The fraction program alone, p(f) for f in [0, 1] with no range reduction
+ * (the reference's fractional benchmark domain, benchmark_exp2_pwl2.cu:
+ * 325-333, 346-371): kinds 5-7 and 9-11 (the 16-bit programs and PWL1). */
+int orc_exp2_fraction(int kind, const float* f, float* p, int64_t n) {
+    if (n < 0 || kind < 5 || kind > 11 || kind == 8) return -1;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) p[i] = kind == 5 ? f[i] + 1.0f : exp2_frac16(kind, f[i]);
+    return 0;
+}
+
 /* kind: 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge, 3 = PWL2 safe (FP32),
- * 4 = PWL2 safe (packed FP16).  out_bf16: BF16 bits into y16, else FP32 into
- * y32. */
+ * 4 = PWL2 safe (packed FP16), 5 = PWL1 safe, 6 = PWL1 safe FP16, 7 = PWL2
+ * safe BF16, 8 = D2 safe without the clamp, 9 = D2 safe FP16, 10 = D2 safe
+ * BF16, 11 = the reference's FP16 hinge.  out_bf16: BF16 bits into y16,
+ * else FP32 into y32. */
 int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n) {
-    if (n < 0 || kind < 0 || kind > 4) return -1;
+    if (n < 0 || kind < 0 || kind > 11) return -1;
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
         float r = exp2_prog(kind, x[i]);

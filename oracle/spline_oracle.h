@@ -95,7 +95,9 @@ int orc_softcap_fwd_bf16(const uint16_t* s, uint16_t* y, int64_t n, float cap);
 int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int64_t n, float cap);
 
 /* ---- B5 exp2: kind 0 = D2 safe, 1 = FA4 D3, 2 = PWL2 hinge, 3 = PWL2 safe
- * (FP32), 4 = PWL2 safe (packed FP16) ---------------------------------------
+ * (FP32), 4 = PWL2 safe (packed FP16), 5 = PWL1 safe, 6 = PWL1 safe FP16,
+ * 7 = PWL2 safe BF16, 8 = D2 safe without the -127 clamp, 9 = D2 safe FP16,
+ * 10 = D2 safe BF16, 11 = the reference's FP16 hinge (clamped at -126) ------
  * The FP32 programs are pinned (p(0) = 1, p(1) = 2, the published fit and
  * error metrics); the deployed 16-bit output rounding is parity unpinned
  * (it lives in the absent FlashAttention-4): here one RNE of the FP32
@@ -103,8 +105,14 @@ int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int
  * p = fma(h, c, fma(f, a, 1)), one FP16 rounding per step) is pinned by its
  * published coefficients, its endpoints after FP16 rounding and its
  * published maximum relative error (appendix_exp2.tex:72-76); FA4's own
- * instruction order is not in the reference tree. */
+ * instruction order is not in the reference tree.  Kind 11 is the
+ * reference's own FP16 program (benchmark_exp2_pwl2.cu:84-99), pinned by its
+ * published fractional error metrics; kinds 5-10 are pinned by their
+ * endpoints and fit errors only (parity unpinned: FA4 absent). */
 int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n);
+/* The fraction program alone on f in [0, 1] (no range reduction), kinds 5-7
+ * and 9-11. */
+int orc_exp2_fraction(int kind, const float* f, float* p, int64_t n);
 
 /* ---- paired sin/cos: prog 0 BF16 D3/D4, 1 BF16 D5/D6, 2 FP16 D3/D4,
  * 3 FP16 D5/D4, 4 FP16 D5/D6, 5 FP16 D7/D6 (half turn) ------------------- */

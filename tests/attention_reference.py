@@ -13,9 +13,13 @@ import torch
 M = {"softmax_native": 0, "softmax_d2": 1, "softmax_d3": 2, "softcap_native": 3, "softcap_d4": 4,
      "sigmoid_native": 5, "sigmoid_b3": 6, "sigmoid_b3_d2": 7, "sigmoid_d3": 8, "sigmoid_d4": 9,
      "sigmoid_d5": 10, "sigmoid_d6": 11, "softmax_pwl2": 12, "softmax_pwl2_safe": 13,
-     "softmax_pwl2_safe_f16": 14}
+     "softmax_pwl2_safe_f16": 14, "softmax_pwl1_safe": 15, "softmax_pwl1_safe_f16": 16,
+     "softmax_pwl2_safe_bf16": 17, "softmax_d2_noclamp": 18, "softmax_d2_safe_f16": 19,
+     "softmax_d2_safe_bf16": 20, "softmax_pwl2_f16": 21}
 EXP2_KIND = {"softmax_d2": 0, "softmax_d3": 1, "softmax_pwl2": 2, "softmax_pwl2_safe": 3,
-             "softmax_pwl2_safe_f16": 4}
+             "softmax_pwl2_safe_f16": 4, "softmax_pwl1_safe": 5, "softmax_pwl1_safe_f16": 6,
+             "softmax_pwl2_safe_bf16": 7, "softmax_d2_noclamp": 8, "softmax_d2_safe_f16": 9,
+             "softmax_d2_safe_bf16": 10, "softmax_pwl2_f16": 11}
 LOG2E = 1.4426950408889634
 
 
@@ -37,7 +41,7 @@ def _exp2_arg(mode, x):
     """The fused kernels clamp the PWL2 exponent at -126 (the reference's
     hinge, clamped at -127, wraps into NaN bits below -126.987: its fraction
     starts below one); the D2 / D3 programs take the reference's -127."""
-    return torch.clamp(x, min=-126.0) if mode == "softmax_pwl2" else x
+    return torch.clamp(x, min=-126.0) if mode in ("softmax_pwl2", "softmax_pwl2_f16") else x
 
 
 def probs_and_grad(oracle, a, mode, grad, scale, cap, bias, lse2, route):
@@ -134,8 +138,10 @@ def _heads(q, k, v):
 
 def reference_fwd(oracle, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=None):
     """(out [B, S, H, D], lse [B, H, S]) in float32; lse is None for the
-    sigmoid modes.  Softmax exponents are taken relative to the row maximum;
-    routed keys (route_slot % route < 4) take the mode's exp2 program."""
+    sigmoid modes.  Softmax exponents are taken relative to the running
+    maximum the fused forward holds at each key's tile (lazy_row_max), then
+    rescaled to the final one; routed keys (route_slot % route < 4) take the
+    mode's exp2 program."""
     qf, kf, vf = _heads(q, k, v)
     a = qf @ kf.transpose(-1, -2)
     n = a.shape[-1]
@@ -154,14 +160,43 @@ def reference_fwd(oracle, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=
     else:
         x = a * np.float32(scale * LOG2E)
     x = x.masked_fill(mask, -math.inf)
-    m = x.amax(-1, keepdim=True)
-    e = torch.exp2((x - m).double()).float()
+    mk, m = lazy_row_max(x)
+    e = torch.exp2((x - mk).double()).float()
     if mode in EXP2_KIND:
-        pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], _exp2_arg(mode, x - m).numpy().reshape(-1),
+        pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], _exp2_arg(mode, x - mk).numpy().reshape(-1),
                                           out_bf16=False)).reshape(x.shape)
         sel = (route_slot(torch.arange(n)) % route) < 4
         e = torch.where(sel, pp, e).masked_fill(mask, 0.0)
+    e = (e.double() * torch.exp2((mk - m).double())).float()  # the rescales as m moves
     l = e.sum(-1, keepdim=True)
     out = (e @ vf) / l
     lse = ((m + torch.log2(l)) * math.log(2.0)).squeeze(-1)
     return out.transpose(1, 2), lse
+
+
+KEY_TILE = 64       # keys per staged tile of the fused forward
+RESCALE_STEP = 8.0  # the forward moves its running maximum only by more than this
+
+
+def lazy_row_max(x):
+    """The fused forward's running maximum of the log2-unit exponents x
+    [..., Sq, Sk] (masked keys -inf): it visits 64-key tiles in order and
+    moves to a tile's maximum only when that exceeds the current one by more
+    than 8 (flash_attn.hip, tile_softmax_state), so each key's exponent is
+    taken against the maximum held at its tile.  Returns (per-key maximum
+    [..., Sq, Sk], final maximum [..., Sq, 1]).  The final one is at most 8
+    below the true row maximum; with the hardware exp2 the result is the same
+    as against the true maximum, while a program's error depends on the
+    fraction of the exponent it is given."""
+    n = x.shape[-1]
+    tiles = (n + KEY_TILE - 1) // KEY_TILE
+    pad = torch.full(x.shape[:-1] + (tiles * KEY_TILE - n,), -math.inf, dtype=x.dtype)
+    tmax = torch.cat([x, pad], -1).reshape(x.shape[:-1] + (tiles, KEY_TILE)).amax(-1)
+    m = torch.full(x.shape[:-1], -math.inf, dtype=torch.float32)
+    held = []
+    for t in range(tiles):
+        mt = tmax[..., t].float()
+        m = torch.where(mt > m + np.float32(RESCALE_STEP), mt, m)
+        held.append(m)
+    held = torch.stack(held, -1)
+    return held.repeat_interleave(KEY_TILE, -1)[..., :n], held[..., -1:]

@@ -166,8 +166,18 @@ def test_forward_program_selection():
     assert sel(seqlen=256, exp2_emu_backend="pwl2_safe", exp2_emu_freq=12)[:2] == (rt.MODE_SOFTMAX_PWL2_SAFE, 12)
     assert sel(seqlen=256, exp2_emu_backend="pwl2_safe_f16", exp2_emu_freq=12)[:2] == \
         (rt.MODE_SOFTMAX_PWL2_SAFE_F16, 12)
-    with pytest.raises(NotImplementedError, match="pwl1_safe_f16"):
-        sel(seqlen=256, exp2_emu_backend="pwl1_safe_f16", exp2_emu_freq=12)
+    # every exp2 backend FA4 accepts resolves to a kernel program
+    from sfu_repro.fa4 import SUPPORTED_EXP2_BACKENDS
+
+    # the reference's list, in its order (src/sfu_repro/fa4.py:33-46)
+    assert SUPPORTED_EXP2_BACKENDS == ("d3", "pwl2", "pwl1_safe", "pwl1_safe_f16", "pwl2_safe", "pwl2_safe_f16",
+                                       "pwl2_safe_bf16", "d2_safe", "d2_safe_noclamp", "d2_safe_f16",
+                                       "d2_safe_bf16", "pwl2_f16")
+    modes = {sel(seqlen=256, exp2_emu_backend=name, exp2_emu_freq=12)[0] for name in SUPPORTED_EXP2_BACKENDS}
+    assert len(modes) == len(SUPPORTED_EXP2_BACKENDS) == 12
+    assert sel(seqlen=256, exp2_emu_backend="pwl2_f16", exp2_emu_freq=32)[:2] == (rt.MODE_SOFTMAX_PWL1_SAFE + 6, 32)
+    with pytest.raises(NotImplementedError, match="d2_safe_bf16_fast"):
+        sel(seqlen=256, exp2_emu_backend="d2_safe_bf16_fast", exp2_emu_freq=12)
     with pytest.raises(NotImplementedError, match="routing frequency 14"):
         sel(seqlen=256, exp2_emu_backend="d3", exp2_emu_freq=14)
     assert sel(seqlen=256, softcap=30.0) == (rt.MODE_SOFTCAP_NATIVE, 4, 30.0, 0.0)

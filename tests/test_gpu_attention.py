@@ -68,7 +68,9 @@ def test_softcap_config3_distribution(spline_ops, cuda):
     assert float((y - ref).abs().max()) < 0.6
 
 
-@pytest.mark.parametrize("kind,name", [(0, "d2"), (1, "d3"), (3, "pwl2_safe"), (4, "pwl2_safe_f16")])
+@pytest.mark.parametrize("kind,name", [(0, "d2"), (1, "d3"), (3, "pwl2_safe"), (4, "pwl2_safe_f16"), (5, "pwl1_safe"),
+                                       (6, "pwl1_safe_f16"), (7, "pwl2_safe_bf16"), (8, "d2_safe_noclamp"),
+                                       (9, "d2_safe_f16"), (10, "d2_safe_bf16"), (11, "pwl2_f16")])
 @pytest.mark.parametrize("out_bf16", [True, False])
 def test_exp2_programs(capi, oracle, cuda, kind, name, out_bf16):
     x = _f32_inputs(11 + kind)

@@ -134,11 +134,10 @@ def test_qk_norm_and_module_patching(cuda):
 
 
 def test_unbuilt_programs_fail_loudly(cuda):
-    cfg = FA4Config(mode="softmax", exp2_emu_backend="pwl1_safe_f16", exp2_emu_freq=12, exp2_emu_freq_bwd=32)
-    module = build_fa4_module(cfg, head_dim=128)
+    cfg = FA4Config(mode="softcap", softcap=30.0, softcap_backend="cute", softcap_backward_mode="analytical")
     q, k, v, _ = _qkv(1, 1, 1, 128, 80)
-    with pytest.raises(NotImplementedError, match="pwl1_safe_f16"):
-        module(q.to(cuda), k.to(cuda), v.to(cuda))
+    with pytest.raises(NotImplementedError, match="cute"):  # at build time, before any launch
+        build_fa4_module(cfg, head_dim=128)(q.to(cuda), k.to(cuda), v.to(cuda))
     with pytest.raises(TypeError, match="bfloat16"):
         build_fa4_module(FA4Config(), head_dim=128)(q.half().to(cuda), k.half().to(cuda), v.half().to(cuda))
 

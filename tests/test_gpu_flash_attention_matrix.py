@@ -36,9 +36,13 @@ def test_forward_matrix(capi, oracle, cuda, mode, d, causal):
     ok, info = _close(got, ref_out, rel=1.5e-2)
     assert ok, ("out", mode, d, causal, info)
     if ref_lse is not None:
-        # hardware modes: FP32 exponent sums; programs: the same programs in
-        # the reference, so only the BF16 products and summation order differ
-        bound = 1e-3 if mode in ("softmax_native", "softcap_native") else 2e-2
+        # hardware modes: FP32 exponent sums; exp2 programs: the same programs
+        # in the reference, given the same exponents (it follows the kernel's
+        # running maximum), so only the dot products' rounding and the
+        # summation order differ (measured up to 1.5e-3); the softcap D4
+        # program: its BF16-rounded capped scores
+        bound = (1e-3 if mode in ("softmax_native", "softcap_native") else 4e-3 if mode.startswith("softmax")
+                 else 2e-2)
         err = (lse.cpu() - ref_lse).abs().max().item()
         assert err < bound, ("lse", mode, d, causal, err)
 
@@ -290,3 +294,33 @@ def test_backward_any_length_equals_padded(capi, cuda, s, d, hq, hkv):
                        route=route, bias=bias)[:3]
             for name, a, b in zip(("dq", "dk", "dv"), got, want):
                 assert torch.equal(a.view(torch.int32), b[:, :s].contiguous().view(torch.int32)), (mode, causal, name)
+
+
+@pytest.mark.parametrize("route", [4, 6])
+@pytest.mark.parametrize("mode", ["softmax_pwl2_safe_f16", "softmax_pwl1_safe_f16", "softmax_d2_safe_f16",
+                                  "softmax_pwl2_f16"])
+def test_packed_f16_programs_odd_query_block_count(capi, oracle, cuda, mode, route):
+    """An odd number of 128-query blocks at head_dim 128: the packed FP16
+    exp2 programs run 8-wave blocks there too, the last one holding 128
+    queries past the sequence.  Non-causal S = 333 (ragged) against the
+    reference; causal S = 384 (aligned) bit for bit against the first 384
+    queries of the same operands at S = 512, an even block count, where each
+    wave sees the same key tiles in the same order."""
+    seed = 1700 + M[mode] + route
+    print(f"fwd odd blocks {mode} route {route} seed {seed}", flush=True)
+    scale = 1 / math.sqrt(128)
+    q, k, v, _ = _inputs(1, 4, 2, 333, seed)
+    out, lse = fwd(capi, cuda, q, k, v, mode, False, scale, route=route)
+    ref_out, ref_lse = reference_fwd(oracle, q, k, v, mode, False, scale, 30.0, route)
+    got = out.cpu().float()
+    assert torch.isfinite(got).all()
+    ok, info = _close(got, ref_out, rel=1.5e-2)
+    assert ok, ("out", mode, route, info)
+    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2
+
+    q, k, v, _ = _inputs(1, 4, 2, 512, seed + 1)
+    out_l, lse_l = fwd(capi, cuda, q, k, v, mode, True, scale, route=route)
+    out_s, lse_s = fwd(capi, cuda, q[:, :384].contiguous(), k[:, :384].contiguous(), v[:, :384].contiguous(),
+                       mode, True, scale, route=route)
+    assert torch.equal(out_s.view(torch.int16), out_l[:, :384].view(torch.int16))
+    assert torch.equal(lse_s, lse_l[..., :384])

@@ -61,7 +61,7 @@ def _max_in_first_tile(seed, s=256, d=128):
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("mode,route", [("softmax_pwl2", 10), ("softmax_pwl2", 6), ("softmax_d2", 6),
                                         ("softmax_d2", 12), ("softmax_pwl2_safe_f16", 12),
-                                        ("softmax_pwl2_safe", 10)])
+                                        ("softmax_pwl2_safe", 10), ("softmax_d2_safe_bf16", 12)])
 def test_forward_routing_is_exact(capi, oracle, cuda, mode, route, causal):
     q, k, v, _ = _max_in_first_tile(700 + route + 3 * causal)
     scale = 1 / math.sqrt(128)

@@ -237,6 +237,73 @@ def test_exp2_full_range_errors_match_published_metrics(oracle, kind, golden):
         assert abs(g - want) <= 2e-8 * max(1.0, want / 1e-4) + 1e-6 * want, (got, golden)
 
 
+def _fractional_h2_error_input():
+    """make_fractional_h2(1 << 20) of autonumerics_zero/cuda_benchmarks/
+    benchmark_exp2_pwl2.cu:325-333: pairs ((2i mod 65521) / 65521,
+    (2i + 1 mod 65521) / 65521) in FP32, rounded to FP16."""
+    i = np.arange(1 << 20, dtype=np.int64)
+    x = (((2 * i) % 65521).astype(np.float32) / np.float32(65521.0)).astype(np.float16)
+    y = (((2 * i + 1) % 65521).astype(np.float32) / np.float32(65521.0)).astype(np.float16)
+    return np.stack([x, y], axis=1).reshape(-1).astype(np.float32)
+
+
+def test_exp2_pwl2_f16_reproduces_the_published_fractional_errors(oracle):
+    """The reference's FP16 hinge (FractionalPwl2Hinge,
+    benchmark_exp2_pwl2.cu:84-99) on its own fractional input set: max_abs,
+    max_rel and rmse against exp2 in double (error_fractional_h2, :346-371)
+    equal evidence/report-data/exp2_pwl2_isolated_gb200.json "fractional_h2" /
+    "pwl2_hinge" to every printed digit.  This pins the FP16 arithmetic the
+    packed programs share: RNE to FP16, the hinge's subtract and maximum, and
+    two single-rounding FMAs in that order."""
+    f = _fractional_h2_error_input()
+    p = oracle.exp2_fraction(oracle.EXP2_PWL2_F16, f).astype(np.float64)
+    ref = np.exp2(f.astype(np.float64))
+    a = np.abs(p - ref)
+    got = (a.max(), (a / ref).max(), np.sqrt((a * a).mean()))
+    for g, want in zip(got, (0.018854463, 0.010940964, 0.00662452431)):
+        assert abs(g - want) <= 5e-10 + 1e-9 * want, (got, want)
+
+
+@pytest.mark.parametrize("kind,max_rel,lo,hi", [
+    # appendix_exp2.tex table: D1 endpoint constrained 6.148e-2
+    ("EXP2_PWL1_SAFE", 6.148e-2, 6.1475e-2, 6.1485e-2),
+    # the fit errors (PWL1 6.148e-2, PWL2 1.074e-2, D2 2.679e-3) plus the
+    # 16-bit rounding of the fraction and of each step
+    ("EXP2_PWL1_SAFE_F16", None, 6.148e-2, 6.30e-2),
+    ("EXP2_PWL2_SAFE_BF16", None, 1.074e-2, 1.60e-2),
+    ("EXP2_D2_SAFE_F16", None, 2.679e-3, 3.4e-3),
+    ("EXP2_D2_SAFE_BF16", None, 2.679e-3, 7.0e-3),
+])
+def test_exp2_remaining_backends_endpoints_and_fit(oracle, kind, max_rel, lo, hi):
+    """The remaining FA4 exp2 backends (this build's 16-bit definitions of the
+    appendix's forms): p(0) = 1 and p(1) = 2 after their rounding, so every
+    integer gives an exact power of two and the value just below an integer
+    meets the next power; maximum relative error on the fit's grid within the
+    form's published fit error and that error plus the 16-bit rounding."""
+    k = getattr(oracle, kind)
+    g = np.linspace(0.0, 1.0, 1_000_001)
+    p = oracle.exp2_fraction(k, g.astype(np.float32)).astype(np.float64)
+    assert p[0] == 1.0 and p[-1] == 2.0
+    rel = np.abs(p / np.exp2(g.astype(np.float32).astype(np.float64)) - 1).max()
+    assert lo <= rel < hi, rel
+    n = np.arange(-126, 9, dtype=np.float32)
+    assert np.array_equal(oracle.exp2(k, n, False), np.exp2(n.astype(np.float64)).astype(np.float32))
+    low = np.array([-np.inf, -127.0, -1000.0, np.nan], dtype=np.float32)
+    assert oracle.exp2(k, low, False).view(np.uint32).tolist() == [0, 0, 0, 0]
+
+
+def test_exp2_d2_noclamp_is_d2_above_the_clamp(oracle):
+    """d2_safe_noclamp is the D2 safe program without the -127 clamp: equal bit
+    for bit from -127 up; below it the exponent field wraps (FA4's unsafe
+    variant), so a score far below the row maximum is not 0."""
+    x = np.concatenate([np.linspace(-127.0, 8.0, 100_001, dtype=np.float32),
+                        np.array([0.0, -0.0, -1e-30, -126.5], dtype=np.float32)])
+    assert np.array_equal(oracle.exp2(oracle.EXP2_D2_NOCLAMP, x, False).view(np.uint32),
+                          oracle.exp2(oracle.EXP2_D2, x, False).view(np.uint32))
+    below = oracle.exp2(oracle.EXP2_D2_NOCLAMP, np.array([-130.0, -200.0], dtype=np.float32), False)
+    assert (below != 0).all()
+
+
 def test_exp2_pwl2_safe_coefficients_endpoints_and_published_errors(oracle):
     """B5 PWL2 "safe" hinge p(f) = 1 + a f + c max(f - 1/2, 0)
     (extras/paper/manuscript/appendix_exp2.tex:22-27).
