@@ -56,6 +56,8 @@ struct AttnParams {
     float cap;       // softcap
     float sig_bias;  // sigmoid attention: p = sigmoid(s + sig_bias)
     int causal;
+    int route;       // exp2 route of the kRouteRuntime instantiations
+    uint32_t rmask;  // and its periodic mask (routes up to 32)
 };
 
 // Softmax scores of 16 accumulator registers (one 32-key tile), in the
@@ -87,25 +89,33 @@ __device__ __forceinline__ void softmax_exponents(const f32x16_t& acc, float sca
     }
 }
 
-// exp2 of a softmax exponent (x <= 8 under the lazy rescale).  Exponent
-// slot i (kt * 16 + r) takes the mode's polynomial when i % ROUTE < 4, the
-// rest v_exp_f32: four of every ROUTE (FA4's routed exp2, four lanes per
-// group of exp2_emu_freq, src/sfu_repro/fa4.py:313-353); ROUTE 4 routes all.
-// The slot is a function of the key index alone (16 bit5 + 4 bits3..4 +
-// bits0..1), which the backward evaluates to route the same keys.
+// Exponent slot i (kt * 16 + r) of the tile takes the mode's polynomial
+// (FA4's routed exp2, four lanes per group of exp2_emu_freq,
+// src/sfu_repro/fa4.py:313-353): i % ROUTE < 4 for a template route (ROUTE 4
+// routes all), bit i of the tile's mask rmask (tile_route_mask) for
+// kRouteRuntime (wave-uniform, so the decision is a scalar branch).  The slot
+// is a function of the key index alone (16 bit5 + 4 bits3..4 + bits0..1),
+// which the backward evaluates to route the same keys.
+template <int ROUTE>
+__device__ __forceinline__ bool slot_routed(int i, uint32_t rmask) {
+    if constexpr (ROUTE == kRouteRuntime) return (rmask >> i) & 1u;
+    else return ROUTE >= 4 && i % ROUTE < 4;
+}
+
+// exp2 of a softmax exponent (x <= 8 under the lazy rescale) in slot i.
 template <int MODE, int ROUTE>
-__device__ __forceinline__ float softmax_exp2(float x, int i) {
+__device__ __forceinline__ float softmax_exp2(float x, int i, uint32_t rmask) {
     if constexpr (attn_has_exp2_program(MODE))
-        if (ROUTE >= 4 && i % ROUTE < 4) return exp2_lane<attn_exp2_kind<MODE>()>(x);
+        if (slot_routed<ROUTE>(i, rmask)) return exp2_lane<attn_exp2_kind<MODE>()>(x);
     return __builtin_amdgcn_exp2f(x);
 }
 
 // Two exponents, slots i (even) and i + 1: the routing groups of four start
-// at multiples of ROUTE (even), so one decision routes both, and the packed
-// FP16 program evaluates them with one instruction per step.
+// at even slots (the route is even), so one decision routes both, and the
+// packed FP16 program evaluates them with one instruction per step.
 template <int MODE, int ROUTE>
-__device__ __forceinline__ void softmax_exp2_pair(float x0, float x1, int i, float& y0, float& y1) {
-    if (ROUTE >= 4 && i % ROUTE < 4) {
+__device__ __forceinline__ void softmax_exp2_pair(float x0, float x1, int i, uint32_t rmask, float& y0, float& y1) {
+    if (slot_routed<ROUTE>(i, rmask)) {
         exp2_pair<attn_exp2_kind<MODE>()>(x0, x1, y0, y1);
     } else {
         y0 = __builtin_amdgcn_exp2f(x0);
@@ -234,7 +244,7 @@ __device__ __forceinline__ void tile_softmax_state(const AttnParams& p, const f3
 template <int MODE, int ROUTE, bool MASKED>
 __device__ __forceinline__ bf16x8_t tile_probs8(const AttnParams& p, const f32x16_t (&sacc)[2],
                                                 const float (&x)[2][16], int kt, int cc, float sl, float m,
-                                                int diag, float (&ls)[4]) {
+                                                int diag, uint32_t rmask, float (&ls)[4]) {
     float pr[8];
     if constexpr (attn_is_sigmoid(MODE)) {
 #pragma unroll
@@ -250,7 +260,7 @@ __device__ __forceinline__ bf16x8_t tile_probs8(const AttnParams& p, const f32x1
             const int r = 8 * cc + e;
             float ev0, ev1;
             softmax_exp2_pair<MODE, ROUTE>(__builtin_fmaf(x[kt][r], sl, -m), __builtin_fmaf(x[kt][r + 1], sl, -m),
-                                           kt * 16 + r, ev0, ev1);
+                                           kt * 16 + r, rmask, ev0, ev1);
             pr[e] = key_masked<MASKED>(diag, kt, r) ? 0.0f : ev0;
             pr[e + 1] = key_masked<MASKED>(diag, kt, r + 1) ? 0.0f : ev1;
             ls[e & 3] += pr[e];
@@ -260,7 +270,7 @@ __device__ __forceinline__ bf16x8_t tile_probs8(const AttnParams& p, const f32x1
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int r = 8 * cc + e;
-            const float ev = softmax_exp2<MODE, ROUTE>(__builtin_fmaf(x[kt][r], sl, -m), kt * 16 + r);
+            const float ev = softmax_exp2<MODE, ROUTE>(__builtin_fmaf(x[kt][r], sl, -m), kt * 16 + r, rmask);
             // v_exp_f32(-inf) is 0; the polynomial programs clamp at -127
             pr[e] = (attn_has_exp2_program(MODE) && key_masked<MASKED>(diag, kt, r)) ? 0.0f : ev;
             ls[e & 3] += pr[e];
@@ -299,7 +309,7 @@ template <int MODE, int ROUTE, bool MASKED, int HD>
 __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t* __restrict__ ks,
                                             const uint16_t* __restrict__ vrow, const bf16x8_t (&qf)[HD / 16],
                                             f32x16_t (&oacc)[HD / 32], float& m, float& l, int diag,
-                                            int h, int c32, float inv_cap) {
+                                            int h, int c32, float inv_cap, uint32_t rmask) {
     f32x16_t sacc[2];
     tile_scores<HD, !fwd_program_heavy<MODE>()>(ks, qf, sacc, h, c32);
     float x[2][16];
@@ -310,7 +320,7 @@ __device__ __forceinline__ void attend_tile(const AttnParams& p, const uint16_t*
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
-            tile_pv8<HD>(vrow, kt, cc, tile_probs8<MODE, ROUTE, MASKED>(p, sacc, x, kt, cc, sl, m, diag, ls), oacc);
+            tile_pv8<HD>(vrow, kt, cc, tile_probs8<MODE, ROUTE, MASKED>(p, sacc, x, kt, cc, sl, m, diag, rmask, ls), oacc);
     if constexpr (!attn_is_sigmoid(MODE)) l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 }
 
@@ -444,10 +454,13 @@ __global__ void __launch_bounds__(64 * W)
         if (more) load(k0 + kAttnBlockK);  // in flight during this tile's math
         if (k0 <= whi) {  // wave-uniform: some key of the tile is visible
             const int diag = (int)(k0 - klast) + 4 * h;
+            const uint32_t rmask = ROUTE == kRouteRuntime ? tile_route_mask(p.route, p.rmask, (int)kb) : 0u;
             if (k0 + kAttnBlockK - 1 > wlo)
-                attend_tile<MODE, ROUTE, true, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap);
+                attend_tile<MODE, ROUTE, true, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap,
+                                                   rmask);
             else
-                attend_tile<MODE, ROUTE, false, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap);
+                attend_tile<MODE, ROUTE, false, HD>(p, ks[buf], vs[buf] + vlane, qf, oacc, m, l, diag, h, c32, inv_cap,
+                                                    rmask);
         }
         if (more) store(buf ^ 1, k0 + kAttnBlockK);
         __syncthreads();
@@ -482,13 +495,9 @@ using namespace pt;
 
 namespace {
 
-constexpr int kRoutes[] = {4, 6, 8, 10, 12, 16, 20, 24, 32};
-
-bool route_supported(int route) {
-    for (int r : kRoutes)
-        if (r == route) return true;
-    return false;
-}
+// any even route >= 4 (FA4's validation, src/sfu_repro/fa4.py:226-233);
+// the ones without a template instantiation take kRouteRuntime
+bool route_supported(int route) { return route >= 4 && route % 2 == 0; }
 
 // Waves (32 queries each) per block.  head_dim 128 runs 8-wave blocks (each
 // staged K / V tile serves 256 queries; one block per CU) except the modes
@@ -536,7 +545,8 @@ void launch_routed(const AttnParams& prm, dim3 grid, hipStream_t st, int route, 
         case 20: launch_fwd<MODE, 20>(prm, grid, st, hd); break;
         case 24: launch_fwd<MODE, 24>(prm, grid, st, hd); break;
         case 32: launch_fwd<MODE, 32>(prm, grid, st, hd); break;
-        default: launch_fwd<MODE, 4>(prm, grid, st, hd); break;
+        case 4: launch_fwd<MODE, 4>(prm, grid, st, hd); break;
+        default: launch_fwd<MODE, kRouteRuntime>(prm, grid, st, hd); break;
     }
 }
 
@@ -575,7 +585,7 @@ extern "C" int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* ls
     if (batch > 65535 || qblocks > 65535 || q_heads > 0x7fffffff) return hipErrorInvalidValue;
     AttnParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out, lse,
                    st[0], st[1], st[2], st[3], q_heads, kv_heads, seq, valid_keys, scale,
-                   cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0};
+                   cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0, exp2_route, host_route_mask(exp2_route)};
     const dim3 grid((unsigned)q_heads, (unsigned)qblocks, (unsigned)batch);
     hipStream_t hst = hs(stream);
     switch (mode) {

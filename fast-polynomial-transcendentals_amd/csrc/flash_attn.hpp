@@ -61,6 +61,48 @@ constexpr int attn_exp2_kind() {
                : kExp2Native;
 }
 
+// exp2 routing (FA4's exp2_emu_freq, any even route >= 4;
+// src/sfu_repro/fa4.py:226-233).  Each lane holds 32 exponents of a 64-key
+// tile; exponent slot i (kt * 16 + r of the forward's accumulators) takes the
+// polynomial when bit i of the tile's routing mask is set, the rest
+// v_exp_f32.  Up to 32 the pattern restarts at every tile, slot % route < 4;
+// above 32 it runs on over the row's tiles, (32 tile + slot) % route < 4, so
+// four of every `route` exponents of a row are routed either way.  Routes 4
+// (every exponent), 6, 8, 10, 12, 16, 20, 24 and 32 are template arguments
+// (the pattern folds into each register's code); kRouteRuntime takes any
+// other route from the kernel arguments, with the host's mask for routes up
+// to 32 and route_mask_running per tile above.
+constexpr int kRouteRuntime = 2;
+constexpr bool route_partial(int route) { return route > 4 || route == kRouteRuntime; }
+
+// The mask of a route of 4..32, the same for every tile.
+__host__ __device__ constexpr uint32_t route_mask_periodic(int route) {
+    uint32_t m = 0;
+    for (int i = 0; i < 32; ++i)
+        if (i % route < 4) m |= 1u << i;
+    return m;
+}
+
+// The mask of the tile-th tile of a row for a route above 32.  Slot i holds
+// g = base + i with base = 32 tile mod route and base + i < 2 route, so
+// g mod route < 4 for g in [0, 4) or [route, route + 4).  tile < 2^17 (the
+// launchers bound S below 2^23), so 32 tile fits an int.
+__host__ __device__ constexpr uint32_t route_mask_running(int route, int tile) {
+    const int base = (32 * tile) % route;
+    const uint32_t head = base < 4 ? (1u << (4 - base)) - 1u : 0u;
+    const uint32_t next = route - base < 32 ? 0xFu << (route - base) : 0u;
+    return head | next;
+}
+
+// Per-tile mask of a kRouteRuntime launch: periodic_mask is the host's
+// route_mask_periodic(route) when route <= 32.
+__device__ __forceinline__ uint32_t tile_route_mask(int route, uint32_t periodic_mask, int tile) {
+    return route <= 32 ? periodic_mask : route_mask_running(route, tile);
+}
+
+// Host side: the periodic mask passed to the kernels (0 without routing).
+constexpr uint32_t host_route_mask(int route) { return route >= 4 && route <= 32 ? route_mask_periodic(route) : 0u; }
+
 constexpr int kHeadDim = 128;
 constexpr int kAttnBlockQ = 128;  // 4 waves x 32 queries
 constexpr int kAttnBlockK = 64;   // keys per staged tile

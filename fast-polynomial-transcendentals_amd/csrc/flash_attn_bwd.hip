@@ -61,14 +61,24 @@ struct AttnBwdParams {
     int64_t hq, hkv, seq;
     float scale, cap, sig_bias;
     int causal;
+    int route;       // exp2 route of the kRouteRuntime instantiations
+    uint32_t rmask;  // and its periodic mask (routes up to 32)
 };
 
 // Routing slot of a key: the position of its exponent among the 32 a lane
 // of the forward kernel holds per 64-key tile (kt * 16 + r).  The forward
-// routes slot % route < 4 to the polynomial; the backward uses the same
-// function of the key, so all three kernels route the same exponents.
+// routes the slots of the tile's routing mask to the polynomial (slot %
+// route < 4 up to route 32); the backward uses the same function of the
+// key, so all three kernels route the same exponents.
 __device__ __forceinline__ int route_slot(int64_t key) {
     return 16 * (int)((key >> 5) & 1) + 4 * (int)((key >> 3) & 3) + (int)(key & 3);
+}
+
+template <int ROUTE>
+__device__ __forceinline__ bool key_routed(const AttnBwdParams& p, int64_t key) {
+    if constexpr (ROUTE == kRouteRuntime)
+        return (tile_route_mask(p.route, p.rmask, (int)(key >> 6)) >> route_slot(key)) & 1u;
+    else return ROUTE > 4 && route_slot(key) % (ROUTE > 4 ? ROUTE : 1) < 4;
 }
 
 
@@ -89,7 +99,7 @@ __device__ __forceinline__ void score_grad2(const AttnBwdParams& p, float inv_ca
         const float x0 = __builtin_fmaf(a0, sl, -lse0), x1 = __builtin_fmaf(a1, sl, -lse1);
         if constexpr (attn_has_exp2_program(MODE) && ROUTE == 4) {
             exp2_pair<attn_exp2_kind<MODE>()>(x0, x1, p0, p1);
-        } else if constexpr (attn_has_exp2_program(MODE) && ROUTE > 4) {
+        } else if constexpr (attn_has_exp2_program(MODE) && route_partial(ROUTE)) {
             if (any_poly) {
                 float q0, q1;
                 exp2_pair<attn_exp2_kind<MODE>()>(x0, x1, q0, q1);
@@ -317,7 +327,7 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
     const int64_t key0 = kb * kKeys + kgroup * 16;
     const int64_t key = key0 + kl;                // this lane's key
     const float inv_cap = 1.0f / p.cap;
-    const bool poly_key = ROUTE > 4 && route_slot(key) % ROUTE < 4;
+    const bool poly_key = key_routed<ROUTE>(p, key);
     // with route 32 three waves in four hold no routed key
     const bool wave_poly = __builtin_amdgcn_ballot_w64(poly_key) != 0;
 
@@ -702,16 +712,20 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
             // 16 (bit 5) + 4 (bits 3-4) + bits 0-1 ignores key bit 2 (h) and
             // the pair shares a group of four, so with the tile parity (key
             // bit 5) fixed the decision is a compile-time constant per pair
+            // (a wave-uniform bit of the 64-key tile's mask for kRouteRuntime)
+            const uint32_t rmask = ROUTE == kRouteRuntime ? tile_route_mask(p.route, p.rmask, (int)(k0 >> 6)) : 0u;
             auto scores = [&](auto par_c) {
                 constexpr int kPar = decltype(par_c)::value;
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) {
-                    const bool poly = ROUTE > 4 && (16 * kPar + 4 * (r >> 2) + (r & 3)) % (ROUTE > 4 ? ROUTE : 1) < 4;
+                    const int slot = 16 * kPar + 4 * (r >> 2) + (r & 3);
+                    const bool poly = ROUTE == kRouteRuntime ? (rmask >> slot) & 1u
+                                                             : ROUTE > 4 && slot % (ROUTE > 4 ? ROUTE : 1) < 4;
                     score_grad2<MODE, GRAD, ROUTE>(p, inv_cap, sacc[r], sacc[r + 1], pacc[r], pacc[r + 1], lse2,
                                                    lse2, dl, dl, poly, poly, pr_[r], pr_[r + 1], ds[r], ds[r + 1]);
                 }
             };
-            if (ROUTE > 4 && ((k0 >> 5) & 1)) scores(std::integral_constant<int, 1>{});
+            if (route_partial(ROUTE) && ((k0 >> 5) & 1)) scores(std::integral_constant<int, 1>{});
             else scores(std::integral_constant<int, 0>{});
             if (need_mask) {
 #pragma unroll
@@ -807,7 +821,8 @@ void launch_bwd_routed(const AttnBwdParams& prm, int64_t batch, hipStream_t st, 
         case 20: launch_bwd<MODE, kGradNatural, 20>(prm, batch, st, hd); break;
         case 24: launch_bwd<MODE, kGradNatural, 24>(prm, batch, st, hd); break;
         case 32: launch_bwd<MODE, kGradNatural, 32>(prm, batch, st, hd); break;
-        default: launch_bwd<MODE, kGradNatural, 4>(prm, batch, st, hd); break;
+        case 4: launch_bwd<MODE, kGradNatural, 4>(prm, batch, st, hd); break;
+        default: launch_bwd<MODE, kGradNatural, kRouteRuntime>(prm, batch, st, hd); break;
     }
 }
 
@@ -835,10 +850,8 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
                          : mode == kAttnSigmoidB3 ? (grad == kGradAlgebraic || grad == kGradDirect)
                                                   : grad == kGradNatural;
     if (!grad_ok) return hipErrorInvalidValue;
-    if (attn_has_exp2_program(mode) && !(exp2_route == 0 || exp2_route == 4 || exp2_route == 6 ||
-                                         exp2_route == 8 || exp2_route == 10 || exp2_route == 12 ||
-                                         exp2_route == 16 || exp2_route == 20 || exp2_route == 24 ||
-                                         exp2_route == 32))
+    // 0 (hardware exp2) or any even route >= 4 (src/sfu_repro/fa4.py:226-233)
+    if (attn_has_exp2_program(mode) && !(exp2_route == 0 || (exp2_route >= 4 && exp2_route % 2 == 0)))
         return hipErrorInvalidValue;
     AttnStrides st[8];
     for (int i = 0; i < 8; ++i) {
@@ -873,7 +886,8 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
     AttnBwdParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
                       sig ? nullptr : lse, sig ? nullptr : delta, (uint16_t*)dq, (uint16_t*)dk,
                       (uint16_t*)dv, grouped ? dkv_workspace : nullptr, st[0], st[1], st[2], st[4], st[5], st[6], st[7], q_heads, kv_heads,
-                      seq, scale, cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0};
+                      seq, scale, cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0, exp2_route,
+                      host_route_mask(exp2_route)};
     switch (mode) {
         case kAttnSoftmaxNative: launch_bwd<kAttnSoftmaxNative, kGradNatural, 0>(prm, batch, hst, hd); break;
         case kAttnSoftmaxExp2D2: launch_bwd_routed<kAttnSoftmaxExp2D2>(prm, batch, hst, exp2_route, hd); break;

@@ -21,9 +21,11 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
   the same hinge on the fraction rounded to FP16, packed FP16, and the rest
   of FA4's list: ``pwl1_safe`` (1 + f), ``pwl1_safe_f16``, ``pwl2_safe_bf16``,
   ``d2_safe_noclamp`` (no -127 clamp), ``d2_safe_f16``, ``d2_safe_bf16`` and
-  ``pwl2_f16`` (the reference's FP16 hinge); see spline_ops_hip.h), key j
-  when slot(j) % freq < 4 with slot(j) = 16 bit5(j) + 4 bits3..4(j) +
-  bits0..1(j), in the forward and the backward alike;
+  ``pwl2_f16`` (the reference's FP16 hinge); see spline_ops_hip.h), for any
+  even ``exp2_emu_freq`` >= 4: key j when slot(j) % freq < 4 with slot(j) =
+  16 bit5(j) + 4 bits3..4(j) + bits0..1(j) up to freq 32, and when
+  (32 (j // 64) + slot(j)) % freq < 4 above it, in the forward and the
+  backward alike;
 * softcap: ``softcap > 0`` with no score_mod -> FP32 hardware tanh; a
   score_mod from ``create_softcap_scoremod_backend(backend="device")`` ->
   the D4 BF16 program (B2), its backward per ``backward_mode``;
@@ -84,7 +86,6 @@ BUILT_EXP2_BACKENDS = {"d3": MODE_SOFTMAX_D3, "d2_safe": MODE_SOFTMAX_D2, "pwl2"
                        **{name: MODE_SOFTMAX_PWL1_SAFE + i for i, name in enumerate(
                            ("pwl1_safe", "pwl1_safe_f16", "pwl2_safe_bf16", "d2_safe_noclamp", "d2_safe_f16",
                             "d2_safe_bf16", "pwl2_f16"))}}
-SUPPORTED_ROUTES = (0, 4, 6, 8, 10, 12, 16, 20, 24, 32)
 _SOFTCAP_BWD = {"analytical": GRAD_ANALYTICAL, "ste": GRAD_STE, "exact_1mt2": GRAD_EXACT_1MT2}
 
 
@@ -259,8 +260,8 @@ def select_forward(*, seqlen: int, softcap: float = 0.0, score_mod=None, sigmoid
             f"exp2 backend {exp2_emu_backend!r} is not part of the reference tree; built: "
             f"{sorted(BUILT_EXP2_BACKENDS)}")
     route = int(exp2_emu_freq)
-    if route not in SUPPORTED_ROUTES:
-        raise NotImplementedError(f"exp2 routing frequency {route} is not built; built: {SUPPORTED_ROUTES[1:]}")
+    if route < 4 or route % 2:
+        raise ValueError(f"exp2 routing frequency must be 0 or an even integer >= 4, got {route}")
     return BUILT_EXP2_BACKENDS[exp2_emu_backend], route, 1.0, 0.0
 
 

@@ -527,12 +527,15 @@ int launch_flash_attention_fwd_bf16(void* out, const void* q, const void* k, con
  *     wrap, so the backward needs a finite lse), 19 d2_safe_f16,
  *     20 d2_safe_bf16, 21 pwl2_f16 (clamped at -126, as mode 12).
  * sigmoid_bias: the bias of the hardware and D3..D6 sigmoid modes.
- * exp2_route (modes 1, 2 and 12..21): key j of a query row takes the polynomial when
- * slot(j) % exp2_route < 4, else v_exp_f32, with slot(j) = 16 bit5(j) +
- * 4 bits3..4(j) + bits0..1(j) (the slot of j's exponent in the kernel's
- * registers), so four of every exp2_route exponents are routed; one of 4
- * (all), 6, 8, 10, 12, 16, 20, 24, 32 (FA4's exp2_emu_freq,
- * src/sfu_repro/fa4.py:223-231). */
+ * exp2_route (modes 1, 2 and 12..21): any even value >= 4 (FA4's
+ * exp2_emu_freq, src/sfu_repro/fa4.py:223-233).  Key j of a query row takes
+ * the polynomial, else v_exp_f32, when slot(j) % exp2_route < 4 for routes
+ * up to 32, with slot(j) = 16 bit5(j) + 4 bits3..4(j) + bits0..1(j) (the
+ * slot of j's exponent among the 32 a lane holds per 64-key tile), and when
+ * (32 (j / 64) + slot(j)) % exp2_route < 4 above 32, so four of every
+ * exp2_route exponents are routed (4: all).  Routes 4, 6, 8, 10, 12, 16, 20,
+ * 24 and 32 run kernels specialised for them; the others read the pattern
+ * from the kernel arguments. */
 int launch_flash_attention_fwd_strided_bf16(void* out, float* lse, const void* q, const void* k,
                                             const void* v, int64_t batch, int64_t q_heads,
                                             int64_t kv_heads, int64_t seq, int64_t head_dim,
@@ -573,8 +576,8 @@ int launch_flash_attention_fwd_strided_keys_bf16(void* out, float* lse, const vo
  *   4 / 5      mode 6 only: y (1 - y) (algebraic) / the B3 factored D4
  *              derivative (direct).
  * exp2_route (modes 1, 2 and 12..21): 0 hardware exp2, 4 the polynomial everywhere,
- * 6..32 the polynomial for the keys the forward routes with that value
- * (FA4's exp2_emu_freq_bwd). */
+ * any other even value the polynomial for the keys the forward routes with
+ * that value (FA4's exp2_emu_freq_bwd). */
 int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float* delta,
                                             float* dkv_workspace, const void* q, const void* k, const void* v,
                                             const void* out, const void* dout, const float* lse,

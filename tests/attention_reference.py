@@ -28,6 +28,15 @@ def route_slot(keys):
     return 16 * ((keys >> 5) & 1) + 4 * ((keys >> 3) & 3) + (keys & 3)
 
 
+def routed_keys(n, route):
+    """Keys 0..n-1 whose exponent takes the polynomial: slot % route < 4 up to
+    route 32 (the pattern restarts at every 64-key tile); above 32 the slot
+    runs on over the tiles, (32 (j // 64) + slot) % route < 4."""
+    keys = torch.arange(n)
+    g = route_slot(keys) if route <= 32 else 32 * (keys >> 6) + route_slot(keys)
+    return (g % route) < 4
+
+
 def default_bias(mode, s):
     return -math.log(s) if mode == "sigmoid_native" or mode.startswith("sigmoid_d") else 0.0
 
@@ -54,7 +63,7 @@ def probs_and_grad(oracle, a, mode, grad, scale, cap, bias, lse2, route):
         if mode in EXP2_KIND and route:
             pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], _exp2_arg(mode, x).numpy().reshape(-1),
                                               out_bf16=False)).reshape(shape)
-            sel = (route_slot(torch.arange(shape[-1])) % route) < 4
+            sel = routed_keys(shape[-1], route)
             p = torch.where(sel, pp, p)
         return p, torch.ones_like(p)
     if mode == "softcap_native":
@@ -140,7 +149,7 @@ def reference_fwd(oracle, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=
     """(out [B, S, H, D], lse [B, H, S]) in float32; lse is None for the
     sigmoid modes.  Softmax exponents are taken relative to the running
     maximum the fused forward holds at each key's tile (lazy_row_max), then
-    rescaled to the final one; routed keys (route_slot % route < 4) take the
+    rescaled to the final one; routed keys (routed_keys) take the
     mode's exp2 program."""
     qf, kf, vf = _heads(q, k, v)
     a = qf @ kf.transpose(-1, -2)
@@ -165,7 +174,7 @@ def reference_fwd(oracle, q, k, v, mode, causal, scale, cap=30.0, route=4, bias=
     if mode in EXP2_KIND:
         pp = torch.from_numpy(oracle.exp2(EXP2_KIND[mode], _exp2_arg(mode, x - mk).numpy().reshape(-1),
                                           out_bf16=False)).reshape(x.shape)
-        sel = (route_slot(torch.arange(n)) % route) < 4
+        sel = routed_keys(n, route)
         e = torch.where(sel, pp, e).masked_fill(mask, 0.0)
     e = (e.double() * torch.exp2((mk - m).double())).float()  # the rescales as m moves
     l = e.sum(-1, keepdim=True)

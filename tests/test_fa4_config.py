@@ -178,8 +178,11 @@ def test_forward_program_selection():
     assert sel(seqlen=256, exp2_emu_backend="pwl2_f16", exp2_emu_freq=32)[:2] == (rt.MODE_SOFTMAX_PWL1_SAFE + 6, 32)
     with pytest.raises(NotImplementedError, match="d2_safe_bf16_fast"):
         sel(seqlen=256, exp2_emu_backend="d2_safe_bf16_fast", exp2_emu_freq=12)
-    with pytest.raises(NotImplementedError, match="routing frequency 14"):
-        sel(seqlen=256, exp2_emu_backend="d3", exp2_emu_freq=14)
+    # any even frequency >= 4 (the reference's validation, fa4.py:226-233)
+    assert sel(seqlen=256, exp2_emu_backend="d3", exp2_emu_freq=14)[:2] == (rt.MODE_SOFTMAX_D3, 14)
+    assert sel(seqlen=256, exp2_emu_backend="d2_safe", exp2_emu_freq=128)[:2] == (rt.MODE_SOFTMAX_D2, 128)
+    with pytest.raises(ValueError, match="even integer"):
+        sel(seqlen=256, exp2_emu_backend="d3", exp2_emu_freq=5)
     assert sel(seqlen=256, softcap=30.0) == (rt.MODE_SOFTCAP_NATIVE, 4, 30.0, 0.0)
     mod = rt.create_softcap_scoremod_backend(30.0, degree=4, backend="device")
     assert sel(seqlen=256, score_mod=mod) == (rt.MODE_SOFTCAP_D4, 4, 30.0, 0.0)

@@ -76,8 +76,9 @@ def _run(capi, cuda, q, k, v, mode, causal, scale, cap):
     return out.cpu().float()
 
 
-# S = 384 runs 4-wave (128-query) blocks, S = 512 the 8-wave (256-query)
-# blocks the launcher picks at head_dim 128 for S a multiple of 256
+# S = 384 (three 128-query blocks) runs 4-wave blocks, S = 512 the 8-wave
+# (256-query) blocks the launcher picks at head_dim 128 for an even number of
+# 128-query blocks (the packed FP16 exp2 programs run 8-wave blocks at both)
 @pytest.mark.parametrize("seq", [384, 512])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("mode", [m for m in MODES if m != "sigmoid_b3"])

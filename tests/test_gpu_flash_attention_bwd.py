@@ -231,7 +231,8 @@ def test_rejected_backward_arguments(capi, cuda):
     assert call(4, 0) != 0          # softcap D4 needs a derivative program
     assert call(0, 1) != 0          # analytical only for softcap D4
     assert call(6, 4) != 0          # B3 outside its fitted length
-    assert call(1, 0, route=7) != 0  # unsupported routing
+    assert call(1, 0, route=7) != 0  # odd routes are invalid
+    assert call(1, 0, route=2) != 0  # so are routes below 4 other than 0
     assert call(4, 1, cap=0.0) != 0
     assert call(22, 0) != 0         # past the last mode (21)
     assert call(-1, 0) != 0

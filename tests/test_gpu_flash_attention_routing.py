@@ -135,3 +135,52 @@ def test_backward_seq_384_four_wave_dq(capi, oracle, cuda, mode, route, causal):
         assert torch.isfinite(got).all(), name
         ok, info = _close(got, ref)
         assert ok, (mode, route, causal, name, info)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("mode,route", [("softmax_pwl1_safe", 14), ("softmax_pwl1_safe_f16", 22),
+                                        ("softmax_pwl2_safe", 40), ("softmax_d2_safe_bf16", 64)])
+def test_runtime_routes(capi, oracle, cuda, mode, route, causal):
+    """Routes without a template instantiation (FA4 accepts any even
+    frequency >= 4) read their pattern from the kernel arguments.  Forward:
+    the lse is much closer to the reference routed this way than to hardware
+    exp2, to the shifted routing and, above 32, to the pattern restarted at
+    every 64-key tile (route 32's).  Backward: discriminated the same way at
+    14 and 22, with the PWL1 programs, whose 6.6 % error stands well above
+    the gradients' BF16 noise (PWL2's 1 % barely clears it at route 14); at
+    40 and 64 (one key in 10 or 16 routed) against the reference at the
+    usual tolerance.  All four programs are continuous at integer exponents,
+    so no exponent rounded to the other side of an integer moves a row."""
+    q, k, v, do = _inputs(1, 4, 2, 256, 1900 + route + causal)
+    scale = 1 / math.sqrt(128)
+    print(f"runtime route {mode} {route} causal {causal}", flush=True)
+    out, lse = fwd(capi, cuda, q, k, v, mode, causal, scale, route=route)
+    lse_c = lse.cpu()
+    l_r = reference_fwd(oracle, q, k, v, mode, causal, scale, route=route)[1]
+    alternatives = [reference_fwd(oracle, q, k, v, "softmax_native", causal, scale)[1]]
+    with _shifted_routing():
+        alternatives.append(reference_fwd(oracle, q, k, v, mode, causal, scale, route=route)[1])
+    if route > 32:
+        alternatives.append(reference_fwd(oracle, q, k, v, mode, causal, scale, route=32)[1])
+    err = (lse_c - l_r).abs().mean().item()
+    gap = min((l_r - a).abs().mean().item() for a in alternatives)
+    print(f"  lse err {err:.3g}, gap {gap:.3g}", flush=True)
+    assert gap > 1e-5
+    assert err < 0.1 * gap, (err, gap)
+    got = bwd(capi, cuda, q, k, v, out, do, lse, mode, 0, causal, scale, route=route)[:3]
+    args = (oracle, q, k, v, out, do, lse, mode, 0, causal, scale, 30.0)
+    ref_r = reference_bwd(*args, route, 0.0)
+    for name, g_, r_ in zip(("dq", "dk", "dv"), got, ref_r):
+        assert torch.isfinite(g_).all(), name
+        ok, info = _close(g_, r_)
+        assert ok, (name, info)
+    if route <= 32:
+        flat = lambda ts: torch.cat([t.reshape(-1).double() for t in ts])
+        ref_h = reference_bwd(*args, 0, 0.0)
+        with _shifted_routing():
+            ref_w = reference_bwd(*args, route, 0.0)
+        g, r, h, w = flat(got), flat(ref_r), flat(ref_h), flat(ref_w)
+        e = (g - r).norm().item()
+        print(f"  bwd err {e:.4g}, gap hw {(r - h).norm().item():.4g}, shifted {(r - w).norm().item():.4g}",
+              flush=True)
+        assert e < 0.8 * (r - h).norm().item() and e < 0.8 * (r - w).norm().item()
