@@ -40,11 +40,14 @@ of the last, partial block are zeroed on chip (queries past the sequence get
 an infinite lse and a zero D in the backward), which is the arithmetic of
 operands zero-padded at the end, and nothing past the sequence is stored.
 
-Combinations whose programs are not part of the reference tree (Sollya
-attention fits, mixed SFU/polynomial
-sigmoid lanes, and the ``cute`` backends -- FA4's CuTe FP32 score programs,
-whose coefficients live in FA4) raise ``NotImplementedError`` naming what is
-missing.
+Combinations that are not built raise ``NotImplementedError`` naming what is
+missing: the ``cute`` backends (FA4's CuTe FP32 score programs, whose
+coefficients live in FA4), mixed SFU/polynomial sigmoid lanes, and score
+programs no reference configuration fuses into attention -- softcap tanh at
+degrees other than 4 or from the Sollya rows, sigmoid attention from the
+Sollya rows, direct sigmoid gradients other than B3's.  Their elementwise
+programs are built (spline_ops), but their attention compositions would be
+FA4's choices, which are not in the reference tree.
 """
 
 from __future__ import annotations
@@ -149,10 +152,12 @@ def _check_softcap_program(softcap: float, degree: int, backend: str, coeff_sour
             "part of the reference tree; backend='device' selects the deployed D4 BF16 program")
     if int(degree) != 4:
         raise NotImplementedError(
-            f"softcap degree {degree}: only the D4 BF16 tanh (spline_structs_odd_bf16.cuh:153-179) "
-            "is part of the reference tree")
+            f"softcap degree {degree} is not built into the fused attention: it carries the deployed D4 BF16 tanh "
+            "(spline_structs_odd_bf16.cuh:153-179), the only softcap degree the reference's configurations use")
     if coeff_source != "current":
-        raise NotImplementedError("Sollya softcap fits are not part of the reference tree")
+        raise NotImplementedError(
+            "Sollya softcap fits are not built into the fused attention (the reference's configurations use the "
+            "current D4 program)")
 
 
 def create_softcap_scoremod_backend(softcap: float, degree: int = 4, backend: str = "device",
@@ -232,7 +237,9 @@ def select_forward(*, seqlen: int, softcap: float = 0.0, score_mod=None, sigmoid
         if sigmoid_sfu_res != 0:
             raise NotImplementedError("mixed SFU / polynomial sigmoid lanes are not built")
         if sigmoid_coeff_source != "current":
-            raise NotImplementedError("Sollya sigmoid-attention fits are not part of the reference tree")
+            raise NotImplementedError(
+                "Sollya sigmoid-attention fits are not built into the fused attention (the reference's "
+                "configurations use the current programs)")
         if sigmoid_poly_backend != "device":
             raise NotImplementedError(
                 f"sigmoid_poly_backend={sigmoid_poly_backend!r}: FA4's CuTe FP32 sigmoid polynomial is not part of "
@@ -257,7 +264,7 @@ def select_forward(*, seqlen: int, softcap: float = 0.0, score_mod=None, sigmoid
         return MODE_SOFTMAX_NATIVE, 4, 1.0, 0.0
     if exp2_emu_backend not in BUILT_EXP2_BACKENDS:
         raise NotImplementedError(
-            f"exp2 backend {exp2_emu_backend!r} is not part of the reference tree; built: "
+            f"exp2 backend {exp2_emu_backend!r} is not one of FA4's backends; built: "
             f"{sorted(BUILT_EXP2_BACKENDS)}")
     route = int(exp2_emu_freq)
     if route < 4 or route % 2:
