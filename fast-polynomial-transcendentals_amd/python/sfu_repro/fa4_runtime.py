@@ -37,8 +37,9 @@ keyword arguments the reference passes (``fa4.py:356-428,430-461``):
 
 Sequence lengths: any.  The kernels read no row past the sequence; the rows
 of the last, partial block are zeroed on chip (queries past the sequence get
-an infinite lse and a zero D in the backward), which is the arithmetic of
-operands zero-padded at the end, and nothing past the sequence is stored.
+an infinite lse -- 0 for the unclamped D2 program, whose exp2(-inf) is NaN --
+and a zero D in the backward), which is the arithmetic of operands
+zero-padded at the end, and nothing past the sequence is stored.
 
 Combinations that are not built raise ``NotImplementedError`` naming what is
 missing: the ``cute`` backends (FA4's CuTe FP32 score programs, whose
