@@ -354,6 +354,7 @@ extern "C" int launch_exp2_pwl2_safe_f16_f32(void* y, const void* x, int64_t siz
     extern "C" int launch_exp2_##NAME##_f32(void* y, const void* x, int64_t size, void* stream) {      \
         return launch_exp2<KIND, false>(y, x, size, stream);                                       \
     }
+PT_EXP2_ENTRY(pwl2, kExp2Pwl2)
 PT_EXP2_ENTRY(pwl1_safe, kExp2Pwl1Safe)
 PT_EXP2_ENTRY(pwl1_safe_f16, kExp2Pwl1SafeF16)
 PT_EXP2_ENTRY(pwl2_safe_bf16, kExp2Pwl2SafeBF16)

@@ -1150,6 +1150,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("exp2_pwl2_safe_f16_f32",
           [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_safe_f16_f32, at::kFloat); },
           "B5 exp2 PWL2 safe hinge on the FP16 fraction (packed FP16), FP32 out");
+    m.def("exp2_pwl2_f32_to_bf16", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_f32_bf16, at::kBFloat16); },
+          "exp2: FP32 range reduction (clamped at -126) + the two-piece PWL2 hinge (FP32), BF16 out");
+    m.def("exp2_pwl2_f32", [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl2_f32, at::kFloat); },
+          "exp2: FP32 range reduction (clamped at -126) + the two-piece PWL2 hinge (FP32), FP32 out");
     m.def("exp2_pwl1_safe_f32_to_bf16",
           [](at::Tensor x) { return exp2_f32_to(x, launch_exp2_pwl1_safe_f32_bf16, at::kBFloat16); },
           "exp2: FP32 range reduction + D1 safe line 1 + f (FP32), BF16 out");

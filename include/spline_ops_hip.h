@@ -325,6 +325,12 @@ int launch_exp2_pwl2_safe_f16_f32(void* y, const void* x, int64_t size, void* st
  * same reduction and exponent add.  The forms are the appendix's
  * (extras/paper/manuscript/appendix_exp2.tex:17-32); their 16-bit programs
  * are not in the reference tree, so the precisions below are this build's:
+ *   pwl2             the reference's two-piece FP32 hinge (benchmark_exp2_pwl2.cu:
+ *                    126-170: offset 0x3F7D4D54, slope 0x3F522364, change
+ *                    0x3EAF5701 at f = 1/2), clamped at -126 instead of the
+ *                    reference's -127: its fraction starts below one
+ *                    (p(0) = 0.98946), so below -126.987 the reference's
+ *                    exponent add produces NaN bits; identical from -126 up;
  *   pwl1_safe        p = 1 + f (FP32), the only endpoint-safe line;
  *   pwl1_safe_f16    p = fp16(fp16(f) + 1);
  *   pwl2_safe_bf16   the PWL2 safe hinge on bf16(f) with bf16(a) = 0.796875,
@@ -342,6 +348,8 @@ int launch_exp2_pwl2_safe_f16_f32(void* y, const void* x, int64_t size, void* st
  *                    clamped at -126 like pwl2 (its fraction starts below one).
  * Every program keeps p(0) = 1 and p(1) = 2 after its rounding except
  * pwl2_f16 (p(0) = 0.98926). */
+int launch_exp2_pwl2_f32_bf16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_pwl2_f32(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_pwl1_safe_f32_bf16(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_pwl1_safe_f32(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_pwl1_safe_f16_f32_bf16(void* y, const void* x, int64_t size, void* stream);

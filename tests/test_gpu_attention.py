@@ -88,6 +88,29 @@ def test_exp2_programs(capi, oracle, cuda, kind, name, out_bf16):
         assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("out_bf16", [True, False])
+def test_exp2_pwl2_program(capi, oracle, cuda, out_bf16):
+    """The reference's two-piece FP32 hinge (FA4 backend pwl2), clamped at
+    -126: bit for bit the oracle's program (the reference's, clamped at -127)
+    on fmax(x, -126), NaN taking the clamp as in v_max_f32.  Below -126.987
+    the reference's clamp would give NaN bits; here every output is finite."""
+    x = _f32_inputs(13)
+    xd = torch.from_numpy(x).to(cuda)
+    xc = np.fmax(x, np.float32(-126.0))
+    if out_bf16:
+        y = torch.empty(x.size, dtype=torch.bfloat16, device=cuda)
+        capi.call("launch_exp2_pwl2_f32_bf16", y, xd, x.size)
+        torch.cuda.synchronize()
+        assert_bits_equal(_host(y), oracle.exp2(2, xc, True), "bf16", "exp2 pwl2 bf16")
+    else:
+        y = torch.empty(x.size, dtype=torch.float32, device=cuda)
+        capi.call("launch_exp2_pwl2_f32", y, xd, x.size)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), oracle.exp2(2, xc, False).view(np.uint32))
+        assert np.isfinite(got[x < 100]).all()
+
+
 def test_exp2_config5_and_native(spline_ops, cuda):
     """BASELINE config 5 recipe (one head block): logits N(0, 4^2) minus the
     row max; D2 relative error vs FP32 torch.exp2 and the native baseline."""
