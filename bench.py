@@ -75,6 +75,10 @@ def parse():
     p.add_argument("--pmc-attention", action="store_true",
                    help="counter pass over the attention forward: each score mode at the "
                         "component shape launched 3 times")
+    p.add_argument("--exp2-harness", action="store_true",
+                   help="only the reference's isolated exp2 harness rows (JSON on stdout)")
+    p.add_argument("--pmc-exp2-harness", action="store_true",
+                   help="counter pass: 3 eager launches of every exp2 harness kernel")
     p.add_argument("--attention-only", action="store_true",
                    help="time only the attention forward rows")
     p.add_argument("--open-weights", action="store_true",
@@ -590,6 +594,123 @@ def probe_rows(lib, reps: int, eager_launches: int = 0):
     for label, _ in launches[:-1]:
         row[f"{label}_speedup"] = round(row["native_us"] / row[f"{label}_us"], 3)
     rows.append(row)
+    return rows
+
+
+# Times (ms per launch) the reference published for its isolated exp2 harness
+# on GB200 (evidence/report-data/exp2_pwl2_isolated_gb200.json, "timings";
+# autonumerics_zero/cuda_benchmarks/benchmark_exp2_pwl2.cu).
+EXP2_HARNESS_GB200_MS = {
+    ("compute", "fp16x2_fractional"): {"native": 0.077942, "pwl2_historical": 0.119328, "pwl2_hinge": 0.041074},
+    ("compute", "f32x2_full"): {"native": 0.077939, "degree3": 0.088147, "pwl2_hinge": 0.09028},
+    ("l2", "fp16x2_fractional"): {"native": 0.006238, "pwl2_historical": 0.006245, "pwl2_hinge": 0.006258},
+    ("l2", "f32x2_full"): {"native": 0.00419, "degree3": 0.00421, "pwl2_hinge": 0.004182},
+    ("hbm", "fp16x2_fractional"): {"native": 0.192331, "pwl2_historical": 0.195184, "pwl2_hinge": 0.188542},
+    ("hbm", "f32x2_full"): {"native": 0.111118, "degree3": 0.111709, "pwl2_hinge": 0.11225},
+}
+
+
+def harness_fractional_pairs(n: int):
+    """The harness's make_fractional_h2(n) (benchmark_exp2_pwl2.cu:325-333):
+    pairs ((2i mod 65521) / 65521, (2i + 1 mod 65521) / 65521), FP32
+    division rounded to FP16; a flat FP16 tensor of 2n values."""
+    import torch
+
+    i = torch.arange(n, dtype=torch.int64)
+    x = (((2 * i) % 65521).float() / 65521.0).half()
+    y = (((2 * i + 1) % 65521).float() / 65521.0).half()
+    return torch.stack([x, y], 1).reshape(-1)
+
+
+def harness_full_pairs(n: int):
+    """The harness's make_full_f32(n) (:335-343): pairs (-16 u, -16 v),
+    u = (2i mod 1048573) / 1048573, v = (2i + 1 mod 1048573) / 1048573."""
+    import torch
+
+    i = torch.arange(n, dtype=torch.int64)
+    u = ((2 * i) % 1048573).float() / 1048573.0
+    v = ((2 * i + 1) % 1048573).float() / 1048573.0
+    return torch.stack([-16.0 * u, -16.0 * v], 1).reshape(-1)
+
+
+def exp2_harness_rows(lib, eager_launches: int = 0):
+    """The reference's isolated exp2 harness (benchmark_exp2_pwl2.cu) on
+    MI355X, with its sizes, inputs and timing: the fractional FP16 programs
+    (hardware v_exp_f16, the historical two-segment fit, the PWL2 hinge) and
+    the full FP32 programs (hardware v_exp_f32, FA4's D3, the PWL2 hinge) in
+    three regimes -- compute (65,536 threads x 8 register-resident chains x
+    256 evaluations), L2 (4 MiB in + 4 MiB out) and HBM (256 MiB + 256 MiB) --
+    each row with the speedups over hardware and the reference's GB200 times
+    and speedups.  Timing: graph replay of 20 launches, median of 9 rounds,
+    variants interleaved (the harness times 20 eager launches per sample,
+    median of 9; on MI355X an eager launch adds about 4.5 us to a 3 us L2
+    kernel, so eager timing would measure the launch path).  65,536 threads are one wave per SIMD on MI355X (1,024 SIMDs),
+    where the chains' dependency latency sets the time; a fourth regime,
+    compute_filled, runs eight times as many threads (eight waves per SIMD),
+    which measures instruction issue rate.  With eager_launches > 0 each kernel is only launched that many
+    times (a counter pass) and nothing is timed."""
+    import ctypes
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    chains, iters = 8, 256
+    names16 = ("native", "pwl2_historical", "pwl2_hinge")
+    names32 = ("native", "degree3", "pwl2_hinge")
+    entry32 = {"native": "native", "degree3": "d3", "pwl2_hinge": "pwl2"}
+    groups = []
+    for regime, threads in (("compute", 1 << 16), ("compute_filled", 1 << 19)):
+        frac_c = harness_fractional_pairs(threads * chains).to(dev)
+        full_c = harness_full_pairs(threads * chains).to(dev)
+        out16 = torch.empty(threads * 2, dtype=torch.float16, device=dev)
+        out32 = torch.empty(threads * 2, dtype=torch.float32, device=dev)
+        groups.append((regime, "fp16x2_fractional", threads,
+                       [(nm, _launcher(lib, "launch_exp2_compute_f16x2", ctypes.c_int(v), out16, frac_c, threads,
+                                       ctypes.c_int(iters))) for v, nm in enumerate(names16)]))
+        groups.append((regime, "f32x2_full", threads,
+                       [(nm, _launcher(lib, "launch_exp2_compute_f32x2", ctypes.c_int(v), out32, full_c, threads,
+                                       ctypes.c_int(iters))) for v, nm in enumerate(names32)]))
+    for regime, pairs16, pairs32 in (("l2", 1 << 20, 1 << 19), ("hbm", 1 << 26, 1 << 25)):
+        x16 = harness_fractional_pairs(pairs16).to(dev)
+        y16 = torch.empty_like(x16)
+        groups.append((regime, "fp16x2_fractional", -2 * x16.numel() * 2,
+                       [(nm, _launcher(lib, f"launch_exp2_fraction_{nm}_f16", y16, x16, x16.numel()))
+                        for nm in names16]))
+        x32 = harness_full_pairs(pairs32).to(dev)
+        y32 = torch.empty_like(x32)
+        groups.append((regime, "f32x2_full", -2 * x32.numel() * 4,
+                       [(nm, _launcher(lib, f"launch_exp2_{entry32[nm]}_f32", y32, x32, x32.numel()))
+                        for nm in names32]))
+    # size > 0: compute threads; size < 0: minus the bytes a memory launch moves
+    rows = []
+    for regime, dtype, size, launches in groups:
+        if eager_launches:
+            for _, fn in launches:
+                for _ in range(eager_launches):
+                    fn()
+            torch.cuda.synchronize()
+            continue
+        times = time_graphs_alternating([fn for _, fn in launches], 20)
+        compute = size > 0
+        evals = size * chains * iters * 2
+        config = (f"{size} threads ({size // (64 * 1024)} waves per SIMD) x {chains} chains x {iters} evaluations"
+                  if compute else f"{-size // 2 >> 20} MiB in + {-size // 2 >> 20} MiB out")
+        row = {"function": "exp2_isolated_harness", "regime": regime, "datatype": dtype, "config": config}
+        native_ms = times[0]
+        for (label, _), ms in zip(launches, times):
+            row[f"{label}_us"] = round(ms * 1e3, 3)
+            if compute:
+                row[f"{label}_ns_per_value"] = round(ms * 1e6 / evals, 7)
+            else:
+                row[f"{label}_gb_s"] = round(-size / (ms * 1e6), 1)
+            gb200 = EXP2_HARNESS_GB200_MS.get((regime, dtype))
+            if gb200:
+                row[f"{label}_gb200_us"] = round(gb200[label] * 1e3, 3)
+            if label != "native":
+                row[f"{label}_speedup"] = round(native_ms / ms, 4)
+                if gb200:
+                    row[f"{label}_gb200_speedup"] = round(gb200["native"] / gb200[label], 4)
+        rows.append(row)
     return rows
 
 
@@ -1328,6 +1449,12 @@ def main():
     if args.attention_only:
         print(json.dumps({"functions": attention_rows(lib, args.sweep_reps)}), flush=True)
         return
+    if args.exp2_harness:
+        print(json.dumps({"functions": exp2_harness_rows(lib)}), flush=True)
+        return
+    if args.pmc_exp2_harness:
+        exp2_harness_rows(lib, eager_launches=3)
+        return
     if args.open_weights:
         print(json.dumps({"models": open_weights_rows()}), flush=True)
         return
@@ -1420,6 +1547,16 @@ def main():
         sweep(lib, args.sweep_reps, emit)
         for row in probe_rows(lib, args.sweep_reps):
             emit(row)
+        harness = exp2_harness_rows(lib)
+        for row in harness:
+            emit(row)
+        # the three harness figures BASELINE quotes (GB200: 1.898, 0.995, 0.995)
+        pick = {(r["regime"], r["datatype"]): r for r in harness}
+        line["exp2_isolated_speedups"] = {
+            "compute_fp16x2_pwl2_hinge": pick[("compute", "fp16x2_fractional")]["pwl2_hinge_speedup"],
+            "compute_filled_fp16x2_pwl2_hinge": pick[("compute_filled", "fp16x2_fractional")]["pwl2_hinge_speedup"],
+            "l2_f32_degree3": pick[("l2", "f32x2_full")]["degree3_speedup"],
+            "hbm_f32_degree3": pick[("hbm", "f32x2_full")]["degree3_speedup"]}
         if not args.no_attention:
             for row in attention_rows(lib, args.sweep_reps):
                 emit(row)

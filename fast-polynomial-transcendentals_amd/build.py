@@ -31,7 +31,7 @@ INCLUDE = os.path.join(ROOT, "include")
 ARCH = os.environ.get("PT_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["launch.hip", "activations.hip", "swiglu.hip", "attention.hip", "experiments.hip", "sincos.hip", "rope.hip", "flash_attn.hip", "flash_attn_bwd.hip"]
+HIP_SOURCES = ["launch.hip", "activations.hip", "swiglu.hip", "attention.hip", "exp2_probes.hip", "experiments.hip", "sincos.hip", "rope.hip", "flash_attn.hip", "flash_attn_bwd.hip"]
 HIP_HEADERS = ["elementwise.hpp", "ops.hpp", "programs.hpp", "trig.hpp", "score_programs.hpp", "flash_attn.hpp"]
 
 HIP_FLAGS = [

@@ -365,6 +365,37 @@ int launch_exp2_d2_safe_bf16_f32(void* y, const void* x, int64_t size, void* str
 int launch_exp2_pwl2_f16_f32_bf16(void* y, const void* x, int64_t size, void* stream);
 int launch_exp2_pwl2_f16_f32(void* y, const void* x, int64_t size, void* stream);
 
+/* ---- isolated exp2 measurements ------------------------------------------
+ * The programs and protocol of the reference's exp2 harness
+ * (autonumerics_zero/cuda_benchmarks/benchmark_exp2_pwl2.cu:24-36, 55-266;
+ * published as evidence/report-data/exp2_pwl2_isolated_gb200.json), which
+ * has no launcher in the reference's extension.
+ * Fractional FP16 programs, f in [0, 1] -> 2^f, FP16 in and out (size in
+ * elements): `native` v_exp_f16 per lane (the reference's h2exp2);
+ * `pwl2_historical` the two-segment fit of FractionalPwl2Historical (:60-82:
+ * f clamped to [0, 0x3BFE], segment from the top mantissa bit of fp16(f + 1),
+ * p = fma(f, slope, offset), (0x3A91, 0x3BEA) / (0x3CA7, 0x3A8C));
+ * `pwl2_hinge` the hinge of FractionalPwl2Hinge (:84-99), the fraction of
+ * launch_exp2_pwl2_f16_*. */
+int launch_exp2_fraction_native_f16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_fraction_pwl2_historical_f16(void* y, const void* x, int64_t size, void* stream);
+int launch_exp2_fraction_pwl2_hinge_f16(void* y, const void* x, int64_t size, void* stream);
+/* Compute probes (compute_h2_kernel / compute_f32_kernel, :203-250):
+ * `threads` threads (the reference's 65,536; a positive multiple of 256, at
+ * most 2^24) in blocks of 256, each reading 8 pairs, in[t + threads c] for
+ * chain c, and running `iterations` rounds of x <- feedback(program(x)),
+ * then storing chain t % 8 to out[t].  in holds 8 threads pairs, out
+ * threads.  f16x2 (FP16 pairs, fractional programs; variant 0 native, 1
+ * pwl2_historical, 2 pwl2_hinge): feedback fma(v, 1/2, -1/2) on chains 0-3,
+ * fma(v, -1/2, 3/2) on 4-7, one FP16 rounding each.  f32x2 (float2 pairs,
+ * full programs on the FP32 range reduction; variant 0 v_exp_f32, 1 FA4 D3,
+ * 2 the PWL2 hinge of launch_exp2_pwl2_*): feedback fma(v, 8, -16) on chains
+ * 0-3, -8 v on 4-7. */
+int launch_exp2_compute_f16x2(int variant, void* out, const void* in, int64_t threads, int iterations,
+                              void* stream);
+int launch_exp2_compute_f32x2(int variant, void* out, const void* in, int64_t threads, int iterations,
+                              void* stream);
+
 /* ---- paired sin/cos tables: FP32 angles [size] -> out [2, size] ----------
  * Plane 0 holds cos, plane 1 sin.  Replaces launch_sincos_*_{bf16,fp16,f32}
  * (declared spline_ops.cpp:16-57, defined sincos_kernels.cu:2125-2668;

@@ -260,6 +260,8 @@ def softcap_bwd_bf16(go: np.ndarray, s: np.ndarray, cap: float) -> np.ndarray:
 EXP2_D2, EXP2_D3, EXP2_PWL2, EXP2_PWL2_SAFE, EXP2_PWL2_SAFE_F16 = 0, 1, 2, 3, 4
 (EXP2_PWL1_SAFE, EXP2_PWL1_SAFE_F16, EXP2_PWL2_SAFE_BF16, EXP2_D2_NOCLAMP, EXP2_D2_SAFE_F16,
  EXP2_D2_SAFE_BF16, EXP2_PWL2_F16) = range(5, 12)
+# fraction-only program (exp2_fraction): the reference's historical two-segment FP16 fit
+EXP2_FRAC_PWL2_HISTORICAL = 12
 # FA4 backend name -> oracle kind
 EXP2_BACKEND_KIND = {"d2_safe": 0, "d3": 1, "pwl2": 2, "pwl2_safe": 3, "pwl2_safe_f16": 4, "pwl1_safe": 5,
                      "pwl1_safe_f16": 6, "pwl2_safe_bf16": 7, "d2_safe_noclamp": 8, "d2_safe_f16": 9,

@@ -802,10 +802,26 @@ static float exp2_prog(int kind, float x) {
 /* The fraction program alone, p(f) for f in [0, 1] with no range reduction
  * (the reference's fractional benchmark domain, benchmark_exp2_pwl2.cu:
  * 325-333, 346-371): kinds 5-7 and 9-11 (the 16-bit programs and PWL1). */
+/* The reference's historical two-segment FP16 fraction
+ * (FractionalPwl2Historical, benchmark_exp2_pwl2.cu:60-82): f clamped to
+ * [0, 0x3BFE] (maxNum / minNum), the segment chosen by the top mantissa bit
+ * of fp16(f + 1) -- the rounded sum is in [1, 2), so the bit is set exactly
+ * when it reaches 1.5 -- and one FP16 FMA with that segment's slope and
+ * offset: (0x3A91, 0x3BEA) = (0.82080078125, 0.9892578125) below,
+ * (0x3CA7, 0x3A8C) = (1.1630859375, 0.818359375) above. */
+static float exp2_frac_two_segment(float fr) {
+    const fmt_t* h = &FMT_F16;
+    double c = h_max(round_fmt((double)fr, h), 0.0);
+    if (!(c <= 0.9990234375)) c = 0.9990234375; /* 0x3BFE; NaN already mapped to 0 */
+    const int upper = h_add(c, 1.0, h) >= 1.5;
+    return (float)h_fma(c, upper ? 1.1630859375 : 0.82080078125, upper ? 0.818359375 : 0.9892578125, h);
+}
+
 int orc_exp2_fraction(int kind, const float* f, float* p, int64_t n) {
-    if (n < 0 || kind < 5 || kind > 11 || kind == 8) return -1;
+    if (n < 0 || kind < 5 || kind > 12 || kind == 8) return -1;
 #pragma omp parallel for schedule(static)
-    for (int64_t i = 0; i < n; ++i) p[i] = kind == 5 ? f[i] + 1.0f : exp2_frac16(kind, f[i]);
+    for (int64_t i = 0; i < n; ++i)
+        p[i] = kind == 5 ? f[i] + 1.0f : kind == 12 ? exp2_frac_two_segment(f[i]) : exp2_frac16(kind, f[i]);
     return 0;
 }
 

@@ -111,7 +111,9 @@ int orc_softcap_bwd_bf16(const uint16_t* go, const uint16_t* s, uint16_t* g, int
  * endpoints and fit errors only (parity unpinned: FA4 absent). */
 int orc_exp2(int kind, int out_bf16, const float* x, uint16_t* y16, float* y32, int64_t n);
 /* The fraction program alone on f in [0, 1] (no range reduction), kinds 5-7
- * and 9-11. */
+ * and 9-11, and 12: the reference's historical two-segment FP16 fit
+ * (benchmark_exp2_pwl2.cu:60-82), pinned by its published fractional error
+ * metrics (exp2_pwl2_isolated_gb200.json, fractional_h2 / pwl2_historical). */
 int orc_exp2_fraction(int kind, const float* f, float* p, int64_t n);
 
 /* ---- paired sin/cos: prog 0 BF16 D3/D4, 1 BF16 D5/D6, 2 FP16 D3/D4,

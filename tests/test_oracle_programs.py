@@ -264,6 +264,26 @@ def test_exp2_pwl2_f16_reproduces_the_published_fractional_errors(oracle):
         assert abs(g - want) <= 5e-10 + 1e-9 * want, (got, want)
 
 
+def test_exp2_two_segment_historical_reproduces_the_published_fractional_errors(oracle):
+    """The reference's historical two-segment FP16 fraction
+    (FractionalPwl2Historical, benchmark_exp2_pwl2.cu:60-82) on its fractional
+    input set: max_abs, max_rel and rmse against exp2 in double equal
+    exp2_pwl2_isolated_gb200.json "fractional_h2" / "pwl2_historical" to every
+    printed digit.  Choosing the segment by f >= 1/2 instead of by the rounded
+    sum's mantissa bit, or swapping a segment's slope and offset, moves them."""
+    f = _fractional_h2_error_input()
+    p = oracle.exp2_fraction(oracle.EXP2_FRAC_PWL2_HISTORICAL, f).astype(np.float64)
+    ref = np.exp2(f.astype(np.float64))
+    a = np.abs(p - ref)
+    got = (a.max(), (a / ref).max(), np.sqrt((a * a).mean()))
+    for g, want in zip(got, (0.01953125, 0.010940964, 0.00662853655)):
+        assert abs(g - want) <= 5e-10 + 1e-9 * want, (got, want)
+    # the segment boundary: fp16(f + 1) rounds 0x37FF (just below 1/2) up to 1.5
+    below = np.array([np.float16(0.49951171875)], dtype=np.float32)
+    assert oracle.exp2_fraction(oracle.EXP2_FRAC_PWL2_HISTORICAL, below)[0] == np.float32(
+        np.float16(0.49951171875 * 1.1630859375 + 0.818359375))
+
+
 @pytest.mark.parametrize("kind,max_rel,lo,hi", [
     # appendix_exp2.tex table: D1 endpoint constrained 6.148e-2
     ("EXP2_PWL1_SAFE", 6.148e-2, 6.1475e-2, 6.1485e-2),
