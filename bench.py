@@ -75,6 +75,11 @@ def parse():
     p.add_argument("--pmc-attention", action="store_true",
                    help="counter pass over the attention forward: each score mode at the "
                         "component shape launched 3 times")
+    p.add_argument("--isolated-sweep", action="store_true",
+                   help="only the paper's isolated FP16 comparison against PyTorch's kernels, with its full "
+                        "protocol (1000 warmup and 1000 timed calls per round at both sizes; JSON on stdout)")
+    p.add_argument("--isolated-sweep-trace", action="store_true",
+                   help="the isolated FP16 comparison with 5 warmup / 20 timed calls, for a kernel trace")
     p.add_argument("--exp2-harness", action="store_true",
                    help="only the reference's isolated exp2 harness rows (JSON on stdout)")
     p.add_argument("--pmc-exp2-harness", action="store_true",
@@ -711,6 +716,113 @@ def exp2_harness_rows(lib, eager_launches: int = 0):
                 if gb200:
                     row[f"{label}_gb200_speedup"] = round(gb200["native"] / gb200[label], 4)
         rows.append(row)
+    return rows
+
+
+# The reference's published isolated FP16 comparison on GB200
+# (evidence/report-data/isolated_function_speedups_fp16.csv): (direction,
+# function, elements) -> (native PyTorch median µs, polynomial median µs).
+ISOLATED_GB200_US = {
+    ("forward", "sigmoid", 4194304): (9.235136, 5.426784), ("forward", "tanh", 4194304): (6.540000, 5.510720),
+    ("forward", "silu", 4194304): (8.425120, 5.485696), ("forward", "gelu", 4194304): (9.029760, 5.396704),
+    ("backward", "sigmoid", 4194304): (11.333536, 5.309024), ("backward", "tanh", 4194304): (11.361472, 5.202080),
+    ("backward", "silu", 4194304): (11.513664, 5.251648), ("backward", "gelu", 4194304): (11.770656, 5.367168),
+    ("forward", "sigmoid", 268435456): (198.864960, 159.258713),
+    ("forward", "tanh", 268435456): (182.325821, 159.583557),
+    ("forward", "silu", 268435456): (202.182587, 159.609665),
+    ("forward", "gelu", 268435456): (272.690674, 160.215546),
+    ("backward", "sigmoid", 268435456): (224.086502, 223.292572),
+    ("backward", "tanh", 268435456): (223.959717, 223.290298),
+    ("backward", "silu", 268435456): (249.981155, 223.315842),
+    ("backward", "gelu", 268435456): (360.584717, 223.251648),
+}
+
+
+def isolated_sweep_rows(full_protocol: bool = False, trace_pass: bool = False):
+    """The paper's isolated FP16 comparison
+    (autonumerics_zero/experiments/benchmark_report_function_speed.py:48-164,
+    published as isolated_function_speedups_fp16.csv): the spline_ops
+    polynomial functions, called through the torch extension as the script
+    calls them (sigmoid D3, tanh D4, SiLU D3, GeLU D5 forward; sigmoid D4,
+    tanh D4, SiLU D3, GeLU D5 backward on (grad_out, x)), against PyTorch's
+    own kernels (torch.sigmoid / tanh, F.silu / gelu, and aten's
+    *_backward, the sigmoid and tanh ones on the precomputed forward output),
+    on torch.randn FP16 (seed 1234) with grad_out = 1, at 4,194,304 and
+    268,435,456 elements, under inference mode.  Timing: warmup calls per
+    path, then 9 rounds alternating which path goes first, each the mean of
+    the timed calls between two events; medians.  The published protocol is
+    1000 warmup and 1000 timed calls (full_protocol); the default run keeps it
+    at 4M elements and uses 20 / 100 at 268M (each call there takes
+    160-360 us, so 100 calls per round already span 16-36 ms).  trace_pass:
+    5 warmup and 20 timed calls per round, for a kernel trace of manageable
+    size."""
+    import statistics
+
+    import torch
+    import torch.nn.functional as F
+
+    import spline_ops as so
+
+    dev = torch.device("cuda:0")
+
+    def time_calls(fn, reps):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) * 1e3 / reps
+
+    rows = []
+    with torch.inference_mode():
+        for size in (4194304, 268435456):
+            warmup, reps = ((5, 20) if trace_pass else (1000, 1000) if full_protocol or size < (1 << 24)
+                            else (20, 100))
+            torch.manual_seed(1234)
+            x = torch.randn(size, device=dev, dtype=torch.float16)
+            go = torch.ones_like(x)
+            ys, yt = torch.sigmoid(x), torch.tanh(x)
+            torch.cuda.synchronize()
+            cases = [("forward", "sigmoid", 3, lambda: torch.sigmoid(x), lambda: so.sigmoid_fwd_d3(x)),
+                     ("forward", "tanh", 4, lambda: torch.tanh(x), lambda: so.tanh_fwd_d4(x)),
+                     ("forward", "silu", 3, lambda: F.silu(x), lambda: so.swish_fwd_d3(x)),
+                     ("forward", "gelu", 5, lambda: F.gelu(x), lambda: so.gelu_fwd_d5(x)),
+                     ("backward", "sigmoid", 4, lambda: torch.ops.aten.sigmoid_backward(go, ys),
+                      lambda: so.sigmoid_bwd_d4(go, x)),
+                     ("backward", "tanh", 4, lambda: torch.ops.aten.tanh_backward(go, yt),
+                      lambda: so.tanh_bwd_d4(go, x)),
+                     ("backward", "silu", 3, lambda: torch.ops.aten.silu_backward(go, x),
+                      lambda: so.swish_bwd_d3(go, x)),
+                     ("backward", "gelu", 5, lambda: torch.ops.aten.gelu_backward(go, x),
+                      lambda: so.gelu_bwd_d5(go, x))]
+            for direction, fn_name, degree, native, poly in cases:
+                for f in (native, poly):
+                    for _ in range(warmup):
+                        f()
+                torch.cuda.synchronize()
+                nat_us, poly_us = [], []
+                for r in range(9):
+                    if r % 2 == 0:
+                        nat_us.append(time_calls(native, reps))
+                        poly_us.append(time_calls(poly, reps))
+                    else:
+                        poly_us.append(time_calls(poly, reps))
+                        nat_us.append(time_calls(native, reps))
+                nat_m, poly_m = statistics.median(nat_us), statistics.median(poly_us)
+                arrays = 2 if direction == "forward" else 3
+                g_nat, g_poly = ISOLATED_GB200_US[(direction, fn_name, size)]
+                rows.append({"function": "isolated_fp16_sweep", "direction": direction, "fn": fn_name,
+                             "degree": degree, "elements": size, "regime": _regime(size.bit_length() - 1),
+                             "protocol": f"{warmup} warmup, {reps} timed calls x 9 alternating rounds",
+                             "torch_native_us": round(nat_m, 3), "poly_us": round(poly_m, 3),
+                             "speedup": round(nat_m / poly_m, 4),
+                             "poly_frac_8tbs": round(arrays * 2 * size / (poly_m * 1e3) / HBM_PEAK_GBS, 4),
+                             "gb200_torch_native_us": g_nat, "gb200_poly_us": g_poly,
+                             "gb200_speedup": round(g_nat / g_poly, 4)})
+            del x, go, ys, yt
+            torch.cuda.empty_cache()
     return rows
 
 
@@ -1452,6 +1564,12 @@ def main():
     if args.exp2_harness:
         print(json.dumps({"functions": exp2_harness_rows(lib)}), flush=True)
         return
+    if args.isolated_sweep_trace:
+        print(json.dumps({"functions": isolated_sweep_rows(trace_pass=True)}), flush=True)
+        return
+    if args.isolated_sweep:
+        print(json.dumps({"functions": isolated_sweep_rows(full_protocol=True)}), flush=True)
+        return
     if args.pmc_exp2_harness:
         exp2_harness_rows(lib, eager_launches=3)
         return
@@ -1549,6 +1667,8 @@ def main():
             emit(row)
         harness = exp2_harness_rows(lib)
         for row in harness:
+            emit(row)
+        for row in isolated_sweep_rows():
             emit(row)
         # the three harness figures BASELINE quotes (GB200: 1.898, 0.995, 0.995)
         pick = {(r["regime"], r["datatype"]): r for r in harness}
