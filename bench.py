@@ -78,6 +78,8 @@ def parse():
     p.add_argument("--isolated-sweep", action="store_true",
                    help="only the paper's isolated FP16 comparison against PyTorch's kernels, with its full "
                         "protocol (1000 warmup and 1000 timed calls per round at both sizes; JSON on stdout)")
+    p.add_argument("--components", action="store_true",
+                   help="only the paper's B1 / B4 one-kernel component rows (JSON on stdout)")
     p.add_argument("--isolated-sweep-trace", action="store_true",
                    help="the isolated FP16 comparison with 5 warmup / 20 timed calls, for a kernel trace")
     p.add_argument("--exp2-harness", action="store_true",
@@ -472,7 +474,84 @@ def attention_rows_at(lib, reps: int, shape, eager_launches: int = 0):
             row[f"{label}_frac_mfma_peak"] = round(fl / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)
         for label, _ in launches[:-1]:
             row[f"{label}_speedup"] = round(row["native_us"] / row[f"{label}_us"], 3)
+        gb200 = ATTN_GB200_US.get((direction, function)) if d == 128 else None
+        if gb200:  # FA4 on GB200: (hardware, polynomial) µs of the same complete attention
+            row["gb200_native_us"], row["gb200_poly_us"] = gb200
+            row["gb200_speedup"] = round(gb200[0] / gb200[1], 3)
         rows.append(row)
+    return rows
+
+
+# The reference's complete-attention component times on GB200
+# (evidence/report-data/b1_b4_100_iteration_phase_probes_gb200.json, rows B2 / B3:
+# FA4, causal GQA B 1, S 4096, Hq 32, Hkv 8, D 128): (hardware µs, polynomial µs).
+ATTN_GB200_US = {("fwd", "B2 softcap 30"): (631.426, 307.547), ("bwd", "B2 softcap 30"): (985.479, 941.942),
+                 ("fwd", "B3 sigmoid attention"): (395.081, 367.973),
+                 ("bwd", "B3 sigmoid attention"): (656.436, 655.868)}
+
+# B1 / B4 one-kernel activations on GB200 (same file, rows B1 / B4): (direction)
+# -> (native µs, polynomial µs).
+COMPONENT_GB200_US = {("B1", "fwd"): (41.245, 39.085), ("B1", "bwd"): (56.015, 55.625),
+                      ("B4", "fwd"): (29.047, 28.946), ("B4", "bwd"): (53.295, 53.026)}
+
+
+def component_rows(lib):
+    """The paper's one-kernel component probes (main.tex:717-743;
+    evidence/report-data/b1_b4_100_iteration_phase_probes_gb200.json): B1,
+    BF16 SiLU D3 on 58,720,256 values (forward, and the standalone direct D3
+    derivative backward); B4, the routed-expert SwiGLU D3 on 24,576 rows x
+    1280 (separate gate and up tensors; forward, and the backward that
+    recomputes the D3 sigmoid and forms both gradients), each against this
+    build's hardware-transcendental kernel of the same layout.  Inputs N(0, 1)
+    BF16 (seed 40).  Protocol as published: 25 warmup launches per variant,
+    5 rounds of 100 launches between two events, the order rotating each
+    round, median of the round means.  Both working sets fit the 256 MiB
+    MALL (235 / 189 MB forward), as they fit GB200's L2-backed memory system
+    in the published run."""
+    import statistics
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(40)
+    n1 = 58720256
+    x = torch.randn(n1, device=dev, generator=g).bfloat16()
+    go = torch.randn(n1, device=dev, generator=g).bfloat16()
+    y = torch.empty_like(x)
+    rows4, hid = 24576, 1280
+    n4 = rows4 * hid
+    gate = torch.randn(n4, device=dev, generator=g).bfloat16()
+    up = torch.randn(n4, device=dev, generator=g).bfloat16()
+    go4 = torch.randn(n4, device=dev, generator=g).bfloat16()
+    o4, gg, gu = torch.empty_like(gate), torch.empty_like(gate), torch.empty_like(gate)
+    cases = [("B1", "fwd", "SiLU D3 BF16, 58,720,256 values", n1, 4 * n1,
+              _launcher(lib, "launch_swish_fwd_native_kernel_bf16", y, x, n1),
+              _launcher(lib, "launch_swish_fwd_d3_kernel_bf16", y, x, n1)),
+             ("B1", "bwd", "SiLU D3 direct derivative BF16, 58,720,256 values", n1, 6 * n1,
+              _launcher(lib, "launch_swish_bwd_native_kernel_bf16", y, go, x, n1),
+              _launcher(lib, "launch_swish_bwd_d3_kernel_bf16", y, go, x, n1)),
+             ("B4", "fwd", "SwiGLU D3 BF16, 24,576 x 1280", n4, 6 * n4,
+              _launcher(lib, "launch_swish_mul_fwd_native_kernel_bf16", o4, gate, up, n4),
+              _launcher(lib, "launch_swish_mul_fwd_d3_kernel_bf16", o4, gate, up, n4)),
+             ("B4", "bwd", "SwiGLU D3 BF16 backward, 24,576 x 1280", n4, 10 * n4,
+              _launcher(lib, "launch_swish_mul_bwd_native_kernel_bf16", gg, gu, go4, gate, up, n4),
+              _launcher(lib, "launch_swish_mul_bwd_d3_kernel_bf16", gg, gu, go4, gate, up, n4))]
+    rows = []
+    for case, direction, config, n, nbytes, native, poly in cases:
+        for fn in (native, poly):
+            for _ in range(25):
+                fn()
+        torch.cuda.synchronize()
+        nat_us, poly_us = [], []
+        for r in range(5):
+            for fn, acc in ((native, nat_us), (poly, poly_us)) if r % 2 == 0 else ((poly, poly_us), (native, nat_us)):
+                acc.append(time_launches(fn, 100, 0) * 1e3)
+        nat_m, poly_m = statistics.median(nat_us), statistics.median(poly_us)
+        g_nat, g_poly = COMPONENT_GB200_US[(case, direction)]
+        rows.append({"function": f"component {case} {direction}", "config": config, "elements": n,
+                     "regime": "mall", "native_us": round(nat_m, 3), "poly_us": round(poly_m, 3),
+                     "speedup": round(nat_m / poly_m, 4), "poly_tb_s": round(nbytes / poly_m / 1e6, 2),
+                     "gb200_native_us": g_nat, "gb200_poly_us": g_poly, "gb200_speedup": round(g_nat / g_poly, 4)})
     return rows
 
 
@@ -1564,6 +1643,9 @@ def main():
     if args.exp2_harness:
         print(json.dumps({"functions": exp2_harness_rows(lib)}), flush=True)
         return
+    if args.components:
+        print(json.dumps({"functions": component_rows(lib)}), flush=True)
+        return
     if args.isolated_sweep_trace:
         print(json.dumps({"functions": isolated_sweep_rows(trace_pass=True)}), flush=True)
         return
@@ -1669,6 +1751,8 @@ def main():
         for row in harness:
             emit(row)
         for row in isolated_sweep_rows():
+            emit(row)
+        for row in component_rows(lib):
             emit(row)
         # the three harness figures BASELINE quotes (GB200: 1.898, 0.995, 0.995)
         pick = {(r["regime"], r["datatype"]): r for r in harness}
