@@ -439,8 +439,15 @@ def attention_rows_at(lib, reps: int, shape, eager_launches: int = 0):
         dq, dk, dv = torch.empty_like(qq), torch.empty_like(k), torch.empty_like(v)
         delta = torch.empty(b, hq, s, dtype=torch.float32, device=dev)
         ws = torch.empty(2, b, hq, s, d, dtype=torch.float32, device=dev)
-        return _launcher(lib, "launch_flash_attention_bwd_strided_bf16", dq, dk, dv, delta, ws, qq, k, v, out, do,
-                         lse, b, hq, hkv, s, d, strides(qq, k, v, out, do, dq, dk, dv), ctypes.c_int(mode),
+        # the library's backward as the binding runs it: dS kept in a
+        # workspace where spline_hip_attn_bwd_ds_bytes says it pays
+        size_fn = lib.spline_hip_attn_bwd_ds_bytes
+        size_fn.restype = ctypes.c_int64
+        nbytes = size_fn(ctypes.c_int64(b), ctypes.c_int64(hq), ctypes.c_int64(s), ctypes.c_int64(d),
+                         ctypes.c_int(mode))
+        ds_ws = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev) if nbytes > 0 else ctypes.c_void_p(0)
+        return _launcher(lib, "launch_flash_attention_bwd_strided_ds_bf16", dq, dk, dv, delta, ws, ds_ws, qq, k, v,
+                         out, do, lse, b, hq, hkv, s, d, strides(qq, k, v, out, do, dq, dk, dv), ctypes.c_int(mode),
                          ctypes.c_int(grad), ctypes.c_int(route_bwd), ctypes.c_int(1), ctypes.c_float(scale),
                          ctypes.c_float(30.0), ctypes.c_float(sigmoid_bias))
 

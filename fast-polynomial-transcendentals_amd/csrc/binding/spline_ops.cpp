@@ -707,6 +707,18 @@ std::vector<at::Tensor> flash_attn_fwd_bf16(at::Tensor q, at::Tensor k, at::Tens
     return {out, lse};
 }
 
+// Largest dS workspace the attention backward allocates: the environment's
+// SPLINE_ATTN_DS_MAX_BYTES (bytes, 0 turns the dS-keeping backward off),
+// 8 GiB by default.
+int64_t attn_ds_max_bytes() {
+    const char* e = std::getenv("SPLINE_ATTN_DS_MAX_BYTES");
+    if (e == nullptr || *e == '\0') return int64_t(8) << 30;
+    char* end = nullptr;
+    const long long v = std::strtoll(e, &end, 10);
+    TORCH_CHECK(end != e && *end == '\0' && v >= 0, "SPLINE_ATTN_DS_MAX_BYTES must be a byte count, got '", e, "'");
+    return (int64_t)v;
+}
+
 std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor out,
                                             at::Tensor dout, at::Tensor lse, int64_t mode, int64_t grad,
                                             int64_t exp2_route, bool causal, double softmax_scale,
@@ -740,10 +752,18 @@ std::vector<at::Tensor> flash_attn_bwd_bf16(at::Tensor q, at::Tensor k, at::Tens
                                  dout.stride(0), dout.stride(2), dout.stride(1), dq.stride(0),
                                  dq.stride(2),   dq.stride(1),   dk.stride(0),   dk.stride(2),
                                  dk.stride(1),   dv.stride(0),   dv.stride(2),   dv.stride(1)};
+    // dS workspace of the dS-keeping backward (B * Hq * S^2 BF16 where it
+    // applies), up to SPLINE_ATTN_DS_MAX_BYTES (default 8 GiB; 0 turns it
+    // off), from the caching allocator
+    const int64_t ds_bytes = spline_hip_attn_bwd_ds_bytes(b, hq, sq, d, (int)mode);
+    at::Tensor ds_ws = ds_bytes > 0 && ds_bytes <= attn_ds_max_bytes()
+                           ? at::empty({ds_bytes / 2}, q.options())
+                           : at::Tensor();
     void* s = current_stream(q);
-    check_launch(launch_flash_attention_bwd_strided_bf16(
+    check_launch(launch_flash_attention_bwd_strided_ds_bf16(
                      dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr<float>(),
-                     hq != hkv ? dkv_ws.data_ptr<float>() : nullptr, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
+                     hq != hkv ? dkv_ws.data_ptr<float>() : nullptr, ds_ws.defined() ? ds_ws.data_ptr() : nullptr,
+                     q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(),
                      lse.data_ptr<float>(), b, hq, hkv, sq, d, strides, (int)mode, (int)grad,
                      (int)exp2_route, causal ? 1 : 0, (float)softmax_scale, (float)softcap,
                      (float)sigmoid_bias, s),

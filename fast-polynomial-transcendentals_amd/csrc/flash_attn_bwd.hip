@@ -15,7 +15,12 @@
 //    forward);
 //  * dQ: a block owns 128 or 256 queries (32 per wave, Q and dO in registers) and
 //    streams 32-key tiles of K and V: S^T = K Q^T and dP^T = V dO^T have
-//    one query per lane, dQ^T += K^T dS^T.
+//    one query per lane, dQ^T += K^T dS^T;
+//  * or, with a dS workspace (launch_flash_attention_bwd_strided_ds_bf16):
+//    the dK/dV kernel also stores dS, one 1 KiB chunk per 32 queries x 16
+//    keys in the order of the B fragments of dQ^T += K^T dS^T, and a light
+//    dQ kernel multiplies those chunks by K, so S, P, dP and the score
+//    program run once instead of twice (bit-identical results).
 // Tiles are staged row-major; the transposed operands Q^T, dO^T and K^T are
 // read from the same rows with transposing LDS loads (ds_read_b64_tr_b16).
 // P is recomputed from the saved log-sum-exp (softmax) or directly (sigmoid
@@ -46,6 +51,25 @@ enum AttnGrad : int {
 
 constexpr int kBwdTile = 32;              // queries (dK/dV) or keys (dQ) per staged tile
 
+// Whether the backward keeps dS in a workspace (the dK/dV kernel stores it,
+// dQ = dS K reads it) rather than recomputing S, P, dP and the score program
+// in the dQ kernel.  Measured on MI355X (causal GQA 32/8, S 4096, graph
+// replay, bit-identical results): head_dim 128 1.05x (hardware softmax) to
+// 1.2-1.3x (softcap D4, B3) for the whole backward; head_dim 64 1.04-1.28x
+// for the modes with a score program, 0.86x for plain softmax, whose
+// recomputing dQ kernel is cheaper there than reading dS (B * Hq * S^2 BF16).
+__host__ __device__ constexpr bool bwd_keeps_ds(int mode, int hd) {
+    return hd == 128 || !attn_is_plain_softmax(mode);
+}
+
+// dS chunk of (batch b, query head, 32-query chunk qc, 16-key group kg):
+// 64 lanes x 16 bytes, chunks ordered (b, head, qc, kg), so the dQ kernel's
+// waves read their chunks contiguously.
+__device__ __forceinline__ int64_t ds_chunk(int64_t b, int64_t hq, int64_t head, int64_t seq, int64_t qc,
+                                            int64_t kg) {
+    return ((b * hq + head) * (seq / 32) + qc) * (seq / 16) + kg;
+}
+
 struct AttnBwdParams {
     const uint16_t* q;
     const uint16_t* k;
@@ -57,6 +81,7 @@ struct AttnBwdParams {
     uint16_t* dk;
     uint16_t* dv;
     float* dkv_ws;  // grouped heads: per-query-head dK, dV partials [2][B, Hq, S, 128]
+    uint16_t* ds;   // dS chunks (bwd_keeps_ds), or null
     AttnStrides qs, ks, vs, dos, dqs, dks, dvs;
     int64_t hq, hkv, seq;
     float scale, cap, sig_bias;
@@ -301,14 +326,22 @@ __device__ __forceinline__ bf16x8_t frag_tr32(const uint16_t* src, int dt, int c
 //    the last row (unconditional loads) and zeroed in LDS, their lse is +inf
 //    and their D 0, and keys past it store nothing, which is the arithmetic
 //    of operands zero-padded at the end.
-template <int MODE, int GRAD, int ROUTE, int HD, int W, bool RAGGED>
+// DSOUT: the kernel also stores dS for the dS-keeping backward (aligned
+// lengths only; each chunk goes through the wave's own 16 x 32 LDS tile).
+// BF16 elements per row of that tile: 72-byte rows keep every 8-byte access
+// aligned and the 16 rows of a lane group on different banks.
+constexpr int kDsRowStride = 36;
+
+template <int MODE, int GRAD, int ROUTE, int HD, int W, bool RAGGED, bool DSOUT = false>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2)))
 flash_bwd_dkdv_kernel(AttnBwdParams p) {
+    static_assert(!(RAGGED && DSOUT), "dS chunks cover whole 32-query by 16-key blocks");
     constexpr bool kSigmoid = attn_is_sigmoid(MODE);
     constexpr int kRS = q_row_stride<HD>(), kChunks = HD / 8;
     constexpr int kThreads = 64 * W, kKeys = 16 * W;  // keys per block
     constexpr int kQT = dkdv_query_tile<MODE>();
     __shared__ __align__(16) BwdQTile<HD, kQT> tiles[2];
+    __shared__ __align__(16) uint16_t dstile[DSOUT ? W : 1][16 * kDsRowStride];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -497,11 +530,39 @@ flash_bwd_dkdv_kernel(AttnBwdParams p) {
                 pf[e] = (__bf16)pr_[e];
                 sf[e] = (__bf16)ds[e];
             }
+            // DSOUT: the chunk's dS (32 queries x the wave's 16 keys) as the
+            // B fragments of the dQ kernel's dQ^T += K^T dS^T: written
+            // row-major (key rows, query columns) to the wave's LDS tile and
+            // read back with transposing loads, lane (hh, c) receiving keys
+            // 4hh .. 4hh+3 and 8+4hh .. 8+4hh+3 of query c (the slot order of
+            // frag_tr32).  LDS accesses of one wave complete in order, so the
+            // wave barriers only keep the compiler from reordering them.
+            u32x2_t ds_lo, ds_hi;
+            if constexpr (DSOUT) {
+                uint16_t* xt = dstile[wave];
+                const u32x4_t w4 = __builtin_bit_cast(u32x4_t, sf);
+                *reinterpret_cast<u32x2_t*>(xt + kl * kDsRowStride + 4 * g) = (u32x2_t){w4.x, w4.y};
+                *reinterpret_cast<u32x2_t*>(xt + kl * kDsRowStride + 16 + 4 * g) = (u32x2_t){w4.z, w4.w};
+                __builtin_amdgcn_wave_barrier();
+                const uint16_t* rs = xt + (4 * (lane >> 5) + ((lane & 15) >> 2)) * kDsRowStride +
+                                     16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+                ds_lo = __builtin_bit_cast(u32x2_t, lds_read_tr16(rs));
+                ds_hi = __builtin_bit_cast(u32x2_t, lds_read_tr16(rs + 8 * kDsRowStride));
+                __builtin_amdgcn_wave_barrier();
+            }
             const int tr_off = (32 * sc + 4 * g + (kl >> 2)) * kRS + 4 * (kl & 3);
 #pragma unroll
             for (int dt = 0; dt < HD / 16; ++dt) {
                 dvacc[dt] = mfma16(frag_tr16<HD>(t.dout + tr_off, dt), pf, dvacc[dt]);
                 dkacc[dt] = mfma16(frag_tr16<HD>(t.q + tr_off, dt), sf, dkacc[dt]);
+            }
+            if constexpr (DSOUT) {
+                // after the MFMAs, whose fragment loads were issued after the
+                // transposing loads, so the store waits for nothing; stored
+                // non-temporally (B * Hq * S^2 BF16 in all, read once)
+                const int64_t chunk = ds_chunk(b, p.hq, head, p.seq, q0 / 32, key0 / 16);
+                __builtin_nontemporal_store((u32x4_t){ds_lo.x, ds_lo.y, ds_hi.x, ds_hi.y},
+                                            reinterpret_cast<u32x4_t*>(p.ds) + chunk * 64 + lane);
             }
         }
         }
@@ -758,6 +819,110 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
         }
 }
 
+// ---------------------------------------------------------------------------
+// dQ from the dS chunks of the dK/dV kernel (the dS-keeping backward):
+// dQ^T += K^T dS^T.  A block of 4 waves owns 128 queries of one query head
+// (32 per wave), streams 64-key tiles of K through LDS (K^T fragments by the
+// transposing loads of frag_tr32) and loads each chunk straight into the B
+// fragment registers.  Every load is issued one tile ahead; the loop is
+// unrolled by the tile parity, so no register copy waits for a load.  Under
+// the causal mask a wave reads the chunks of keys up to its last query,
+// the ones the dK/dV kernel wrote.  S a multiple of 128.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2)))
+flash_bwd_dq_ds_kernel(AttnBwdParams p) {
+    constexpr int kRS = k_row_stride<HD>(), kChunks = HD / 8;
+    constexpr int kKT = 64;                   // keys per staged tile
+    constexpr int kRowsPass = 256 / kChunks;  // K rows one pass of the block moves
+    constexpr int kPasses = kKT / kRowsPass;
+    __shared__ __align__(16) uint16_t ktile[2][kKT * kRS];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, c32 = lane & 31;
+    const int64_t nqb = p.seq / 128;
+    const int64_t head = blockIdx.x, b = blockIdx.z;
+    const int64_t qb = p.causal ? nqb - 1 - (int64_t)blockIdx.y : (int64_t)blockIdx.y;
+    const int64_t kvh = head / (p.hq / p.hkv);
+    const int64_t q0 = qb * 128 + wave * 32;
+    const int64_t qrow = q0 + c32;
+    const u32x4_t* dsrc = reinterpret_cast<const u32x4_t*>(p.ds) + ds_chunk(b, p.hq, head, p.seq, q0 / 32, 0) * 64 + lane;
+    const int64_t kglim = p.causal ? q0 / 16 + 1 : p.seq / 16 - 1;  // the wave's last 16-key group
+
+    f32x16_t dqacc[HD / 32];
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) dqacc[dt] = (f32x16_t){};
+
+    const int krow = tid / kChunks, kcol = (tid % kChunks) * 8;
+    const uint16_t* kp = p.k + b * p.ks.b + kvh * p.ks.h + krow * p.ks.s + kcol;
+    u32x4_t kr[2][kPasses];  // K rows of the tiles two ahead, by tile parity
+    u32x4_t dsf[2][4];       // dS fragments of this tile and the next, by parity
+    const int64_t ktiles = p.seq / kKT;
+    const int64_t ncausal = p.causal ? (qb + 1) * (128 / kKT) : ktiles;
+    const int64_t nkt = ncausal < ktiles ? ncausal : ktiles;
+    const int tr_off = (4 * h + ((lane & 15) >> 2)) * kRS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+    auto kload = [&](int par, int64_t t) {
+#pragma unroll
+        for (int j = 0; j < kPasses; ++j)
+            kr[par][j] = *reinterpret_cast<const u32x4_t*>(kp + (t * kKT + kRowsPass * j) * p.ks.s);
+    };
+    auto kstore = [&](int par) {
+#pragma unroll
+        for (int j = 0; j < kPasses; ++j)
+            *reinterpret_cast<u32x4_t*>(&ktile[par][(krow + kRowsPass * j) * kRS + kcol]) = kr[par][j];
+    };
+    auto dload = [&](int par, int64_t t) {  // groups past the causal limit were not written: zero
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const int64_t kg = 4 * t + cc;
+            dsf[par][cc] = kg <= kglim ? __builtin_nontemporal_load(dsrc + kg * 64) : (u32x4_t){0u, 0u, 0u, 0u};
+        }
+    };
+    // tile t of parity P: K of tile t in ktile[P], its dS in dsf[P]; issue K
+    // of t + 2 (into kr[P], whose tile is staged) and dS of t + 1, stage K of
+    // t + 1 after the products
+    auto step = [&](auto par_c, int64_t t) {
+        constexpr int P = decltype(par_c)::value;
+        if (t + 2 < nkt) kload(P, t + 2);
+        if (t + 1 < nkt) dload(P ^ 1, t + 1);
+        if (4 * t <= kglim) {  // wave-uniform
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                if (4 * t + cc <= kglim) {
+                    const bf16x8_t sf = __builtin_bit_cast(bf16x8_t, dsf[P][cc]);
+#pragma unroll
+                    for (int dt = 0; dt < HD / 32; ++dt)
+                        dqacc[dt] = mfma32(frag_tr32<HD>(ktile[P] + tr_off, dt, cc), sf, dqacc[dt]);
+                }
+            }
+        }
+        if (t + 1 < nkt) kstore(P ^ 1);
+        __syncthreads();
+    };
+    kload(0, 0);
+    kstore(0);
+    if (nkt > 1) kload(1, 1);
+    dload(0, 0);
+    __syncthreads();
+    for (int64_t t = 0; t < nkt; t += 2) {
+        step(std::integral_constant<int, 0>{}, t);
+        if (t + 1 < nkt) step(std::integral_constant<int, 1>{}, t + 1);
+    }
+
+    uint16_t* dqr = p.dq + b * p.dqs.b + head * p.dqs.h + qrow * p.dqs.s;
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = dt * 32 + 8 * g + 4 * h;
+            const u32x2_t w = {pack_bf(dqacc[dt][4 * g], dqacc[dt][4 * g + 1]),
+                               pack_bf(dqacc[dt][4 * g + 2], dqacc[dt][4 * g + 3])};
+            *reinterpret_cast<u32x2_t*>(dqr + d) = w;
+        }
+}
+
 }  // namespace pt
 
 using namespace pt;
@@ -772,8 +937,16 @@ void launch_bwd_shape(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
     // each query tile once per 128 keys (measured on MI355X)
     constexpr int kW = attn_is_sigmoid(MODE) ? 4 : 8;
     const dim3 kgrid((unsigned)prm.hq, (unsigned)((prm.seq + 16 * kW - 1) / (16 * kW)), (unsigned)batch);
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE, HD, kW, RAGGED>), kgrid, dim3(64 * kW), 0, st,
-                       prm);
+    // the dS-keeping backward: the launcher passes a workspace only for
+    // aligned lengths and the modes bwd_keeps_ds selects
+    constexpr bool kKeepsDs = !RAGGED && bwd_keeps_ds(MODE, HD);
+    if (kKeepsDs && prm.ds != nullptr) {
+        hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE, HD, kW, false, kKeepsDs>), kgrid, dim3(64 * kW),
+                           0, st, prm);
+    } else {
+        hipLaunchKernelGGL((flash_bwd_dkdv_kernel<MODE, GRAD, ROUTE, HD, kW, RAGGED>), kgrid, dim3(64 * kW), 0, st,
+                           prm);
+    }
     if (prm.dkv_ws != nullptr) {
         const int64_t n = batch * prm.hkv * prm.seq * (HD / 8);
         hipLaunchKernelGGL((attn_dkv_reduce_kernel<HD>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
@@ -785,6 +958,10 @@ void launch_bwd_shape(const AttnBwdParams& prm, int64_t batch, hipStream_t st) {
     // sigmoid at head_dim 128, 4 otherwise (measured on MI355X: +2-6 % for
     // the dQ kernel of those modes, -1-3 % for softcap and the sigmoid
     // polynomials)
+    if (kKeepsDs && prm.ds != nullptr) {
+        hipLaunchKernelGGL((flash_bwd_dq_ds_kernel<HD>), grid, dim3(256), 0, st, prm);
+        return;
+    }
     constexpr int kQW = HD == 128 && (attn_is_plain_softmax(MODE) || MODE == kAttnSigmoidNative) ? 8 : 4;
     if (grid.y % (kQW / 4) == 0) {  // whole kQW-wave blocks over the 128-row blocks
         const dim3 qgrid(grid.x, grid.y / (kQW / 4), grid.z);
@@ -832,11 +1009,26 @@ bool bwd_stride_ok(const AttnStrides& t) {
 
 }  // namespace
 
-extern "C" int launch_flash_attention_bwd_strided_bf16(
-    void* dq, void* dk, void* dv, float* delta, float* dkv_workspace, const void* q, const void* k, const void* v,
-    const void* out, const void* dout, const float* lse, int64_t batch, int64_t q_heads,
-    int64_t kv_heads, int64_t seq, int64_t head_dim, const int64_t* strides, int mode, int grad,
-    int exp2_route, int causal, float scale, float cap, float sigmoid_bias, void* stream) {
+namespace {
+
+// Bytes of the dS workspace of the dS-keeping backward, 0 where it does not
+// apply (lengths that are not a multiple of 128, plain softmax at head_dim
+// 64, invalid shapes) or would exceed 2^56 bytes.
+int64_t ds_workspace_bytes(int64_t batch, int64_t q_heads, int64_t seq, int64_t head_dim, int mode) {
+    if (batch <= 0 || q_heads <= 0 || seq <= 0 || seq % 128 != 0 || (head_dim != 64 && head_dim != 128) ||
+        mode < 0 || mode >= kAttnModes || !bwd_keeps_ds(mode, (int)head_dim))
+        return 0;
+    const unsigned __int128 bytes = (unsigned __int128)batch * (unsigned __int128)q_heads *
+                                    (unsigned __int128)seq * (unsigned __int128)seq * 2u;
+    return bytes > ((unsigned __int128)1 << 56) ? 0 : (int64_t)bytes;
+}
+
+// The backward with or without a dS workspace (null: the recomputing dQ
+// kernel).
+int bwd_run(void* dq, void* dk, void* dv, float* delta, float* dkv_workspace, void* ds_workspace, const void* q,
+            const void* k, const void* v, const void* out, const void* dout, const float* lse, int64_t batch,
+            int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim, const int64_t* strides, int mode,
+            int grad, int exp2_route, int causal, float scale, float cap, float sigmoid_bias, void* stream) {
     if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || seq < 0 || (head_dim != 64 && head_dim != 128) || !strides)
         return hipErrorInvalidValue;
     const int hd = (int)head_dim;
@@ -883,9 +1075,12 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
                                (const uint16_t*)out, (const uint16_t*)dout, delta, st[3], st[4], q_heads, seq,
                                rows);
     }
+    const bool keep_ds = ds_workspace != nullptr && ds_workspace_bytes(batch, q_heads, seq, head_dim, mode) > 0;
+    if (keep_ds && !aligned16(ds_workspace)) return hipErrorInvalidValue;
     AttnBwdParams prm{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
                       sig ? nullptr : lse, sig ? nullptr : delta, (uint16_t*)dq, (uint16_t*)dk,
-                      (uint16_t*)dv, grouped ? dkv_workspace : nullptr, st[0], st[1], st[2], st[4], st[5], st[6], st[7], q_heads, kv_heads,
+                      (uint16_t*)dv, grouped ? dkv_workspace : nullptr, keep_ds ? (uint16_t*)ds_workspace : nullptr,
+                      st[0], st[1], st[2], st[4], st[5], st[6], st[7], q_heads, kv_heads,
                       seq, scale, cap > 0.0f ? cap : 1.0f, sigmoid_bias, causal != 0, exp2_route,
                       host_route_mask(exp2_route)};
     switch (mode) {
@@ -938,6 +1133,32 @@ extern "C" int launch_flash_attention_bwd_strided_bf16(
         case kAttnSigmoidD6: launch_bwd<kAttnSigmoidD6, kGradNatural, 0>(prm, batch, hst, hd); break;
     }
     return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int launch_flash_attention_bwd_strided_bf16(
+    void* dq, void* dk, void* dv, float* delta, float* dkv_workspace, const void* q, const void* k, const void* v,
+    const void* out, const void* dout, const float* lse, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t seq, int64_t head_dim, const int64_t* strides, int mode, int grad,
+    int exp2_route, int causal, float scale, float cap, float sigmoid_bias, void* stream) {
+    return bwd_run(dq, dk, dv, delta, dkv_workspace, nullptr, q, k, v, out, dout, lse, batch, q_heads, kv_heads, seq,
+                   head_dim, strides, mode, grad, exp2_route, causal, scale, cap, sigmoid_bias, stream);
+}
+
+extern "C" int64_t spline_hip_attn_bwd_ds_bytes(int64_t batch, int64_t q_heads, int64_t seq, int64_t head_dim,
+                                                int mode) {
+    return ds_workspace_bytes(batch, q_heads, seq, head_dim, mode);
+}
+
+extern "C" int launch_flash_attention_bwd_strided_ds_bf16(
+    void* dq, void* dk, void* dv, float* delta, float* dkv_workspace, void* ds_workspace, const void* q,
+    const void* k, const void* v, const void* out, const void* dout, const float* lse, int64_t batch,
+    int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim, const int64_t* strides, int mode, int grad,
+    int exp2_route, int causal, float scale, float cap, float sigmoid_bias, void* stream) {
+    return bwd_run(dq, dk, dv, delta, dkv_workspace, ds_workspace, q, k, v, out, dout, lse, batch, q_heads,
+                   kv_heads, seq, head_dim, strides, mode, grad, exp2_route, causal, scale, cap, sigmoid_bias,
+                   stream);
 }
 
 // ---------------------------------------------------------------------------

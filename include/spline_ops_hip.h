@@ -624,6 +624,25 @@ int launch_flash_attention_bwd_strided_bf16(void* dq, void* dk, void* dv, float*
                                             int64_t seq, int64_t head_dim, const int64_t* strides,
                                             int mode, int grad, int exp2_route, int causal,
                                             float scale, float cap, float sigmoid_bias, void* stream);
+/* Backward that keeps dS: no counterpart in the reference (FA4's backward is
+ * not part of its tree).  Same arguments and results as
+ * launch_flash_attention_bwd_strided_bf16, bit for bit, plus `ds_workspace`:
+ * spline_hip_attn_bwd_ds_bytes(batch, q_heads, seq, head_dim, mode) bytes of
+ * device memory, 16-byte aligned, whose contents need no initialisation.
+ * The dK/dV kernel stores dS there (only the chunks the causal mask keeps)
+ * and the dQ kernel multiplies it by K instead of recomputing S, P, dP and
+ * the score program.  Where the size helper returns 0 (S not a multiple of
+ * 128, plain softmax at head_dim 64, where recomputing is cheaper) or
+ * ds_workspace is null, the call is the recomputing backward. */
+int64_t spline_hip_attn_bwd_ds_bytes(int64_t batch, int64_t q_heads, int64_t seq, int64_t head_dim, int mode);
+int launch_flash_attention_bwd_strided_ds_bf16(void* dq, void* dk, void* dv, float* delta,
+                                               float* dkv_workspace, void* ds_workspace, const void* q,
+                                               const void* k, const void* v, const void* out,
+                                               const void* dout, const float* lse, int64_t batch,
+                                               int64_t q_heads, int64_t kv_heads, int64_t seq,
+                                               int64_t head_dim, const int64_t* strides, int mode, int grad,
+                                               int exp2_route, int causal, float scale, float cap,
+                                               float sigmoid_bias, void* stream);
 /* Allocation-free form of launch_flash_attention_bwd_strided_bf16: no
  * counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -20,7 +20,7 @@ def declared_symbols():
     """Function names declared by include/spline_ops_hip.h (after macro expansion)."""
     out = subprocess.run(["gcc", "-E", "-P", "-x", "c", HEADER], check=True,
                          stdout=subprocess.PIPE, text=True).stdout
-    names = re.findall(r"\bint\s+(\w+)\s*\(", out)
+    names = re.findall(r"\b(?:int|int64_t)\s+(\w+)\s*\(", out)
     return sorted(set(names))
 
 

@@ -203,15 +203,20 @@ def test_no_register_spills_outside_the_measured_exception(metadata):
     spill up to 4 registers / 20 bytes.  No forward kernel spills: the
     packed FP16 exp2 programs, whose 4-wave head_dim-128 blocks would (both
     lanes of each packed pair stay live), run 8-wave blocks at head_dim 128
-    whatever the number of query blocks, so those kernels are not built."""
+    whatever the number of query blocks, so those kernels are not built.
+    The softcap dK/dV kernels at head_dim 64 that also store dS for the
+    dS-keeping backward spill up to 10 registers / 28 bytes (measured: that
+    backward is still 1.1-1.3x the recomputing one)."""
     assert len(metadata) > 900
     softmax = r"(0|1|2|1[2-9]|2[01])"  # modes with an exp2 program or the hardware exp2
-    aligned = re.compile(rf"pt::flash_bwd_dkdv_kernel<{softmax}, 0, \d+, 64, 8, false>$")
-    ragged = re.compile(rf"pt::flash_bwd_dkdv_kernel<{softmax}, 0, \d+, 64, 8, true>$|"
-                        r"pt::flash_bwd_dkdv_kernel<4, \d, 0, 64, 8, true>$")
+    aligned = re.compile(rf"pt::flash_bwd_dkdv_kernel<{softmax}, 0, \d+, 64, 8, false, false>$")
+    ragged = re.compile(rf"pt::flash_bwd_dkdv_kernel<{softmax}, 0, \d+, 64, 8, true, false>$|"
+                        r"pt::flash_bwd_dkdv_kernel<4, \d, 0, 64, 8, true, false>$")
+    keeps_ds = re.compile(r"pt::flash_bwd_dkdv_kernel<[34], \d, 0, 64, 8, false, true>$")
     forward = [n for n, spill, scratch in metadata if "flash_fwd_kernel<" in n and (spill or scratch)]
     assert not forward, forward
     bad = [(n, spill, scratch) for n, spill, scratch in metadata
            if (spill or scratch) and not (aligned.search(n) and spill <= 4 and scratch <= 16)
-           and not (ragged.search(n) and spill <= 4 and scratch <= 20)]
+           and not (ragged.search(n) and spill <= 4 and scratch <= 20)
+           and not (keeps_ds.search(n) and spill <= 10 and scratch <= 28)]
     assert not bad, bad
