@@ -31,6 +31,38 @@ struct B3Consts {
     static constexpr float clamp = bf16_value(6.0f);
 };
 
+// The six coefficients of each row as FP16 pairs, two to a word: every
+// coefficient of the deployed rows is exactly an FP16 value (the smallest,
+// 0.11328125 / 4096 = 29 * 2^-20, an FP16 subnormal), so one 32-bit select
+// per word picks two of the lane's row coefficients and v_fma_mix_f32 reads
+// each half as the exact FP32 operand of its FMA: three selects per score
+// where one per coefficient took six, with the same FMAs and roundings.
+constexpr bool f16_exact(float c) { return (float)(_Float16)c == c; }
+constexpr uint32_t f16_word(float hi, float lo) {
+    return ((uint32_t)f16_bits_rne(hi) << 16) | f16_bits_rne(lo);
+}
+struct B3Pairs {
+    using C = B3Consts;
+    // [c3 : c2], [c1 : c0] and the derivative's [slope : intercept], row 0 / 1
+    static constexpr uint32_t c32_0 = f16_word(C::r0[3], C::r0[2]), c32_1 = f16_word(C::r1[3], C::r1[2]);
+    static constexpr uint32_t c10_0 = f16_word(C::r0[1], C::r0[0]), c10_1 = f16_word(C::r1[1], C::r1[0]);
+    static constexpr uint32_t g10_0 = f16_word(C::g0[1], C::g0[0]), g10_1 = f16_word(C::g1[1], C::g1[0]);
+};
+static_assert(f16_exact(B3Consts::r0[0]) && f16_exact(B3Consts::r0[1]) && f16_exact(B3Consts::r0[2]) &&
+              f16_exact(B3Consts::r0[3]) && f16_exact(B3Consts::r1[0]) && f16_exact(B3Consts::r1[1]) &&
+              f16_exact(B3Consts::r1[2]) && f16_exact(B3Consts::r1[3]) && f16_exact(B3Consts::g0[0]) &&
+              f16_exact(B3Consts::g0[1]) && f16_exact(B3Consts::g1[0]) && f16_exact(B3Consts::g1[1]),
+              "a B3 coefficient is not an FP16 value");
+
+// The row's pair word, kept opaque so that the compiler selects the packed
+// word (one v_cndmask_b32) instead of folding the FP16 widening back into
+// two selects of FP32 constants.
+__device__ __forceinline__ h2_t b3_row_pair(bool row, uint32_t w0, uint32_t w1) {
+    uint32_t r = row ? w1 : w0;
+    asm("" : "+v"(r));
+    return as_h2(r);
+}
+
 // One lane on a BF16 value held in FP32.  NaN follows the audit's Python
 // semantics: the clamp keeps NaN, max(0, NaN) gives 0, the derivative is NaN.
 // OPEN_Y (probability only) returns y before its final rounding, for callers
@@ -40,19 +72,23 @@ template <bool WITH_GRAD, bool OPEN_Y = false>
 __device__ __forceinline__ void b3_lane(float x, float& y, float& dy) {
     static_assert(!(WITH_GRAD && OPEN_Y), "the derivative multiplies the rounded probability");
     using C = B3Consts;
+    using P = B3Pairs;
     const bool row = x >= C::split;
     const float xc = __builtin_elementwise_minimum(
         __builtin_elementwise_maximum(x, -C::clamp), C::clamp);
-    float f = bfma(xc, row ? C::r1[3] : C::r0[3], row ? C::r1[2] : C::r0[2]);
-    f = bfma(xc, f, row ? C::r1[1] : C::r0[1]);
+    const h2_t c32 = b3_row_pair(row, P::c32_0, P::c32_1);
+    const h2_t c10 = b3_row_pair(row, P::c10_0, P::c10_1);
+    float f = bfma(xc, (float)c32.y, (float)c32.x);
+    f = bfma(xc, f, (float)c10.y);
     // y = max(0, bf16(v)) taken as bf16(max(0, v)): RNE is monotone and maps
     // 0 to +0, so both give +0 for v <= 0 (and for NaN) and bf16(v) for v > 0.
     // The maximum then reads the FMA's own result, which needs no NaN
     // quieting, instead of the bits of the packed rounding.
-    const float v = __builtin_fmaf(xc, f, row ? C::r1[0] : C::r0[0]);
+    const float v = __builtin_fmaf(xc, f, (float)c10.x);
     y = OPEN_Y ? (v > 0.0f ? v : 0.0f) : rbf(v > 0.0f ? v : 0.0f);
     if constexpr (WITH_GRAD) {
-        const float fac = bfma(xc, row ? C::g1[1] : C::g0[1], row ? C::g1[0] : C::g0[0]);
+        const h2_t g = b3_row_pair(row, P::g10_0, P::g10_1);
+        const float fac = bfma(xc, (float)g.y, (float)g.x);
         dy = y * fac;  // rounded once by the final pack
     }
 }
