@@ -396,7 +396,10 @@ def attention_rows_at(lib, reps: int, shape, eager_launches: int = 0):
     hardware exp/rcp.  Causal FLOPs: forward 4 B Hq S^2 D / 2 (two products
     over the lower triangle), backward 2.5x that (five products, the usual
     FlashAttention count; the kernels recompute S and dP once more, so they
-    issue 7/5 of it).  The bound is the dense BF16 MFMA peak.  With
+    issue 7/5 of it).  The bound is the dense BF16 MFMA peak.  The softmax
+    rows also carry PyTorch's own scaled_dot_product_attention on the same
+    operands (torch_sdpa_us, its backend, and every kernel's
+    `<label>_vs_torch_sdpa` = SDPA time / kernel time).  With
     eager_launches > 0 each case is only launched that many times (a counter
     pass) and nothing is timed."""
     import ctypes
@@ -486,7 +489,71 @@ def attention_rows_at(lib, reps: int, shape, eager_launches: int = 0):
             row["gb200_native_us"], row["gb200_poly_us"] = gb200
             row["gb200_speedup"] = round(gb200[0] / gb200[1], 3)
         rows.append(row)
+    if not eager_launches:
+        # PyTorch's own causal softmax attention on the same operands: the
+        # baseline a user without this library runs (softmax rows only; the
+        # softcap and sigmoid functions have no SDPA counterpart)
+        sdpa = torch_sdpa_times(q, k, v, do, reps)
+        for row in rows:
+            direction = row["function"].split()[0].split("_")[1]
+            if "softmax" not in row["function"] or direction not in sdpa:
+                continue
+            us, backend = sdpa[direction]
+            row["torch_sdpa_us"], row["torch_sdpa_backend"] = round(us, 2), backend
+            for key in [k_ for k_ in row if k_.endswith("_us") and k_ != "torch_sdpa_us"]:
+                row[key[:-3] + "_vs_torch_sdpa"] = round(us / row[key], 3)
     return rows
+
+
+def torch_sdpa_times(q, k, v, do, reps: int):
+    """PyTorch-ROCm's causal softmax attention on the same BF16 operands
+    ([B, H, S, D], K and V expanded to the query heads):
+    torch.nn.functional.scaled_dot_product_attention restricted to its flash
+    and memory-efficient backends, the faster of the two per direction.  The
+    math backend is never enabled (it runs batched BF16 products on
+    transposed views); a backend this build of torch lacks raises and is
+    skipped.  Forward: the call; backward: torch.autograd.grad of one
+    retained forward (dQ, dK, dV).  Eager launches between two events on the
+    current stream, median of 3 rounds.  Returns {"fwd"|"bwd": (µs, backend)}."""
+    import statistics
+
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    rep = q.shape[1] // k.shape[1]
+    kr = k.repeat_interleave(rep, dim=1).contiguous()
+    vr = v.repeat_interleave(rep, dim=1).contiguous()
+    n = max(5, reps // 10)
+    best = {}
+    for name, backend in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([backend]):
+                qq, kk, vv = (t.detach().clone().requires_grad_() for t in (q, kr, vr))
+                out = sdpa(qq, kk, vv, is_causal=True)
+                calls = (("fwd", lambda: sdpa(q, kr, vr, is_causal=True)),
+                         ("bwd", lambda: torch.autograd.grad(out, (qq, kk, vv), do, retain_graph=True)))
+                for direction, fn in calls:
+                    for _ in range(3):
+                        fn()
+                    torch.cuda.synchronize()
+                    rounds = []
+                    for _ in range(3):
+                        start = torch.cuda.Event(enable_timing=True)
+                        stop = torch.cuda.Event(enable_timing=True)
+                        start.record()
+                        for _ in range(n):
+                            fn()
+                        stop.record()
+                        torch.cuda.synchronize()
+                        rounds.append(start.elapsed_time(stop) * 1e3 / n)
+                    us = statistics.median(rounds)
+                    if direction not in best or us < best[direction][0]:
+                        best[direction] = (us, name)
+                del qq, kk, vv, out
+        except RuntimeError:
+            continue
+    return best
 
 
 # The reference's complete-attention component times on GB200
