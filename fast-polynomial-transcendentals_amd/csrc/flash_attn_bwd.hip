@@ -824,10 +824,12 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
 // dQ^T += K^T dS^T.  A block of 4 waves owns 128 queries of one query head
 // (32 per wave), streams 64-key tiles of K through LDS (K^T fragments by the
 // transposing loads of frag_tr32) and loads each chunk straight into the B
-// fragment registers.  Every load is issued one tile ahead; the loop is
-// unrolled by the tile parity, so no register copy waits for a load.  Under
-// the causal mask a wave reads the chunks of keys up to its last query,
-// the ones the dK/dV kernel wrote.  S a multiple of 128.
+// fragment registers.  K is loaded one tile ahead and dS two (a ring of
+// three fragment sets: measured on MI355X 1.02x for the whole head_dim-128
+// backward against one tile ahead, bit-identical); the loop is unrolled by
+// six, so every ring index is static and no register copy waits for a
+// load.  Under the causal mask a wave multiplies the chunks of keys up to
+// its last query, the ones the dK/dV kernel wrote.  S a multiple of 128.
 // ---------------------------------------------------------------------------
 template <int HD>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 4 : 2)))
@@ -856,59 +858,65 @@ flash_bwd_dq_ds_kernel(AttnBwdParams p) {
 
     const int krow = tid / kChunks, kcol = (tid % kChunks) * 8;
     const uint16_t* kp = p.k + b * p.ks.b + kvh * p.ks.h + krow * p.ks.s + kcol;
-    u32x4_t kr[2][kPasses];  // K rows of the tiles two ahead, by tile parity
-    u32x4_t dsf[2][4];       // dS fragments of this tile and the next, by parity
+    u32x4_t kr[kPasses];  // K rows of the next tile
+    u32x4_t dsf[3][4];    // dS fragments of this tile and the next two, by t mod 3
     const int64_t ktiles = p.seq / kKT;
     const int64_t ncausal = p.causal ? (qb + 1) * (128 / kKT) : ktiles;
     const int64_t nkt = ncausal < ktiles ? ncausal : ktiles;
     const int tr_off = (4 * h + ((lane & 15) >> 2)) * kRS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    auto kload = [&](int par, int64_t t) {
+    auto kload = [&](int64_t t) {
 #pragma unroll
         for (int j = 0; j < kPasses; ++j)
-            kr[par][j] = *reinterpret_cast<const u32x4_t*>(kp + (t * kKT + kRowsPass * j) * p.ks.s);
+            kr[j] = *reinterpret_cast<const u32x4_t*>(kp + (t * kKT + kRowsPass * j) * p.ks.s);
     };
     auto kstore = [&](int par) {
 #pragma unroll
         for (int j = 0; j < kPasses; ++j)
-            *reinterpret_cast<u32x4_t*>(&ktile[par][(krow + kRowsPass * j) * kRS + kcol]) = kr[par][j];
+            *reinterpret_cast<u32x4_t*>(&ktile[par][(krow + kRowsPass * j) * kRS + kcol]) = kr[j];
     };
-    auto dload = [&](int par, int64_t t) {  // groups past the causal limit were not written: zero
+    // Every 16-key group of the tiles a wave walks lies inside the
+    // workspace (group < S / 16); groups past the causal limit hold no dS
+    // and the products skip them.
+    auto dload = [&](int slot, int64_t t) {
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            const int64_t kg = 4 * t + cc;
-            dsf[par][cc] = kg <= kglim ? __builtin_nontemporal_load(dsrc + kg * 64) : (u32x4_t){0u, 0u, 0u, 0u};
-        }
+        for (int cc = 0; cc < 4; ++cc) dsf[slot][cc] = __builtin_nontemporal_load(dsrc + (4 * t + cc) * 64);
     };
-    // tile t of parity P: K of tile t in ktile[P], its dS in dsf[P]; issue K
-    // of t + 2 (into kr[P], whose tile is staged) and dS of t + 1, stage K of
-    // t + 1 after the products
-    auto step = [&](auto par_c, int64_t t) {
-        constexpr int P = decltype(par_c)::value;
-        if (t + 2 < nkt) kload(P, t + 2);
-        if (t + 1 < nkt) dload(P ^ 1, t + 1);
+    // tile t: K in ktile[t % 2], dS in dsf[t % 3]; issue K of t + 1 (staged
+    // after the products) and dS of t + 2
+    auto step = [&](auto kpar_c, auto dslot_c, int64_t t) {
+        constexpr int KP = decltype(kpar_c)::value, DS = decltype(dslot_c)::value;
+        if (t + 1 < nkt) kload(t + 1);
+        if (t + 2 < nkt) dload((DS + 2) % 3, t + 2);
         if (4 * t <= kglim) {  // wave-uniform
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
                 if (4 * t + cc <= kglim) {
-                    const bf16x8_t sf = __builtin_bit_cast(bf16x8_t, dsf[P][cc]);
+                    const bf16x8_t sf = __builtin_bit_cast(bf16x8_t, dsf[DS][cc]);
 #pragma unroll
                     for (int dt = 0; dt < HD / 32; ++dt)
-                        dqacc[dt] = mfma32(frag_tr32<HD>(ktile[P] + tr_off, dt, cc), sf, dqacc[dt]);
+                        dqacc[dt] = mfma32(frag_tr32<HD>(ktile[KP] + tr_off, dt, cc), sf, dqacc[dt]);
                 }
             }
         }
-        if (t + 1 < nkt) kstore(P ^ 1);
+        if (t + 1 < nkt) kstore(KP ^ 1);
         __syncthreads();
     };
-    kload(0, 0);
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    kload(0);
     kstore(0);
-    if (nkt > 1) kload(1, 1);
     dload(0, 0);
+    if (nkt > 1) dload(1, 1);
     __syncthreads();
-    for (int64_t t = 0; t < nkt; t += 2) {
-        step(std::integral_constant<int, 0>{}, t);
-        if (t + 1 < nkt) step(std::integral_constant<int, 1>{}, t + 1);
+    for (int64_t t = 0; t < nkt; t += 6) {
+        step(I0{}, I0{}, t);
+        if (t + 1 < nkt) step(I1{}, I1{}, t + 1);
+        if (t + 2 < nkt) step(I0{}, I2{}, t + 2);
+        if (t + 3 < nkt) step(I1{}, I0{}, t + 3);
+        if (t + 4 < nkt) step(I0{}, I1{}, t + 4);
+        if (t + 5 < nkt) step(I1{}, I2{}, t + 5);
     }
 
     uint16_t* dqr = p.dq + b * p.dqs.b + head * p.dqs.h + qrow * p.dqs.s;
