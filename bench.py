@@ -551,7 +551,7 @@ def torch_sdpa_times(q, k, v, do, reps: int):
                     if direction not in best or us < best[direction][0]:
                         best[direction] = (us, name)
                 del qq, kk, vv, out
-        except RuntimeError:
+        except (RuntimeError, NotImplementedError):
             continue
     return best
 
